@@ -1,0 +1,173 @@
+"""ctypes loader of libgt_attn.so.
+
+Same conventions as the reference's loader (gguf_train/_C.py): one CDLL with its argtypes and
+restypes declared up front, `check_ptr` / `check_rc` turning a NULL / non-zero native result
+into a Python exception built from the thread-local `gt_last_error()`, and the
+"IndexError: " message prefix mapping to IndexError (gguf_train/_C.py:680-710).
+
+The library is built in-tree (python -m gguf_train_amd._build).  Importing this module never
+builds, downloads or falls back to anything: a missing library is an ImportError.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from ctypes import POINTER, c_char_p, c_float, c_int, c_int64, c_size_t, c_uint64, c_void_p
+from pathlib import Path
+
+_PKG_DIR = Path(__file__).resolve().parent
+LIB_PATH = _PKG_DIR / "libgt_attn.so"
+
+# dtype / device codes (csrc/gguf_train.h:22-44)
+GT_F32, GT_F16, GT_BF16, GT_F64 = 0, 1, 2, 3
+GT_I8, GT_U8, GT_I16, GT_I32, GT_I64, GT_BOOL = 4, 5, 6, 7, 8, 9
+GT_Q_BASE = 100
+GT_Q8_0 = GT_Q_BASE + 8
+GT_DEV_CPU, GT_DEV_CUDA = 0, 1
+
+
+def _load_native() -> ctypes.CDLL:
+    if not LIB_PATH.exists():
+        raise ImportError(
+            f"{LIB_PATH} is not built; build it with `python -m gguf_train_amd._build --lib` "
+            "(hipcc, gfx950). There is no CPU fallback."
+        )
+    return ctypes.CDLL(str(LIB_PATH))
+
+
+def _configure(lib: ctypes.CDLL) -> ctypes.CDLL:
+    p_i64 = POINTER(c_int64)
+    p_vp = POINTER(c_void_p)
+
+    lib.gt_init.argtypes = []
+    lib.gt_init.restype = None
+    lib.gt_device_count.argtypes = [c_int]
+    lib.gt_device_count.restype = c_int
+    lib.gt_device_name.argtypes = [c_int, c_int, c_char_p, c_int]
+    lib.gt_device_name.restype = None
+    lib.gt_device_memory.argtypes = [c_int, c_int, POINTER(c_size_t), POINTER(c_size_t)]
+    lib.gt_device_memory.restype = None
+    lib.gt_synchronize.argtypes = [c_int, c_int]
+    lib.gt_synchronize.restype = None
+    lib.gt_last_error.argtypes = []
+    lib.gt_last_error.restype = c_char_p
+    lib.gt_clear_error.argtypes = []
+    lib.gt_clear_error.restype = None
+    lib.gt_set_last_error.argtypes = [c_char_p]
+    lib.gt_set_last_error.restype = None
+    lib.gt_set_stream.argtypes = [c_void_p]
+    lib.gt_set_stream.restype = None
+    lib.gt_get_stream.argtypes = []
+    lib.gt_get_stream.restype = c_void_p
+
+    lib.gt_tensor_empty.argtypes = [c_int, p_i64, c_int, c_int, c_int]
+    lib.gt_tensor_empty.restype = c_void_p
+    lib.gt_tensor_from_data.argtypes = [c_int, p_i64, c_int, c_int, c_int, c_void_p, c_size_t]
+    lib.gt_tensor_from_data.restype = c_void_p
+    lib.gt_tensor_from_external.argtypes = [c_int, p_i64, p_i64, c_int, c_void_p, c_uint64]
+    lib.gt_tensor_from_external.restype = c_void_p
+    lib.gt_external_released.argtypes = [POINTER(c_uint64), c_int64]
+    lib.gt_external_released.restype = c_int64
+    lib.gt_tensor_from_device_ptr.argtypes = [c_int, p_i64, p_i64, c_int, c_int, c_void_p, c_uint64]
+    lib.gt_tensor_from_device_ptr.restype = c_void_p
+    lib.gt_tensor_clone.argtypes = [c_void_p]
+    lib.gt_tensor_clone.restype = c_void_p
+    lib.gt_tensor_view.argtypes = [c_void_p, c_int, p_i64, p_i64, c_int64]
+    lib.gt_tensor_view.restype = c_void_p
+    lib.gt_tensor_contiguous.argtypes = [c_void_p]
+    lib.gt_tensor_contiguous.restype = c_void_p
+    lib.gt_tensor_to_dtype.argtypes = [c_void_p, c_int]
+    lib.gt_tensor_to_dtype.restype = c_void_p
+    lib.gt_tensor_to_device.argtypes = [c_void_p, c_int, c_int]
+    lib.gt_tensor_to_device.restype = c_void_p
+    lib.gt_tensor_free.argtypes = [c_void_p]
+    lib.gt_tensor_free.restype = None
+
+    lib.gt_tensor_ndim.argtypes = [c_void_p]
+    lib.gt_tensor_ndim.restype = c_int
+    lib.gt_tensor_shape.argtypes = [c_void_p, p_i64]
+    lib.gt_tensor_shape.restype = None
+    lib.gt_tensor_strides.argtypes = [c_void_p, p_i64]
+    lib.gt_tensor_strides.restype = None
+    lib.gt_tensor_offset.argtypes = [c_void_p]
+    lib.gt_tensor_offset.restype = c_int64
+    lib.gt_tensor_numel.argtypes = [c_void_p]
+    lib.gt_tensor_numel.restype = c_int64
+    lib.gt_tensor_dtype.argtypes = [c_void_p]
+    lib.gt_tensor_dtype.restype = c_int
+    lib.gt_tensor_device_type.argtypes = [c_void_p]
+    lib.gt_tensor_device_type.restype = c_int
+    lib.gt_tensor_device_index.argtypes = [c_void_p]
+    lib.gt_tensor_device_index.restype = c_int
+    lib.gt_tensor_is_contiguous.argtypes = [c_void_p]
+    lib.gt_tensor_is_contiguous.restype = c_int
+    lib.gt_tensor_data_ptr.argtypes = [c_void_p]
+    lib.gt_tensor_data_ptr.restype = c_uint64
+    lib.gt_tensor_storage_nbytes.argtypes = [c_void_p]
+    lib.gt_tensor_storage_nbytes.restype = c_size_t
+    lib.gt_tensor_nbytes.argtypes = [c_void_p]
+    lib.gt_tensor_nbytes.restype = c_size_t
+    lib.gt_tensor_elem_size.argtypes = [c_int]
+    lib.gt_tensor_elem_size.restype = c_size_t
+    lib.gt_tensor_copy_to_host.argtypes = [c_void_p, c_void_p, c_size_t]
+    lib.gt_tensor_copy_to_host.restype = c_int
+    lib.gt_tensor_copy_from_host.argtypes = [c_void_p, c_void_p, c_size_t]
+    lib.gt_tensor_copy_from_host.restype = c_int
+    lib.gt_tensor_copy_inplace.argtypes = [c_void_p, c_void_p]
+    lib.gt_tensor_copy_inplace.restype = c_int
+    lib.gt_tensor_to_dlpack.argtypes = [c_void_p]
+    lib.gt_tensor_to_dlpack.restype = c_void_p
+
+    # attention (csrc/gguf_train.h:311; gguf_train/_C.py:471-472)
+    lib.gt_flash_attention.argtypes = [c_void_p, c_void_p, c_void_p, c_void_p, c_float, c_int]
+    lib.gt_flash_attention.restype = c_void_p
+    lib.gt_flash_attention_lse.argtypes = [c_void_p, c_void_p, c_void_p, c_void_p, c_float, c_int, p_vp, p_vp]
+    lib.gt_flash_attention_lse.restype = c_int
+    lib.gt_flash_attention_backward.argtypes = [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+                                                c_void_p, c_float, c_int, p_vp, p_vp, p_vp]
+    lib.gt_flash_attention_backward.restype = c_int
+
+    # Q8_0 (csrc/gguf_train.h:376-377)
+    lib.gt_quantize.argtypes = [c_void_p, c_int]
+    lib.gt_quantize.restype = c_void_p
+    lib.gt_dequantize.argtypes = [c_void_p, c_int]
+    lib.gt_dequantize.restype = c_void_p
+
+    lib.gt_init()
+    return lib
+
+
+lib = _configure(_load_native())
+
+
+def last_error() -> str:
+    msg = lib.gt_last_error()
+    return msg.decode("utf-8", errors="replace") if msg else ""
+
+
+_NATIVE_ERROR_TYPES = {"IndexError": IndexError}
+
+
+def _native_error(ctx: str, err: str, fallback: str) -> Exception:
+    for name, exc_type in _NATIVE_ERROR_TYPES.items():
+        tag = name + ": "
+        if err.startswith(tag):
+            return exc_type(err[len(tag):])
+    if ctx and err:
+        return RuntimeError(err if err.startswith(ctx + ":") else f"{ctx}: {err}")
+    return RuntimeError(err or ctx or fallback)
+
+
+def check_ptr(ptr: int | None, ctx: str = "") -> int:
+    if not ptr:
+        raise _native_error(ctx, last_error(), "Native operation returned NULL")
+    return ptr
+
+
+def check_rc(rc: int, ctx: str = "") -> None:
+    if rc != 0:
+        raise _native_error(ctx, last_error(), f"Native operation failed with code {rc}")
+
+
+def device_count() -> int:
+    return int(lib.gt_device_count(GT_DEV_CUDA))

@@ -1,0 +1,25 @@
+"""gguf_train_amd - MI355X (gfx950) attention for GGUF_train's operator API.
+
+The product is libgt_attn.so (hand-written HIP kernels behind the reference's C ABI,
+include/gt_attn.h).  This package is its Python host: the ctypes loader (_C), the
+PyTorch <-> handle bridge (_bridge), FlashAttentionFn, scaled_dot_product_attention and
+MultiheadAttention with the reference's signatures, and the GGUF Q8_0 codec.
+"""
+
+from . import _C
+from ._bridge import QuantizedTensor
+from ._functions import FlashAttentionFn
+from ._ops import dequantize, flash_attention, flash_attention_backward, flash_attention_lse, quantize
+from . import nn
+
+__all__ = [
+    "_C",
+    "QuantizedTensor",
+    "FlashAttentionFn",
+    "flash_attention",
+    "flash_attention_lse",
+    "flash_attention_backward",
+    "quantize",
+    "dequantize",
+    "nn",
+]

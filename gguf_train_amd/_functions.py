@@ -1,0 +1,42 @@
+"""Autograd Functions of the attention path.
+
+`FlashAttentionFn` keeps the reference's signature and behaviour
+(gguf_train/_functions.py:1922-1965): forward(ctx, q, k, v, mask, scale, is_causal) saves
+its inputs, sets ctx.scale (1/sqrt(D) when None) and ctx.is_causal, and calls the native
+gt_flash_attention; the backward returns (dq, dk, dv, None, None, None) with a GQA group's
+gradients summed into its kv head.  The reference's Python backward composition
+(matmul/softmax over full (B,H,L,S) intermediates) is replaced by the native recompute-based
+gt_flash_attention_backward, which works from the saved output and log-sum-exp.
+
+The Function subclasses torch.autograd.Function, whose engine - like the reference engine
+(gguf_train/_autograd_engine.py:325-326) - casts each gradient to its input's dtype.
+"""
+
+from __future__ import annotations
+
+import math
+
+import torch
+
+from . import _ops
+
+
+class FlashAttentionFn(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, q, k, v, mask, scale, is_causal):
+        ctx.scale = float(scale) if scale is not None else (1.0 / math.sqrt(q.shape[-1]))
+        ctx.is_causal = bool(is_causal)
+        if any(ctx.needs_input_grad[:3]):
+            out, lse = _ops.flash_attention_lse(q, k, v, mask, ctx.scale, ctx.is_causal)
+            ctx.save_for_backward(q, k, v, mask, out, lse)
+        else:
+            out = _ops.flash_attention(q, k, v, mask, ctx.scale, ctx.is_causal)
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        if grad_out is None:
+            return (None,) * 6
+        q, k, v, mask, out, lse = ctx.saved_tensors
+        dq, dk, dv = _ops.flash_attention_backward(grad_out, q, k, v, mask, out, lse, ctx.scale, ctx.is_causal)
+        return (dq, dk, dv, None, None, None)

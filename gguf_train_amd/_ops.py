@@ -1,0 +1,79 @@
+"""Thin Python calls of the native attention and Q8_0 entry points on PyTorch tensors."""
+
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _C
+from ._bridge import QuantizedTensor, adopt, adopt_quantized, bind_stream, borrow
+
+_GT_DTYPE = {torch.float32: _C.GT_F32, torch.float16: _C.GT_F16, torch.bfloat16: _C.GT_BF16,
+             torch.float64: _C.GT_F64}
+
+
+def _device_of(*ts) -> torch.device:
+    for t in ts:
+        if t is not None:
+            return t.device
+    return torch.device("cpu")
+
+
+def flash_attention(q, k, v, mask=None, scale: float = 0.0, is_causal: bool = False) -> torch.Tensor:
+    """gt_flash_attention (csrc/gguf_train.h:311) on PyTorch tensors."""
+    bind_stream(_device_of(q))
+    hq, hk, hv = borrow(q), borrow(k), borrow(v)
+    hm = borrow(mask) if mask is not None else None
+    ptr = _C.lib.gt_flash_attention(hq.ptr, hk.ptr, hv.ptr, hm.ptr if hm else None, ctypes.c_float(scale),
+                                    1 if is_causal else 0)
+    return adopt(ptr, "flash_attention")
+
+
+def flash_attention_lse(q, k, v, mask=None, scale: float = 0.0, is_causal: bool = False):
+    """Forward that also returns the per-row log-sum-exp (B, H, L) needed by the backward."""
+    bind_stream(_device_of(q))
+    hq, hk, hv = borrow(q), borrow(k), borrow(v)
+    hm = borrow(mask) if mask is not None else None
+    po, pl = ctypes.c_void_p(), ctypes.c_void_p()
+    rc = _C.lib.gt_flash_attention_lse(hq.ptr, hk.ptr, hv.ptr, hm.ptr if hm else None, ctypes.c_float(scale),
+                                       1 if is_causal else 0, ctypes.byref(po), ctypes.byref(pl))
+    _C.check_rc(rc, "flash_attention")
+    return adopt(po.value, "flash_attention"), adopt(pl.value, "flash_attention")
+
+
+def flash_attention_backward(dout, q, k, v, mask, out, lse, scale: float, is_causal: bool):
+    """Native recompute-based backward: (dq, dk, dv) in float32 (float64 for float64 inputs)."""
+    bind_stream(_device_of(q))
+    hg, hq, hk, hv = borrow(dout), borrow(q), borrow(k), borrow(v)
+    hm = borrow(mask) if mask is not None else None
+    ho = borrow(out) if out is not None else None
+    hl = borrow(lse) if lse is not None else None
+    pq, pk, pv = ctypes.c_void_p(), ctypes.c_void_p(), ctypes.c_void_p()
+    rc = _C.lib.gt_flash_attention_backward(hg.ptr, hq.ptr, hk.ptr, hv.ptr, hm.ptr if hm else None,
+                                            ho.ptr if ho else None, hl.ptr if hl else None, ctypes.c_float(scale),
+                                            1 if is_causal else 0, ctypes.byref(pq), ctypes.byref(pk),
+                                            ctypes.byref(pv))
+    _C.check_rc(rc, "flash_attention_backward")
+    return (adopt(pq.value, "flash_attention_backward"), adopt(pk.value, "flash_attention_backward"),
+            adopt(pv.value, "flash_attention_backward"))
+
+
+def quantize(t: torch.Tensor, qtype: str = "q8_0") -> QuantizedTensor:
+    """gt_quantize (csrc/gguf_train.h:376); rows of last-dim length, GGUF Q8_0 blocks."""
+    if qtype != "q8_0":
+        raise ValueError(f"unsupported quantization type {qtype!r} (only 'q8_0')")
+    bind_stream(t.device)
+    h = borrow(t)
+    ptr = _C.lib.gt_quantize(h.ptr, _C.GT_Q8_0 - _C.GT_Q_BASE)
+    return adopt_quantized(ptr, t.shape, "quantize")
+
+
+def dequantize(qt: QuantizedTensor, dtype: torch.dtype = torch.float32) -> torch.Tensor:
+    """gt_dequantize (csrc/gguf_train.h:377): y = float(qs) * float(d), then `dtype`."""
+    if dtype not in _GT_DTYPE:
+        raise ValueError(f"unsupported dequantize dtype {dtype}")
+    bind_stream(qt.device)
+    h = borrow(qt)
+    ptr = _C.lib.gt_dequantize(h.ptr, _GT_DTYPE[dtype])
+    return adopt(ptr, "dequantize")

@@ -1,0 +1,49 @@
+// Parameters shared by the attention kernels and the host-side dispatcher.
+//
+// Layouts (elements, innermost dimension contiguous):
+//   q  (B, H,   L, D)   element (b,h,l,d)  at q + b*q_sb + h*q_sh + l*q_sl + d
+//   k  (B, Hkv, S, D)   element (b,g,s,d)  at k + b*k_sb + g*k_sh + s*k_ss + d
+//   v  (B, Hkv, S, Dv)  element (b,g,s,d)  at v + b*v_sb + g*v_sh + s*v_ss + d
+//   o  (B, H,   L, Dv)  dense
+//   lse (B, H, L)       dense, natural-log log-sum-exp of the scaled, masked scores
+//   mask                element (b,h,l,s) at mask + b*m_sb + h*m_sh + l*m_sl + s*m_ss; a
+//                       broadcast dimension has stride 0.  mask_bool: bytes, 0 = blocked;
+//                       otherwise values of the compute precision (float, or double for the
+//                       float64 path) added to the scores.
+// Query head h reads kv head h / (H / Hkv) (csrc/gt_ops_nn.cpp:2432,2471).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+struct AttnFwdArgs {
+    const void *q;
+    const void *k;
+    const void *v;
+    const void *mask;
+    void *o;
+    void *lse;  // float (double on the float64 path) or null
+    int64_t B, H, Hkv, L, S, D, Dv;
+    int64_t q_sb, q_sh, q_sl;
+    int64_t k_sb, k_sh, k_ss;
+    int64_t v_sb, v_sh, v_ss;
+    int64_t m_sb, m_sh, m_sl, m_ss;
+    float scale;
+    int causal;
+    int mask_bool;
+    int out_dtype;  // gt_dtype of o
+};
+
+struct AttnBwdArgs {
+    AttnFwdArgs f;         // q/k/v/mask/o/lse as in the forward (o and lse are inputs here)
+    const void *dout;      // (B,H,L,Dv) dense, compute dtype
+    void *dq;              // (B,H,L,D) dense, float (double on the float64 path)
+    void *dk;              // (B,Hkv,S,D) dense
+    void *dv;              // (B,Hkv,S,Dv) dense
+    void *delta;           // (B,H,L) scratch: rowsum(P * dP)
+};
+
+// Launchers.  `cd` is the compute dtype of q/k/v (GT_F32/GT_F16/GT_BF16/GT_F64).
+hipError_t launch_attn_generic_fwd(const AttnFwdArgs &a, int cd, hipStream_t s);
+hipError_t launch_attn_generic_bwd(const AttnBwdArgs &a, int cd, hipStream_t s);

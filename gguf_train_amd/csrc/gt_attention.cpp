@@ -1,0 +1,413 @@
+// Attention entry points of libgt_attn.so: argument validation with the reference's messages,
+// operand staging onto the device, kernel selection, and the Q8_0 codec entry points.
+//
+// gt_flash_attention keeps the contract of csrc/gt_ops_nn.cpp:2423-2525; the kernels it
+// dispatches to live in attn_generic.hip (any dtype/shape), attn_decode.hip (single-query
+// split-K over the KV length, fp16/bf16/Q8_0 K/V) and attn_prefill.hip (fp16/bf16 MFMA).
+
+#include "attn_common.h"
+#include "gt_internal.h"
+
+#include <cmath>
+#include <string>
+#include <vector>
+
+namespace {
+
+// Owns the temporaries of one call.
+struct Temps {
+    std::vector<gt_tensor *> list;
+    gt_tensor *keep(gt_tensor *t) {
+        if (t) list.push_back(t);
+        return t;
+    }
+    ~Temps() {
+        for (gt_tensor *t : list) gt_tensor_free(t);
+    }
+};
+
+bool inner_contiguous(const gt_tensor *t) { return t->ndim == 0 || t->shape[t->ndim - 1] <= 1 || t->strides[t->ndim - 1] == 1; }
+
+// A device view of `t` in dtype `cd` whose innermost dimension is contiguous: `t` itself when
+// it already is one, otherwise a dense converted copy (kept in `tmp`).
+const gt_tensor *stage(const gt_tensor *t, int dev, int cd, Temps &tmp) {
+    if (t->device_type == GT_DEV_CUDA && t->device_index == dev && t->dtype == cd && inner_contiguous(t)) return t;
+    return tmp.keep(gt_to_device_dense(t, dev, cd));
+}
+
+// Same checks and messages as csrc/gt_ops_nn.cpp:2425-2454.
+bool validate(const char *who, const gt_tensor *q, const gt_tensor *k, const gt_tensor *v, const gt_tensor *mask) {
+    if (!q || !k || !v || q->ndim != 4 || k->ndim != 4 || v->ndim != 4) {
+        gt_set_error("flash_attention expects 4D q, k, v tensors (B, H, L, D)");
+        return false;
+    }
+    const int64_t B = q->shape[0], H = q->shape[1], L = q->shape[2], D = q->shape[3];
+    const int64_t Hkv = k->shape[1], S = k->shape[2];
+    if (Hkv == 0 || H % Hkv != 0) {
+        gt_set_error("flash_attention: num_heads must be divisible by num_kv_heads");
+        return false;
+    }
+    if (k->shape[0] != B || v->shape[0] != B || v->shape[1] != Hkv || v->shape[2] != S || k->shape[3] != D) {
+        gt_set_error("flash_attention: q (B, H, L, D), k (B, H_kv, S, D) and v (B, H_kv, S, Dv) do not fit together");
+        return false;
+    }
+    if (mask) {
+        const int64_t want[4] = {B, H, L, S};
+        bool fits = mask->ndim == 2 || mask->ndim == 4;
+        for (int i = 0; fits && i < mask->ndim; ++i) {
+            const int64_t m = mask->shape[i];
+            fits = (m == 1 || m == want[4 - mask->ndim + i]);
+        }
+        if (!fits) {
+            std::string shape = "[";
+            for (int i = 0; i < mask->ndim; ++i) shape += (i ? ", " : "") + std::to_string(mask->shape[i]);
+            gt_set_error("flash_attention: attn_mask of shape " + shape + "] cannot be broadcast to the attention weights [" +
+                         std::to_string(B) + ", " + std::to_string(H) + ", " + std::to_string(L) + ", " +
+                         std::to_string(S) + "]");
+            return false;
+        }
+        if (gt_is_quantized(mask->dtype)) {
+            gt_set_error(std::string(who) + ": a quantized attn_mask is not supported");
+            return false;
+        }
+    }
+    if (!gt_is_float(q->dtype)) {
+        gt_set_error(std::string(who) + ": q must be float32, float16, bfloat16 or float64, got " + gt_dtype_name(q->dtype));
+        return false;
+    }
+    for (const gt_tensor *t : {k, v}) {
+        if (!gt_is_float(t->dtype) && t->dtype != GT_Q8_0) {
+            gt_set_error(std::string(who) + ": k and v must be float32, float16, bfloat16, float64 or q8_0, got " +
+                         gt_dtype_name(t->dtype));
+            return false;
+        }
+        if (t->dtype == GT_Q8_0 && (t->shape[3] % 32 != 0 || !gt_is_dense(t) || t->offset != 0)) {
+            gt_set_error(std::string(who) + ": a q8_0 k/v must be contiguous with a head size that is a multiple of 32");
+            return false;
+        }
+    }
+    return true;
+}
+
+// Compute dtype of q/k/v: float64 if any operand is float64; the common dtype when all agree
+// on float32/float16/bfloat16; float32 otherwise (every such widening is exact).
+int compute_dtype(const gt_tensor *q, const gt_tensor *k, const gt_tensor *v) {
+    const int dq = q->dtype, dk = k->dtype == GT_Q8_0 ? GT_F32 : k->dtype, dv = v->dtype == GT_Q8_0 ? GT_F32 : v->dtype;
+    if (dq == GT_F64 || dk == GT_F64 || dv == GT_F64) return GT_F64;
+    if (dq == dk && dk == dv) return dq;
+    return GT_F32;
+}
+
+// Fills the mask fields of `a`: a bool mask is read as bytes; any other dtype is staged as
+// additive values of the compute precision.  Broadcast dimensions get stride 0.
+bool stage_mask(const gt_tensor *mask, int dev, int cd, AttnFwdArgs &a, Temps &tmp) {
+    a.mask = nullptr;
+    a.mask_bool = 0;
+    a.m_sb = a.m_sh = a.m_sl = a.m_ss = 0;
+    if (!mask) return true;
+    const int want = mask->dtype == GT_BOOL ? GT_BOOL : (cd == GT_F64 ? GT_F64 : GT_F32);
+    const gt_tensor *m = mask;
+    if (!(m->device_type == GT_DEV_CUDA && m->device_index == dev && m->dtype == want)) {
+        m = tmp.keep(gt_to_device_dense(mask, dev, want));
+        if (!m) return false;
+    }
+    int64_t st[4] = {0, 0, 0, 0}, sh[4] = {1, 1, 1, 1};
+    for (int i = 0; i < m->ndim; ++i) {
+        sh[4 - m->ndim + i] = m->shape[i];
+        st[4 - m->ndim + i] = m->strides[i];
+    }
+    for (int i = 0; i < 4; ++i) if (sh[i] == 1) st[i] = 0;
+    a.mask = gt_data(m);
+    a.mask_bool = want == GT_BOOL;
+    a.m_sb = st[0];
+    a.m_sh = st[1];
+    a.m_sl = st[2];
+    a.m_ss = st[3];
+    return true;
+}
+
+void fill_qkv(AttnFwdArgs &a, const gt_tensor *q, const gt_tensor *k, const gt_tensor *v) {
+    a.q = gt_data(q);
+    a.k = gt_data(k);
+    a.v = gt_data(v);
+    a.B = q->shape[0];
+    a.H = q->shape[1];
+    a.L = q->shape[2];
+    a.D = q->shape[3];
+    a.Hkv = k->shape[1];
+    a.S = k->shape[2];
+    a.Dv = v->shape[3];
+    a.q_sb = q->strides[0];
+    a.q_sh = q->strides[1];
+    a.q_sl = q->strides[2];
+    if (k->dtype == GT_Q8_0) {  // dense block rows: strides counted in elements of the logical tensor
+        a.k_sb = k->shape[1] * k->shape[2] * k->shape[3];
+        a.k_sh = k->shape[2] * k->shape[3];
+        a.k_ss = k->shape[3];
+    } else {
+        a.k_sb = k->strides[0];
+        a.k_sh = k->strides[1];
+        a.k_ss = k->strides[2];
+    }
+    if (v->dtype == GT_Q8_0) {
+        a.v_sb = v->shape[1] * v->shape[2] * v->shape[3];
+        a.v_sh = v->shape[2] * v->shape[3];
+        a.v_ss = v->shape[3];
+    } else {
+        a.v_sb = v->strides[0];
+        a.v_sh = v->strides[1];
+        a.v_ss = v->strides[2];
+    }
+}
+
+// Moves a device result into a new host tensor when the caller's q lives on the host.
+gt_tensor *deliver(gt_tensor *dev_t, bool to_host) {
+    if (!dev_t || !to_host) return dev_t;
+    gt_tensor *h = gt_new_tensor(dev_t->ndim, dev_t->shape, dev_t->dtype, GT_DEV_CPU, 0);
+    if (h && !gt_copy_device_to_host(h, dev_t)) {
+        gt_tensor_free(h);
+        h = nullptr;
+    }
+    gt_tensor_free(dev_t);
+    return h;
+}
+
+int attention_forward(const char *who, const gt_tensor *q, const gt_tensor *k, const gt_tensor *v,
+                      const gt_tensor *mask, float scale, int is_causal, gt_tensor **out_o, gt_tensor **out_lse) {
+    if (out_o) *out_o = nullptr;
+    if (out_lse) *out_lse = nullptr;
+    if (!validate(who, q, k, v, mask)) return -1;
+    const int dev = q->device_type == GT_DEV_CUDA ? q->device_index : 0;
+    const bool host_io = q->device_type != GT_DEV_CUDA;
+    if (!gt_device_ok(dev)) return -1;
+    const int64_t B = q->shape[0], H = q->shape[1], L = q->shape[2], D = q->shape[3];
+    const int64_t Dv = v->shape[3];
+    if (scale <= 0.0f) scale = 1.0f / std::sqrt((float)D);  // csrc/gt_ops_nn.cpp:2433
+
+    const int cd = compute_dtype(q, k, v);
+    const int lse_dtype = cd == GT_F64 ? GT_F64 : GT_F32;
+    const int64_t osh[4] = {B, H, L, Dv}, lsh[3] = {B, H, L};
+    gt_tensor *o = gt_new_tensor(4, osh, q->dtype, GT_DEV_CUDA, dev);
+    gt_tensor *lse = out_lse ? gt_new_tensor(3, lsh, lse_dtype, GT_DEV_CUDA, dev) : nullptr;
+    if (!o || (out_lse && !lse)) {
+        gt_tensor_free(o);
+        gt_tensor_free(lse);
+        return -1;
+    }
+    Temps tmp;
+    bool ok = true;
+    if (o->numel > 0 || (lse && lse->numel > 0)) {
+        // Q8_0 K/V are dequantized to float32 for the generic kernel (exact values).
+        const gt_tensor *qs = stage(q, dev, cd, tmp);
+        const gt_tensor *ks = k->dtype == GT_Q8_0 ? tmp.keep(gt_dequantize(k, cd)) : stage(k, dev, cd, tmp);
+        const gt_tensor *vs = v->dtype == GT_Q8_0 ? tmp.keep(gt_dequantize(v, cd)) : stage(v, dev, cd, tmp);
+        if (ks && ks->device_type != GT_DEV_CUDA) ks = stage(ks, dev, cd, tmp);
+        if (vs && vs->device_type != GT_DEV_CUDA) vs = stage(vs, dev, cd, tmp);
+        ok = qs && ks && vs;
+        AttnFwdArgs a{};
+        if (ok) {
+            fill_qkv(a, qs, ks, vs);
+            ok = stage_mask(mask, dev, cd, a, tmp);
+        }
+        if (ok) {
+            a.o = gt_data(o);
+            a.lse = lse ? gt_data(lse) : nullptr;
+            a.scale = scale;
+            a.causal = is_causal ? 1 : 0;
+            a.out_dtype = q->dtype;
+            ok = gt_hip_check(launch_attn_generic_fwd(a, cd, gt_stream()), "flash_attention kernel");
+        }
+    }
+    if (!ok) {
+        gt_tensor_free(o);
+        gt_tensor_free(lse);
+        return -1;
+    }
+    o = deliver(o, host_io);
+    if (lse) lse = deliver(lse, host_io);
+    if (!o || (out_lse && !lse)) {
+        gt_tensor_free(o);
+        gt_tensor_free(lse);
+        return -1;
+    }
+    if (out_o) *out_o = o; else gt_tensor_free(o);
+    if (out_lse) *out_lse = lse;
+    return 0;
+}
+
+}  // namespace
+
+extern "C" gt_tensor *gt_flash_attention(const gt_tensor *q, const gt_tensor *k, const gt_tensor *v,
+                                         const gt_tensor *mask, float scale, int is_causal) {
+    gt_tensor *o = nullptr;
+    if (attention_forward("flash_attention", q, k, v, mask, scale, is_causal, &o, nullptr) != 0) return nullptr;
+    return o;
+}
+
+extern "C" int gt_flash_attention_lse(const gt_tensor *q, const gt_tensor *k, const gt_tensor *v, const gt_tensor *mask,
+                                      float scale, int is_causal, gt_tensor **out, gt_tensor **lse) {
+    if (!out || !lse) {
+        gt_set_error("flash_attention_lse: out and lse must not be NULL");
+        return -1;
+    }
+    return attention_forward("flash_attention_lse", q, k, v, mask, scale, is_causal, out, lse);
+}
+
+extern "C" int gt_flash_attention_backward(const gt_tensor *grad_out, const gt_tensor *q, const gt_tensor *k,
+                                           const gt_tensor *v, const gt_tensor *mask, const gt_tensor *out,
+                                           const gt_tensor *lse, float scale, int is_causal, gt_tensor **dq,
+                                           gt_tensor **dk, gt_tensor **dv) {
+    const char *who = "flash_attention_backward";
+    if (!dq || !dk || !dv) {
+        gt_set_error("flash_attention_backward: dq, dk and dv must not be NULL");
+        return -1;
+    }
+    *dq = *dk = *dv = nullptr;
+    if (!validate(who, q, k, v, mask)) return -1;
+    if (k->dtype == GT_Q8_0 || v->dtype == GT_Q8_0) {
+        gt_set_error("flash_attention_backward: q8_0 k/v have no gradient");
+        return -1;
+    }
+    const int64_t B = q->shape[0], H = q->shape[1], L = q->shape[2], D = q->shape[3];
+    const int64_t Hkv = k->shape[1], S = k->shape[2], Dv = v->shape[3];
+    if (!grad_out || grad_out->ndim != 4 || grad_out->shape[0] != B || grad_out->shape[1] != H ||
+        grad_out->shape[2] != L || grad_out->shape[3] != Dv) {
+        gt_set_error("flash_attention_backward: grad_out must have the output's shape (B, H, L, Dv)");
+        return -1;
+    }
+    if (lse && (lse->ndim != 3 || lse->shape[0] != B || lse->shape[1] != H || lse->shape[2] != L)) {
+        gt_set_error("flash_attention_backward: lse must have shape (B, H, L)");
+        return -1;
+    }
+    const int dev = q->device_type == GT_DEV_CUDA ? q->device_index : 0;
+    const bool host_io = q->device_type != GT_DEV_CUDA;
+    if (!gt_device_ok(dev)) return -1;
+    if (scale <= 0.0f) scale = 1.0f / std::sqrt((float)D);
+    const int cd = compute_dtype(q, k, v);
+    const int gd = cd == GT_F64 ? GT_F64 : GT_F32;
+    Temps tmp;
+
+    // the log-sum-exp residual: given, or recomputed by a forward pass
+    const gt_tensor *lse_s = nullptr;
+    if (lse) {
+        lse_s = (lse->device_type == GT_DEV_CUDA && lse->device_index == dev && lse->dtype == gd && gt_is_dense(lse))
+                    ? lse
+                    : tmp.keep(gt_to_device_dense(lse, dev, gd));
+    } else {
+        gt_tensor *o2 = nullptr, *l2 = nullptr;
+        if (attention_forward(who, q, k, v, mask, scale, is_causal, &o2, &l2) != 0) return -1;
+        tmp.keep(o2);
+        lse_s = l2->device_type == GT_DEV_CUDA ? tmp.keep(l2) : tmp.keep(gt_to_device_dense(tmp.keep(l2), dev, gd));
+    }
+    (void)out;  // the generic backward forms delta = rowsum(P * dP) itself
+    const int64_t qsh[4] = {B, H, L, D}, ksh[4] = {B, Hkv, S, D}, vsh[4] = {B, Hkv, S, Dv}, rsh[3] = {B, H, L};
+    gt_tensor *gq = gt_new_tensor(4, qsh, gd, GT_DEV_CUDA, dev);
+    gt_tensor *gk = gt_new_tensor(4, ksh, gd, GT_DEV_CUDA, dev);
+    gt_tensor *gv = gt_new_tensor(4, vsh, gd, GT_DEV_CUDA, dev);
+    gt_tensor *delta = tmp.keep(gt_new_tensor(3, rsh, gd, GT_DEV_CUDA, dev));
+    const gt_tensor *qs = stage(q, dev, cd, tmp), *ks = stage(k, dev, cd, tmp), *vs = stage(v, dev, cd, tmp);
+    const gt_tensor *gos = grad_out->device_type == GT_DEV_CUDA && grad_out->device_index == dev &&
+                                   grad_out->dtype == cd && gt_is_dense(grad_out)
+                               ? grad_out
+                               : tmp.keep(gt_to_device_dense(grad_out, dev, cd));
+    bool ok = gq && gk && gv && delta && qs && ks && vs && gos && lse_s;
+    AttnBwdArgs a{};
+    if (ok) {
+        fill_qkv(a.f, qs, ks, vs);
+        ok = stage_mask(mask, dev, cd, a.f, tmp);
+    }
+    if (ok) {
+        a.f.lse = gt_data(lse_s);
+        a.f.scale = scale;
+        a.f.causal = is_causal ? 1 : 0;
+        a.f.out_dtype = cd;
+        a.dout = gt_data(gos);
+        a.dq = gt_data(gq);
+        a.dk = gt_data(gk);
+        a.dv = gt_data(gv);
+        a.delta = gt_data(delta);
+        ok = gt_hip_check(launch_attn_generic_bwd(a, cd, gt_stream()), "flash_attention_backward kernel");
+    }
+    if (ok) {
+        gq = deliver(gq, host_io);
+        gk = deliver(gk, host_io);
+        gv = deliver(gv, host_io);
+        ok = gq && gk && gv;
+    }
+    if (!ok) {
+        gt_tensor_free(gq);
+        gt_tensor_free(gk);
+        gt_tensor_free(gv);
+        return -1;
+    }
+    *dq = gq;
+    *dk = gk;
+    *dv = gv;
+    return 0;
+}
+
+// ---------------------------------------------------------------------------------------------
+// Q8_0 codec (csrc/gt_ops_extra.cpp:2002-2009 -> csrc/gt_core.cpp:784-847)
+// ---------------------------------------------------------------------------------------------
+
+extern "C" gt_tensor *gt_quantize(const gt_tensor *t, int ggml_type_id) {
+    if (!t) {
+        gt_set_error("quantize: NULL tensor");
+        return nullptr;
+    }
+    if (ggml_type_id != GT_Q8_0 - GT_Q_BASE) {
+        gt_set_error("quantize: only q8_0 (ggml type 8) is supported, got ggml type " + std::to_string(ggml_type_id));
+        return nullptr;
+    }
+    if (gt_is_quantized(t->dtype)) {
+        gt_set_error("quantize: the tensor is already quantized");
+        return nullptr;
+    }
+    if (t->numel % 32 != 0) {
+        gt_set_error("Tensor size must be a multiple of ggml quantization block size");
+        return nullptr;
+    }
+    const int dev = t->device_type == GT_DEV_CUDA ? t->device_index : 0;
+    if (!gt_device_ok(dev)) return nullptr;
+    Temps tmp;
+    const gt_tensor *f = (t->device_type == GT_DEV_CUDA && t->dtype == GT_F32 && gt_is_dense(t))
+                             ? t
+                             : tmp.keep(gt_to_device_dense(t, dev, GT_F32));
+    if (!f) return nullptr;
+    gt_tensor *out = gt_new_tensor(t->ndim, t->shape, GT_Q8_0, GT_DEV_CUDA, dev);
+    if (!out) return nullptr;
+    if (!gt_hip_check(gt_launch_q8_0_quantize((const float *)gt_data(f), gt_data(out), t->numel / 32, gt_stream()),
+                      "q8_0 quantize kernel")) {
+        gt_tensor_free(out);
+        return nullptr;
+    }
+    return deliver(out, t->device_type != GT_DEV_CUDA);
+}
+
+extern "C" gt_tensor *gt_dequantize(const gt_tensor *t, int out_dtype) {
+    if (!t) {
+        gt_set_error("dequantize: NULL tensor");
+        return nullptr;
+    }
+    if (t->dtype != GT_Q8_0) {
+        gt_set_error(std::string("dequantize: expected a q8_0 tensor, got ") + gt_dtype_name(t->dtype));
+        return nullptr;
+    }
+    if (out_dtype != GT_F32 && out_dtype != GT_F16 && out_dtype != GT_BF16 && out_dtype != GT_F64) {
+        gt_set_error(std::string("dequantize: unsupported output dtype ") + gt_dtype_name(out_dtype));
+        return nullptr;
+    }
+    const int dev = t->device_type == GT_DEV_CUDA ? t->device_index : 0;
+    if (!gt_device_ok(dev)) return nullptr;
+    Temps tmp;
+    const gt_tensor *src = t->device_type == GT_DEV_CUDA ? t : tmp.keep(gt_to_device_dense(t, dev, GT_Q8_0));
+    if (!src) return nullptr;
+    gt_tensor *out = gt_new_tensor(t->ndim, t->shape, out_dtype, GT_DEV_CUDA, dev);
+    if (!out) return nullptr;
+    if (!gt_hip_check(gt_launch_q8_0_dequantize(gt_data(src), gt_data(out), out_dtype, t->numel / 32, gt_stream()),
+                      "q8_0 dequantize kernel")) {
+        gt_tensor_free(out);
+        return nullptr;
+    }
+    return deliver(out, t->device_type != GT_DEV_CUDA);
+}

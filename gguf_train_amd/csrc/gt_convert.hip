@@ -1,0 +1,238 @@
+// Element conversion / layout copy kernels and the GGUF Q8_0 codec.
+//
+// Conversion follows the reference's per-element semantics (csrc/gt_internal.h:243-301): a
+// value is read as double and written back through float for float16/bfloat16, so a float64
+// source is rounded twice (double -> float -> half) exactly as the reference does.
+//
+// Q8_0 (ggml block_q8_0, 34 bytes: fp16 d, int8 qs[32]) follows ggml's reference quantizer
+// (quantize_row_q8_0_ref in ggml-quants.c, reached from ggml_quantize_chunk,
+// csrc/gt_core.cpp:819-832) and its to_float (csrc/gt_core.cpp:800-808):
+//   amax = max|x|, d = amax/127, id = d ? 1/d : 0, qs = roundf(x*id), d stored as fp16 (RNE);
+//   y = (float)qs * (float)d.
+// HBM-bound byte work: one wave handles two blocks with one lane per value, so loads and
+// stores are coalesced; no LDS is needed.
+
+#include "gt_internal.h"
+
+#include <cmath>
+
+namespace {
+
+__device__ inline uint32_t f2u(float f) { return __float_as_uint(f); }
+__device__ inline float u2f(uint32_t u) { return __uint_as_float(u); }
+
+// IEEE binary16 <-> binary32, round to nearest even (bit-exact with the host converter).
+__device__ inline uint16_t d_f32_to_f16(float f) {
+    const uint32_t x = f2u(f);
+    const uint32_t sign = (x >> 16) & 0x8000u;
+    const uint32_t ax = x & 0x7fffffffu;
+    if (ax > 0x7f800000u) return (uint16_t)(sign | 0x7e00u | ((ax >> 13) & 0x3ffu));
+    if (ax >= 0x477ff000u) return (uint16_t)(sign | 0x7c00u);
+    if (ax < 0x38800000u) {
+        if (ax < 0x33000000u) return (uint16_t)sign;
+        const uint32_t m = (ax & 0x7fffffu) | 0x800000u;
+        const int shift = 126 - (int)(ax >> 23);
+        uint32_t r = m >> shift;
+        const uint32_t rem = m & ((1u << shift) - 1u), half = 1u << (shift - 1);
+        if (rem > half || (rem == half && (r & 1u))) ++r;
+        return (uint16_t)(sign | r);
+    }
+    uint32_t r = (ax >> 13) - (112u << 10);
+    const uint32_t rem = ax & 0x1fffu;
+    if (rem > 0x1000u || (rem == 0x1000u && (r & 1u))) ++r;
+    return (uint16_t)(sign | r);
+}
+
+__device__ inline float d_f16_to_f32(uint16_t h) {
+    const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+    uint32_t e = (h >> 10) & 0x1fu, m = h & 0x3ffu, x;
+    if (e == 0) {
+        if (m == 0) {
+            x = sign;
+        } else {
+            e = 113;
+            while (!(m & 0x400u)) {
+                m <<= 1;
+                --e;
+            }
+            x = sign | (e << 23) | ((m & 0x3ffu) << 13);
+        }
+    } else if (e == 31) {
+        x = sign | 0x7f800000u | (m << 13);
+    } else {
+        x = sign | ((e + 112u) << 23) | (m << 13);
+    }
+    return u2f(x);
+}
+
+__device__ inline uint16_t d_f32_to_bf16(float f) {
+    const uint32_t u = f2u(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+    return (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+}
+
+__device__ inline double read_elem(const void *p, int dtype, int64_t i) {
+    switch (dtype) {
+        case GT_F32: return ((const float *)p)[i];
+        case GT_F64: return ((const double *)p)[i];
+        case GT_F16: return d_f16_to_f32(((const uint16_t *)p)[i]);
+        case GT_BF16: return u2f((uint32_t)((const uint16_t *)p)[i] << 16);
+        case GT_I8: return ((const int8_t *)p)[i];
+        case GT_U8: return ((const uint8_t *)p)[i];
+        case GT_I16: return ((const int16_t *)p)[i];
+        case GT_I32: return ((const int32_t *)p)[i];
+        case GT_I64: return (double)((const int64_t *)p)[i];
+        case GT_BOOL: return ((const uint8_t *)p)[i] ? 1.0 : 0.0;
+        default: return 0.0;
+    }
+}
+
+__device__ inline void write_elem(void *p, int dtype, int64_t i, double v) {
+    switch (dtype) {
+        case GT_F32: ((float *)p)[i] = (float)v; break;
+        case GT_F64: ((double *)p)[i] = v; break;
+        case GT_F16: ((uint16_t *)p)[i] = d_f32_to_f16((float)v); break;
+        case GT_BF16: ((uint16_t *)p)[i] = d_f32_to_bf16((float)v); break;
+        case GT_I8: ((int8_t *)p)[i] = (int8_t)v; break;
+        case GT_U8: ((uint8_t *)p)[i] = (uint8_t)v; break;
+        case GT_I16: ((int16_t *)p)[i] = (int16_t)v; break;
+        case GT_I32: ((int32_t *)p)[i] = (int32_t)v; break;
+        case GT_I64: ((int64_t *)p)[i] = (int64_t)v; break;
+        case GT_BOOL: ((uint8_t *)p)[i] = v != 0.0 ? 1 : 0; break;
+        default: break;
+    }
+}
+
+__device__ inline bool is_int(int dt) {
+    return dt == GT_I8 || dt == GT_U8 || dt == GT_I16 || dt == GT_I32 || dt == GT_I64;
+}
+
+__device__ inline int64_t read_int(const void *p, int dtype, int64_t i) {
+    switch (dtype) {
+        case GT_I8: return ((const int8_t *)p)[i];
+        case GT_U8: return ((const uint8_t *)p)[i];
+        case GT_I16: return ((const int16_t *)p)[i];
+        case GT_I32: return ((const int32_t *)p)[i];
+        default: return ((const int64_t *)p)[i];
+    }
+}
+
+__device__ inline void write_int(void *p, int dtype, int64_t i, int64_t v) {
+    switch (dtype) {
+        case GT_I8: ((int8_t *)p)[i] = (int8_t)v; break;
+        case GT_U8: ((uint8_t *)p)[i] = (uint8_t)v; break;
+        case GT_I16: ((int16_t *)p)[i] = (int16_t)v; break;
+        case GT_I32: ((int32_t *)p)[i] = (int32_t)v; break;
+        default: ((int64_t *)p)[i] = v; break;
+    }
+}
+
+__device__ inline int64_t offset_of(const gt_layout &l, int64_t linear) {
+    int64_t off = 0;
+    for (int d = l.ndim - 1; d >= 0; --d) {
+        const int64_t c = linear % l.shape[d];
+        linear /= l.shape[d];
+        off += c * l.strides[d];
+    }
+    return off;
+}
+
+__device__ inline void copy_bytes(void *dst, const void *src, int n) {
+    switch (n) {
+        case 1: *(uint8_t *)dst = *(const uint8_t *)src; break;
+        case 2: *(uint16_t *)dst = *(const uint16_t *)src; break;
+        case 4: *(uint32_t *)dst = *(const uint32_t *)src; break;
+        default: *(uint64_t *)dst = *(const uint64_t *)src; break;
+    }
+}
+
+__global__ void convert_kernel(const void *__restrict__ src, int sdt, gt_layout sl, void *__restrict__ dst, int ddt,
+                               gt_layout dl, int64_t numel, int es) {
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < numel; i += stride) {
+        const int64_t so = offset_of(sl, i), doff = offset_of(dl, i);
+        if (sdt == ddt) {
+            copy_bytes((char *)dst + doff * es, (const char *)src + so * es, es);
+        } else if (is_int(sdt) && is_int(ddt)) {
+            write_int(dst, ddt, doff, read_int(src, sdt, so));  // exact beyond 2^53
+        } else {
+            write_elem(dst, ddt, doff, read_elem(src, sdt, so));
+        }
+    }
+}
+
+// 64 lanes = two blocks of 32 values; lane j of a half handles value j of its block.
+__global__ void q8_0_quantize_kernel(const float *__restrict__ x, uint8_t *__restrict__ out, int64_t nblocks) {
+    const int lane = threadIdx.x & 63;
+    const int64_t wave = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+    const int64_t blk = wave * 2 + (lane >> 5);
+    const int j = lane & 31;
+    const bool live = blk < nblocks;
+    const float v = live ? x[blk * 32 + j] : 0.0f;
+    float amax = fabsf(v);
+    // max over the 32 lanes of this half (xor offsets < 32 stay inside the half)
+    for (int off = 16; off >= 1; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+    const float d = __fdiv_rn(amax, 127.0f);
+    const float id = d != 0.0f ? __fdiv_rn(1.0f, d) : 0.0f;
+    if (!live) return;
+    uint8_t *b = out + blk * 34;
+    const float x0 = v * id;
+    b[2 + j] = (uint8_t)(int8_t)roundf(x0);
+    if (j == 0) {
+        const uint16_t h = d_f32_to_f16(d);
+        b[0] = (uint8_t)(h & 0xff);
+        b[1] = (uint8_t)(h >> 8);
+    }
+}
+
+__global__ void q8_0_dequantize_kernel(const uint8_t *__restrict__ in, void *__restrict__ out, int dst_dtype,
+                                       int64_t nblocks) {
+    const int lane = threadIdx.x & 63;
+    const int64_t wave = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+    const int64_t blk = wave * 2 + (lane >> 5);
+    const int j = lane & 31;
+    if (blk >= nblocks) return;
+    const uint8_t *b = in + blk * 34;
+    const float d = d_f16_to_f32((uint16_t)(b[0] | (b[1] << 8)));
+    const float y = (float)(int8_t)b[2 + j] * d;
+    const int64_t i = blk * 32 + j;
+    switch (dst_dtype) {
+        case GT_F32: ((float *)out)[i] = y; break;
+        case GT_F64: ((double *)out)[i] = (double)y; break;
+        case GT_F16: ((uint16_t *)out)[i] = d_f32_to_f16(y); break;
+        case GT_BF16: ((uint16_t *)out)[i] = d_f32_to_bf16(y); break;
+        default: write_elem(out, dst_dtype, i, (double)y); break;
+    }
+}
+
+inline unsigned grid_for(int64_t n, int block) {
+    const int64_t g = (n + block - 1) / block;
+    return (unsigned)(g < 65536 * 16 ? (g > 0 ? g : 1) : 65536 * 16);
+}
+
+}  // namespace
+
+hipError_t gt_launch_convert(const void *src, int src_dtype, const gt_layout &src_layout, void *dst, int dst_dtype,
+                             const gt_layout &dst_layout, int64_t numel, hipStream_t stream) {
+    if (numel <= 0) return hipSuccess;
+    const int es = (int)gt_elem_bytes(src_dtype);
+    hipLaunchKernelGGL(convert_kernel, dim3(grid_for(numel, 256)), dim3(256), 0, stream, src, src_dtype, src_layout, dst,
+                       dst_dtype, dst_layout, numel, es);
+    return hipGetLastError();
+}
+
+hipError_t gt_launch_q8_0_quantize(const float *src, void *dst, int64_t nblocks, hipStream_t stream) {
+    if (nblocks <= 0) return hipSuccess;
+    const int64_t waves = (nblocks + 1) / 2;
+    hipLaunchKernelGGL(q8_0_quantize_kernel, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, stream, src,
+                       (uint8_t *)dst, nblocks);
+    return hipGetLastError();
+}
+
+hipError_t gt_launch_q8_0_dequantize(const void *src, void *dst, int dst_dtype, int64_t nblocks, hipStream_t stream) {
+    if (nblocks <= 0) return hipSuccess;
+    const int64_t waves = (nblocks + 1) / 2;
+    hipLaunchKernelGGL(q8_0_dequantize_kernel, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, stream,
+                       (const uint8_t *)src, dst, dst_dtype, nblocks);
+    return hipGetLastError();
+}

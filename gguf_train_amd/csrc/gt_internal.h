@@ -1,0 +1,106 @@
+// Internal declarations of libgt_attn.so: tensor handle, storage, device memory pool, errors,
+// and the launchers each .hip translation unit exports to the host-side API code.
+//
+// The handle carries the same field meanings as the reference's gt_tensor
+// (csrc/gt_internal.h:30-70): shape/strides in elements, element offset, dtype code, device,
+// shared storage.  The struct layout itself is private; callers only hold pointers.
+#pragma once
+
+#include "../../include/gt_attn.h"
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <memory>
+#include <string>
+
+// ---- errors (thread-local message, csrc/gt_core.cpp:7-23) ---------------------------------
+void gt_set_error(const std::string &msg);
+// Records a HIP failure as "<what>: <hip error string>" and returns false.
+bool gt_hip_check(hipError_t e, const char *what);
+
+// ---- devices / streams ----------------------------------------------------------------------
+// True when HIP device `idx` exists; otherwise sets the error message and returns false.
+bool gt_device_ok(int idx);
+// The calling thread's current stream (gt_set_stream).
+hipStream_t gt_stream();
+
+// ---- storage ----------------------------------------------------------------------------------
+enum gt_storage_kind { GT_STORE_HOST = 0, GT_STORE_DEVICE = 1, GT_STORE_EXTERNAL = 2 };
+
+struct gt_storage {
+    void *ptr = nullptr;     // first byte (host or device address)
+    size_t nbytes = 0;       // bytes reachable from ptr
+    size_t capacity = 0;     // bytes actually allocated (pool block size)
+    int64_t numel = 0;       // elements reachable (bounds of views)
+    int device_type = GT_DEV_CPU;
+    int device_index = 0;
+    int kind = GT_STORE_HOST;
+    uint64_t token = 0;      // external memory: reported by gt_external_released
+    hipStream_t stream = nullptr;  // stream the pool may reuse a device block on
+    ~gt_storage();
+};
+
+struct gt_tensor {
+    int ndim = 0;
+    int64_t shape[GT_MAX_DIMS] = {};
+    int64_t strides[GT_MAX_DIMS] = {};
+    int64_t offset = 0;
+    int64_t numel = 1;
+    int dtype = GT_F32;
+    int device_type = GT_DEV_CPU;
+    int device_index = 0;
+    std::shared_ptr<gt_storage> storage;
+};
+
+// ---- dtype helpers ----------------------------------------------------------------------------
+size_t gt_elem_bytes(int dtype);  // 0 for unknown and quantized dtypes
+inline bool gt_is_quantized(int dtype) { return dtype >= GT_Q_BASE; }
+inline bool gt_is_float(int dtype) {
+    return dtype == GT_F32 || dtype == GT_F16 || dtype == GT_BF16 || dtype == GT_F64;
+}
+// Bytes of `numel` elements of `dtype` (Q8_0: numel/32 blocks of 34 bytes).
+size_t gt_dtype_nbytes(int dtype, int64_t numel);
+const char *gt_dtype_name(int dtype);
+
+inline int64_t gt_numel_of(int ndim, const int64_t *shape) {
+    int64_t n = 1;
+    for (int i = 0; i < ndim; ++i) n *= shape[i];
+    return n;
+}
+void gt_default_strides(int ndim, const int64_t *shape, int64_t *strides);
+bool gt_is_dense(const gt_tensor *t);  // contiguous row-major (size-1 dims ignored)
+
+// New tensor with fresh storage (pool-backed on the device).  Sets the error on failure.
+gt_tensor *gt_new_tensor(int ndim, const int64_t *shape, int dtype, int device_type, int device_index);
+// Base address of element 0 of `t` (storage ptr + offset * element size).
+void *gt_data(const gt_tensor *t);
+
+// Device-resident, element-converted copy helpers used by the op layer.  Each returns a new
+// tensor on device `dev` or NULL (error set).
+//   gt_to_device_dense: contiguous copy on the device, converted to `dtype` (-1 keeps it).
+gt_tensor *gt_to_device_dense(const gt_tensor *t, int dev, int dtype);
+// Copies the device tensor `src` into host tensor `dst` (same shape, dense), waiting for it.
+bool gt_copy_device_to_host(gt_tensor *dst, const gt_tensor *src);
+
+// Stream-ordered scratch memory from the pool (freed back to the pool in stream order).
+struct gt_scratch {
+    std::shared_ptr<gt_storage> st;
+    void *ptr() const { return st ? st->ptr : nullptr; }
+};
+bool gt_scratch_alloc(gt_scratch &s, size_t nbytes, int dev);
+
+// ---- launchers (defined in the .hip files) -------------------------------------------------
+struct gt_layout {
+    int ndim;
+    int64_t shape[GT_MAX_DIMS];
+    int64_t strides[GT_MAX_DIMS];
+};
+// Element-wise copy with conversion between two layouts of the same shape (any strides, any
+// supported dtype): dst[dst_layout(i)] = convert(src[src_layout(i)]) for i < numel.
+hipError_t gt_launch_convert(const void *src, int src_dtype, const gt_layout &src_layout, void *dst, int dst_dtype,
+                             const gt_layout &dst_layout, int64_t numel, hipStream_t stream);
+// Q8_0 (ggml block_q8_0) quantize `nrows` rows of `row_len` floats (row_len % 32 == 0).
+hipError_t gt_launch_q8_0_quantize(const float *src, void *dst, int64_t nblocks, hipStream_t stream);
+// Q8_0 dequantize into `dst_dtype` (f32/f16/bf16/f64).
+hipError_t gt_launch_q8_0_dequantize(const void *src, void *dst, int dst_dtype, int64_t nblocks, hipStream_t stream);

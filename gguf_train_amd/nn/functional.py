@@ -1,0 +1,88 @@
+"""`scaled_dot_product_attention` with the reference's signature and semantics
+(gguf_train/nn/functional.py:724-767).
+
+- scale defaults to 1/sqrt(D) (computed in Python double, handed to C as float32);
+- attn_mask: bool True = may attend, float = added to the scores; it is checked against the
+  attention weights (B, H, L, S) from the right and reshaped to 4-D;
+- is_causal masks s > l (top-left aligned);
+- dropout_p == 0 runs the fused native kernel through FlashAttentionFn; dropout_p > 0 runs the
+  reference's explicit composition (matmul, softmax, dropout, matmul);
+- inside autocast, q/k/v (and a float mask) are cast to the autocast dtype
+  (gguf_train/_tensor.py:261-283, gguf_train/amp.py:8-10);
+- k/v may be QuantizedTensor (GGUF Q8_0); they are read as their dequantized values and carry
+  no gradient.
+"""
+
+from __future__ import annotations
+
+import math
+
+import torch
+
+from .._bridge import QuantizedTensor
+from .._functions import FlashAttentionFn
+from .. import _ops
+
+
+def _autocast_lower(*ts):
+    """Casts floating-point operands to the active autocast dtype (the reference's
+    _AUTOCAST_LOWER policy); returns them unchanged outside autocast."""
+    out = []
+    for t in ts:
+        if isinstance(t, torch.Tensor) and t.is_floating_point():
+            dev = t.device.type
+            if torch.is_autocast_enabled(dev):
+                t = t.to(torch.get_autocast_dtype(dev))
+        out.append(t)
+    return out
+
+
+def scaled_dot_product_attention(
+    query,
+    key,
+    value,
+    attn_mask=None,
+    dropout_p: float = 0.0,
+    is_causal: bool = False,
+    scale: float | None = None,
+    enable_gqa: bool = False,
+):
+    (enable_gqa,)  # GQA follows from the head counts, as in the reference
+    query, key, value, attn_mask = _autocast_lower(query, key, value, attn_mask)
+    sc = (1.0 / math.sqrt(query.shape[-1])) if scale is None else float(scale)
+    if attn_mask is not None:
+        if query.ndim == 4 and key.ndim == 4:
+            want = (query.shape[0], query.shape[1], query.shape[2], key.shape[2])
+            if attn_mask.ndim > 4 or any(m != 1 and m != w for m, w in zip(reversed(attn_mask.shape), reversed(want))):
+                raise RuntimeError(
+                    f"scaled_dot_product_attention: attn_mask of shape {list(attn_mask.shape)} cannot be broadcast "
+                    f"to the attention weights {list(want)}"
+                )
+            if attn_mask.ndim != 4:
+                attn_mask = attn_mask.reshape((1,) * (4 - attn_mask.ndim) + tuple(attn_mask.shape))
+    quantized = isinstance(key, QuantizedTensor) or isinstance(value, QuantizedTensor)
+    with torch.autocast(query.device.type, enabled=False):
+        if quantized:
+            if dropout_p != 0.0:
+                raise RuntimeError("scaled_dot_product_attention: dropout is not supported with q8_0 key/value")
+            return _ops.flash_attention(query, key, value, attn_mask, sc, is_causal)
+        if dropout_p == 0.0:
+            return FlashAttentionFn.apply(query, key, value, attn_mask, sc, is_causal)
+        # dropout: the reference's explicit composition (gguf_train/nn/functional.py:750-767)
+        B, H, L, D = query.shape
+        H_kv = key.shape[1]
+        k_u = key if H == H_kv else key.repeat_interleave(H // H_kv, dim=1)
+        v_u = value if H == H_kv else value.repeat_interleave(H // H_kv, dim=1)
+        scores = query.matmul(k_u.transpose(-2, -1).contiguous()) * sc
+        if is_causal:
+            S = key.shape[-2]
+            cm = torch.ones((L, S), dtype=query.dtype, device=query.device).triu(diagonal=1) * (-1e9)
+            scores = scores + cm
+        if attn_mask is not None:
+            if attn_mask.dtype == torch.bool:
+                scores = scores.masked_fill(~attn_mask, -1e9)
+            else:
+                scores = scores + attn_mask
+        probs = torch.softmax(scores, dim=-1)
+        probs = torch.nn.functional.dropout(probs, p=dropout_p, training=True)
+        return probs.matmul(v_u)

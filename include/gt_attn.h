@@ -1,0 +1,183 @@
+/*
+ * gt_attn.h - C ABI of libgt_attn.so, the MI355X (gfx950) attention library.
+ *
+ * The entry points below carry the names, argument meanings, return conventions and error
+ * behaviour of GGUF_train's native ABI (csrc/gguf_train.h), so the reference's ctypes loader
+ * (gguf_train/_C.py) can bind them unchanged.  Every declaration cites the reference
+ * declaration it replaces; entry points the reference does not have say so.
+ *
+ * Conventions shared with the reference:
+ *   - a tensor is an opaque `gt_tensor *` handle: shape and strides counted in elements, an
+ *     element offset, a dtype code and a device (csrc/gt_internal.h:30-70);
+ *   - a function returning `gt_tensor *` returns a NEW handle owned by the caller (release it
+ *     with gt_tensor_free) or NULL on failure; a function returning `int` returns 0 on success;
+ *   - on failure the message is stored per thread and read with gt_last_error()
+ *     (csrc/gt_core.cpp:7-23); nothing throws or aborts across this boundary.
+ *
+ * Devices: GT_DEV_CPU tensors live in host memory, GT_DEV_CUDA tensors in HIP device memory
+ * (the reference files HIP/ROCm GPUs under GT_DEV_CUDA, csrc/gt_core.cpp:86-87).  All compute
+ * runs on the GPU: host inputs are copied to the device and host outputs copied back, the
+ * reverse of the reference's device->host staging (csrc/gt_core.cpp:314-329).  There is no
+ * CPU compute path: without a HIP device every compute entry point fails with a message.
+ *
+ * Ordering: work is enqueued on the calling thread's current stream (gt_set_stream; the null
+ * stream by default).  Device results may still be in flight when a call returns; every call
+ * that hands bytes to the host (gt_tensor_copy_to_host, host outputs) waits for them.
+ */
+#ifndef GT_ATTN_H
+#define GT_ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define GT_API __attribute__((visibility("default")))
+
+/* csrc/gguf_train.h:20 */
+#define GT_MAX_DIMS 12
+
+/* dtype codes: csrc/gguf_train.h:22-36.  Quantized types are GT_Q_BASE + ggml type id. */
+enum gt_dtype {
+    GT_F32 = 0,
+    GT_F16 = 1,
+    GT_BF16 = 2,
+    GT_F64 = 3,
+    GT_I8 = 4,
+    GT_U8 = 5,
+    GT_I16 = 6,
+    GT_I32 = 7,
+    GT_I64 = 8,
+    GT_BOOL = 9,
+    GT_C64 = 10,
+    GT_C128 = 11,
+    GT_Q_BASE = 100
+};
+/* GGUF Q8_0: blocks of 32 values, {fp16 d, int8 qs[32]} = 34 bytes (ggml type 8;
+ * gguf_train/_dtype.py:85 names it 108). */
+#define GT_Q8_0 (GT_Q_BASE + 8)
+
+/* device codes: csrc/gguf_train.h:38-44 */
+enum gt_device_type {
+    GT_DEV_CPU = 0,
+    GT_DEV_CUDA = 1,
+    GT_DEV_MPS = 2,
+    GT_DEV_VULKAN = 3,
+    GT_DEV_META = 4
+};
+
+typedef struct gt_tensor gt_tensor;
+
+/* ---- runtime / errors ------------------------------------------------------------------ */
+
+/* csrc/gguf_train.h:170.  Idempotent; called by every entry point that needs it. */
+GT_API void gt_init(void);
+/* csrc/gguf_train.h:175.  Number of HIP devices for GT_DEV_CUDA, 1 for GT_DEV_CPU. */
+GT_API int gt_device_count(int device_type);
+/* csrc/gguf_train.h:176 */
+GT_API void gt_device_name(int device_type, int idx, char *buf, int buf_len);
+/* csrc/gguf_train.h:177 */
+GT_API void gt_device_memory(int device_type, int idx, size_t *free_bytes, size_t *total_bytes);
+/* csrc/gguf_train.h:178.  Waits for all work this library enqueued on the device. */
+GT_API void gt_synchronize(int device_type, int idx);
+/* csrc/gguf_train.h:182-185 */
+GT_API const char *gt_last_error(void);
+GT_API void gt_clear_error(void);
+GT_API void gt_set_last_error(const char *msg);
+
+/* No counterpart in the reference (its calls are synchronous and stream-less).  Sets the HIP
+ * stream (a hipStream_t, NULL = the null stream) that this thread's calls enqueue on, so a
+ * host that keeps its own current stream (e.g. PyTorch) stays ordered with this library. */
+GT_API void gt_set_stream(void *stream);
+GT_API void *gt_get_stream(void);
+
+/* ---- tensor lifecycle & metadata: csrc/gguf_train.h:188-227 ----------------------------- */
+
+GT_API gt_tensor *gt_tensor_empty(int ndim, const int64_t *shape, int dtype, int device_type, int device_index);
+GT_API gt_tensor *gt_tensor_from_data(int ndim, const int64_t *shape, int dtype, int device_type, int device_index,
+                                      const void *data, size_t nbytes);
+/* csrc/gguf_train.h:191-198: host memory owned by the caller, nothing copied; `token` is
+ * reported by gt_external_released() once the last handle on that memory is gone. */
+GT_API gt_tensor *gt_tensor_from_external(int ndim, const int64_t *shape, const int64_t *strides, int dtype,
+                                          void *data, uint64_t token);
+GT_API int64_t gt_external_released(uint64_t *tokens, int64_t capacity);
+/* No counterpart in the reference: device memory owned by the caller (e.g. a PyTorch CUDA
+ * tensor), borrowed without a copy.  The caller keeps the memory alive while any handle on
+ * it exists; `token` (non-zero) is reported by gt_external_released() like host memory. */
+GT_API gt_tensor *gt_tensor_from_device_ptr(int ndim, const int64_t *shape, const int64_t *strides, int dtype,
+                                            int device_index, void *data, uint64_t token);
+GT_API gt_tensor *gt_tensor_clone(const gt_tensor *t);
+GT_API gt_tensor *gt_tensor_view(const gt_tensor *t, int ndim, const int64_t *shape, const int64_t *strides,
+                                 int64_t offset);
+GT_API gt_tensor *gt_tensor_contiguous(const gt_tensor *t);
+GT_API gt_tensor *gt_tensor_to_dtype(const gt_tensor *t, int dtype);
+GT_API gt_tensor *gt_tensor_to_device(const gt_tensor *t, int device_type, int device_index);
+GT_API void gt_tensor_free(gt_tensor *t);
+
+GT_API int gt_tensor_ndim(const gt_tensor *t);
+GT_API void gt_tensor_shape(const gt_tensor *t, int64_t *out);
+GT_API void gt_tensor_strides(const gt_tensor *t, int64_t *out);
+GT_API int64_t gt_tensor_offset(const gt_tensor *t);
+GT_API int64_t gt_tensor_numel(const gt_tensor *t);
+GT_API int gt_tensor_dtype(const gt_tensor *t);
+GT_API int gt_tensor_device_type(const gt_tensor *t);
+GT_API int gt_tensor_device_index(const gt_tensor *t);
+GT_API int gt_tensor_is_contiguous(const gt_tensor *t);
+GT_API uint64_t gt_tensor_data_ptr(const gt_tensor *t);
+GT_API size_t gt_tensor_storage_nbytes(const gt_tensor *t);
+GT_API size_t gt_tensor_nbytes(const gt_tensor *t);
+GT_API size_t gt_tensor_elem_size(int dtype);
+
+/* csrc/gguf_train.h:222-224: dense row-major copies; they wait for the device. */
+GT_API int gt_tensor_copy_to_host(const gt_tensor *t, void *dst, size_t dst_bytes);
+GT_API int gt_tensor_copy_from_host(gt_tensor *t, const void *src, size_t src_bytes);
+GT_API int gt_tensor_copy_inplace(gt_tensor *dst, const gt_tensor *src);
+
+/* No counterpart in the reference: a DLPack (DLManagedTensor, unversioned ABI) describing the
+ * tensor's memory without a copy; it holds a reference on the storage until its deleter runs.
+ * Returns NULL on failure.  Lets hosts such as PyTorch adopt results zero-copy. */
+GT_API void *gt_tensor_to_dlpack(const gt_tensor *t);
+
+/* ---- attention ------------------------------------------------------------------------ */
+
+/* csrc/gguf_train.h:311 (implementation csrc/gt_ops_nn.cpp:2423-2525).
+ * q (B,H,L,D), k (B,Hkv,S,D), v (B,Hkv,S,Dv); H % Hkv == 0, head h reads kv head h/(H/Hkv).
+ * mask: NULL, (L,S) or 4-D, every dim 1 or full; bool = may attend, other dtypes are added.
+ * scale <= 0 means 1/sqrt(D).  is_causal masks s > l (top-left aligned).  A row with nothing
+ * to attend to yields 0.  Output (B,H,L,Dv) contiguous, dtype of q, device of q.
+ * k and v may also be GT_Q8_0 (contiguous), read as their dequantized values. */
+GT_API gt_tensor *gt_flash_attention(const gt_tensor *q, const gt_tensor *k, const gt_tensor *v,
+                                     const gt_tensor *mask, float scale, int is_causal);
+
+/* No counterpart in the reference: gt_flash_attention that also returns the per-row
+ * log-sum-exp of the scaled, masked scores (B,H,L) float32 (+inf for a row with nothing to
+ * attend to), the residual the backward needs.  Out-params follow gt_layer_norm_backward's
+ * convention (csrc/gguf_train.h:284).  Returns 0 on success. */
+GT_API int gt_flash_attention_lse(const gt_tensor *q, const gt_tensor *k, const gt_tensor *v, const gt_tensor *mask,
+                                  float scale, int is_causal, gt_tensor **out, gt_tensor **lse);
+
+/* Replaces the Python composition FlashAttentionFn.backward (gguf_train/_functions.py:1933-1965)
+ * with a native recompute-based backward.  dq (B,H,L,D), dk (B,Hkv,S,D), dv (B,Hkv,S,Dv) are
+ * float32 for float16/bfloat16/float32 inputs and float64 for float64 inputs; gradients of
+ * a GQA group are summed into its kv head.  Returns 0 on success. */
+GT_API int gt_flash_attention_backward(const gt_tensor *grad_out, const gt_tensor *q, const gt_tensor *k,
+                                       const gt_tensor *v, const gt_tensor *mask, const gt_tensor *out,
+                                       const gt_tensor *lse, float scale, int is_causal, gt_tensor **dq,
+                                       gt_tensor **dk, gt_tensor **dv);
+
+/* ---- GGUF Q8_0 ------------------------------------------------------------------------ */
+
+/* csrc/gguf_train.h:376 (gt_tensor_to_dtype, csrc/gt_core.cpp:784-847): quantizes rows of
+ * last-dim length (one flat row when that is not a multiple of 32).  Only GT_Q8_0
+ * (ggml_type_id 8) is supported. */
+GT_API gt_tensor *gt_quantize(const gt_tensor *t, int ggml_type_id);
+/* csrc/gguf_train.h:377: y = float(qs[j]) * float(d), then converted to out_dtype. */
+GT_API gt_tensor *gt_dequantize(const gt_tensor *t, int out_dtype);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GT_ATTN_H */

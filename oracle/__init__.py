@@ -1,0 +1,196 @@
+"""CPU oracle for the attention path - TEST INFRASTRUCTURE ONLY.
+
+numpy front end of oracle/oracle_attn.c (a float64 C restatement of the reference's
+gt_flash_attention, csrc/gt_ops_nn.cpp:2423-2525, of FlashAttentionFn.backward,
+gguf_train/_functions.py:1933-1965, and of the GGUF Q8_0 codec, csrc/gt_core.cpp:800-832).
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg import this package, as
+the checker; the product (gguf_train_amd) never does.
+
+Arrays are passed as numpy arrays; bfloat16 data travels as its uint16 bit patterns wrapped
+in `BF16(bits)`.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+from pathlib import Path
+
+import numpy as np
+
+_HERE = Path(__file__).resolve().parent
+LIB_PATH = _HERE / "liboracle_attn.so"
+
+F32, F16, BF16_CODE, F64, I8, U8, I16, I32, I64, BOOL = 0, 1, 2, 3, 4, 5, 6, 7, 8, 9
+
+_lib = None
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(f"{LIB_PATH} is not built (python oracle/build.py)")
+        L = ctypes.CDLL(str(LIB_PATH))
+        vp, i64, c_int = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int
+        L.oracle_flash_attention.argtypes = [vp, c_int, vp, c_int, vp, c_int, vp, c_int, c_int, vp,
+                                             i64, i64, i64, i64, i64, i64, i64, ctypes.c_float, c_int,
+                                             vp, c_int, vp, c_int]
+        L.oracle_flash_attention.restype = c_int
+        L.oracle_flash_attention_backward.argtypes = [vp, c_int, vp, c_int, vp, c_int, vp, c_int, vp, c_int,
+                                                      c_int, vp, i64, i64, i64, i64, i64, i64, i64,
+                                                      ctypes.c_float, c_int, vp, vp, vp, c_int]
+        L.oracle_flash_attention_backward.restype = c_int
+        for name in ("oracle_f32_to_f16_array", "oracle_f16_to_f32_array", "oracle_f32_to_bf16_array",
+                     "oracle_bf16_to_f32_array"):
+            getattr(L, name).argtypes = [vp, vp, i64]
+            getattr(L, name).restype = None
+        L.oracle_q8_0_quantize.argtypes = [vp, vp, i64]
+        L.oracle_q8_0_dequantize.argtypes = [vp, vp, i64]
+        L.oracle_max_threads.restype = c_int
+        _lib = L
+    return _lib
+
+
+@dataclass
+class BF16:
+    """bfloat16 data as uint16 bit patterns."""
+
+    bits: np.ndarray
+
+    @property
+    def shape(self):
+        return self.bits.shape
+
+
+def _code(a) -> tuple[np.ndarray, int]:
+    if isinstance(a, BF16):
+        return np.ascontiguousarray(a.bits, dtype=np.uint16), BF16_CODE
+    a = np.ascontiguousarray(a)
+    codes = {np.float32: F32, np.float16: F16, np.float64: F64, np.int8: I8, np.uint8: U8, np.int16: I16,
+             np.int32: I32, np.int64: I64, np.bool_: BOOL}
+    for t, c in codes.items():
+        if a.dtype == t:
+            return a, c
+    raise TypeError(f"oracle: unsupported dtype {a.dtype}")
+
+
+def _ptr(a: np.ndarray):
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+# ---- conversions ---------------------------------------------------------------------------
+
+def f32_to_f16_bits(x) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty(x.shape, dtype=np.uint16)
+    lib().oracle_f32_to_f16_array(_ptr(x), _ptr(y), x.size)
+    return y
+
+
+def f16_bits_to_f32(h) -> np.ndarray:
+    h = np.ascontiguousarray(h, dtype=np.uint16)
+    y = np.empty(h.shape, dtype=np.float32)
+    lib().oracle_f16_to_f32_array(_ptr(h), _ptr(y), h.size)
+    return y
+
+
+def f32_to_bf16_bits(x) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty(x.shape, dtype=np.uint16)
+    lib().oracle_f32_to_bf16_array(_ptr(x), _ptr(y), x.size)
+    return y
+
+
+def bf16_bits_to_f32(b) -> np.ndarray:
+    b = np.ascontiguousarray(b, dtype=np.uint16)
+    y = np.empty(b.shape, dtype=np.float32)
+    lib().oracle_bf16_to_f32_array(_ptr(b), _ptr(y), b.size)
+    return y
+
+
+def to_f64(a) -> np.ndarray:
+    """Values of an oracle input as float64."""
+    if isinstance(a, BF16):
+        return bf16_bits_to_f32(a.bits).astype(np.float64)
+    return np.asarray(a).astype(np.float64)
+
+
+# ---- attention -----------------------------------------------------------------------------
+
+def flash_attention(q, k, v, mask=None, scale: float = -1.0, is_causal: bool = False, out_dtype=None,
+                    nthreads: int = 0, return_lse: bool = False):
+    """gt_flash_attention on dense inputs.  Output dtype = q's dtype unless `out_dtype` (a code)
+    is given; float16/bfloat16 outputs come back as uint16 bit patterns."""
+    qa, qc = _code(q)
+    ka, kc = _code(k)
+    va, vc = _code(v)
+    B, H, L, D = qa.shape
+    _, Hkv, S, Dv = va.shape
+    oc = qc if out_dtype is None else out_dtype
+    out = np.empty((B, H, L, Dv), dtype={F32: np.float32, F64: np.float64, F16: np.uint16, BF16_CODE: np.uint16}[oc])
+    lse = np.empty((B, H, L), dtype=np.float64) if return_lse else None
+    if mask is not None:
+        ma, mc = _code(mask)
+        mshape = (ctypes.c_int64 * 4)(*ma.shape, *([0] * (4 - ma.ndim)))
+        mptr, mnd = _ptr(ma), ma.ndim
+    else:
+        ma, mc, mshape, mptr, mnd = None, 0, None, None, 0
+    rc = lib().oracle_flash_attention(_ptr(qa), qc, _ptr(ka), kc, _ptr(va), vc, mptr, mc, mnd,
+                                      ctypes.cast(mshape, ctypes.c_void_p) if mshape is not None else None,
+                                      B, H, Hkv, L, S, D, Dv, float(scale), int(bool(is_causal)),
+                                      _ptr(out), oc, _ptr(lse) if lse is not None else None, int(nthreads))
+    if rc != 0:
+        raise ValueError("oracle_flash_attention: inconsistent shapes")
+    return (out, lse) if return_lse else out
+
+
+def flash_attention_backward(dout, q, k, v, mask=None, scale: float = -1.0, is_causal: bool = False,
+                             nthreads: int = 0):
+    """FlashAttentionFn.backward in float64: returns (dq, dk, dv) as float64 arrays."""
+    ga, gc = _code(dout)
+    qa, qc = _code(q)
+    ka, kc = _code(k)
+    va, vc = _code(v)
+    B, H, L, D = qa.shape
+    _, Hkv, S, Dv = va.shape
+    dq = np.empty((B, H, L, D), dtype=np.float64)
+    dk = np.empty((B, Hkv, S, D), dtype=np.float64)
+    dv = np.empty((B, Hkv, S, Dv), dtype=np.float64)
+    if mask is not None:
+        ma, mc = _code(mask)
+        mshape = (ctypes.c_int64 * 4)(*ma.shape, *([0] * (4 - ma.ndim)))
+        mptr, mnd = _ptr(ma), ma.ndim
+    else:
+        ma, mc, mshape, mptr, mnd = None, 0, None, None, 0
+    rc = lib().oracle_flash_attention_backward(_ptr(ga), gc, _ptr(qa), qc, _ptr(ka), kc, _ptr(va), vc, mptr, mc, mnd,
+                                               ctypes.cast(mshape, ctypes.c_void_p) if mshape is not None else None,
+                                               B, H, Hkv, L, S, D, Dv, float(scale), int(bool(is_causal)),
+                                               _ptr(dq), _ptr(dk), _ptr(dv), int(nthreads))
+    if rc != 0:
+        raise ValueError("oracle_flash_attention_backward: inconsistent shapes")
+    return dq, dk, dv
+
+
+# ---- Q8_0 ----------------------------------------------------------------------------------
+
+def q8_0_quantize(x) -> np.ndarray:
+    """float32 values (size a multiple of 32) -> ggml block_q8_0 bytes, shape (nblocks*34,)."""
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1)
+    if x.size % 32:
+        raise ValueError("q8_0 needs a multiple of 32 values")
+    out = np.empty(x.size // 32 * 34, dtype=np.uint8)
+    lib().oracle_q8_0_quantize(_ptr(x), _ptr(out), x.size // 32)
+    return out
+
+
+def q8_0_dequantize(blocks) -> np.ndarray:
+    b = np.ascontiguousarray(blocks, dtype=np.uint8).reshape(-1)
+    n = b.size // 34
+    y = np.empty(n * 32, dtype=np.float32)
+    lib().oracle_q8_0_dequantize(_ptr(b), _ptr(y), n)
+    return y
+
+
+def max_threads() -> int:
+    return int(lib().oracle_max_threads())

@@ -1,0 +1,79 @@
+"""Backward parity: gt_flash_attention_backward against the float64 oracle restatement of
+FlashAttentionFn.backward (gguf_train/_functions.py:1933-1965) on the same rounded inputs, the
+kernel's float32 gradients compared before the autograd engine casts them; plus gradcheck in
+float64 (tests/test_autograd.py:137-140) and the autograd wiring."""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import gguf_train_amd as g
+import oracle
+from gguf_train_amd.nn import functional as F
+
+from _util import assert_close, randn, to_oracle
+
+pytestmark = pytest.mark.gpu
+
+
+def oracle_grads(dout, q, k, v, mask=None, is_causal=False, scale=-1.0):
+    return oracle.flash_attention_backward(to_oracle(dout), to_oracle(q), to_oracle(k), to_oracle(v),
+                                           mask=None if mask is None else to_oracle(mask), scale=scale,
+                                           is_causal=is_causal)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("B,H,Hkv,L,S,D", [(2, 4, 4, 20, 20, 64), (1, 4, 2, 13, 29, 32), (2, 2, 1, 33, 17, 128)])
+@pytest.mark.parametrize("causal", [False, True])
+def test_native_backward_matches_oracle(dev, dtype, B, H, Hkv, L, S, D, causal):
+    seed = 7 * B + L + S
+    q, k, v = randn((B, H, L, D), seed, dtype), randn((B, Hkv, S, D), seed + 1, dtype), randn((B, Hkv, S, D), seed + 2, dtype)
+    dout = randn((B, H, L, D), seed + 3, dtype)
+    # key padding, as the training configuration: valid length per sequence, -inf beyond
+    lens = np.random.default_rng(seed).integers(S // 2 + 1, S + 1, size=B)
+    mask = torch.zeros(B, 1, 1, S)
+    for b, n in enumerate(lens):
+        mask[b, ..., n:] = float("-inf")
+    out, lse = g.flash_attention_lse(q.to(dev), k.to(dev), v.to(dev), mask.to(dev), 0.0, causal)
+    dq, dk, dv = g.flash_attention_backward(dout.to(dev), q.to(dev), k.to(dev), v.to(dev), mask.to(dev), out, lse,
+                                            0.0, causal)
+    assert dq.dtype == dk.dtype == dv.dtype == torch.float32
+    wq, wk, wv = oracle_grads(dout, q, k, v, mask=mask, is_causal=causal)
+    tol_dtype = torch.float32 if dtype == torch.float32 else torch.bfloat16
+    assert_close(dq, wq, tol_dtype, "dq")
+    assert_close(dk, wk, tol_dtype, "dk")
+    assert_close(dv, wv, tol_dtype, "dv")
+
+
+def test_gradcheck_float64(dev):
+    torch.manual_seed(0)
+    q, k, v = (torch.randn(1, 2, 4, 8, dtype=torch.float64, device=dev, requires_grad=True) for _ in range(3))
+    assert torch.autograd.gradcheck(lambda a, b, c: F.scaled_dot_product_attention(a, b, c, is_causal=True),
+                                    (q, k, v), eps=1e-6, atol=1e-5, rtol=1e-3)
+
+
+def test_autograd_wiring_and_grad_dtypes(dev):
+    q = randn((2, 4, 16, 64), 1, torch.bfloat16).to(dev).requires_grad_()
+    k = randn((2, 2, 16, 64), 2, torch.bfloat16).to(dev).requires_grad_()
+    v = randn((2, 2, 16, 64), 3, torch.bfloat16).to(dev).requires_grad_()
+    out = F.scaled_dot_product_attention(q, k, v, is_causal=True)
+    dout = randn((2, 4, 16, 64), 4, torch.bfloat16).to(dev)
+    out.backward(dout)
+    assert q.grad.dtype == k.grad.dtype == v.grad.dtype == torch.bfloat16
+    wq, wk, wv = oracle_grads(dout, q, k, v, is_causal=True)
+    for got, want in ((q.grad, wq), (k.grad, wk), (v.grad, wv)):
+        # bf16 rounding of the gradient itself on top of the kernel tolerance
+        err = np.abs(got.float().cpu().numpy() - want) / np.maximum(1.0, np.abs(want))
+        assert err.max() < 2e-3 + 2 ** -8
+
+
+def test_backward_without_saved_lse(dev):
+    q, k, v = randn((1, 2, 9, 16), 5), randn((1, 2, 9, 16), 6), randn((1, 2, 9, 16), 7)
+    dout = randn((1, 2, 9, 16), 8)
+    dq, dk, dv = g.flash_attention_backward(dout.to(dev), q.to(dev), k.to(dev), v.to(dev), None, None, None, 0.0, True)
+    wq, wk, wv = oracle_grads(dout, q, k, v, is_causal=True)
+    assert_close(dq, wq, torch.float32, "dq")
+    assert_close(dk, wk, torch.float32, "dk")
+    assert_close(dv, wv, torch.float32, "dv")

@@ -1,0 +1,102 @@
+"""MultiheadAttention on the GPU against the reference test's explicit implementation
+(tests/test_pooling_and_attention.py:176-260): every layout, need_weights on/off, nine mask
+combinations."""
+
+import itertools
+import math
+
+import pytest
+import torch
+
+from gguf_train_amd.nn import MultiheadAttention
+
+pytestmark = pytest.mark.gpu
+NEG_INF = float("-inf")
+
+
+def mha_reference(m, q, k, v, key_padding_mask=None, attn_mask=None):
+    E, H = m.embed_dim, m.num_heads
+    D = E // H
+    B, L, _ = q.shape
+    S = k.shape[1]
+
+    def project(x, i):
+        y = x.matmul(m.in_proj_weight[i * E:(i + 1) * E].transpose(0, 1)) + m.in_proj_bias[i * E:(i + 1) * E]
+        return y.reshape(B, x.shape[1], H, D).transpose(1, 2)
+
+    scores = project(q, 0).matmul(project(k, 1).transpose(-2, -1)) / math.sqrt(D)
+    for mask, shape in ((attn_mask, None), (key_padding_mask, (B, 1, 1, S))):
+        if mask is None:
+            continue
+        if shape is None:
+            shape = (1, 1, L, S) if mask.ndim == 2 else (B, H, L, S)
+        mask = mask.reshape(shape)
+        scores = scores.masked_fill(mask, NEG_INF) if mask.dtype == torch.bool else scores + mask
+    weights = torch.softmax(scores, dim=-1)
+    out = weights.matmul(project(v, 2)).transpose(1, 2).reshape(B, L, E)
+    return out.matmul(m.out_proj.weight.transpose(0, 1)) + m.out_proj.bias, weights
+
+
+def masks(batch, L, S, H, dev):
+    kpm = torch.zeros(batch, S, dtype=torch.bool)
+    kpm[:, -1] = True
+    if batch > 1:
+        kpm[1, 1] = True
+    causal = torch.triu(torch.ones(L, S), diagonal=1).bool()
+    per_head = torch.rand(batch * H, L, S) < 0.3
+    per_head[:, :, 0] = False
+    d = {
+        "none": (None, None),
+        "bool kpm": (kpm, None),
+        "float kpm": (torch.zeros(batch, S).masked_fill(kpm, NEG_INF), None),
+        "bool attn": (None, causal),
+        "float attn": (None, torch.zeros(L, S).masked_fill(causal, NEG_INF)),
+        "3D bool attn": (None, per_head),
+        "bool kpm + bool attn": (kpm, causal),
+        "bool kpm + float attn": (kpm, torch.zeros(L, S).masked_fill(causal, NEG_INF)),
+        "float kpm + 3D bool attn": (torch.zeros(batch, S).masked_fill(kpm, NEG_INF), per_head),
+    }
+    return {n: tuple(None if t is None else t.to(dev) for t in pair) for n, pair in d.items()}
+
+
+def test_matches_the_reference_in_every_layout(dev):
+    E, H, B, L, S = 8, 2, 3, 4, 5
+    torch.manual_seed(0)
+    for batch_first, batched, need_weights in itertools.product((False, True), (True, False), (True, False)):
+        m = MultiheadAttention(E, H, batch_first=batch_first).to(dev)
+        with torch.no_grad():
+            m.in_proj_bias.copy_(torch.randn(3 * E) * 0.1)
+        m.eval()
+        batch = B if batched else 1
+        q, k, v = (torch.randn(batch, n, E, device=dev) for n in (L, S, S))
+
+        def layout(x):
+            if not batched:
+                return x[0]
+            return x if batch_first else x.transpose(0, 1)
+
+        for name, (kpm, am) in masks(batch, L, S, H, dev).items():
+            with torch.no_grad():
+                want, weights = mha_reference(m, q, k, v, kpm, am)
+                out, got_w = m(layout(q), layout(k), layout(v), key_padding_mask=kpm if (batched or kpm is None) else kpm[0],
+                               attn_mask=am, need_weights=need_weights)
+            assert (out - layout(want)).abs().max().item() < 1e-4, name
+            if need_weights:
+                avg = weights.mean(dim=1)
+                assert (got_w - (avg if batched else avg[0])).abs().max().item() < 1e-4, name
+            else:
+                assert got_w is None
+
+
+def test_gradients_reach_every_parameter(dev):
+    torch.manual_seed(4)
+    m = MultiheadAttention(8, 2, batch_first=True).to(dev)
+    x = torch.randn(2, 4, 8, device=dev)
+    kpm = torch.tensor([[False, False, False, True], [False, False, True, True]], device=dev)
+    causal = torch.triu(torch.ones(4, 4, device=dev), diagonal=1).bool()
+    for need_weights in (True, False):
+        m.zero_grad()
+        out, _ = m(x, x, x, key_padding_mask=kpm, attn_mask=causal, need_weights=need_weights)
+        out.sum().backward()
+        for name, p in m.named_parameters():
+            assert p.grad is not None and torch.isfinite(p.grad).all(), name
