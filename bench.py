@@ -1,0 +1,249 @@
+#!/usr/bin/env python
+"""Attention-path benchmark on one MI355X.
+
+A step is one call of the native entry point gt_flash_attention (through the C ABI, on
+handles made once over device-resident inputs) over one batch of synthetic data:
+
+  prefill      causal SDPA fp16, B=4 H=32 L=S=2048 D=128, q/k/v ~ 0.5*N(0,1)   (headline)
+  decode       GQA decode fp16, B=32 Hq=32 Hkv=8, one query row, KV length 4096, D=128
+  decode_q8_0  GQA decode over a GGUF Q8_0 K/V cache, B=16 Hq=32 Hkv=8, KV length 8192, D=128
+  train        bf16 forward + backward, B=8 H=16 L=S=1024 D=64, causal + key padding (-inf)
+  fp32         fp32 causal forward, B=1 H=4 L=S=128 D=64 (the parity configuration)
+
+The JSON line's `value` is the headline (prefill) TFLOP/s; the other configurations are
+reported under "configs".  Work is counted algorithmically: attention FLOPs = 4*D per
+unmasked (query, key) pair and head, backward = 2.5x forward; decode bytes = K + V (read once
+per kv head) + Q + O, Q8_0 = 34 bytes per 32 values.
+
+cpu_baseline: the float64 CPU restatement of the reference's gt_flash_attention (the oracle,
+OpenMP over (batch, head) like csrc/gt_ops_nn.cpp:2468) on a bounded sample of the headline
+workload, on this host's cores.
+"""
+
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+PEAK_FP16_TFLOPS = 2516.6  # dense MFMA fp16/bf16, MI355X
+PEAK_HBM_GBS = 8000.0
+
+
+def parse_args():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--configs", default="prefill,decode,decode_q8_0,train,fp32")
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    p.add_argument("--cpu-heads", type=int, default=8, help="heads of the headline workload in the CPU sample")
+    return p.parse_args()
+
+
+def causal_pairs(L, valid=None):
+    """Unmasked (query, key) pairs of a causal L x L block with keys limited to `valid`."""
+    v = L if valid is None else valid
+    return v * (v + 1) // 2 + (L - v) * v
+
+
+class Runner:
+    """Calls gt_flash_attention (or the backward) on fixed borrowed handles."""
+
+    def __init__(self):
+        import torch
+
+        from gguf_train_amd import _C, _bridge
+
+        self.torch, self.C, self.bridge = torch, _C, _bridge
+        self.dev = torch.device("cuda:0")
+        _bridge.bind_stream(self.dev)
+
+    def handles(self, *ts):
+        return [self.bridge.borrow(t) if t is not None else None for t in ts]
+
+    def time_steps(self, step, steps, warmup):
+        torch = self.torch
+        for _ in range(warmup):
+            step(0)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        e0.record()
+        for i in range(steps):
+            step(i)
+        e1.record()
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        return e0.elapsed_time(e1) / steps, wall * 1e3 / steps
+
+
+def bench_forward(r: Runner, name, cfg, steps, warmup):
+    torch = r.torch
+    lib = r.C.lib
+    B, H, Hkv, L, S, D = cfg["B"], cfg["H"], cfg["Hkv"], cfg["L"], cfg["S"], cfg["D"]
+    dt = cfg["dtype"]
+    g = torch.Generator(device=r.dev).manual_seed(1234)
+    nbuf = cfg.get("rotate", 1)
+    sets = []
+    for _ in range(nbuf):
+        q = (torch.randn(B, H, L, D, device=r.dev, generator=g) * cfg.get("amp", 1.0)).to(dt)
+        k = (torch.randn(B, Hkv, S, D, device=r.dev, generator=g) * cfg.get("amp", 1.0))
+        v = (torch.randn(B, Hkv, S, D, device=r.dev, generator=g) * cfg.get("amp", 1.0))
+        if cfg.get("q8_0"):
+            from gguf_train_amd import quantize
+
+            k, v = quantize(k), quantize(v)
+        else:
+            k, v = k.to(dt), v.to(dt)
+        sets.append((q, k, v))
+    hs = [r.handles(*s) for s in sets]
+    causal = 1 if cfg.get("causal") else 0
+
+    def step(i):
+        hq, hk, hv = hs[i % nbuf]
+        p = lib.gt_flash_attention(hq.ptr, hk.ptr, hv.ptr, None, ctypes.c_float(0.0), causal)
+        if not p:
+            raise RuntimeError(r.C.last_error())
+        lib.gt_tensor_free(p)
+
+    ms, wall_ms = r.time_steps(step, steps, warmup)
+    out = {"ms_per_step": ms, "wall_ms_per_step": wall_ms}
+    es = 2 if dt != torch.float32 else 4
+    if "decode" in name:
+        if cfg.get("q8_0"):
+            kv = 2 * B * Hkv * S * D // 32 * 34
+        else:
+            kv = 2 * B * Hkv * S * D * es
+        nbytes = kv + 2 * B * H * D * es
+        out.update(bytes_per_step=nbytes, value=nbytes / (ms * 1e-3) / 1e9, unit="GB/s",
+                   frac_of_peak=nbytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, rotated_buffers=nbuf)
+    else:
+        pairs = causal_pairs(L) if causal else L * S
+        flops = 4 * D * pairs * B * H
+        out.update(flop_per_step=flops, value=flops / (ms * 1e-3) / 1e12, unit="TFLOP/s",
+                   frac_of_peak=flops / (ms * 1e-3) / 1e12 / (PEAK_FP16_TFLOPS if dt != torch.float32 else 157.3))
+    return out
+
+
+def bench_train(r: Runner, cfg, steps, warmup):
+    import numpy as np
+
+    torch = r.torch
+    lib = r.C.lib
+    B, H, L, D = cfg["B"], cfg["H"], cfg["L"], cfg["D"]
+    dt = cfg["dtype"]
+    g = torch.Generator(device=r.dev).manual_seed(99)
+    q, k, v, dout = (torch.randn(B, H, L, D, device=r.dev, generator=g).to(dt) for _ in range(4))
+    lens = np.random.default_rng(5).integers(512, 1025, size=B)
+    mask = torch.zeros(B, 1, 1, L, device=r.dev)
+    for b, n in enumerate(lens):
+        mask[b, ..., int(n):] = float("-inf")
+    hq, hk, hv, hm, hg = r.handles(q, k, v, mask, dout)
+
+    def step(i):
+        po, pl = ctypes.c_void_p(), ctypes.c_void_p()
+        rc = lib.gt_flash_attention_lse(hq.ptr, hk.ptr, hv.ptr, hm.ptr, ctypes.c_float(0.0), 1, ctypes.byref(po),
+                                        ctypes.byref(pl))
+        if rc:
+            raise RuntimeError(r.C.last_error())
+        dq, dk, dv = ctypes.c_void_p(), ctypes.c_void_p(), ctypes.c_void_p()
+        rc = lib.gt_flash_attention_backward(hg.ptr, hq.ptr, hk.ptr, hv.ptr, hm.ptr, po, pl, ctypes.c_float(0.0), 1,
+                                             ctypes.byref(dq), ctypes.byref(dk), ctypes.byref(dv))
+        if rc:
+            raise RuntimeError(r.C.last_error())
+        for p in (po, pl, dq, dk, dv):
+            lib.gt_tensor_free(p)
+
+    ms, wall_ms = r.time_steps(step, steps, warmup)
+    fwd = sum(4 * D * causal_pairs(L, int(n)) * H for n in lens)
+    flops = int(fwd * 3.5)
+    return {"ms_per_step": ms, "wall_ms_per_step": wall_ms, "flop_per_step": flops, "forward_flop": fwd,
+            "value": flops / (ms * 1e-3) / 1e12, "unit": "TFLOP/s",
+            "frac_of_peak": flops / (ms * 1e-3) / 1e12 / PEAK_FP16_TFLOPS, "valid_lengths": [int(x) for x in lens]}
+
+
+def cpu_baseline(heads: int):
+    """The oracle (fp64 restatement of gt_flash_attention) on `heads` heads of the headline
+    workload (one sequence, L=S=2048, D=128, causal, fp16 inputs), OpenMP over heads."""
+    import numpy as np
+
+    import oracle
+
+    threads = min(16, os.cpu_count() or 1)
+    rng = np.random.default_rng(7)
+    L, D = 2048, 128
+    q, k, v = ((rng.standard_normal((1, heads, L, D)) * 0.5).astype(np.float16) for _ in range(3))
+    t0 = time.perf_counter()
+    oracle.flash_attention(q, k, v, is_causal=True, nthreads=threads)
+    sec = time.perf_counter() - t0
+    flops = 4 * D * causal_pairs(L) * heads
+    return {"value": flops / sec / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "sample": f"{heads} heads of one sequence of the prefill workload (L=S=2048, D=128, causal, fp16), "
+                      f"{sec:.1f} s"}
+
+
+CONFIGS = {
+    "prefill": dict(B=4, H=32, Hkv=32, L=2048, S=2048, D=128, dtype="float16", causal=True, amp=0.5),
+    "decode": dict(B=32, H=32, Hkv=8, L=1, S=4096, D=128, dtype="float16", rotate=2),
+    "decode_q8_0": dict(B=16, H=32, Hkv=8, L=1, S=8192, D=128, dtype="float16", q8_0=True, rotate=3),
+    "train": dict(B=8, H=16, L=1024, D=64, dtype="bfloat16"),
+    "fp32": dict(B=1, H=4, Hkv=4, L=128, S=128, D=64, dtype="float32", causal=True),
+}
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
+              "(the attention path has no multi-GPU exchange)", file=sys.stderr)
+        return 2
+    import torch
+
+    r = Runner()
+    results = {}
+    for name in [c for c in args.configs.split(",") if c]:
+        cfg = dict(CONFIGS[name])
+        cfg["dtype"] = getattr(torch, cfg["dtype"])
+        if name == "train":
+            results[name] = bench_train(r, cfg, args.steps, args.warmup)
+        else:
+            results[name] = bench_forward(r, name, cfg, args.steps, args.warmup)
+        print(f"[bench] {name}: {json.dumps(results[name])}", file=sys.stderr, flush=True)
+
+    head = results.get("prefill") or next(iter(results.values()))
+    line = {
+        "metric": "SDPA prefill TFLOP/s + decode KV GB/s on 1 MI355X (% roofline) vs ggml CPU",
+        "value": head["value"],
+        "unit": head["unit"],
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": head["ms_per_step"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic",
+        "config": {"workload": "causal prefill SDPA fp16, B=4 H=32 L=S=2048 D=128",
+                   "batch": 4, "heads": 32, "seq_len": 2048, "head_dim": 128, "causal": True},
+        "roofline": {"bound": "mfma", "achieved": head["value"], "peak": PEAK_FP16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": head["value"] / PEAK_FP16_TFLOPS, "traffic": None},
+        "configs": results,
+    }
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline(args.cpu_heads)
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    raise SystemExit(main())

@@ -44,6 +44,18 @@ struct AttnBwdArgs {
     void *delta;           // (B,H,L) scratch: rowsum(P * dP)
 };
 
+// Single-query (L == 1) split-K decode: per-chunk partials, then a merge.
+struct DecodeArgs {
+    AttnFwdArgs f;
+    float *part_o;   // (B*H, nsplit, D) unnormalised chunk outputs
+    float *part_ml;  // (B*H, nsplit, 2) chunk max (log2 domain) and sum of exp2
+    int nsplit;
+};
+
 // Launchers.  `cd` is the compute dtype of q/k/v (GT_F32/GT_F16/GT_BF16/GT_F64).
 hipError_t launch_attn_generic_fwd(const AttnFwdArgs &a, int cd, hipStream_t s);
 hipError_t launch_attn_generic_bwd(const AttnBwdArgs &a, int cd, hipStream_t s);
+
+bool attn_decode_supported(const AttnFwdArgs &f, int cd);
+int attn_decode_splits(int64_t S);
+hipError_t launch_attn_decode(const DecodeArgs &a, int cd, hipStream_t s);

@@ -160,6 +160,23 @@ void fill_qkv(AttnFwdArgs &a, const gt_tensor *q, const gt_tensor *k, const gt_t
     }
 }
 
+// Picks the kernel for a staged forward: split-K decode for single-query rows, the generic
+// kernel otherwise.
+bool dispatch_forward(const AttnFwdArgs &a, int cd, int dev) {
+    if (a.out_dtype == cd && attn_decode_supported(a, cd)) {
+        DecodeArgs da{};
+        da.f = a;
+        da.nsplit = attn_decode_splits(a.S);
+        const size_t rows = (size_t)(a.B * a.H) * (size_t)da.nsplit;
+        gt_scratch ws;
+        if (!gt_scratch_alloc(ws, rows * (size_t)(a.D + 2) * sizeof(float), dev)) return false;
+        da.part_o = (float *)ws.ptr();
+        da.part_ml = da.part_o + rows * (size_t)a.D;
+        return gt_hip_check(launch_attn_decode(da, cd, gt_stream()), "flash_attention decode kernel");
+    }
+    return gt_hip_check(launch_attn_generic_fwd(a, cd, gt_stream()), "flash_attention kernel");
+}
+
 // Moves a device result into a new host tensor when the caller's q lives on the host.
 gt_tensor *deliver(gt_tensor *dev_t, bool to_host) {
     if (!dev_t || !to_host) return dev_t;
@@ -215,7 +232,7 @@ int attention_forward(const char *who, const gt_tensor *q, const gt_tensor *k, c
             a.scale = scale;
             a.causal = is_causal ? 1 : 0;
             a.out_dtype = q->dtype;
-            ok = gt_hip_check(launch_attn_generic_fwd(a, cd, gt_stream()), "flash_attention kernel");
+            ok = dispatch_forward(a, cd, dev);
         }
     }
     if (!ok) {

@@ -42,9 +42,9 @@ def test_native_backward_matches_oracle(dev, dtype, B, H, Hkv, L, S, D, causal):
     assert dq.dtype == dk.dtype == dv.dtype == torch.float32
     wq, wk, wv = oracle_grads(dout, q, k, v, mask=mask, is_causal=causal)
     tol_dtype = torch.float32 if dtype == torch.float32 else torch.bfloat16
-    assert_close(dq, wq, tol_dtype, "dq")
-    assert_close(dk, wk, tol_dtype, "dk")
-    assert_close(dv, wv, tol_dtype, "dv")
+    assert_close(dq, wq, tol_dtype, "dq", out_dtype=torch.float32)
+    assert_close(dk, wk, tol_dtype, "dk", out_dtype=torch.float32)
+    assert_close(dv, wv, tol_dtype, "dv", out_dtype=torch.float32)
 
 
 def test_gradcheck_float64(dev):

@@ -1,0 +1,76 @@
+"""Single-query (decode) attention, the split-K kernel: GQA group sizes, head sizes, KV lengths
+that are not multiples of the chunk, key-padding masks, causal (top-left: key 0 only), and the
+invariant that decoding row t equals row t of a causal prefill (tests/test_llama_bridge.py:105-111)."""
+
+import numpy as np
+import pytest
+import torch
+
+import gguf_train_amd as g
+
+from _util import assert_close, oracle_forward, randn
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("G,D", [(1, 64), (2, 128), (4, 128), (8, 128), (4, 256), (8, 64)])
+@pytest.mark.parametrize("S", [1, 255, 256, 1000, 4096])
+def test_decode_matches_oracle(dev, dtype, G, D, S):
+    B, Hkv = 3, 2
+    seed = G * 100 + D + S
+    q = randn((B, Hkv * G, 1, D), seed, dtype)
+    k, v = randn((B, Hkv, S, D), seed + 1, dtype), randn((B, Hkv, S, D), seed + 2, dtype)
+    got = g.flash_attention(q.to(dev), k.to(dev), v.to(dev))
+    assert_close(got, oracle_forward(q, k, v), dtype, f"decode G={G} D={D} S={S}")
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_decode_with_key_padding_and_bool_masks(dev, dtype):
+    B, H, Hkv, S, D = 4, 8, 2, 700, 128
+    q = randn((B, H, 1, D), 1, dtype)
+    k, v = randn((B, Hkv, S, D), 2, dtype), randn((B, Hkv, S, D), 3, dtype)
+    lens = [700, 1, 333, 512]
+    add = torch.zeros(B, 1, 1, S)
+    allowed = torch.zeros(B, 1, 1, S, dtype=torch.bool)
+    for b, n in enumerate(lens):
+        add[b, ..., n:] = float("-inf")
+        allowed[b, ..., :n] = True
+    want = oracle_forward(q, k, v, mask=add)
+    assert_close(g.flash_attention(q.to(dev), k.to(dev), v.to(dev), add.to(dev)), want, dtype, "additive")
+    assert_close(g.flash_attention(q.to(dev), k.to(dev), v.to(dev), allowed.to(dev)), want, dtype, "bool")
+    per_head = torch.rand(B, H, 1, S) < 0.5
+    per_head[..., 0] = True
+    assert_close(g.flash_attention(q.to(dev), k.to(dev), v.to(dev), per_head.to(dev)),
+                 oracle_forward(q, k, v, mask=per_head), dtype, "per-head bool")
+    nothing = torch.zeros(B, 1, 1, S, dtype=torch.bool)
+    out = g.flash_attention(q.to(dev), k.to(dev), v.to(dev), nothing.to(dev))
+    assert torch.equal(out.cpu(), torch.zeros(B, H, 1, D, dtype=dtype))
+
+
+def test_decode_causal_sees_key_zero_only(dev):
+    q = randn((2, 4, 1, 128), 5, torch.float16)
+    k, v = randn((2, 2, 300, 128), 6, torch.float16), randn((2, 2, 300, 128), 7, torch.float16)
+    got = g.flash_attention(q.to(dev), k.to(dev), v.to(dev), None, 0.0, True).cpu()
+    want = v[:, :, :1].repeat_interleave(2, dim=1)
+    assert torch.equal(got, want)
+
+
+def test_decode_row_equals_prefill_row(dev):
+    B, H, Hkv, T, D = 2, 8, 2, 513, 128
+    q = randn((B, H, T, D), 8, torch.float16).to(dev)
+    k, v = randn((B, Hkv, T, D), 9, torch.float16).to(dev), randn((B, Hkv, T, D), 10, torch.float16).to(dev)
+    full = g.flash_attention(q, k, v, None, 0.0, True)
+    for t in (0, 100, 512):
+        row = g.flash_attention(q[:, :, t:t + 1], k[:, :, :t + 1], v[:, :, :t + 1])
+        diff = (row.float() - full[:, :, t:t + 1].float()).abs().max().item()
+        assert diff <= 2e-3, (t, diff)
+
+
+def test_decode_lse(dev):
+    q = randn((2, 4, 1, 64), 11, torch.bfloat16)
+    k, v = randn((2, 1, 900, 64), 12, torch.bfloat16), randn((2, 1, 900, 64), 13, torch.bfloat16)
+    out, lse = g.flash_attention_lse(q.to(dev), k.to(dev), v.to(dev))
+    want_o, want_l = oracle_forward(q, k, v, return_lse=True)
+    assert_close(out, want_o, torch.bfloat16, "out")
+    assert np.abs(lse.cpu().numpy() - want_l).max() < 1e-4
