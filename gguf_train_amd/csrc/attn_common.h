@@ -59,3 +59,6 @@ hipError_t launch_attn_generic_bwd(const AttnBwdArgs &a, int cd, hipStream_t s);
 bool attn_decode_supported(const AttnFwdArgs &f, int cd);
 int attn_decode_splits(int64_t S);
 hipError_t launch_attn_decode(const DecodeArgs &a, int cd, hipStream_t s);
+
+bool attn_prefill_supported(const AttnFwdArgs &f, int cd);
+hipError_t launch_attn_prefill(const AttnFwdArgs &a, int cd, hipStream_t s);

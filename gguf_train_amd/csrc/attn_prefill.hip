@@ -1,0 +1,344 @@
+// Fused attention forward on gfx950 MFMA (fp16 / bf16 inputs, fp32 softmax and accumulation).
+//
+// Replaces the reference's scalar fp64 loop (csrc/gt_ops_nn.cpp:2423-2525) for L > 1 with
+// the same semantics: scale, top-left causal mask, bool/additive mask, rows with nothing to
+// attend to -> 0, output rounded from fp32 to the input dtype.
+//
+// Workgroup: 4 wavefronts, BM = 128 query rows (32 per wavefront), key/value tiles of BN = 64
+// rows staged in LDS (double buffered, one barrier per tile; the next tile's global loads are
+// in flight while the current tile is computed).  Per tile and wavefront:
+//   S^T (keys x queries) = K . Q^T    v_mfma_f32_32x32x16_{f16,bf16}; Q^T stays in registers
+//                                      as the B operand, K rows come from LDS (ds_read_b128).
+//   online softmax in the log2 domain: every lane owns one query row (lane % 32) and 32 of
+//   its scores, so max/sum are in-lane plus one exchange between the two wave halves
+//   (v_permlane32_swap).  The O rescale is skipped when no row's max moved.
+//   O^T (d x queries) += V^T . P^T    P^T is the S^T accumulator converted in place (the
+//                                      MFMA's k index is permuted to match the accumulator
+//                                      layout); V^T fragments come from the row-major V tile
+//                                      through ds_read_b64_tr_b16.
+// bf16 P is split into hi + lo bf16 parts (two MFMAs) so the probabilities keep ~16 bits.
+// Causal tiles above the diagonal are never loaded; query tiles run heaviest first.
+
+#include "attn_common.h"
+#include "gt_internal.h"
+
+#include <cmath>
+
+namespace {
+
+constexpr int BM = 128;
+constexpr int BN = 64;
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+
+template <typename T>
+struct Mfma;
+template <>
+struct Mfma<_Float16> {
+    typedef half8 V8;
+    static constexpr bool kSplitP = false;
+    static __device__ inline f32x16 mma(V8 a, V8 b, f32x16 c) { return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0); }
+    static __device__ inline uint32_t pack(float x, float y) {
+        typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+        h2 v = {(_Float16)x, (_Float16)y};
+        return __builtin_bit_cast(uint32_t, v);
+    }
+    static __device__ inline float round(float x) { return (float)(_Float16)x; }
+};
+template <>
+struct Mfma<__bf16> {
+    typedef bf16x8 V8;
+    static constexpr bool kSplitP = true;
+    static __device__ inline f32x16 mma(V8 a, V8 b, f32x16 c) { return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0); }
+    static __device__ inline uint32_t pack(float x, float y) {
+        typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+        b2 v = {(__bf16)x, (__bf16)y};
+        return __builtin_bit_cast(uint32_t, v);
+    }
+    static __device__ inline float round(float x) { return (float)(__bf16)x; }
+};
+
+template <typename T>
+__device__ inline void store4(T *dst, float a, float b, float c, float d) {
+    u32x2 v = {Mfma<T>::pack(a, b), Mfma<T>::pack(c, d)};
+    *(u32x2 *)dst = v;
+}
+
+__device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// max / sum of v over lanes l and l ^ 32
+__device__ inline float xhalf_max(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ inline float xhalf_sum(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// Row pitches (in elements) of the LDS tiles: K rows are read 16 bytes per lane by 32 lanes of
+// different rows (pitch = 16 mod 128 bytes: no bank conflict); V rows are read by the
+// transposing read, 4 rows x 32 bytes per 16 lanes (pitch = 32 mod 128 bytes).
+template <int D>
+struct Pitch {
+    static constexpr int K = D + 8;
+    static constexpr int V = D + 16;
+};
+
+// MASK: 0 = none, 1 = bool bytes, 2 = additive float.
+template <typename T, int D, bool CAUSAL, int MASK>
+__global__ __launch_bounds__(256, 2) void prefill_fwd_kernel(AttnFwdArgs a, int nq) {
+    using M = Mfma<T>;
+    using V8 = typename M::V8;
+    constexpr int KP = Pitch<D>::K, VP = Pitch<D>::V;
+    constexpr int DT = D / 16;  // k-steps of S^T = K.Q^T
+    constexpr int DB = D / 32;  // d blocks of O^T
+    constexpr int CH = D / 8;   // 16-byte chunks per row
+    constexpr int NLD = BN * CH / 256;  // 16-byte loads per thread per tile and operand
+    __shared__ __attribute__((aligned(16))) T sK[2][BN * KP];
+    __shared__ __attribute__((aligned(16))) T sV[2][BN * VP];
+
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int lrow = lane & 31, half = lane >> 5;
+    const int64_t BH = a.B * a.H;
+    const int qt = nq - 1 - (int)(blockIdx.x / BH);  // heaviest query tiles first
+    const int64_t bh = (int64_t)blockIdx.x % BH;
+    const int64_t b = bh / a.H, h = bh % a.H, hk = h / (a.H / a.Hkv);
+    const int L = (int)a.L, S = (int)a.S;
+    const int q0 = qt * BM;
+    const int wq0 = q0 + 32 * w;  // first query row of this wavefront
+    const int lq = wq0 + lrow;    // this lane's query row
+
+    // Q^T fragments (B operand): lane holds Q[lq][16t + 8*half + 0..7]; rows past L read row L-1
+    V8 qf[DT];
+    {
+        const T *qr = (const T *)a.q + b * a.q_sb + h * a.q_sh + (int64_t)min(lq, L - 1) * a.q_sl + 8 * half;
+#pragma unroll
+        for (int t = 0; t < DT; ++t) qf[t] = __builtin_bit_cast(V8, *(const u32x4 *)(qr + 16 * t));
+    }
+
+    const T *kbase = (const T *)a.k + b * a.k_sb + hk * a.k_sh;
+    const T *vbase = (const T *)a.v + b * a.v_sb + hk * a.v_sh;
+    const int kv_end = CAUSAL ? min(q0 + BM, S) : S;
+    const int ntiles = (kv_end + BN - 1) / BN;
+    const float c = a.scale * kLog2e;  // raw score -> log2 domain
+
+    f32x16 o[DB];
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) o[db][i] = 0.0f;
+    float m = -INFINITY;  // running max of this lane's row, log2 domain
+    float lsum = 0.0f;    // this lane's share of the running sum
+
+    // tile staging: chunk (row, col) of 16 bytes; rows past S repeat row S-1 (finite values,
+    // masked to -inf / weight 0 below), so the loads need no branches
+    u32x4 kreg[NLD], vreg[NLD];
+    auto load_tile = [&](int j) {
+#pragma unroll
+        for (int i = 0; i < NLD; ++i) {
+            const int cidx = tid + 256 * i, row = cidx / CH, col = cidx % CH;
+            const int key = min(j * BN + row, S - 1);
+            kreg[i] = *(const u32x4 *)(kbase + (int64_t)key * a.k_ss + 8 * col);
+            vreg[i] = *(const u32x4 *)(vbase + (int64_t)key * a.v_ss + 8 * col);
+        }
+    };
+    auto store_tile = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < NLD; ++i) {
+            const int cidx = tid + 256 * i, row = cidx / CH, col = cidx % CH;
+            *(u32x4 *)&sK[buf][row * KP + 8 * col] = kreg[i];
+            *(u32x4 *)&sV[buf][row * VP + 8 * col] = vreg[i];
+        }
+    };
+
+    load_tile(0);
+    store_tile(0);
+    if (ntiles > 1) load_tile(1);
+    __syncthreads();
+    const int g16 = lane >> 4, i16 = lane & 15;
+    for (int j = 0; j < ntiles; ++j) {
+        const int buf = j & 1;
+        const int k0 = j * BN;
+        const T *cK = sK[buf];
+        const T *cV = sV[buf];
+
+        // a wavefront whose rows all precede this tile (causal) has nothing to do here
+        if (!CAUSAL || k0 <= wq0 + 31) {
+            // ---- S^T = K . Q^T ----
+            f32x16 s[2];
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+                for (int i = 0; i < 16; ++i) s[kb][i] = 0.0f;
+#pragma unroll
+                for (int t = 0; t < DT; ++t) {
+                    const V8 kf = *(const V8 *)&cK[(32 * kb + lrow) * KP + 16 * t + 8 * half];
+                    s[kb] = M::mma(kf, qf[t], s[kb]);
+                }
+            }
+
+            // ---- masks: s[kb][i] is (key = k0 + 32kb + 8(i/4) + 4half + i%4, query = lq) ----
+            const bool edge = k0 + BN > S || (CAUSAL && k0 + BN - 1 > wq0);
+            if (MASK != 0 || edge) {
+#pragma unroll
+                for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) {
+                        const int key = k0 + 32 * kb + 8 * (i / 4) + 4 * half + (i % 4);
+                        float x = s[kb][i];
+                        if (MASK != 0) {
+                            const int64_t mi = b * a.m_sb + h * a.m_sh + (int64_t)min(lq, L - 1) * a.m_sl +
+                                               (int64_t)min(key, S - 1) * a.m_ss;
+                            if (MASK == 1) {
+                                x = ((const uint8_t *)a.mask)[mi] ? x : -INFINITY;
+                            } else {
+                                x = fmaf(((const float *)a.mask)[mi], 1.0f / a.scale, x);
+                            }
+                        }
+                        const bool blocked = key >= S || (CAUSAL && key > lq);
+                        s[kb][i] = blocked ? -INFINITY : x;
+                    }
+                }
+            }
+
+            // ---- online softmax ----
+            float tmax = -INFINITY;
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) tmax = fmaxf(tmax, s[kb][i]);
+            tmax = xhalf_max(tmax);
+            // a row with nothing visible yet keeps m = -inf, alpha = 1 and p = 0 (no branch:
+            // the MFMAs below combine the two lanes of each row and run for the whole wave)
+            const float mnew = fmaxf(m, tmax * c);
+            const bool none = mnew == -INFINITY;
+            const float msub = none ? 0.0f : mnew;
+            if (!__all(mnew == m)) {
+                const float alpha = none ? 1.0f : fast_exp2(m - mnew);
+                lsum *= alpha;
+#pragma unroll
+                for (int db = 0; db < DB; ++db)
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) o[db][i] *= alpha;
+            }
+            m = mnew;
+
+            // P^T as B operands: k-step (kb, hs) takes accumulator entries 8hs .. 8hs+7
+            V8 pb[2][2], pl[2][2];
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+                for (int hs = 0; hs < 2; ++hs) {
+                    float p[8];
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        p[e] = fast_exp2(fmaf(s[kb][8 * hs + e], c, -msub));
+                        lsum += p[e];
+                    }
+                    u32x4 pk = {M::pack(p[0], p[1]), M::pack(p[2], p[3]), M::pack(p[4], p[5]), M::pack(p[6], p[7])};
+                    pb[kb][hs] = __builtin_bit_cast(V8, pk);
+                    if constexpr (M::kSplitP) {
+                        float r[8];
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) r[e] = p[e] - M::round(p[e]);
+                        u32x4 rk = {M::pack(r[0], r[1]), M::pack(r[2], r[3]), M::pack(r[4], r[5]), M::pack(r[6], r[7])};
+                        pl[kb][hs] = __builtin_bit_cast(V8, rk);
+                    }
+                }
+            }
+
+            // ---- O^T += V^T . P^T ----
+#pragma unroll
+            for (int db = 0; db < DB; ++db) {
+#pragma unroll
+                for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+                    for (int hs = 0; hs < 2; ++hs) {
+                        // keys 32kb + 16hs + 8r + 4(g16/2) + i16/4, columns 32db + 16(g16%2) + 4(i16%4)
+                        const int row = 32 * kb + 16 * hs + 4 * (g16 >> 1) + (i16 >> 2);
+                        const int col = 32 * db + 16 * (g16 & 1) + 4 * (i16 & 3);
+                        const T *p0 = &cV[row * VP + col];
+                        const T *p1 = &cV[(row + 8) * VP + col];
+                        const s16x4 v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                            (lds_s16x4 *)(__attribute__((address_space(3))) char *)p0);
+                        const s16x4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                            (lds_s16x4 *)(__attribute__((address_space(3))) char *)p1);
+                        const u32x2 w0 = __builtin_bit_cast(u32x2, v0), w1 = __builtin_bit_cast(u32x2, v1);
+                        const V8 av = __builtin_bit_cast(V8, u32x4{w0[0], w0[1], w1[0], w1[1]});
+                        o[db] = M::mma(av, pb[kb][hs], o[db]);
+                        if constexpr (M::kSplitP) o[db] = M::mma(av, pl[kb][hs], o[db]);
+                    }
+                }
+            }
+        }
+
+        // stage tile j+1 (loaded during this tile) into the other buffer, prefetch tile j+2
+        if (j + 1 < ntiles) {
+            store_tile(buf ^ 1);
+            if (j + 2 < ntiles) load_tile(j + 2);
+        }
+        __syncthreads();
+    }
+
+    // ---- epilogue: normalise, store O (B,H,L,D) and the log-sum-exp ----
+    const float ltot = xhalf_sum(lsum);
+    const float inv = ltot > 0.0f ? 1.0f / ltot : 0.0f;
+    if (lq < L) {
+        T *orow = (T *)a.o + (bh * a.L + lq) * D;
+#pragma unroll
+        for (int db = 0; db < DB; ++db)
+#pragma unroll
+            for (int g = 0; g < 4; ++g)
+                store4<T>(orow + 32 * db + 8 * g + 4 * half, o[db][4 * g] * inv, o[db][4 * g + 1] * inv,
+                          o[db][4 * g + 2] * inv, o[db][4 * g + 3] * inv);
+        if (a.lse && half == 0) ((float *)a.lse)[bh * a.L + lq] = ltot > 0.0f ? (m + log2f(ltot)) * kLn2 : INFINITY;
+    }
+}
+
+template <typename T, int D>
+hipError_t launch_variant(const AttnFwdArgs &a, int nq, int64_t grid, hipStream_t s) {
+    const int mode = !a.mask ? 0 : (a.mask_bool ? 1 : 2);
+#define GT_PREFILL_LAUNCH(C, MK) \
+    hipLaunchKernelGGL((prefill_fwd_kernel<T, D, C, MK>), dim3((unsigned)grid), dim3(256), 0, s, a, nq)
+    if (a.causal) {
+        if (mode == 0) GT_PREFILL_LAUNCH(true, 0);
+        else if (mode == 1) GT_PREFILL_LAUNCH(true, 1);
+        else GT_PREFILL_LAUNCH(true, 2);
+    } else {
+        if (mode == 0) GT_PREFILL_LAUNCH(false, 0);
+        else if (mode == 1) GT_PREFILL_LAUNCH(false, 1);
+        else GT_PREFILL_LAUNCH(false, 2);
+    }
+#undef GT_PREFILL_LAUNCH
+    return hipGetLastError();
+}
+
+}  // namespace
+
+bool attn_prefill_supported(const AttnFwdArgs &f, int cd) {
+    if (cd != GT_F16 && cd != GT_BF16) return false;
+    if (f.out_dtype != cd || f.D != f.Dv || (f.D != 64 && f.D != 128)) return false;
+    if (f.L < 1 || f.S < 1 || !(f.scale > 0.0f)) return false;
+    if (f.L >= (1LL << 30) || f.S >= (1LL << 30)) return false;  // 32-bit row indices
+    const int64_t strides[] = {f.q_sb, f.q_sh, f.q_sl, f.k_sb, f.k_sh, f.k_ss, f.v_sb, f.v_sh, f.v_ss};
+    for (int64_t st : strides) if (st % 8 != 0) return false;
+    for (const void *p : {f.q, f.k, f.v}) if ((uintptr_t)p % 16 != 0) return false;
+    return true;
+}
+
+hipError_t launch_attn_prefill(const AttnFwdArgs &a, int cd, hipStream_t s) {
+    const int nq = (int)((a.L + BM - 1) / BM);
+    const int64_t grid = (int64_t)nq * a.B * a.H;
+    if (grid <= 0) return hipSuccess;
+    if (cd == GT_F16) return a.D == 128 ? launch_variant<_Float16, 128>(a, nq, grid, s) : launch_variant<_Float16, 64>(a, nq, grid, s);
+    return a.D == 128 ? launch_variant<__bf16, 128>(a, nq, grid, s) : launch_variant<__bf16, 64>(a, nq, grid, s);
+}

@@ -160,8 +160,8 @@ void fill_qkv(AttnFwdArgs &a, const gt_tensor *q, const gt_tensor *k, const gt_t
     }
 }
 
-// Picks the kernel for a staged forward: split-K decode for single-query rows, the generic
-// kernel otherwise.
+// Picks the kernel for a staged forward: split-K decode for single-query rows, the MFMA
+// prefill kernel for fp16/bf16 with head size 64/128, the generic kernel otherwise.
 bool dispatch_forward(const AttnFwdArgs &a, int cd, int dev) {
     if (a.out_dtype == cd && attn_decode_supported(a, cd)) {
         DecodeArgs da{};
@@ -174,6 +174,8 @@ bool dispatch_forward(const AttnFwdArgs &a, int cd, int dev) {
         da.part_ml = da.part_o + rows * (size_t)a.D;
         return gt_hip_check(launch_attn_decode(da, cd, gt_stream()), "flash_attention decode kernel");
     }
+    if (attn_prefill_supported(a, cd))
+        return gt_hip_check(launch_attn_prefill(a, cd, gt_stream()), "flash_attention prefill kernel");
     return gt_hip_check(launch_attn_generic_fwd(a, cd, gt_stream()), "flash_attention kernel");
 }
 
