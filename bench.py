@@ -150,17 +150,17 @@ def bench_train(r: Runner, cfg, steps, warmup):
     hq, hk, hv, hm, hg = r.handles(q, k, v, mask, dout)
 
     def step(i):
-        po, pl = ctypes.c_void_p(), ctypes.c_void_p()
-        rc = lib.gt_flash_attention_lse(hq.ptr, hk.ptr, hv.ptr, hm.ptr, ctypes.c_float(0.0), 1, ctypes.byref(po),
-                                        ctypes.byref(pl))
+        po, pl, p32 = ctypes.c_void_p(), ctypes.c_void_p(), ctypes.c_void_p()
+        rc = lib.gt_flash_attention_train(hq.ptr, hk.ptr, hv.ptr, hm.ptr, ctypes.c_float(0.0), 1, ctypes.byref(po),
+                                          ctypes.byref(pl), ctypes.byref(p32))
         if rc:
             raise RuntimeError(r.C.last_error())
         dq, dk, dv = ctypes.c_void_p(), ctypes.c_void_p(), ctypes.c_void_p()
-        rc = lib.gt_flash_attention_backward(hg.ptr, hq.ptr, hk.ptr, hv.ptr, hm.ptr, po, pl, ctypes.c_float(0.0), 1,
+        rc = lib.gt_flash_attention_backward(hg.ptr, hq.ptr, hk.ptr, hv.ptr, hm.ptr, p32, pl, ctypes.c_float(0.0), 1,
                                              ctypes.byref(dq), ctypes.byref(dk), ctypes.byref(dv))
         if rc:
             raise RuntimeError(r.C.last_error())
-        for p in (po, pl, dq, dk, dv):
+        for p in (po, pl, p32, dq, dk, dv):
             lib.gt_tensor_free(p)
 
     ms, wall_ms = r.time_steps(step, steps, warmup)

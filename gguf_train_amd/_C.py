@@ -123,6 +123,8 @@ def _configure(lib: ctypes.CDLL) -> ctypes.CDLL:
     lib.gt_flash_attention.restype = c_void_p
     lib.gt_flash_attention_lse.argtypes = [c_void_p, c_void_p, c_void_p, c_void_p, c_float, c_int, p_vp, p_vp]
     lib.gt_flash_attention_lse.restype = c_int
+    lib.gt_flash_attention_train.argtypes = [c_void_p, c_void_p, c_void_p, c_void_p, c_float, c_int, p_vp, p_vp, p_vp]
+    lib.gt_flash_attention_train.restype = c_int
     lib.gt_flash_attention_backward.argtypes = [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                                                 c_void_p, c_float, c_int, p_vp, p_vp, p_vp]
     lib.gt_flash_attention_backward.restype = c_int

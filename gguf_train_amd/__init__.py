@@ -9,7 +9,8 @@ MultiheadAttention with the reference's signatures, and the GGUF Q8_0 codec.
 from . import _C
 from ._bridge import QuantizedTensor
 from ._functions import FlashAttentionFn
-from ._ops import dequantize, flash_attention, flash_attention_backward, flash_attention_lse, quantize
+from ._ops import (dequantize, flash_attention, flash_attention_backward, flash_attention_lse, flash_attention_train,
+                   quantize)
 from . import nn
 
 __all__ = [
@@ -18,6 +19,7 @@ __all__ = [
     "FlashAttentionFn",
     "flash_attention",
     "flash_attention_lse",
+    "flash_attention_train",
     "flash_attention_backward",
     "quantize",
     "dequantize",

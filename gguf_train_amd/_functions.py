@@ -27,8 +27,9 @@ class FlashAttentionFn(torch.autograd.Function):
         ctx.scale = float(scale) if scale is not None else (1.0 / math.sqrt(q.shape[-1]))
         ctx.is_causal = bool(is_causal)
         if any(ctx.needs_input_grad[:3]):
-            out, lse = _ops.flash_attention_lse(q, k, v, mask, ctx.scale, ctx.is_causal)
-            ctx.save_for_backward(q, k, v, mask, out, lse)
+            # the unrounded float32 output (float16/bfloat16 inputs) makes rowsum(dO * O) exact
+            out, lse, out32 = _ops.flash_attention_train(q, k, v, mask, ctx.scale, ctx.is_causal)
+            ctx.save_for_backward(q, k, v, mask, out if out32 is None else out32, lse)
         else:
             out = _ops.flash_attention(q, k, v, mask, ctx.scale, ctx.is_causal)
         return out

@@ -42,6 +42,20 @@ def flash_attention_lse(q, k, v, mask=None, scale: float = 0.0, is_causal: bool 
     return adopt(po.value, "flash_attention"), adopt(pl.value, "flash_attention")
 
 
+def flash_attention_train(q, k, v, mask=None, scale: float = 0.0, is_causal: bool = False):
+    """Training forward: (out, lse, out32) where out32 is the float32 output before rounding
+    (None for float32/float64 inputs, whose `out` is already exact)."""
+    bind_stream(_device_of(q))
+    hq, hk, hv = borrow(q), borrow(k), borrow(v)
+    hm = borrow(mask) if mask is not None else None
+    po, pl, p32 = ctypes.c_void_p(), ctypes.c_void_p(), ctypes.c_void_p()
+    rc = _C.lib.gt_flash_attention_train(hq.ptr, hk.ptr, hv.ptr, hm.ptr if hm else None, ctypes.c_float(scale),
+                                         1 if is_causal else 0, ctypes.byref(po), ctypes.byref(pl), ctypes.byref(p32))
+    _C.check_rc(rc, "flash_attention")
+    out32 = adopt(p32.value, "flash_attention") if p32.value else None
+    return adopt(po.value, "flash_attention"), adopt(pl.value, "flash_attention"), out32
+
+
 def flash_attention_backward(dout, q, k, v, mask, out, lse, scale: float, is_causal: bool):
     """Native recompute-based backward: (dq, dk, dv) in float32 (float64 for float64 inputs)."""
     bind_stream(_device_of(q))

@@ -1,0 +1,442 @@
+// Recompute-based attention backward on gfx950 MFMA (fp16 / bf16 inputs, fp32 gradients).
+//
+// Replaces the reference's Python composition (gguf_train/_functions.py:1933-1965), which
+// materialises (B,H,L,S) scores, probabilities and their gradients, with three kernels that
+// keep everything in registers and LDS and recompute P from the forward's log-sum-exp:
+//   delta:  D_q = sum_d dO[q,d] * O[q,d]  (= sum_s P[q,s] dP[q,s], the rowsum in dS)
+//   dK/dV:  a workgroup owns 128 keys of one kv head (32 per wavefront, K and V rows held in
+//           registers) and walks over the query tiles of every query head of its GQA group:
+//             S = Q.K^T, dP = dO.V^T          (keys on lanes: the accumulator layout)
+//             P = exp2(S*scale*log2e - lse*log2e), dS = P * (dP - D_q)
+//             dV += P^T.dO, dK += dS^T.Q      (P, dS feed the MFMA A operand in place; dO and Q
+//                                              are read transposed from row-major LDS tiles)
+//   dQ:     the forward's structure (a workgroup owns 128 query rows, loops over key tiles):
+//             S^T = K.Q^T, dP^T = V.dO^T, dS^T as above, dQ^T += K^T.dS^T
+// dK and dV of a GQA group are summed in registers (no atomics).  bf16 P and dS are split
+// into hi + lo bf16 operands so the products keep ~16 bits.  Masks: top-left causal,
+// bool / additive (read per element), keys >= S and queries >= L contribute nothing.
+
+#include "attn_common.h"
+#include "gt_internal.h"
+#include "mfma_util.h"
+
+#include <cmath>
+
+namespace {
+
+using namespace gtmfma;
+
+constexpr int BKV = 128;  // keys per dK/dV workgroup (32 per wavefront)
+constexpr int BQ = 64;    // query rows per dK/dV step
+constexpr int BMQ = 128;  // query rows per dQ workgroup (32 per wavefront)
+constexpr int BNK = 64;   // key rows per dQ step
+
+// ---- delta = rowsum(dO * O) ------------------------------------------------------------------
+
+template <typename T>
+__device__ inline float to_f(T x) { return (float)x; }
+
+template <typename T, typename TO, int D>
+__global__ __launch_bounds__(256) void bwd_delta_kernel(const T *__restrict__ dout, const TO *__restrict__ o,
+                                                        float *__restrict__ delta, int64_t rows) {
+    constexpr int PER = D / 16;  // values per lane, 16 lanes per row
+    const int64_t row = ((int64_t)blockIdx.x * 256 + threadIdx.x) / 16;
+    const int sub = threadIdx.x % 16;
+    float acc = 0.0f;
+    if (row < rows) {
+        const T *g = dout + row * D + sub * PER;
+        const TO *x = o + row * D + sub * PER;
+#pragma unroll
+        for (int e = 0; e < PER; ++e) acc = fmaf(to_f(g[e]), to_f(x[e]), acc);
+    }
+#pragma unroll
+    for (int m = 1; m < 16; m <<= 1) acc += __shfl_xor(acc, m, 64);
+    if (row < rows && sub == 0) delta[row] = acc;
+}
+
+// Mask value for (b, h, query, key) under the compile-time mask mode: returns false when the
+// position is blocked; `add` receives an additive term in raw-score units.
+template <int MASK>
+__device__ inline bool mask_at(const AttnFwdArgs &f, int64_t b, int64_t h, int q, int key, float inv_scale,
+                               float &add) {
+    add = 0.0f;
+    if (MASK == 0) return true;
+    const int64_t mi = b * f.m_sb + h * f.m_sh + (int64_t)q * f.m_sl + (int64_t)key * f.m_ss;
+    if (MASK == 1) return ((const uint8_t *)f.mask)[mi] != 0;
+    add = ((const float *)f.mask)[mi] * inv_scale;
+    return true;
+}
+
+// ---- dK, dV ----------------------------------------------------------------------------------
+
+template <typename T, int D, bool CAUSAL, int MASK>
+__global__ __launch_bounds__(256) void bwd_dkdv_kernel(AttnBwdArgs a, int nkt) {
+    using M = Mfma<T>;
+    using V8 = typename M::V8;
+    constexpr int DT = D / 16, DB = D / 32, CH = D / 8;
+    constexpr int QP = D + 16;              // Q / dO tile pitch (transposed reads)
+    constexpr int NLD = BQ * CH / 256;      // 16-byte loads per thread per tile and operand
+    static_assert(NLD >= 1, "tile split over the threads");
+    __shared__ __attribute__((aligned(16))) T sQ[2][BQ * QP];
+    __shared__ __attribute__((aligned(16))) T sG[2][BQ * QP];  // dO
+    __shared__ __attribute__((aligned(16))) float sL[2][BQ];    // lse * log2(e)
+    __shared__ __attribute__((aligned(16))) float sD[2][BQ];    // delta
+
+    const AttnFwdArgs &f = a.f;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int lrow = lane & 31, half = lane >> 5;
+    const int g16 = lane >> 4, i16 = lane & 15;
+    const int kt = (int)(blockIdx.x % nkt);
+    const int64_t bk = blockIdx.x / nkt, b = bk / f.Hkv, hk = bk % f.Hkv;
+    const int G = (int)(f.H / f.Hkv);
+    const int L = (int)f.L, S = (int)f.S;
+    const int k0 = kt * BKV, wk0 = k0 + 32 * w, key = wk0 + lrow;  // this lane's key (n index)
+    const float c = f.scale * kLog2e, inv_scale = 1.0f / f.scale;
+
+    // K and V rows of this lane's key as B operands (B[k = d][n = key])
+    V8 kf[DT], vf[DT];
+    {
+        const int kk = min(key, S - 1);
+        const T *kr = (const T *)f.k + b * f.k_sb + hk * f.k_sh + (int64_t)kk * f.k_ss + 8 * half;
+        const T *vr = (const T *)f.v + b * f.v_sb + hk * f.v_sh + (int64_t)kk * f.v_ss + 8 * half;
+#pragma unroll
+        for (int t = 0; t < DT; ++t) {
+            kf[t] = __builtin_bit_cast(V8, *(const u32x4 *)(kr + 16 * t));
+            vf[t] = __builtin_bit_cast(V8, *(const u32x4 *)(vr + 16 * t));
+        }
+    }
+    f32x16 dk[DB], dv[DB];
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) dk[db][i] = dv[db][i] = 0.0f;
+
+    // the query steps: every query head of the group, queries that can see a key of this tile
+    const int qstart = CAUSAL ? (k0 / BQ) * BQ : 0;
+    const int nqs = L > qstart ? (L - qstart + BQ - 1) / BQ : 0;
+    const int nsteps = nqs * G;
+
+    u32x4 qreg[NLD], greg[NLD];
+    float lreg = 0.0f, dreg = 0.0f;
+    auto load_step = [&](int st) {
+        const int hh = st / nqs, qs0 = qstart + (st % nqs) * BQ;
+        const int64_t h = hk * G + hh;
+        const T *qb = (const T *)f.q + b * f.q_sb + h * f.q_sh;
+        const T *gb = (const T *)a.dout + ((b * f.H + h) * f.L) * D;
+#pragma unroll
+        for (int i = 0; i < NLD; ++i) {
+            const int cidx = tid + 256 * i, row = cidx / CH, col = cidx % CH;
+            const int q = min(qs0 + row, L - 1);
+            qreg[i] = *(const u32x4 *)(qb + (int64_t)q * f.q_sl + 8 * col);
+            greg[i] = *(const u32x4 *)(gb + (int64_t)q * D + 8 * col);
+        }
+        if (tid < BQ) {
+            const int64_t r = (b * f.H + h) * f.L + min(qs0 + tid, L - 1);
+            lreg = ((const float *)f.lse)[r] * kLog2e;
+            dreg = ((const float *)a.delta)[r];
+        }
+    };
+    auto store_step = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < NLD; ++i) {
+            const int cidx = tid + 256 * i, row = cidx / CH, col = cidx % CH;
+            *(u32x4 *)&sQ[buf][row * QP + 8 * col] = qreg[i];
+            *(u32x4 *)&sG[buf][row * QP + 8 * col] = greg[i];
+        }
+        if (tid < BQ) {
+            sL[buf][tid] = lreg;
+            sD[buf][tid] = dreg;
+        }
+    };
+
+    if (nsteps > 0) {
+        load_step(0);
+        store_step(0);
+        if (nsteps > 1) load_step(1);
+    }
+    __syncthreads();
+    for (int st = 0; st < nsteps; ++st) {
+        const int buf = st & 1;
+        const int hh = st / nqs, qs0 = qstart + (st % nqs) * BQ;
+        const int64_t h = hk * G + hh;
+        const T *cQ = sQ[buf];
+        const T *cG = sG[buf];
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb) {
+            const int q0 = qs0 + 32 * qb;
+            if (CAUSAL && q0 + 31 < wk0) continue;  // every query of the block precedes our keys
+            f32x16 s, dp;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) s[i] = dp[i] = 0.0f;
+#pragma unroll
+            for (int t = 0; t < DT; ++t) {
+                const V8 qa = *(const V8 *)&cQ[(32 * qb + lrow) * QP + 16 * t + 8 * half];
+                const V8 ga = *(const V8 *)&cG[(32 * qb + lrow) * QP + 16 * t + 8 * half];
+                s = M::mma(qa, kf[t], s);
+                dp = M::mma(ga, vf[t], dp);
+            }
+            // s[i], dp[i]: query q0 + 8(i/4) + 4half + i%4, key `key`
+            float p[16], ds[16];
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const int qi = 32 * qb + 8 * g + 4 * half;  // 4 consecutive queries
+                const f32x4 l4 = *(const f32x4 *)&sL[buf][qi];
+                const f32x4 d4 = *(const f32x4 *)&sD[buf][qi];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int i = 4 * g + e, q = qs0 + qi + e;
+                    float add;
+                    bool ok = key < S && q < L && (!CAUSAL || key <= q);
+                    if (MASK != 0) ok = ok && mask_at<MASK>(f, b, h, min(q, L - 1), min(key, S - 1), inv_scale, add);
+                    else add = 0.0f;
+                    const float pv = ok ? fast_exp2(fmaf(s[i] + add, c, -l4[e])) : 0.0f;
+                    p[i] = pv;
+                    ds[i] = pv * (dp[i] - d4[e]);
+                }
+            }
+            V8 pa[2], pal[2], da[2], dal[2];
+#pragma unroll
+            for (int hs = 0; hs < 2; ++hs) {
+                pack8<T>(p + 8 * hs, pa[hs], pal[hs]);
+                pack8<T>(ds + 8 * hs, da[hs], dal[hs]);
+            }
+#pragma unroll
+            for (int db = 0; db < DB; ++db) {
+#pragma unroll
+                for (int hs = 0; hs < 2; ++hs) {
+                    const int row = 32 * qb + 16 * hs + 4 * (g16 >> 1) + (i16 >> 2);
+                    const int col = 32 * db + 16 * (g16 & 1) + 4 * (i16 & 3);
+                    const V8 gt = read_tr8<T>(&cG[row * QP + col], &cG[(row + 8) * QP + col]);
+                    const V8 qt = read_tr8<T>(&cQ[row * QP + col], &cQ[(row + 8) * QP + col]);
+                    dv[db] = M::mma(pa[hs], gt, dv[db]);
+                    dk[db] = M::mma(da[hs], qt, dk[db]);
+                    if constexpr (M::kSplit) {
+                        dv[db] = M::mma(pal[hs], gt, dv[db]);
+                        dk[db] = M::mma(dal[hs], qt, dk[db]);
+                    }
+                }
+            }
+        }
+        if (st + 1 < nsteps) {
+            store_step(buf ^ 1);
+            if (st + 2 < nsteps) load_step(st + 2);
+        }
+        __syncthreads();
+    }
+
+    // dK[key][d] (scaled) and dV[key][d]: accumulator row = key wk0 + 8(i/4) + 4half + i%4, column d
+    float *dkp = (float *)a.dk + (bk * f.S) * D;
+    float *dvp = (float *)a.dv + (bk * f.S) * D;
+#pragma unroll
+    for (int db = 0; db < DB; ++db) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int kr = wk0 + 8 * (i / 4) + 4 * half + (i % 4);
+            if (kr < S) {
+                dkp[(int64_t)kr * D + 32 * db + lrow] = dk[db][i] * f.scale;
+                dvp[(int64_t)kr * D + 32 * db + lrow] = dv[db][i];
+            }
+        }
+    }
+}
+
+// ---- dQ --------------------------------------------------------------------------------------
+
+template <typename T, int D, bool CAUSAL, int MASK>
+__global__ __launch_bounds__(256) void bwd_dq_kernel(AttnBwdArgs a, int nq) {
+    using M = Mfma<T>;
+    using V8 = typename M::V8;
+    constexpr int DT = D / 16, DB = D / 32, CH = D / 8;
+    constexpr int KP = D + 16;  // K tile: row reads and transposed reads
+    constexpr int VP = D + 8;   // V tile: row reads
+    constexpr int NLD = BNK * CH / 256;
+    __shared__ __attribute__((aligned(16))) T sK[2][BNK * KP];
+    __shared__ __attribute__((aligned(16))) T sV[2][BNK * VP];
+
+    const AttnFwdArgs &f = a.f;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int lrow = lane & 31, half = lane >> 5;
+    const int g16 = lane >> 4, i16 = lane & 15;
+    const int64_t BH = f.B * f.H;
+    const int qt = nq - 1 - (int)(blockIdx.x / BH);
+    const int64_t bh = (int64_t)blockIdx.x % BH;
+    const int64_t b = bh / f.H, h = bh % f.H, hk = h / (f.H / f.Hkv);
+    const int L = (int)f.L, S = (int)f.S;
+    const int q0 = qt * BMQ, wq0 = q0 + 32 * w, lq = wq0 + lrow;
+    const int lqc = min(lq, L - 1);
+    const float c = f.scale * kLog2e, inv_scale = 1.0f / f.scale;
+
+    V8 qf[DT], gf[DT];
+    {
+        const T *qr = (const T *)f.q + b * f.q_sb + h * f.q_sh + (int64_t)lqc * f.q_sl + 8 * half;
+        const T *gr = (const T *)a.dout + (bh * f.L + lqc) * D + 8 * half;
+#pragma unroll
+        for (int t = 0; t < DT; ++t) {
+            qf[t] = __builtin_bit_cast(V8, *(const u32x4 *)(qr + 16 * t));
+            gf[t] = __builtin_bit_cast(V8, *(const u32x4 *)(gr + 16 * t));
+        }
+    }
+    const float lse2 = ((const float *)f.lse)[bh * f.L + lqc] * kLog2e;
+    const float dlt = ((const float *)a.delta)[bh * f.L + lqc];
+
+    f32x16 dq[DB];
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) dq[db][i] = 0.0f;
+
+    const T *kbase = (const T *)f.k + b * f.k_sb + hk * f.k_sh;
+    const T *vbase = (const T *)f.v + b * f.v_sb + hk * f.v_sh;
+    const int kv_end = CAUSAL ? min(q0 + BMQ, S) : S;
+    const int ntiles = (kv_end + BNK - 1) / BNK;
+    u32x4 kreg[NLD], vreg[NLD];
+    auto load_tile = [&](int j) {
+#pragma unroll
+        for (int i = 0; i < NLD; ++i) {
+            const int cidx = tid + 256 * i, row = cidx / CH, col = cidx % CH;
+            const int kk = min(j * BNK + row, S - 1);
+            kreg[i] = *(const u32x4 *)(kbase + (int64_t)kk * f.k_ss + 8 * col);
+            vreg[i] = *(const u32x4 *)(vbase + (int64_t)kk * f.v_ss + 8 * col);
+        }
+    };
+    auto store_tile = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < NLD; ++i) {
+            const int cidx = tid + 256 * i, row = cidx / CH, col = cidx % CH;
+            *(u32x4 *)&sK[buf][row * KP + 8 * col] = kreg[i];
+            *(u32x4 *)&sV[buf][row * VP + 8 * col] = vreg[i];
+        }
+    };
+
+    if (ntiles > 0) {
+        load_tile(0);
+        store_tile(0);
+        if (ntiles > 1) load_tile(1);
+    }
+    __syncthreads();
+    for (int j = 0; j < ntiles; ++j) {
+        const int buf = j & 1, k0 = j * BNK;
+        const T *cK = sK[buf];
+        const T *cV = sV[buf];
+        if (!CAUSAL || k0 <= wq0 + 31) {
+            f32x16 s[2], dp[2];
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+                for (int i = 0; i < 16; ++i) s[kb][i] = dp[kb][i] = 0.0f;
+#pragma unroll
+                for (int t = 0; t < DT; ++t) {
+                    const V8 ka = *(const V8 *)&cK[(32 * kb + lrow) * KP + 16 * t + 8 * half];
+                    const V8 va = *(const V8 *)&cV[(32 * kb + lrow) * VP + 16 * t + 8 * half];
+                    s[kb] = M::mma(ka, qf[t], s[kb]);
+                    dp[kb] = M::mma(va, gf[t], dp[kb]);
+                }
+            }
+            // s[kb][i]: key k0 + 32kb + 8(i/4) + 4half + i%4, query lq
+            V8 sb[2][2], sl[2][2];
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) {
+                float ds[16];
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    const int kk = k0 + 32 * kb + 8 * (i / 4) + 4 * half + (i % 4);
+                    float add;
+                    bool ok = kk < S && lq < L && (!CAUSAL || kk <= lq);
+                    if (MASK != 0) ok = ok && mask_at<MASK>(f, b, h, lqc, min(kk, S - 1), inv_scale, add);
+                    else add = 0.0f;
+                    const float pv = ok ? fast_exp2(fmaf(s[kb][i] + add, c, -lse2)) : 0.0f;
+                    ds[i] = pv * (dp[kb][i] - dlt);
+                }
+                pack8<T>(ds, sb[kb][0], sl[kb][0]);
+                pack8<T>(ds + 8, sb[kb][1], sl[kb][1]);
+            }
+            // dQ^T += K^T . dS^T
+#pragma unroll
+            for (int db = 0; db < DB; ++db) {
+#pragma unroll
+                for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+                    for (int hs = 0; hs < 2; ++hs) {
+                        const int row = 32 * kb + 16 * hs + 4 * (g16 >> 1) + (i16 >> 2);
+                        const int col = 32 * db + 16 * (g16 & 1) + 4 * (i16 & 3);
+                        const V8 kt = read_tr8<T>(&cK[row * KP + col], &cK[(row + 8) * KP + col]);
+                        dq[db] = M::mma(kt, sb[kb][hs], dq[db]);
+                        if constexpr (M::kSplit) dq[db] = M::mma(kt, sl[kb][hs], dq[db]);
+                    }
+                }
+            }
+        }
+        if (j + 1 < ntiles) {
+            store_tile(buf ^ 1);
+            if (j + 2 < ntiles) load_tile(j + 2);
+        }
+        __syncthreads();
+    }
+    if (lq < L) {
+        float *row = (float *)a.dq + (bh * f.L + lq) * D;
+#pragma unroll
+        for (int db = 0; db < DB; ++db)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const f32x4 v = {dq[db][4 * g] * f.scale, dq[db][4 * g + 1] * f.scale, dq[db][4 * g + 2] * f.scale,
+                                 dq[db][4 * g + 3] * f.scale};
+                *(f32x4 *)(row + 32 * db + 8 * g + 4 * half) = v;
+            }
+    }
+}
+
+template <typename T, int D, bool CAUSAL, int MASK>
+hipError_t launch_bwd_typed(const AttnBwdArgs &a, hipStream_t s) {
+    const AttnFwdArgs &f = a.f;
+    const int64_t rows = f.B * f.H * f.L;
+    const dim3 dgrid((unsigned)((rows * 16 + 255) / 256));
+    if (a.o_f32)
+        hipLaunchKernelGGL((bwd_delta_kernel<T, float, D>), dgrid, dim3(256), 0, s, (const T *)a.dout,
+                           (const float *)f.o, (float *)a.delta, rows);
+    else
+        hipLaunchKernelGGL((bwd_delta_kernel<T, T, D>), dgrid, dim3(256), 0, s, (const T *)a.dout, (const T *)f.o,
+                           (float *)a.delta, rows);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const int nkt = (int)((f.S + BKV - 1) / BKV);
+    hipLaunchKernelGGL((bwd_dkdv_kernel<T, D, CAUSAL, MASK>), dim3((unsigned)(nkt * f.B * f.Hkv)), dim3(256), 0, s, a,
+                       nkt);
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const int nq = (int)((f.L + BMQ - 1) / BMQ);
+    hipLaunchKernelGGL((bwd_dq_kernel<T, D, CAUSAL, MASK>), dim3((unsigned)(nq * f.B * f.H)), dim3(256), 0, s, a, nq);
+    return hipGetLastError();
+}
+
+template <typename T, int D>
+hipError_t launch_bwd_d(const AttnBwdArgs &a, hipStream_t s) {
+    const int mode = !a.f.mask ? 0 : (a.f.mask_bool ? 1 : 2);
+    if (a.f.causal) {
+        if (mode == 0) return launch_bwd_typed<T, D, true, 0>(a, s);
+        if (mode == 1) return launch_bwd_typed<T, D, true, 1>(a, s);
+        return launch_bwd_typed<T, D, true, 2>(a, s);
+    }
+    if (mode == 0) return launch_bwd_typed<T, D, false, 0>(a, s);
+    if (mode == 1) return launch_bwd_typed<T, D, false, 1>(a, s);
+    return launch_bwd_typed<T, D, false, 2>(a, s);
+}
+
+}  // namespace
+
+bool attn_bwd_mfma_supported(const AttnBwdArgs &a, int cd) {
+    const AttnFwdArgs &f = a.f;
+    if (cd != GT_F16 && cd != GT_BF16) return false;
+    if (f.D != f.Dv || (f.D != 64 && f.D != 128)) return false;
+    if (f.L < 1 || f.S < 1 || !(f.scale > 0.0f) || !f.o || !f.lse) return false;
+    if (f.L >= (1LL << 30) || f.S >= (1LL << 30)) return false;
+    const int64_t strides[] = {f.q_sb, f.q_sh, f.q_sl, f.k_sb, f.k_sh, f.k_ss, f.v_sb, f.v_sh, f.v_ss};
+    for (int64_t st : strides) if (st % 8 != 0) return false;
+    for (const void *p : {f.q, f.k, f.v, (const void *)a.dout, (const void *)f.o})
+        if ((uintptr_t)p % 16 != 0) return false;
+    return true;
+}
+
+hipError_t launch_attn_bwd_mfma(const AttnBwdArgs &a, int cd, hipStream_t s) {
+    if (cd == GT_F16) return a.f.D == 128 ? launch_bwd_d<_Float16, 128>(a, s) : launch_bwd_d<_Float16, 64>(a, s);
+    return a.f.D == 128 ? launch_bwd_d<__bf16, 128>(a, s) : launch_bwd_d<__bf16, 64>(a, s);
+}

@@ -24,6 +24,7 @@ struct AttnFwdArgs {
     const void *mask;
     void *o;
     void *lse;  // float (double on the float64 path) or null
+    void *o32;  // optional float32 copy of o before rounding (training forward), or null
     int64_t B, H, Hkv, L, S, D, Dv;
     int64_t q_sb, q_sh, q_sl;
     int64_t k_sb, k_sh, k_ss;
@@ -38,6 +39,7 @@ struct AttnFwdArgs {
 struct AttnBwdArgs {
     AttnFwdArgs f;         // q/k/v/mask/o/lse as in the forward (o and lse are inputs here)
     const void *dout;      // (B,H,L,Dv) dense, compute dtype
+    int o_f32;             // f.o is float32 (the training forward's unrounded output)
     void *dq;              // (B,H,L,D) dense, float (double on the float64 path)
     void *dk;              // (B,Hkv,S,D) dense
     void *dv;              // (B,Hkv,S,Dv) dense
@@ -62,3 +64,10 @@ hipError_t launch_attn_decode(const DecodeArgs &a, int cd, hipStream_t s);
 
 bool attn_prefill_supported(const AttnFwdArgs &f, int cd);
 hipError_t launch_attn_prefill(const AttnFwdArgs &a, int cd, hipStream_t s);
+
+bool attn_decode_q8_supported(const AttnFwdArgs &f, int q_dtype);
+hipError_t launch_attn_decode_q8(const DecodeArgs &a, hipStream_t s);
+hipError_t launch_attn_decode_merge(const DecodeArgs &a, int out_dtype, hipStream_t s);
+
+bool attn_bwd_mfma_supported(const AttnBwdArgs &a, int cd);
+hipError_t launch_attn_bwd_mfma(const AttnBwdArgs &a, int cd, hipStream_t s);

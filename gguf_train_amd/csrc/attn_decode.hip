@@ -306,7 +306,27 @@ hipError_t launch_d(const DecodeArgs &a, int G, hipStream_t s) {
     }
 }
 
+template <typename TO>
+hipError_t launch_merge_t(const DecodeArgs &a, hipStream_t s) {
+    const int64_t rows = a.f.B * a.f.H;
+    const dim3 grid((unsigned)((rows + 3) / 4));
+    switch (a.f.D) {
+        case 64: hipLaunchKernelGGL((decode_merge_kernel<TO, 64>), grid, dim3(256), 0, s, a); break;
+        case 128: hipLaunchKernelGGL((decode_merge_kernel<TO, 128>), grid, dim3(256), 0, s, a); break;
+        case 256: hipLaunchKernelGGL((decode_merge_kernel<TO, 256>), grid, dim3(256), 0, s, a); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
 }  // namespace
+
+hipError_t launch_attn_decode_merge(const DecodeArgs &a, int out_dtype, hipStream_t s) {
+    if (out_dtype == GT_F16) return launch_merge_t<_Float16>(a, s);
+    if (out_dtype == GT_BF16) return launch_merge_t<__bf16>(a, s);
+    if (out_dtype == GT_F32) return launch_merge_t<float>(a, s);
+    return hipErrorInvalidValue;
+}
 
 int attn_decode_splits(int64_t S) { return (int)((S + kChunk - 1) / kChunk); }
 

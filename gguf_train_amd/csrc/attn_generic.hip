@@ -132,7 +132,10 @@ __global__ __launch_bounds__(256) void generic_fwd_kernel(AttnFwdArgs a, int64_t
 #pragma unroll
         for (int j = 0; j < kDvChunk / 64; ++j) {
             const int64_t d = dv0 + lane + 64 * j;
-            if (d < a.Dv) store_out<A>(a.o, a.out_dtype, row * a.Dv + d, acc[j] * inv);
+            if (d < a.Dv) {
+                store_out<A>(a.o, a.out_dtype, row * a.Dv + d, acc[j] * inv);
+                if (a.o32) store_out<A>(a.o32, GT_F32, row * a.Dv + d, acc[j] * inv);
+            }
         }
         if (dv0 == 0 && a.lse && lane == 0) {
             ((A *)a.lse)[row] = lsum > (A)0 ? m + acc_log(lsum) : (A)__builtin_huge_val();

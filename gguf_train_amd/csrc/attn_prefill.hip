@@ -21,6 +21,7 @@
 
 #include "attn_common.h"
 #include "gt_internal.h"
+#include "mfma_util.h"
 
 #include <cmath>
 
@@ -28,60 +29,12 @@ namespace {
 
 constexpr int BM = 128;
 constexpr int BN = 64;
-constexpr float kLog2e = 1.4426950408889634f;
-constexpr float kLn2 = 0.6931471805599453f;
-
-typedef _Float16 half8 __attribute__((ext_vector_type(8)));
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef float f32x16 __attribute__((ext_vector_type(16)));
-typedef short s16x4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
-
-template <typename T>
-struct Mfma;
-template <>
-struct Mfma<_Float16> {
-    typedef half8 V8;
-    static constexpr bool kSplitP = false;
-    static __device__ inline f32x16 mma(V8 a, V8 b, f32x16 c) { return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0); }
-    static __device__ inline uint32_t pack(float x, float y) {
-        typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-        h2 v = {(_Float16)x, (_Float16)y};
-        return __builtin_bit_cast(uint32_t, v);
-    }
-    static __device__ inline float round(float x) { return (float)(_Float16)x; }
-};
-template <>
-struct Mfma<__bf16> {
-    typedef bf16x8 V8;
-    static constexpr bool kSplitP = true;
-    static __device__ inline f32x16 mma(V8 a, V8 b, f32x16 c) { return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0); }
-    static __device__ inline uint32_t pack(float x, float y) {
-        typedef __bf16 b2 __attribute__((ext_vector_type(2)));
-        b2 v = {(__bf16)x, (__bf16)y};
-        return __builtin_bit_cast(uint32_t, v);
-    }
-    static __device__ inline float round(float x) { return (float)(__bf16)x; }
-};
+using namespace gtmfma;
 
 template <typename T>
 __device__ inline void store4(T *dst, float a, float b, float c, float d) {
     u32x2 v = {Mfma<T>::pack(a, b), Mfma<T>::pack(c, d)};
     *(u32x2 *)dst = v;
-}
-
-__device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
-
-// max / sum of v over lanes l and l ^ 32
-__device__ inline float xhalf_max(float v) {
-    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
-}
-__device__ inline float xhalf_sum(float v) {
-    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
 // Row pitches (in elements) of the LDS tiles: K rows are read 16 bytes per lane by 32 lanes of
@@ -244,15 +197,7 @@ __global__ __launch_bounds__(256, 2) void prefill_fwd_kernel(AttnFwdArgs a, int 
                         p[e] = fast_exp2(fmaf(s[kb][8 * hs + e], c, -msub));
                         lsum += p[e];
                     }
-                    u32x4 pk = {M::pack(p[0], p[1]), M::pack(p[2], p[3]), M::pack(p[4], p[5]), M::pack(p[6], p[7])};
-                    pb[kb][hs] = __builtin_bit_cast(V8, pk);
-                    if constexpr (M::kSplitP) {
-                        float r[8];
-#pragma unroll
-                        for (int e = 0; e < 8; ++e) r[e] = p[e] - M::round(p[e]);
-                        u32x4 rk = {M::pack(r[0], r[1]), M::pack(r[2], r[3]), M::pack(r[4], r[5]), M::pack(r[6], r[7])};
-                        pl[kb][hs] = __builtin_bit_cast(V8, rk);
-                    }
+                    pack8<T>(p, pb[kb][hs], pl[kb][hs]);
                 }
             }
 
@@ -266,16 +211,9 @@ __global__ __launch_bounds__(256, 2) void prefill_fwd_kernel(AttnFwdArgs a, int 
                         // keys 32kb + 16hs + 8r + 4(g16/2) + i16/4, columns 32db + 16(g16%2) + 4(i16%4)
                         const int row = 32 * kb + 16 * hs + 4 * (g16 >> 1) + (i16 >> 2);
                         const int col = 32 * db + 16 * (g16 & 1) + 4 * (i16 & 3);
-                        const T *p0 = &cV[row * VP + col];
-                        const T *p1 = &cV[(row + 8) * VP + col];
-                        const s16x4 v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                            (lds_s16x4 *)(__attribute__((address_space(3))) char *)p0);
-                        const s16x4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                            (lds_s16x4 *)(__attribute__((address_space(3))) char *)p1);
-                        const u32x2 w0 = __builtin_bit_cast(u32x2, v0), w1 = __builtin_bit_cast(u32x2, v1);
-                        const V8 av = __builtin_bit_cast(V8, u32x4{w0[0], w0[1], w1[0], w1[1]});
+                        const V8 av = read_tr8<T>(&cV[row * VP + col], &cV[(row + 8) * VP + col]);
                         o[db] = M::mma(av, pb[kb][hs], o[db]);
-                        if constexpr (M::kSplitP) o[db] = M::mma(av, pl[kb][hs], o[db]);
+                        if constexpr (M::kSplit) o[db] = M::mma(av, pl[kb][hs], o[db]);
                     }
                 }
             }
@@ -301,6 +239,17 @@ __global__ __launch_bounds__(256, 2) void prefill_fwd_kernel(AttnFwdArgs a, int 
                 store4<T>(orow + 32 * db + 8 * g + 4 * half, o[db][4 * g] * inv, o[db][4 * g + 1] * inv,
                           o[db][4 * g + 2] * inv, o[db][4 * g + 3] * inv);
         if (a.lse && half == 0) ((float *)a.lse)[bh * a.L + lq] = ltot > 0.0f ? (m + log2f(ltot)) * kLn2 : INFINITY;
+        if (a.o32) {
+            float *row32 = (float *)a.o32 + (bh * a.L + lq) * D;
+#pragma unroll
+            for (int db = 0; db < DB; ++db)
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const f32x4 v = {o[db][4 * g] * inv, o[db][4 * g + 1] * inv, o[db][4 * g + 2] * inv,
+                                     o[db][4 * g + 3] * inv};
+                    *(f32x4 *)(row32 + 32 * db + 8 * g + 4 * half) = v;
+                }
+        }
     }
 }
 

@@ -163,7 +163,7 @@ void fill_qkv(AttnFwdArgs &a, const gt_tensor *q, const gt_tensor *k, const gt_t
 // Picks the kernel for a staged forward: split-K decode for single-query rows, the MFMA
 // prefill kernel for fp16/bf16 with head size 64/128, the generic kernel otherwise.
 bool dispatch_forward(const AttnFwdArgs &a, int cd, int dev) {
-    if (a.out_dtype == cd && attn_decode_supported(a, cd)) {
+    if (a.out_dtype == cd && !a.o32 && attn_decode_supported(a, cd)) {
         DecodeArgs da{};
         da.f = a;
         da.nsplit = attn_decode_splits(a.S);
@@ -191,10 +191,40 @@ gt_tensor *deliver(gt_tensor *dev_t, bool to_host) {
     return h;
 }
 
+// Single-query attention straight from Q8_0 K/V blocks.  Returns 1 when it ran, 0 when the
+// shapes do not suit the kernel (the caller then dequantizes), -1 on error.
+int run_q8_decode(const gt_tensor *q, const gt_tensor *k, const gt_tensor *v, const gt_tensor *mask, float scale,
+                  int is_causal, int dev, gt_tensor *o, gt_tensor *lse, Temps &tmp) {
+    const gt_tensor *qs = stage(q, dev, GT_F16, tmp);
+    const gt_tensor *ks = k->device_type == GT_DEV_CUDA && k->device_index == dev ? k : tmp.keep(gt_to_device_dense(k, dev, -1));
+    const gt_tensor *vs = v->device_type == GT_DEV_CUDA && v->device_index == dev ? v : tmp.keep(gt_to_device_dense(v, dev, -1));
+    if (!qs || !ks || !vs) return -1;
+    AttnFwdArgs a{};
+    fill_qkv(a, qs, ks, vs);
+    a.o = gt_data(o);
+    a.lse = lse ? gt_data(lse) : nullptr;
+    a.scale = scale;
+    a.causal = is_causal ? 1 : 0;
+    a.out_dtype = GT_F16;
+    if (!attn_decode_q8_supported(a, GT_F16)) return 0;
+    if (!stage_mask(mask, dev, GT_F16, a, tmp)) return -1;
+    DecodeArgs da{};
+    da.f = a;
+    da.nsplit = attn_decode_splits(a.S);
+    const size_t rows = (size_t)(a.B * a.H) * (size_t)da.nsplit;
+    gt_scratch ws;
+    if (!gt_scratch_alloc(ws, rows * (size_t)(a.D + 2) * sizeof(float), dev)) return -1;
+    da.part_o = (float *)ws.ptr();
+    da.part_ml = da.part_o + rows * (size_t)a.D;
+    return gt_hip_check(launch_attn_decode_q8(da, gt_stream()), "flash_attention q8_0 decode kernel") ? 1 : -1;
+}
+
 int attention_forward(const char *who, const gt_tensor *q, const gt_tensor *k, const gt_tensor *v,
-                      const gt_tensor *mask, float scale, int is_causal, gt_tensor **out_o, gt_tensor **out_lse) {
+                      const gt_tensor *mask, float scale, int is_causal, gt_tensor **out_o, gt_tensor **out_lse,
+                      gt_tensor **out_o32 = nullptr) {
     if (out_o) *out_o = nullptr;
     if (out_lse) *out_lse = nullptr;
+    if (out_o32) *out_o32 = nullptr;
     if (!validate(who, q, k, v, mask)) return -1;
     const int dev = q->device_type == GT_DEV_CUDA ? q->device_index : 0;
     const bool host_io = q->device_type != GT_DEV_CUDA;
@@ -208,14 +238,24 @@ int attention_forward(const char *who, const gt_tensor *q, const gt_tensor *k, c
     const int64_t osh[4] = {B, H, L, Dv}, lsh[3] = {B, H, L};
     gt_tensor *o = gt_new_tensor(4, osh, q->dtype, GT_DEV_CUDA, dev);
     gt_tensor *lse = out_lse ? gt_new_tensor(3, lsh, lse_dtype, GT_DEV_CUDA, dev) : nullptr;
-    if (!o || (out_lse && !lse)) {
+    // the unrounded float32 output, for a training forward of a float16/bfloat16 call
+    const bool want32 = out_o32 && (q->dtype == GT_F16 || q->dtype == GT_BF16);
+    gt_tensor *o32 = want32 ? gt_new_tensor(4, osh, GT_F32, GT_DEV_CUDA, dev) : nullptr;
+    if (!o || (out_lse && !lse) || (want32 && !o32)) {
         gt_tensor_free(o);
         gt_tensor_free(lse);
+        gt_tensor_free(o32);
         return -1;
     }
     Temps tmp;
     bool ok = true;
-    if (o->numel > 0 || (lse && lse->numel > 0)) {
+    int q8 = 0;  // 1: the Q8_0 decode kernel ran
+    if ((o->numel > 0 || (lse && lse->numel > 0)) && k->dtype == GT_Q8_0 && v->dtype == GT_Q8_0 &&
+        q->dtype == GT_F16 && L == 1 && !o32) {
+        q8 = run_q8_decode(q, k, v, mask, scale, is_causal, dev, o, lse, tmp);
+        ok = q8 >= 0;
+    }
+    if (q8 == 0 && (o->numel > 0 || (lse && lse->numel > 0))) {
         // Q8_0 K/V are dequantized to float32 for the generic kernel (exact values).
         const gt_tensor *qs = stage(q, dev, cd, tmp);
         const gt_tensor *ks = k->dtype == GT_Q8_0 ? tmp.keep(gt_dequantize(k, cd)) : stage(k, dev, cd, tmp);
@@ -231,6 +271,7 @@ int attention_forward(const char *who, const gt_tensor *q, const gt_tensor *k, c
         if (ok) {
             a.o = gt_data(o);
             a.lse = lse ? gt_data(lse) : nullptr;
+            a.o32 = o32 ? gt_data(o32) : nullptr;
             a.scale = scale;
             a.causal = is_causal ? 1 : 0;
             a.out_dtype = q->dtype;
@@ -240,17 +281,21 @@ int attention_forward(const char *who, const gt_tensor *q, const gt_tensor *k, c
     if (!ok) {
         gt_tensor_free(o);
         gt_tensor_free(lse);
+        gt_tensor_free(o32);
         return -1;
     }
     o = deliver(o, host_io);
     if (lse) lse = deliver(lse, host_io);
-    if (!o || (out_lse && !lse)) {
+    if (o32) o32 = deliver(o32, host_io);
+    if (!o || (out_lse && !lse) || (want32 && !o32)) {
         gt_tensor_free(o);
         gt_tensor_free(lse);
+        gt_tensor_free(o32);
         return -1;
     }
     if (out_o) *out_o = o; else gt_tensor_free(o);
     if (out_lse) *out_lse = lse;
+    if (out_o32) *out_o32 = o32;
     return 0;
 }
 
@@ -270,6 +315,16 @@ extern "C" int gt_flash_attention_lse(const gt_tensor *q, const gt_tensor *k, co
         return -1;
     }
     return attention_forward("flash_attention_lse", q, k, v, mask, scale, is_causal, out, lse);
+}
+
+extern "C" int gt_flash_attention_train(const gt_tensor *q, const gt_tensor *k, const gt_tensor *v,
+                                        const gt_tensor *mask, float scale, int is_causal, gt_tensor **out,
+                                        gt_tensor **lse, gt_tensor **out32) {
+    if (!out || !lse || !out32) {
+        gt_set_error("flash_attention_train: out, lse and out32 must not be NULL");
+        return -1;
+    }
+    return attention_forward("flash_attention_train", q, k, v, mask, scale, is_causal, out, lse, out32);
 }
 
 extern "C" int gt_flash_attention_backward(const gt_tensor *grad_out, const gt_tensor *q, const gt_tensor *k,
@@ -306,19 +361,25 @@ extern "C" int gt_flash_attention_backward(const gt_tensor *grad_out, const gt_t
     const int gd = cd == GT_F64 ? GT_F64 : GT_F32;
     Temps tmp;
 
-    // the log-sum-exp residual: given, or recomputed by a forward pass
-    const gt_tensor *lse_s = nullptr;
-    if (lse) {
-        lse_s = (lse->device_type == GT_DEV_CUDA && lse->device_index == dev && lse->dtype == gd && gt_is_dense(lse))
-                    ? lse
-                    : tmp.keep(gt_to_device_dense(lse, dev, gd));
-    } else {
+    // the forward's residuals (output and log-sum-exp): given, or recomputed by a forward pass
+    const gt_tensor *lse_s = nullptr, *out_s = nullptr;
+    if (!lse || !out) {
         gt_tensor *o2 = nullptr, *l2 = nullptr;
         if (attention_forward(who, q, k, v, mask, scale, is_causal, &o2, &l2) != 0) return -1;
         tmp.keep(o2);
-        lse_s = l2->device_type == GT_DEV_CUDA ? tmp.keep(l2) : tmp.keep(gt_to_device_dense(tmp.keep(l2), dev, gd));
+        tmp.keep(l2);
+        lse = l2;
+        out = o2;
     }
-    (void)out;  // the generic backward forms delta = rowsum(P * dP) itself
+    lse_s = (lse->device_type == GT_DEV_CUDA && lse->device_index == dev && lse->dtype == gd && gt_is_dense(lse))
+                ? lse
+                : tmp.keep(gt_to_device_dense(lse, dev, gd));
+    // a float32 `out` (the training forward's unrounded output) gives the exact rowsum(dO * O)
+    const int od = (out->dtype == GT_F32 && cd != GT_F64) ? GT_F32 : cd;
+    out_s = (out->device_type == GT_DEV_CUDA && out->device_index == dev && out->dtype == od && gt_is_dense(out))
+                ? out
+                : tmp.keep(gt_to_device_dense(out, dev, od));
+    if (!lse_s || !out_s) return -1;
     const int64_t qsh[4] = {B, H, L, D}, ksh[4] = {B, Hkv, S, D}, vsh[4] = {B, Hkv, S, Dv}, rsh[3] = {B, H, L};
     gt_tensor *gq = gt_new_tensor(4, qsh, gd, GT_DEV_CUDA, dev);
     gt_tensor *gk = gt_new_tensor(4, ksh, gd, GT_DEV_CUDA, dev);
@@ -345,7 +406,12 @@ extern "C" int gt_flash_attention_backward(const gt_tensor *grad_out, const gt_t
         a.dk = gt_data(gk);
         a.dv = gt_data(gv);
         a.delta = gt_data(delta);
-        ok = gt_hip_check(launch_attn_generic_bwd(a, cd, gt_stream()), "flash_attention_backward kernel");
+        a.f.o = const_cast<void *>(gt_data(out_s));
+        a.o_f32 = od == GT_F32 && cd != GT_F32;
+        if (attn_bwd_mfma_supported(a, cd))
+            ok = gt_hip_check(launch_attn_bwd_mfma(a, cd, gt_stream()), "flash_attention_backward kernel");
+        else
+            ok = gt_hip_check(launch_attn_generic_bwd(a, cd, gt_stream()), "flash_attention_backward kernel");
     }
     if (ok) {
         gq = deliver(gq, host_io);

@@ -158,6 +158,13 @@ GT_API gt_tensor *gt_flash_attention(const gt_tensor *q, const gt_tensor *k, con
 GT_API int gt_flash_attention_lse(const gt_tensor *q, const gt_tensor *k, const gt_tensor *v, const gt_tensor *mask,
                                   float scale, int is_causal, gt_tensor **out, gt_tensor **lse);
 
+/* No counterpart in the reference: the training forward.  As gt_flash_attention_lse, plus
+ * out32 = the float32 output before it is rounded to float16/bfloat16 (for float32/float64
+ * inputs out32 is NULL and `out` itself is exact).  Passing out32 as the backward's `out`
+ * makes its rowsum(dO * O) exact.  Returns 0 on success. */
+GT_API int gt_flash_attention_train(const gt_tensor *q, const gt_tensor *k, const gt_tensor *v, const gt_tensor *mask,
+                                    float scale, int is_causal, gt_tensor **out, gt_tensor **lse, gt_tensor **out32);
+
 /* Replaces the Python composition FlashAttentionFn.backward (gguf_train/_functions.py:1933-1965)
  * with a native recompute-based backward.  dq (B,H,L,D), dk (B,Hkv,S,D), dv (B,Hkv,S,Dv) are
  * float32 for float16/bfloat16/float32 inputs and float64 for float64 inputs; gradients of
@@ -166,6 +173,8 @@ GT_API int gt_flash_attention_backward(const gt_tensor *grad_out, const gt_tenso
                                        const gt_tensor *v, const gt_tensor *mask, const gt_tensor *out,
                                        const gt_tensor *lse, float scale, int is_causal, gt_tensor **dq,
                                        gt_tensor **dk, gt_tensor **dv);
+/* (out may be NULL together with lse: the forward is then recomputed.  A float32 out, from
+ * gt_flash_attention_train, is used as is.) */
 
 /* ---- GGUF Q8_0 ------------------------------------------------------------------------ */
 

@@ -36,9 +36,9 @@ def test_native_backward_matches_oracle(dev, dtype, B, H, Hkv, L, S, D, causal):
     mask = torch.zeros(B, 1, 1, S)
     for b, n in enumerate(lens):
         mask[b, ..., n:] = float("-inf")
-    out, lse = g.flash_attention_lse(q.to(dev), k.to(dev), v.to(dev), mask.to(dev), 0.0, causal)
-    dq, dk, dv = g.flash_attention_backward(dout.to(dev), q.to(dev), k.to(dev), v.to(dev), mask.to(dev), out, lse,
-                                            0.0, causal)
+    out, lse, out32 = g.flash_attention_train(q.to(dev), k.to(dev), v.to(dev), mask.to(dev), 0.0, causal)
+    dq, dk, dv = g.flash_attention_backward(dout.to(dev), q.to(dev), k.to(dev), v.to(dev), mask.to(dev),
+                                            out if out32 is None else out32, lse, 0.0, causal)
     assert dq.dtype == dk.dtype == dv.dtype == torch.float32
     wq, wk, wv = oracle_grads(dout, q, k, v, mask=mask, is_causal=causal)
     tol_dtype = torch.float32 if dtype == torch.float32 else torch.bfloat16

@@ -50,3 +50,71 @@ def test_attention_over_a_q8_0_cache(dev, qdtype):
     vd = torch.from_numpy(oracle.q8_0_dequantize(oracle.q8_0_quantize(v.numpy())).reshape(v.shape))
     want = oracle_forward(q, kd, vd)
     assert_close(got, want, torch.float16 if qdtype != torch.float32 else torch.float32, "q8_0 decode")
+
+
+@pytest.mark.parametrize("G,D", [(1, 64), (2, 128), (4, 128), (8, 128), (4, 64), (8, 64)])
+@pytest.mark.parametrize("S", [1, 255, 256, 1000, 8192])
+def test_q8_0_decode_kernel_shapes(dev, G, D, S):
+    B, Hkv = 2, 2
+    seed = G * 1000 + D + S
+    q = randn((B, Hkv * G, 1, D), seed, torch.float16)
+    k, v = randn((B, Hkv, S, D), seed + 1), randn((B, Hkv, S, D), seed + 2)
+    kb, vb = oracle.q8_0_quantize(k.numpy()), oracle.q8_0_quantize(v.numpy())
+    kq = g.QuantizedTensor(torch.from_numpy(kb).to(dev), tuple(k.shape))
+    vq = g.QuantizedTensor(torch.from_numpy(vb).to(dev), tuple(v.shape))
+    got = g.flash_attention(q.to(dev), kq, vq)
+    kd = torch.from_numpy(oracle.q8_0_dequantize(kb).reshape(k.shape))
+    vd = torch.from_numpy(oracle.q8_0_dequantize(vb).reshape(v.shape))
+    assert_close(got, oracle_forward(q, kd, vd), torch.float16, f"q8_0 G={G} D={D} S={S}")
+
+
+def test_q8_0_decode_masks_and_causal(dev):
+    B, H, Hkv, S, D = 3, 8, 2, 600, 128
+    q = randn((B, H, 1, D), 21, torch.float16)
+    k, v = randn((B, Hkv, S, D), 22), randn((B, Hkv, S, D), 23)
+    kq, vq = g.quantize(k.to(dev)), g.quantize(v.to(dev))
+    kd, vd = g.dequantize(kq).cpu(), g.dequantize(vq).cpu()
+    lens = [600, 3, 257]
+    add = torch.zeros(B, 1, 1, S)
+    for b, n in enumerate(lens):
+        add[b, ..., n:] = float("-inf")
+    got = g.flash_attention(q.to(dev), kq, vq, add.to(dev))
+    assert_close(got, oracle_forward(q, kd, vd, mask=add), torch.float16, "q8_0 key padding")
+    got = g.flash_attention(q.to(dev), kq, vq, (add == 0).to(dev))
+    assert_close(got, oracle_forward(q, kd, vd, mask=add), torch.float16, "q8_0 bool")
+    got = g.flash_attention(q.to(dev), kq, vq, None, 0.0, True)
+    assert_close(got, oracle_forward(q, kd, vd, is_causal=True), torch.float16, "q8_0 causal")
+
+
+@pytest.mark.parametrize("S", [2, 64, 300])
+def test_q8_0_decode_structured_inputs(dev, S):
+    """Isolates the phases of the Q8_0 decode kernel: identical V rows make the output that row
+    whatever the weights; all-zero K makes the weights uniform (output = mean of V)."""
+    B, H, Hkv, D = 1, 4, 1, 128
+    q = randn((B, H, 1, D), 31, torch.float16)
+    k = randn((B, Hkv, S, D), 32)
+    vrow = randn((D,), 33)
+    v_same = vrow.expand(B, Hkv, S, D).contiguous()
+    kq = g.quantize(k.to(dev))
+    vq_same = g.quantize(v_same.to(dev))
+    row = g.dequantize(vq_same).cpu()[0, 0, 0]
+    got = g.flash_attention(q.to(dev), kq, vq_same).float().cpu()
+    assert (got - row.expand(B, H, 1, D)).abs().max().item() < 2e-3, "identical V rows"
+    v = randn((B, Hkv, S, D), 34)
+    vq = g.quantize(v.to(dev))
+    kz = g.quantize(torch.zeros(B, Hkv, S, D, device=dev))
+    got = g.flash_attention(q.to(dev), kz, vq).float().cpu()
+    mean = g.dequantize(vq).cpu().mean(dim=2, keepdim=True).expand(B, H, 1, D)
+    assert (got - mean).abs().max().item() < 2e-3, "uniform weights"
+
+
+def test_q8_0_decode_lse_exposes_the_scores(dev):
+    B, H, Hkv, S, D = 1, 4, 1, 40, 128
+    q = randn((B, H, 1, D), 41, torch.float16)
+    k, v = randn((B, Hkv, S, D), 42), randn((B, Hkv, S, D), 43)
+    kq, vq = g.quantize(k.to(dev)), g.quantize(v.to(dev))
+    kd, vd = g.dequantize(kq).cpu(), g.dequantize(vq).cpu()
+    out, lse = g.flash_attention_lse(q.to(dev), kq, vq)
+    want_o, want_l = oracle_forward(q, kd, vd, return_lse=True)
+    assert np.abs(lse.cpu().numpy() - want_l).max() < 1e-3, (lse.cpu().numpy().ravel(), want_l.ravel())
+    assert_close(out, want_o, torch.float16, "q8_0 out")
