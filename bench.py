@@ -9,6 +9,8 @@ handles made once over device-resident inputs) over one batch of synthetic data:
   decode_q8_0  GQA decode over a GGUF Q8_0 K/V cache, B=16 Hq=32 Hkv=8, KV length 8192, D=128
   train        bf16 forward + backward, B=8 H=16 L=S=1024 D=64, causal + key padding (-inf)
   fp32         fp32 causal forward, B=1 H=4 L=S=128 D=64 (the parity configuration)
+  copy         (not in the default list) a plain 1 GiB device copy, the calibration workload
+               for the HBM byte counters (FETCH_SIZE / WRITE_SIZE) of the traffic figures
 
 The JSON line's `value` is the headline (prefill) TFLOP/s; the other configurations are
 reported under "configs".  Work is counted algorithmically: attention FLOPs = 4*D per
@@ -171,6 +173,23 @@ def bench_train(r: Runner, cfg, steps, warmup):
             "frac_of_peak": flops / (ms * 1e-3) / 1e12 / PEAK_FP16_TFLOPS, "valid_lengths": [int(x) for x in lens]}
 
 
+def bench_copy(r: Runner, steps, warmup):
+    """torch's device-to-device copy of 1 GiB: reads and writes exactly 2^30 bytes each."""
+    torch = r.torch
+    n = 1 << 29
+    x = torch.ones(n, dtype=torch.float16, device=r.dev)
+    y = torch.empty_like(x)
+
+    def step(i):
+        y.copy_(x)
+
+    ms, wall_ms = r.time_steps(step, steps, warmup)
+    nbytes = 2 * x.numel() * x.element_size()
+    return {"ms_per_step": ms, "wall_ms_per_step": wall_ms, "bytes_per_step": nbytes, "read_bytes": nbytes // 2,
+            "write_bytes": nbytes // 2, "value": nbytes / (ms * 1e-3) / 1e9, "unit": "GB/s",
+            "frac_of_peak": nbytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS}
+
+
 def cpu_baseline(heads: int):
     """The oracle (fp64 restatement of gt_flash_attention) on `heads` heads of the headline
     workload (one sequence, L=S=2048, D=128, causal, fp16 inputs), OpenMP over heads."""
@@ -197,6 +216,7 @@ CONFIGS = {
     "decode_q8_0": dict(B=16, H=32, Hkv=8, L=1, S=8192, D=128, dtype="float16", q8_0=True, rotate=3),
     "train": dict(B=8, H=16, L=1024, D=64, dtype="bfloat16"),
     "fp32": dict(B=1, H=4, Hkv=4, L=128, S=128, D=64, dtype="float32", causal=True),
+    "copy": dict(dtype="float16"),
 }
 
 
@@ -215,6 +235,8 @@ def main():
         cfg["dtype"] = getattr(torch, cfg["dtype"])
         if name == "train":
             results[name] = bench_train(r, cfg, args.steps, args.warmup)
+        elif name == "copy":
+            results[name] = bench_copy(r, args.steps, args.warmup)
         else:
             results[name] = bench_forward(r, name, cfg, args.steps, args.warmup)
         print(f"[bench] {name}: {json.dumps(results[name])}", file=sys.stderr, flush=True)

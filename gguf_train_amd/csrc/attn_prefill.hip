@@ -5,8 +5,13 @@
 // attend to -> 0, output rounded from fp32 to the input dtype.
 //
 // Workgroup: 4 wavefronts, BM = 128 query rows (32 per wavefront), key/value tiles of BN = 64
-// rows staged in LDS (double buffered, one barrier per tile; the next tile's global loads are
-// in flight while the current tile is computed).  Per tile and wavefront:
+// rows in LDS, double buffered: global_load_lds_dwordx4 writes the next tile straight into LDS
+// while the current one is computed (no staging registers), one barrier per tile.  Tiles are
+// unpadded; 16-byte chunk c of row r sits at chunk c ^ f(r), which keeps both the row reads of
+// K (16 rows per LDS cycle) and the transposed reads of V (4 rows x 4 chunks per cycle) free of
+// bank conflicts on the 64-bank LDS: f(r) = (r ^ 4r) mod 16 for 16-chunk rows (D = 128),
+// f(r) = (2r + r/4) mod 8 for 8-chunk rows (D = 64).
+// Per tile and wavefront:
 //   S^T (keys x queries) = K . Q^T    v_mfma_f32_32x32x16_{f16,bf16}; Q^T stays in registers
 //                                      as the B operand, K rows come from LDS (ds_read_b128).
 //   online softmax in the log2 domain: every lane owns one query row (lane % 32) and 32 of
@@ -37,33 +42,62 @@ __device__ inline void store4(T *dst, float a, float b, float c, float d) {
     *(u32x2 *)dst = v;
 }
 
-// Row pitches (in elements) of the LDS tiles: K rows are read 16 bytes per lane by 32 lanes of
-// different rows (pitch = 16 mod 128 bytes: no bank conflict); V rows are read by the
-// transposing read, 4 rows x 32 bytes per 16 lanes (pitch = 32 mod 128 bytes).
 template <int D>
-struct Pitch {
-    static constexpr int K = D + 8;
-    static constexpr int V = D + 16;
-};
+__device__ inline int swz(int r) {
+    if constexpr (D == 128) return (r ^ (r << 2)) & 15;
+    return (2 * r + (r >> 2)) & 7;
+}
+
+// One global_load_lds_dwordx4: lane l copies 16 bytes from gbase + voff to LDS byte address
+// lds + 16 l.  Issued from assembly so that the compiler does not see an LDS write it would
+// have to wait for (vmcnt(0)) before every later LDS read, which would serialise the prefetch
+// of the next tile with the compute of the current one; callers wait for it explicitly
+// (vmcnt(0) + barrier) before reading the destination.  m0 is saved and restored.
+__device__ inline void lds_dma16(uint32_t lds, const void *gbase, uint32_t voff) {
+    uint32_t save;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %1\n\t"
+        "global_load_lds_dwordx4 %2, %3\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(save)
+        : "s"(lds), "v"(voff), "s"(gbase)
+        : "memory");
+}
+
+__device__ inline uint32_t lds_addr(const void *p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
+}
 
 // MASK: 0 = none, 1 = bool bytes, 2 = additive float.
 template <typename T, int D, bool CAUSAL, int MASK>
 __global__ __launch_bounds__(256, 2) void prefill_fwd_kernel(AttnFwdArgs a, int nq) {
     using M = Mfma<T>;
     using V8 = typename M::V8;
-    constexpr int KP = Pitch<D>::K, VP = Pitch<D>::V;
-    constexpr int DT = D / 16;  // k-steps of S^T = K.Q^T
-    constexpr int DB = D / 32;  // d blocks of O^T
-    constexpr int CH = D / 8;   // 16-byte chunks per row
-    constexpr int NLD = BN * CH / 256;  // 16-byte loads per thread per tile and operand
-    __shared__ __attribute__((aligned(16))) T sK[2][BN * KP];
-    __shared__ __attribute__((aligned(16))) T sV[2][BN * VP];
+    constexpr int DT = D / 16;            // k-steps of S^T = K.Q^T
+    constexpr int DB = D / 32;            // d blocks of O^T
+    constexpr int CH = D / 8;             // 16-byte chunks per row
+    constexpr int TILE = BN * D;          // elements per tile
+    constexpr int NPW = BN * CH / 64 / 4; // 1 KB wave loads per operand, wave and tile
+    __shared__ __attribute__((aligned(1024))) T sK[2][TILE];
+    __shared__ __attribute__((aligned(1024))) T sV[2][TILE];
 
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int lrow = lane & 31, half = lane >> 5;
     const int64_t BH = a.B * a.H;
-    const int qt = nq - 1 - (int)(blockIdx.x / BH);  // heaviest query tiles first
-    const int64_t bh = (int64_t)blockIdx.x % BH;
+    // Heaviest query tiles first.  Workgroups are dealt to the 8 XCDs round robin (x % 8), so
+    // when the heads split evenly, XCD x takes heads [x*BH/8, (x+1)*BH/8) and their K/V stay in
+    // its own L2.
+    int qt;
+    int64_t bh;
+    if (BH % 8 == 0) {
+        const int64_t hpx = BH / 8, i = blockIdx.x / 8;
+        qt = nq - 1 - (int)(i / hpx);
+        bh = (int64_t)(blockIdx.x % 8) * hpx + i % hpx;
+    } else {
+        qt = nq - 1 - (int)(blockIdx.x / BH);
+        bh = (int64_t)blockIdx.x % BH;
+    }
     const int64_t b = bh / a.H, h = bh % a.H, hk = h / (a.H / a.Hkv);
     const int L = (int)a.L, S = (int)a.S;
     const int q0 = qt * BM;
@@ -92,139 +126,142 @@ __global__ __launch_bounds__(256, 2) void prefill_fwd_kernel(AttnFwdArgs a, int 
     float m = -INFINITY;  // running max of this lane's row, log2 domain
     float lsum = 0.0f;    // this lane's share of the running sum
 
-    // tile staging: chunk (row, col) of 16 bytes; rows past S repeat row S-1 (finite values,
-    // masked to -inf / weight 0 below), so the loads need no branches
-    u32x4 kreg[NLD], vreg[NLD];
-    auto load_tile = [&](int j) {
+    // Tile j into buffer `buf`: wave w issues NPW 1 KB loads per operand; lane `lane` of load n
+    // fills 16-byte slot (w*NPW + n)*64 + lane = row*CH + (col ^ swz<D>(row)).  Rows past S repeat
+    // row S-1 (finite values, masked to -inf / weight 0 below).  Byte offsets from the (b, kv
+    // head) base fit 32 bits (checked by the launcher).
+    const int wu = __builtin_amdgcn_readfirstlane(w);
+    const uint32_t k_row = (uint32_t)a.k_ss * 2, v_row = (uint32_t)a.v_ss * 2;
+    int lrow_n[NPW];
+    uint32_t lcol_n[NPW];
 #pragma unroll
-        for (int i = 0; i < NLD; ++i) {
-            const int cidx = tid + 256 * i, row = cidx / CH, col = cidx % CH;
-            const int key = min(j * BN + row, S - 1);
-            kreg[i] = *(const u32x4 *)(kbase + (int64_t)key * a.k_ss + 8 * col);
-            vreg[i] = *(const u32x4 *)(vbase + (int64_t)key * a.v_ss + 8 * col);
-        }
-    };
-    auto store_tile = [&](int buf) {
+    for (int n = 0; n < NPW; ++n) {
+        const int slot = (w * NPW + n) * 64 + lane;
+        lrow_n[n] = slot / CH;
+        lcol_n[n] = 16u * (uint32_t)((slot % CH) ^ swz<D>(slot / CH));
+    }
+    auto issue_tile = [&](int j, int buf) {
+        const uint32_t dk = lds_addr(&sK[buf][0]) + wu * NPW * 1024;
+        const uint32_t dv = lds_addr(&sV[buf][0]) + wu * NPW * 1024;
 #pragma unroll
-        for (int i = 0; i < NLD; ++i) {
-            const int cidx = tid + 256 * i, row = cidx / CH, col = cidx % CH;
-            *(u32x4 *)&sK[buf][row * KP + 8 * col] = kreg[i];
-            *(u32x4 *)&sV[buf][row * VP + 8 * col] = vreg[i];
+        for (int n = 0; n < NPW; ++n) {
+            const uint32_t key = (uint32_t)min(j * BN + lrow_n[n], S - 1);
+            lds_dma16(dk + n * 1024, kbase, key * k_row + lcol_n[n]);
+            lds_dma16(dv + n * 1024, vbase, key * v_row + lcol_n[n]);
         }
     };
 
-    load_tile(0);
-    store_tile(0);
-    if (ntiles > 1) load_tile(1);
-    __syncthreads();
+    issue_tile(0, 0);
     const int g16 = lane >> 4, i16 = lane & 15;
     for (int j = 0; j < ntiles; ++j) {
         const int buf = j & 1;
         const int k0 = j * BN;
+        // this wave's loads of tile j are done; the barrier makes everyone's visible and
+        // guarantees tile j-1 (the other buffer) is no longer read
+        __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
+        __syncthreads();
+        if (j + 1 < ntiles) issue_tile(j + 1, buf ^ 1);
         const T *cK = sK[buf];
         const T *cV = sV[buf];
 
         // a wavefront whose rows all precede this tile (causal) has nothing to do here
-        if (!CAUSAL || k0 <= wq0 + 31) {
-            // ---- S^T = K . Q^T ----
-            f32x16 s[2];
+        if (CAUSAL && k0 > wq0 + 31) continue;
+
+        // ---- S^T = K . Q^T ----
+        f32x16 s[2];
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+            const int row = 32 * kb + lrow;
+            V8 kf[DT];
+#pragma unroll
+            for (int t = 0; t < DT; ++t) kf[t] = *(const V8 *)&cK[row * D + 8 * ((2 * t + half) ^ swz<D>(row))];
+#pragma unroll
+            for (int i = 0; i < 16; ++i) s[kb][i] = 0.0f;
+#pragma unroll
+            for (int t = 0; t < DT; ++t) s[kb] = M::mma(kf[t], qf[t], s[kb]);
+        }
+
+        // ---- masks: s[kb][i] is (key = k0 + 32kb + 8(i/4) + 4half + i%4, query = lq) ----
+        const bool edge = k0 + BN > S || (CAUSAL && k0 + BN - 1 > wq0);
+        if (MASK != 0 || edge) {
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
-                for (int i = 0; i < 16; ++i) s[kb][i] = 0.0f;
-#pragma unroll
-                for (int t = 0; t < DT; ++t) {
-                    const V8 kf = *(const V8 *)&cK[(32 * kb + lrow) * KP + 16 * t + 8 * half];
-                    s[kb] = M::mma(kf, qf[t], s[kb]);
-                }
-            }
-
-            // ---- masks: s[kb][i] is (key = k0 + 32kb + 8(i/4) + 4half + i%4, query = lq) ----
-            const bool edge = k0 + BN > S || (CAUSAL && k0 + BN - 1 > wq0);
-            if (MASK != 0 || edge) {
-#pragma unroll
-                for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-                    for (int i = 0; i < 16; ++i) {
-                        const int key = k0 + 32 * kb + 8 * (i / 4) + 4 * half + (i % 4);
-                        float x = s[kb][i];
-                        if (MASK != 0) {
-                            const int64_t mi = b * a.m_sb + h * a.m_sh + (int64_t)min(lq, L - 1) * a.m_sl +
-                                               (int64_t)min(key, S - 1) * a.m_ss;
-                            if (MASK == 1) {
-                                x = ((const uint8_t *)a.mask)[mi] ? x : -INFINITY;
-                            } else {
-                                x = fmaf(((const float *)a.mask)[mi], 1.0f / a.scale, x);
-                            }
+                for (int i = 0; i < 16; ++i) {
+                    const int key = k0 + 32 * kb + 8 * (i / 4) + 4 * half + (i % 4);
+                    float x = s[kb][i];
+                    if (MASK != 0) {
+                        const int64_t mi = b * a.m_sb + h * a.m_sh + (int64_t)min(lq, L - 1) * a.m_sl +
+                                           (int64_t)min(key, S - 1) * a.m_ss;
+                        if (MASK == 1) {
+                            x = ((const uint8_t *)a.mask)[mi] ? x : -INFINITY;
+                        } else {
+                            x = fmaf(((const float *)a.mask)[mi], 1.0f / a.scale, x);
                         }
-                        const bool blocked = key >= S || (CAUSAL && key > lq);
-                        s[kb][i] = blocked ? -INFINITY : x;
                     }
+                    const bool blocked = key >= S || (CAUSAL && key > lq);
+                    s[kb][i] = blocked ? -INFINITY : x;
                 }
             }
+        }
 
-            // ---- online softmax ----
-            float tmax = -INFINITY;
+        // ---- online softmax ----
+        float tmax = -INFINITY;
 #pragma unroll
-            for (int kb = 0; kb < 2; ++kb)
+        for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-                for (int i = 0; i < 16; ++i) tmax = fmaxf(tmax, s[kb][i]);
-            tmax = xhalf_max(tmax);
-            // a row with nothing visible yet keeps m = -inf, alpha = 1 and p = 0 (no branch:
-            // the MFMAs below combine the two lanes of each row and run for the whole wave)
-            const float mnew = fmaxf(m, tmax * c);
-            const bool none = mnew == -INFINITY;
-            const float msub = none ? 0.0f : mnew;
-            if (!__all(mnew == m)) {
-                const float alpha = none ? 1.0f : fast_exp2(m - mnew);
-                lsum *= alpha;
+            for (int i = 0; i < 16; ++i) tmax = fmaxf(tmax, s[kb][i]);
+        tmax = xhalf_max(tmax);
+        // a row with nothing visible yet keeps m = -inf, alpha = 1 and p = 0 (no branch:
+        // the MFMAs below combine the two lanes of each row and run for the whole wave)
+        const float mnew = fmaxf(m, tmax * c);
+        const bool none = mnew == -INFINITY;
+        const float msub = none ? 0.0f : mnew;
+        if (!__all(mnew == m)) {
+            const float alpha = none ? 1.0f : fast_exp2(m - mnew);
+            lsum *= alpha;
 #pragma unroll
-                for (int db = 0; db < DB; ++db)
+            for (int db = 0; db < DB; ++db)
 #pragma unroll
-                    for (int i = 0; i < 16; ++i) o[db][i] *= alpha;
+                for (int i = 0; i < 16; ++i) o[db][i] *= alpha;
+        }
+        m = mnew;
+
+        // P^T as B operands: k-step (kb, hs) takes accumulator entries 8hs .. 8hs+7
+        V8 pb[2][2], pl[2][2];
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+            for (int hs = 0; hs < 2; ++hs) {
+                float p[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    p[e] = fast_exp2(fmaf(s[kb][8 * hs + e], c, -msub));
+                    lsum += p[e];
+                }
+                pack8<T>(p, pb[kb][hs], pl[kb][hs]);
             }
-            m = mnew;
+        }
 
-            // P^T as B operands: k-step (kb, hs) takes accumulator entries 8hs .. 8hs+7
-            V8 pb[2][2], pl[2][2];
+        // ---- O^T += V^T . P^T ----
+#pragma unroll
+        for (int db = 0; db < DB; ++db) {
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
                 for (int hs = 0; hs < 2; ++hs) {
-                    float p[8];
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) {
-                        p[e] = fast_exp2(fmaf(s[kb][8 * hs + e], c, -msub));
-                        lsum += p[e];
-                    }
-                    pack8<T>(p, pb[kb][hs], pl[kb][hs]);
-                }
-            }
-
-            // ---- O^T += V^T . P^T ----
-#pragma unroll
-            for (int db = 0; db < DB; ++db) {
-#pragma unroll
-                for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-                    for (int hs = 0; hs < 2; ++hs) {
-                        // keys 32kb + 16hs + 8r + 4(g16/2) + i16/4, columns 32db + 16(g16%2) + 4(i16%4)
-                        const int row = 32 * kb + 16 * hs + 4 * (g16 >> 1) + (i16 >> 2);
-                        const int col = 32 * db + 16 * (g16 & 1) + 4 * (i16 & 3);
-                        const V8 av = read_tr8<T>(&cV[row * VP + col], &cV[(row + 8) * VP + col]);
-                        o[db] = M::mma(av, pb[kb][hs], o[db]);
-                        if constexpr (M::kSplit) o[db] = M::mma(av, pl[kb][hs], o[db]);
-                    }
+                    // rows (keys) 32kb + 16hs + 4(g16/2) + i16/4 (+8), column 32db + 16(g16%2) + 4(i16%4)
+                    const int row = 32 * kb + 16 * hs + 4 * (g16 >> 1) + (i16 >> 2);
+                    const int col = 32 * db + 16 * (g16 & 1) + 4 * (i16 & 3);
+                    const int chunk = col >> 3, within = col & 7;
+                    const T *p0 = &cV[row * D + 8 * (chunk ^ swz<D>(row)) + within];
+                    const T *p1 = &cV[(row + 8) * D + 8 * (chunk ^ swz<D>(row + 8)) + within];
+                    const V8 av = read_tr8<T>(p0, p1);
+                    o[db] = M::mma(av, pb[kb][hs], o[db]);
+                    if constexpr (M::kSplit) o[db] = M::mma(av, pl[kb][hs], o[db]);
                 }
             }
         }
-
-        // stage tile j+1 (loaded during this tile) into the other buffer, prefetch tile j+2
-        if (j + 1 < ntiles) {
-            store_tile(buf ^ 1);
-            if (j + 2 < ntiles) load_tile(j + 2);
-        }
-        __syncthreads();
     }
 
     // ---- epilogue: normalise, store O (B,H,L,D) and the log-sum-exp ----
@@ -279,8 +316,11 @@ bool attn_prefill_supported(const AttnFwdArgs &f, int cd) {
     if (f.L < 1 || f.S < 1 || !(f.scale > 0.0f)) return false;
     if (f.L >= (1LL << 30) || f.S >= (1LL << 30)) return false;  // 32-bit row indices
     const int64_t strides[] = {f.q_sb, f.q_sh, f.q_sl, f.k_sb, f.k_sh, f.k_ss, f.v_sb, f.v_sh, f.v_ss};
-    for (int64_t st : strides) if (st % 8 != 0) return false;
+    for (int64_t st : strides) if (st % 8 != 0 || st < 0) return false;
     for (const void *p : {f.q, f.k, f.v}) if ((uintptr_t)p % 16 != 0) return false;
+    // K/V tiles are addressed by 32-bit byte offsets from the (batch, kv head) base
+    if ((f.S - 1) * f.k_ss * 2 + f.D * 2 > 0xffffffffLL) return false;
+    if ((f.S - 1) * f.v_ss * 2 + f.Dv * 2 > 0xffffffffLL) return false;
     return true;
 }
 
