@@ -43,8 +43,9 @@ PEAK_HBM_GBS = 8000.0
 def parse_args():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=20)
-    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--steps", type=int, default=100)
+    # the GPU clocks take tens of milliseconds to settle: warm up for ~200 steps
+    p.add_argument("--warmup", type=int, default=200)
     p.add_argument("--configs", default="prefill,decode,decode_q8_0,train,fp32")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--cpu-heads", type=int, default=8, help="heads of the headline workload in the CPU sample")

@@ -4,9 +4,12 @@
 // the same semantics: scale, top-left causal mask, bool/additive mask, rows with nothing to
 // attend to -> 0, output rounded from fp32 to the input dtype.
 //
-// Workgroup: 4 wavefronts, BM = 128 query rows (32 per wavefront), key/value tiles of BN = 64
-// rows in LDS, double buffered: global_load_lds_dwordx4 writes the next tile straight into LDS
-// while the current one is computed (no staging registers), one barrier per tile.  Tiles are
+// Workgroup: 8 wavefronts (two per SIMD), query tiles of BM = 256 rows (32 per wavefront), so
+// each K/V tile brought into LDS serves 256 queries.  A workgroup runs the query tiles p and
+// nq-1-p of one head one after the other: under the causal mask their key ranges add up to
+// the same length for every p, so all workgroups carry equal work.  K/V tiles of BN = 64 rows
+// stream through NST LDS stages: global_load_lds_dwordx4 writes tile s+NST-1 straight into LDS
+// (no staging registers) while tile s is computed, with one barrier per tile.  Tiles are
 // unpadded; 16-byte chunk c of row r sits at chunk c ^ f(r), which keeps both the row reads of
 // K (16 rows per LDS cycle) and the transposed reads of V (4 rows x 4 chunks per cycle) free of
 // bank conflicts on the 64-bank LDS: f(r) = (r ^ 4r) mod 16 for 16-chunk rows (D = 128),
@@ -16,13 +19,14 @@
 //                                      as the B operand, K rows come from LDS (ds_read_b128).
 //   online softmax in the log2 domain: every lane owns one query row (lane % 32) and 32 of
 //   its scores, so max/sum are in-lane plus one exchange between the two wave halves
-//   (v_permlane32_swap).  The O rescale is skipped when no row's max moved.
+//   (v_permlane32_swap).  O and l are rescaled only when a row's max grows by more than
+//   kLazy (the result O / l does not depend on the reference point).
 //   O^T (d x queries) += V^T . P^T    P^T is the S^T accumulator converted in place (the
 //                                      MFMA's k index is permuted to match the accumulator
 //                                      layout); V^T fragments come from the row-major V tile
 //                                      through ds_read_b64_tr_b16.
 // bf16 P is split into hi + lo bf16 parts (two MFMAs) so the probabilities keep ~16 bits.
-// Causal tiles above the diagonal are never loaded; query tiles run heaviest first.
+// Causal tiles above the diagonal are never loaded.
 
 #include "attn_common.h"
 #include "gt_internal.h"
@@ -32,8 +36,11 @@
 
 namespace {
 
-constexpr int BM = 128;
-constexpr int BN = 64;
+constexpr int NW = 8;           // wavefronts per workgroup
+constexpr int BM = 32 * NW;     // query rows per tile
+constexpr int BN = 64;          // keys per K/V tile
+constexpr int NST = 4;          // K/V tile stages in LDS
+constexpr float kLazy = 8.0f;   // rescale threshold, log2 domain: probabilities stay <= 256
 using namespace gtmfma;
 
 template <typename T>
@@ -51,8 +58,8 @@ __device__ inline int swz(int r) {
 // One global_load_lds_dwordx4: lane l copies 16 bytes from gbase + voff to LDS byte address
 // lds + 16 l.  Issued from assembly so that the compiler does not see an LDS write it would
 // have to wait for (vmcnt(0)) before every later LDS read, which would serialise the prefetch
-// of the next tile with the compute of the current one; callers wait for it explicitly
-// (vmcnt(0) + barrier) before reading the destination.  m0 is saved and restored.
+// of later tiles with the compute of the current one; the kernel waits for it explicitly
+// (vmcnt + barrier) before reading the destination.  m0 is saved and restored.
 __device__ inline void lds_dma16(uint32_t lds, const void *gbase, uint32_t voff) {
     uint32_t save;
     asm volatile(
@@ -69,68 +76,68 @@ __device__ inline uint32_t lds_addr(const void *p) {
     return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
 }
 
+// s_waitcnt vmcnt(n) (expcnt and lgkmcnt left alone), n a compile-time constant < 16
+template <int N>
+__device__ inline void wait_vm() {
+    static_assert(N >= 0 && N < 16, "vmcnt");
+    __builtin_amdgcn_s_waitcnt(0x0f70 | N);
+}
+
+// Keys covered by query tile qt: all of them, or up to the tile's last row (causal, top-left).
+template <bool CAUSAL>
+__device__ inline int key_tiles(int qt, int S) {
+    const int kv_end = CAUSAL ? min(qt * BM + BM, S) : S;
+    return (kv_end + BN - 1) / BN;
+}
+
 // MASK: 0 = none, 1 = bool bytes, 2 = additive float.
 template <typename T, int D, bool CAUSAL, int MASK>
-__global__ __launch_bounds__(256, 2) void prefill_fwd_kernel(AttnFwdArgs a, int nq) {
+__global__ __launch_bounds__(64 * NW, 1) void prefill_fwd_kernel(AttnFwdArgs a, int nq, int npairs) {
     using M = Mfma<T>;
     using V8 = typename M::V8;
-    constexpr int DT = D / 16;            // k-steps of S^T = K.Q^T
-    constexpr int DB = D / 32;            // d blocks of O^T
-    constexpr int CH = D / 8;             // 16-byte chunks per row
-    constexpr int TILE = BN * D;          // elements per tile
-    constexpr int NPW = BN * CH / 64 / 4; // 1 KB wave loads per operand, wave and tile
-    __shared__ __attribute__((aligned(1024))) T sK[2][TILE];
-    __shared__ __attribute__((aligned(1024))) T sV[2][TILE];
+    constexpr int DT = D / 16;             // k-steps of S^T = K.Q^T
+    constexpr int DB = D / 32;             // d blocks of O^T
+    constexpr int CH = D / 8;              // 16-byte chunks per row
+    constexpr int TILE = BN * D;           // elements per tile
+    constexpr int NPW = BN * CH / 64 / NW; // 1 KB wave loads per operand, wave and tile
+    constexpr int PER = 2 * NPW;           // loads per wave and tile (K and V)
+    static_assert(NPW >= 1 && PER * (NST - 2) < 16, "tile split");
+    __shared__ __attribute__((aligned(1024))) T sK[NST][TILE];
+    __shared__ __attribute__((aligned(1024))) T sV[NST][TILE];
 
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wavefront index, uniform
     const int lrow = lane & 31, half = lane >> 5;
+    const int g16 = lane >> 4, i16 = lane & 15;
     const int64_t BH = a.B * a.H;
-    // Heaviest query tiles first.  Workgroups are dealt to the 8 XCDs round robin (x % 8), so
-    // when the heads split evenly, XCD x takes heads [x*BH/8, (x+1)*BH/8) and their K/V stay in
-    // its own L2.
-    int qt;
+    // Workgroups are dealt to the 8 XCDs round robin (x % 8); when the heads split evenly,
+    // XCD x takes heads [x*BH/8, (x+1)*BH/8), so their K/V stay in its own L2.
+    int pair;
     int64_t bh;
     if (BH % 8 == 0) {
         const int64_t hpx = BH / 8, i = blockIdx.x / 8;
-        qt = nq - 1 - (int)(i / hpx);
-        bh = (int64_t)(blockIdx.x % 8) * hpx + i % hpx;
+        pair = (int)(i % npairs);
+        bh = (int64_t)(blockIdx.x % 8) * hpx + i / npairs;
     } else {
-        qt = nq - 1 - (int)(blockIdx.x / BH);
-        bh = (int64_t)blockIdx.x % BH;
+        pair = (int)(blockIdx.x % npairs);
+        bh = (int64_t)blockIdx.x / npairs;
     }
     const int64_t b = bh / a.H, h = bh % a.H, hk = h / (a.H / a.Hkv);
     const int L = (int)a.L, S = (int)a.S;
-    const int q0 = qt * BM;
-    const int wq0 = q0 + 32 * w;  // first query row of this wavefront
-    const int lq = wq0 + lrow;    // this lane's query row
-
-    // Q^T fragments (B operand): lane holds Q[lq][16t + 8*half + 0..7]; rows past L read row L-1
-    V8 qf[DT];
-    {
-        const T *qr = (const T *)a.q + b * a.q_sb + h * a.q_sh + (int64_t)min(lq, L - 1) * a.q_sl + 8 * half;
-#pragma unroll
-        for (int t = 0; t < DT; ++t) qf[t] = __builtin_bit_cast(V8, *(const u32x4 *)(qr + 16 * t));
-    }
+    const int qa = nq - 1 - pair, qb = pair;  // the heavier tile first
+    const int nparts = qa == qb ? 1 : 2;
+    const int na = key_tiles<CAUSAL>(qa, S);
+    const int total = na + (nparts == 2 ? key_tiles<CAUSAL>(qb, S) : 0);
 
     const T *kbase = (const T *)a.k + b * a.k_sb + hk * a.k_sh;
     const T *vbase = (const T *)a.v + b * a.v_sb + hk * a.v_sh;
-    const int kv_end = CAUSAL ? min(q0 + BM, S) : S;
-    const int ntiles = (kv_end + BN - 1) / BN;
     const float c = a.scale * kLog2e;  // raw score -> log2 domain
 
-    f32x16 o[DB];
-#pragma unroll
-    for (int db = 0; db < DB; ++db)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) o[db][i] = 0.0f;
-    float m = -INFINITY;  // running max of this lane's row, log2 domain
-    float lsum = 0.0f;    // this lane's share of the running sum
-
-    // Tile j into buffer `buf`: wave w issues NPW 1 KB loads per operand; lane `lane` of load n
-    // fills 16-byte slot (w*NPW + n)*64 + lane = row*CH + (col ^ swz<D>(row)).  Rows past S repeat
-    // row S-1 (finite values, masked to -inf / weight 0 below).  Byte offsets from the (b, kv
-    // head) base fit 32 bits (checked by the launcher).
-    const int wu = __builtin_amdgcn_readfirstlane(w);
+    // Flat step s (key tile s of part 0, then key tile s - na of part 1) goes to stage s % NST;
+    // wave w issues NPW 1 KB loads per operand: lane `lane` of load n fills 16-byte slot
+    // (w*NPW + n)*64 + lane = row*CH + (col ^ swz<D>(row)).  Rows past S repeat row S-1 (finite
+    // values, masked to -inf / weight 0 below).  Byte offsets from the (b, kv head) base fit
+    // 32 bits (checked by the launcher).
     const uint32_t k_row = (uint32_t)a.k_ss * 2, v_row = (uint32_t)a.v_ss * 2;
     int lrow_n[NPW];
     uint32_t lcol_n[NPW];
@@ -140,161 +147,194 @@ __global__ __launch_bounds__(256, 2) void prefill_fwd_kernel(AttnFwdArgs a, int 
         lrow_n[n] = slot / CH;
         lcol_n[n] = 16u * (uint32_t)((slot % CH) ^ swz<D>(slot / CH));
     }
-    auto issue_tile = [&](int j, int buf) {
-        const uint32_t dk = lds_addr(&sK[buf][0]) + wu * NPW * 1024;
-        const uint32_t dv = lds_addr(&sV[buf][0]) + wu * NPW * 1024;
+    auto issue = [&](int step) {
+        const int kt = step < na ? step : step - na;
+        const int st = step % NST;
+        const uint32_t dk = lds_addr(&sK[st][0]) + w * NPW * 1024;
+        const uint32_t dv = lds_addr(&sV[st][0]) + w * NPW * 1024;
 #pragma unroll
         for (int n = 0; n < NPW; ++n) {
-            const uint32_t key = (uint32_t)min(j * BN + lrow_n[n], S - 1);
+            const uint32_t key = (uint32_t)min(kt * BN + lrow_n[n], S - 1);
             lds_dma16(dk + n * 1024, kbase, key * k_row + lcol_n[n]);
             lds_dma16(dv + n * 1024, vbase, key * v_row + lcol_n[n]);
         }
     };
 
-    issue_tile(0, 0);
-    const int g16 = lane >> 4, i16 = lane & 15;
-    for (int j = 0; j < ntiles; ++j) {
-        const int buf = j & 1;
-        const int k0 = j * BN;
-        // this wave's loads of tile j are done; the barrier makes everyone's visible and
-        // guarantees tile j-1 (the other buffer) is no longer read
-        __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
-        __syncthreads();
-        if (j + 1 < ntiles) issue_tile(j + 1, buf ^ 1);
-        const T *cK = sK[buf];
-        const T *cV = sV[buf];
+#pragma unroll
+    for (int st = 0; st < NST - 1; ++st)
+        if (st < total) issue(st);
 
-        // a wavefront whose rows all precede this tile (causal) has nothing to do here
-        if (CAUSAL && k0 > wq0 + 31) continue;
+    int step = 0;
+    for (int part = 0; part < nparts; ++part) {
+        const int qt = part == 0 ? qa : qb;
+        const int ntiles = part == 0 ? na : total - na;
+        const int q0 = qt * BM;
+        const int wq0 = q0 + 32 * w;  // first query row of this wavefront
+        const int lq = wq0 + lrow;    // this lane's query row
 
-        // ---- S^T = K . Q^T ----
-        f32x16 s[2];
+        // Q^T fragments (B operand): lane holds Q[lq][16t + 8*half + 0..7]; rows past L read row L-1
+        V8 qf[DT];
+        {
+            const T *qr = (const T *)a.q + b * a.q_sb + h * a.q_sh + (int64_t)min(lq, L - 1) * a.q_sl + 8 * half;
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
-            const int row = 32 * kb + lrow;
-            V8 kf[DT];
-#pragma unroll
-            for (int t = 0; t < DT; ++t) kf[t] = *(const V8 *)&cK[row * D + 8 * ((2 * t + half) ^ swz<D>(row))];
-#pragma unroll
-            for (int i = 0; i < 16; ++i) s[kb][i] = 0.0f;
-#pragma unroll
-            for (int t = 0; t < DT; ++t) s[kb] = M::mma(kf[t], qf[t], s[kb]);
+            for (int t = 0; t < DT; ++t) qf[t] = __builtin_bit_cast(V8, *(const u32x4 *)(qr + 16 * t));
         }
 
-        // ---- masks: s[kb][i] is (key = k0 + 32kb + 8(i/4) + 4half + i%4, query = lq) ----
-        const bool edge = k0 + BN > S || (CAUSAL && k0 + BN - 1 > wq0);
-        if (MASK != 0 || edge) {
+        f32x16 o[DB];
+#pragma unroll
+        for (int db = 0; db < DB; ++db)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) o[db][i] = 0.0f;
+        float m = -INFINITY;  // reference point of this lane's row, log2 domain
+        float lsum = 0.0f;    // this lane's share of the running sum
+
+        for (int j = 0; j < ntiles; ++j, ++step) {
+            const int k0 = j * BN;
+            // Tile `step` is complete once at most the loads of the tiles issued after it are
+            // outstanding (vector memory loads complete in order); the barrier then makes every
+            // wavefront's part visible and guarantees stage (step-1) % NST is no longer read.
+            const int later = min(NST - 2, total - 1 - step);
+            if (later >= 2) wait_vm<2 * PER>();
+            else if (later == 1) wait_vm<PER>();
+            else wait_vm<0>();
+            __syncthreads();
+            if (step + NST - 1 < total) issue(step + NST - 1);
+            const T *cK = sK[step % NST];
+            const T *cV = sV[step % NST];
+
+            // (causal) a wavefront whose rows all precede this tile still runs it: every score
+            // is masked to -inf and p = 0; skipping it makes the compiler copy O on every tile
+            // ---- S^T = K . Q^T ----
+            f32x16 s[2];
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb) {
+                const int row = 32 * kb + lrow;
+                V8 kf[DT];
 #pragma unroll
-                for (int i = 0; i < 16; ++i) {
-                    const int key = k0 + 32 * kb + 8 * (i / 4) + 4 * half + (i % 4);
-                    float x = s[kb][i];
-                    if (MASK != 0) {
-                        const int64_t mi = b * a.m_sb + h * a.m_sh + (int64_t)min(lq, L - 1) * a.m_sl +
-                                           (int64_t)min(key, S - 1) * a.m_ss;
-                        if (MASK == 1) {
-                            x = ((const uint8_t *)a.mask)[mi] ? x : -INFINITY;
-                        } else {
-                            x = fmaf(((const float *)a.mask)[mi], 1.0f / a.scale, x);
+                for (int t = 0; t < DT; ++t) kf[t] = *(const V8 *)&cK[row * D + 8 * ((2 * t + half) ^ swz<D>(row))];
+#pragma unroll
+                for (int i = 0; i < 16; ++i) s[kb][i] = 0.0f;
+#pragma unroll
+                for (int t = 0; t < DT; ++t) s[kb] = M::mma(kf[t], qf[t], s[kb]);
+            }
+
+            // ---- masks: s[kb][i] is (key = k0 + 32kb + 8(i/4) + 4half + i%4, query = lq) ----
+            const bool edge = k0 + BN > S || (CAUSAL && k0 + BN - 1 > wq0);
+            if (MASK != 0 || edge) {
+#pragma unroll
+                for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) {
+                        const int key = k0 + 32 * kb + 8 * (i / 4) + 4 * half + (i % 4);
+                        float x = s[kb][i];
+                        if (MASK != 0) {
+                            const int64_t mi = b * a.m_sb + h * a.m_sh + (int64_t)min(lq, L - 1) * a.m_sl +
+                                               (int64_t)min(key, S - 1) * a.m_ss;
+                            if (MASK == 1) {
+                                x = ((const uint8_t *)a.mask)[mi] ? x : -INFINITY;
+                            } else {
+                                x = fmaf(((const float *)a.mask)[mi], 1.0f / a.scale, x);
+                            }
                         }
+                        const bool blocked = key >= S || (CAUSAL && key > lq);
+                        s[kb][i] = blocked ? -INFINITY : x;
                     }
-                    const bool blocked = key >= S || (CAUSAL && key > lq);
-                    s[kb][i] = blocked ? -INFINITY : x;
                 }
             }
-        }
 
-        // ---- online softmax ----
-        float tmax = -INFINITY;
+            // ---- online softmax ----
+            float tmax = -INFINITY;
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
+            for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-            for (int i = 0; i < 16; ++i) tmax = fmaxf(tmax, s[kb][i]);
-        tmax = xhalf_max(tmax);
-        // a row with nothing visible yet keeps m = -inf, alpha = 1 and p = 0 (no branch:
-        // the MFMAs below combine the two lanes of each row and run for the whole wave)
-        const float mnew = fmaxf(m, tmax * c);
-        const bool none = mnew == -INFINITY;
-        const float msub = none ? 0.0f : mnew;
-        if (!__all(mnew == m)) {
-            const float alpha = none ? 1.0f : fast_exp2(m - mnew);
-            lsum *= alpha;
+                for (int i = 0; i < 16; ++i) tmax = fmaxf(tmax, s[kb][i]);
+            tmax = xhalf_max(tmax);
+            // Lazy rescaling: the reference point m of a row only moves when the tile's max
+            // exceeds it by more than kLazy, so p = 2^(s c - m) stays below 2^kLazy.  A row with
+            // nothing visible yet keeps m = -inf and p = 0 (no branch: the MFMAs below combine
+            // the two lanes of each row and run for the whole wave).
+            const float tm = tmax * c;
+            const bool move = tm > m + kLazy;
+            if (!__all(!move)) {
+                const float mnew = move ? tm : m;
+                const float alpha = move ? fast_exp2(m - mnew) : 1.0f;  // m = -inf: 0 (O and l are 0)
+                lsum *= alpha;
 #pragma unroll
-            for (int db = 0; db < DB; ++db)
+                for (int db = 0; db < DB; ++db)
 #pragma unroll
-                for (int i = 0; i < 16; ++i) o[db][i] *= alpha;
-        }
-        m = mnew;
-
-        // P^T as B operands: k-step (kb, hs) takes accumulator entries 8hs .. 8hs+7
-        V8 pb[2][2], pl[2][2];
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-            for (int hs = 0; hs < 2; ++hs) {
-                float p[8];
-#pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    p[e] = fast_exp2(fmaf(s[kb][8 * hs + e], c, -msub));
-                    lsum += p[e];
-                }
-                pack8<T>(p, pb[kb][hs], pl[kb][hs]);
+                    for (int i = 0; i < 16; ++i) o[db][i] *= alpha;
+                m = mnew;
             }
-        }
+            const float msub = m == -INFINITY ? 0.0f : m;
 
-        // ---- O^T += V^T . P^T ----
-#pragma unroll
-        for (int db = 0; db < DB; ++db) {
+            // P^T as B operands: k-step (kb, hs) takes accumulator entries 8hs .. 8hs+7
+            V8 pb[2][2], pl[2][2];
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
                 for (int hs = 0; hs < 2; ++hs) {
-                    // rows (keys) 32kb + 16hs + 4(g16/2) + i16/4 (+8), column 32db + 16(g16%2) + 4(i16%4)
-                    const int row = 32 * kb + 16 * hs + 4 * (g16 >> 1) + (i16 >> 2);
-                    const int col = 32 * db + 16 * (g16 & 1) + 4 * (i16 & 3);
-                    const int chunk = col >> 3, within = col & 7;
-                    const T *p0 = &cV[row * D + 8 * (chunk ^ swz<D>(row)) + within];
-                    const T *p1 = &cV[(row + 8) * D + 8 * (chunk ^ swz<D>(row + 8)) + within];
-                    const V8 av = read_tr8<T>(p0, p1);
-                    o[db] = M::mma(av, pb[kb][hs], o[db]);
-                    if constexpr (M::kSplit) o[db] = M::mma(av, pl[kb][hs], o[db]);
+                    float p[8];
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) p[e] = fast_exp2(fmaf(s[kb][8 * hs + e], c, -msub));
+                    pack8<T>(p, pb[kb][hs], pl[kb][hs]);
+                    lsum = sum8<T>(p, pb[kb][hs], lsum);
+                }
+            }
+
+            // ---- O^T += V^T . P^T ----
+#pragma unroll
+            for (int db = 0; db < DB; ++db) {
+#pragma unroll
+                for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+                    for (int hs = 0; hs < 2; ++hs) {
+                        // rows (keys) 32kb + 16hs + 4(g16/2) + i16/4 (+8), column 32db + 16(g16%2) + 4(i16%4)
+                        const int row = 32 * kb + 16 * hs + 4 * (g16 >> 1) + (i16 >> 2);
+                        const int col = 32 * db + 16 * (g16 & 1) + 4 * (i16 & 3);
+                        const int chunk = col >> 3, within = col & 7;
+                        const T *p0 = &cV[row * D + 8 * (chunk ^ swz<D>(row)) + within];
+                        const T *p1 = &cV[(row + 8) * D + 8 * (chunk ^ swz<D>(row + 8)) + within];
+                        const V8 av = read_tr8<T>(p0, p1);
+                        o[db] = M::mma(av, pb[kb][hs], o[db]);
+                        if constexpr (M::kSplit) o[db] = M::mma(av, pl[kb][hs], o[db]);
+                    }
                 }
             }
         }
-    }
 
-    // ---- epilogue: normalise, store O (B,H,L,D) and the log-sum-exp ----
-    const float ltot = xhalf_sum(lsum);
-    const float inv = ltot > 0.0f ? 1.0f / ltot : 0.0f;
-    if (lq < L) {
-        T *orow = (T *)a.o + (bh * a.L + lq) * D;
-#pragma unroll
-        for (int db = 0; db < DB; ++db)
-#pragma unroll
-            for (int g = 0; g < 4; ++g)
-                store4<T>(orow + 32 * db + 8 * g + 4 * half, o[db][4 * g] * inv, o[db][4 * g + 1] * inv,
-                          o[db][4 * g + 2] * inv, o[db][4 * g + 3] * inv);
-        if (a.lse && half == 0) ((float *)a.lse)[bh * a.L + lq] = ltot > 0.0f ? (m + log2f(ltot)) * kLn2 : INFINITY;
-        if (a.o32) {
-            float *row32 = (float *)a.o32 + (bh * a.L + lq) * D;
+        // ---- epilogue: normalise, store O (B,H,L,D) and the log-sum-exp ----
+        const float ltot = xhalf_sum(lsum);
+        const float inv = ltot > 0.0f ? 1.0f / ltot : 0.0f;
+        if (lq < L) {
+            T *orow = (T *)a.o + (bh * a.L + lq) * D;
 #pragma unroll
             for (int db = 0; db < DB; ++db)
 #pragma unroll
-                for (int g = 0; g < 4; ++g) {
-                    const f32x4 v = {o[db][4 * g] * inv, o[db][4 * g + 1] * inv, o[db][4 * g + 2] * inv,
-                                     o[db][4 * g + 3] * inv};
-                    *(f32x4 *)(row32 + 32 * db + 8 * g + 4 * half) = v;
-                }
+                for (int g = 0; g < 4; ++g)
+                    store4<T>(orow + 32 * db + 8 * g + 4 * half, o[db][4 * g] * inv, o[db][4 * g + 1] * inv,
+                              o[db][4 * g + 2] * inv, o[db][4 * g + 3] * inv);
+            if (a.lse && half == 0)
+                ((float *)a.lse)[bh * a.L + lq] = ltot > 0.0f ? (m + log2f(ltot)) * kLn2 : INFINITY;
+            if (a.o32) {
+                float *row32 = (float *)a.o32 + (bh * a.L + lq) * D;
+#pragma unroll
+                for (int db = 0; db < DB; ++db)
+#pragma unroll
+                    for (int g = 0; g < 4; ++g) {
+                        const f32x4 v = {o[db][4 * g] * inv, o[db][4 * g + 1] * inv, o[db][4 * g + 2] * inv,
+                                         o[db][4 * g + 3] * inv};
+                        *(f32x4 *)(row32 + 32 * db + 8 * g + 4 * half) = v;
+                    }
+            }
         }
     }
 }
 
 template <typename T, int D>
-hipError_t launch_variant(const AttnFwdArgs &a, int nq, int64_t grid, hipStream_t s) {
+hipError_t launch_variant(const AttnFwdArgs &a, int nq, int npairs, int64_t grid, hipStream_t s) {
     const int mode = !a.mask ? 0 : (a.mask_bool ? 1 : 2);
 #define GT_PREFILL_LAUNCH(C, MK) \
-    hipLaunchKernelGGL((prefill_fwd_kernel<T, D, C, MK>), dim3((unsigned)grid), dim3(256), 0, s, a, nq)
+    hipLaunchKernelGGL((prefill_fwd_kernel<T, D, C, MK>), dim3((unsigned)grid), dim3(64 * NW), 0, s, a, nq, npairs)
     if (a.causal) {
         if (mode == 0) GT_PREFILL_LAUNCH(true, 0);
         else if (mode == 1) GT_PREFILL_LAUNCH(true, 1);
@@ -326,8 +366,13 @@ bool attn_prefill_supported(const AttnFwdArgs &f, int cd) {
 
 hipError_t launch_attn_prefill(const AttnFwdArgs &a, int cd, hipStream_t s) {
     const int nq = (int)((a.L + BM - 1) / BM);
-    const int64_t grid = (int64_t)nq * a.B * a.H;
+    const int npairs = (nq + 1) / 2;  // query tiles p and nq-1-p share a workgroup
+    const int64_t grid = (int64_t)npairs * a.B * a.H;
     if (grid <= 0) return hipSuccess;
-    if (cd == GT_F16) return a.D == 128 ? launch_variant<_Float16, 128>(a, nq, grid, s) : launch_variant<_Float16, 64>(a, nq, grid, s);
-    return a.D == 128 ? launch_variant<__bf16, 128>(a, nq, grid, s) : launch_variant<__bf16, 64>(a, nq, grid, s);
+    if (grid > 0x7fffffffLL) return hipErrorInvalidConfiguration;
+    if (cd == GT_F16)
+        return a.D == 128 ? launch_variant<_Float16, 128>(a, nq, npairs, grid, s)
+                          : launch_variant<_Float16, 64>(a, nq, npairs, grid, s);
+    return a.D == 128 ? launch_variant<__bf16, 128>(a, nq, npairs, grid, s)
+                      : launch_variant<__bf16, 64>(a, nq, npairs, grid, s);
 }

@@ -75,6 +75,27 @@ __device__ inline void pack8(const float *x, typename Mfma<T>::V8 &hi, typename 
     }
 }
 
+// acc + the sum of 8 probabilities x whose operand form is `hi` (pack8).  fp16: the rounded
+// values the MFMA consumes, summed pairwise with v_dot2_f32_f16 (products by 1 are exact, fp32
+// accumulation), 4 instructions instead of 8; bf16: the fp32 values.
+template <typename T>
+__device__ inline float sum8(const float *x, typename Mfma<T>::V8 hi, float acc) {
+    if constexpr (Mfma<T>::kSplit) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc += x[e];
+    } else {
+        typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+        const h2 one = {(_Float16)1.0f, (_Float16)1.0f};
+        const u32x4 u = __builtin_bit_cast(u32x4, hi);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const uint32_t ue = u[e];  // through a scalar: bit-casting a vector element reads element 0
+            acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, ue), one, acc, false);
+        }
+    }
+    return acc;
+}
+
 // Column fragment of a row-major LDS tile: rows row0 .. row0+3 and row0+8 .. row0+11 (8 values)
 // of one column per lane, as laid out by the caller's addressing (see the header comment).
 template <typename T>
