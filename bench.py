@@ -25,11 +25,15 @@ workload, on this host's cores.
 from __future__ import annotations
 
 import argparse
+import csv
 import ctypes
 import json
 import math
 import os
+import re
+import subprocess
 import sys
+import tempfile
 import time
 from pathlib import Path
 
@@ -49,6 +53,9 @@ def parse_args():
     p.add_argument("--configs", default="prefill,decode,decode_q8_0,train,fp32")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--cpu-heads", type=int, default=8, help="heads of the headline workload in the CPU sample")
+    p.add_argument("--measure-traffic", action="store_true",
+                   help="run rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes over the benchmark's kernels (child "
+                        "processes), calibrate them against a plain copy and write the summary under profiles/")
     return p.parse_args()
 
 
@@ -211,6 +218,78 @@ def cpu_baseline(heads: int):
                       f"{sec:.1f} s"}
 
 
+# Dominant kernel of each configuration (substring of its symbol) for the HBM byte counters.
+TRAFFIC_KERNELS = {
+    "prefill": "prefill_fwd_kernelIDF16_Li128ELb1ELi0E",
+    "decode": "decode_split_kernelIDF16_Li128ELi4E",
+    "decode_q8_0": "decode_q8_split_kernel<128, 4>",
+}
+TRAFFIC_FILE = ROOT / "profiles" / "hbm_traffic_prefill_decode.md"
+
+
+def _pmc_average(counter, config):
+    """Average per-dispatch value of `counter` (KiB for FETCH_SIZE / WRITE_SIZE) for every kernel
+    of `python bench.py --configs <config>`, from one rocprofv3 --pmc pass."""
+    with tempfile.TemporaryDirectory() as d:
+        cmd = ["rocprofv3", "--pmc", counter, "-d", d, "-o", "run", "--output-format", "csv", "--",
+               sys.executable, str(ROOT / "bench.py"), "--configs", config, "--no-cpu", "--steps", "3", "--warmup", "1"]
+        print("[traffic] " + " ".join(cmd[:4] + ["<tmp>"] + cmd[6:]), file=sys.stderr, flush=True)
+        subprocess.run(cmd, check=True, timeout=120, stdout=subprocess.DEVNULL, stderr=subprocess.DEVNULL)
+        files = list(Path(d).rglob("*counter_collection.csv"))
+        if not files:
+            raise RuntimeError(f"rocprofv3 wrote no counter file for {counter} / {config}")
+        vals = {}
+        with open(files[0]) as f:
+            for row in csv.DictReader(f):
+                if row["Counter_Name"] == counter:
+                    vals.setdefault(row["Kernel_Name"], []).append(float(row["Counter_Value"]))
+    return {k: sum(v) / len(v) for k, v in vals.items()}
+
+
+def measure_traffic():
+    """HBM bytes per launch of the dominant kernels: FETCH_SIZE and WRITE_SIZE (KiB per dispatch),
+    each scaled by what the same counter reads for a plain device copy of known size."""
+    copy_bytes = 1 << 30  # bench_copy: reads and writes 1 GiB
+    cal = {}
+    for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+        avg = _pmc_average(counter, "copy")
+        kib = max(v for k, v in avg.items() if "copy" in k.lower())
+        cal[counter] = {"KiB": kib, "factor": copy_bytes / 1024 / kib}
+    rows = {}
+    for config, pat in TRAFFIC_KERNELS.items():
+        r = {}
+        for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+            avg = _pmc_average(counter, config)
+            hits = [v for k, v in avg.items() if pat in k]
+            if not hits:
+                raise RuntimeError(f"no dispatch of {pat} in {config}")
+            r[counter] = hits[0]
+        r["bytes"] = (r["FETCH_SIZE"] * cal["FETCH_SIZE"]["factor"] + r["WRITE_SIZE"] * cal["WRITE_SIZE"]["factor"]) * 1024
+        rows[config] = r
+    lines = ["# HBM traffic per launch of the benchmark's dominant kernels", "",
+             "Command: `python bench.py --measure-traffic` (each pass: `rocprofv3 --pmc <COUNTER> -d <tmp> -o run "
+             "--output-format csv -- python bench.py --configs <config> --no-cpu --steps 3 --warmup 1`).", "",
+             "Calibration (plain 1 GiB device copy, `--configs copy`):", ""]
+    for c, v in cal.items():
+        lines.append(f"- {c}: {v['KiB']:.0f} KiB per copy of 1048576 KiB -> factor {v['factor']:.4f}")
+    lines += ["", "| config | kernel | FETCH_SIZE KiB | WRITE_SIZE KiB | traffic bytes per launch |", "|---|---|---|---|---|"]
+    for config, r in rows.items():
+        lines.append(f"| {config} | `{TRAFFIC_KERNELS[config]}` | {r['FETCH_SIZE']:.0f} | {r['WRITE_SIZE']:.0f} | "
+                     f"traffic_bytes[{config}] = {r['bytes']:.0f} |")
+    TRAFFIC_FILE.parent.mkdir(exist_ok=True)
+    TRAFFIC_FILE.write_text("\n".join(lines) + "\n")
+    print("\n".join(lines))
+
+
+def committed_traffic(config):
+    """HBM bytes per launch of the config's dominant kernel as last measured by --measure-traffic."""
+    try:
+        m = re.search(r"traffic_bytes\[" + re.escape(config) + r"\] = (\d+)", TRAFFIC_FILE.read_text())
+    except OSError:
+        return None
+    return int(m.group(1)) if m else None
+
+
 CONFIGS = {
     "prefill": dict(B=4, H=32, Hkv=32, L=2048, S=2048, D=128, dtype="float16", causal=True, amp=0.5),
     "decode": dict(B=32, H=32, Hkv=8, L=1, S=4096, D=128, dtype="float16", rotate=2),
@@ -223,6 +302,9 @@ CONFIGS = {
 
 def main():
     args = parse_args()
+    if args.measure_traffic:
+        measure_traffic()
+        return 0
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
               "(the attention path has no multi-GPU exchange)", file=sys.stderr)
@@ -243,6 +325,15 @@ def main():
         print(f"[bench] {name}: {json.dumps(results[name])}", file=sys.stderr, flush=True)
 
     head = results.get("prefill") or next(iter(results.values()))
+    for name in TRAFFIC_KERNELS:
+        if name in results:
+            results[name]["traffic_bytes"] = committed_traffic(name)
+    if head["unit"] == "TFLOP/s":
+        roofline = {"bound": "mfma", "achieved": head["value"], "peak": PEAK_FP16_TFLOPS, "unit": "TFLOP/s",
+                    "frac": head["value"] / PEAK_FP16_TFLOPS, "traffic": committed_traffic("prefill")}
+    else:
+        roofline = {"bound": "hbm", "achieved": head["value"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                    "frac": head["value"] / PEAK_HBM_GBS, "traffic": None}
     line = {
         "metric": "SDPA prefill TFLOP/s + decode KV GB/s on 1 MI355X (% roofline) vs ggml CPU",
         "value": head["value"],
@@ -258,8 +349,7 @@ def main():
         "data": "synthetic",
         "config": {"workload": "causal prefill SDPA fp16, B=4 H=32 L=S=2048 D=128",
                    "batch": 4, "heads": 32, "seq_len": 2048, "head_dim": 128, "causal": True},
-        "roofline": {"bound": "mfma", "achieved": head["value"], "peak": PEAK_FP16_TFLOPS, "unit": "TFLOP/s",
-                     "frac": head["value"] / PEAK_FP16_TFLOPS, "traffic": None},
+        "roofline": roofline,
         "configs": results,
     }
     if not args.no_cpu:
