@@ -59,13 +59,14 @@ hipError_t launch_attn_generic_fwd(const AttnFwdArgs &a, int cd, hipStream_t s);
 hipError_t launch_attn_generic_bwd(const AttnBwdArgs &a, int cd, hipStream_t s);
 
 bool attn_decode_supported(const AttnFwdArgs &f, int cd);
-int attn_decode_splits(int64_t S);
+int attn_decode_splits(const AttnFwdArgs &f, int cd);
 hipError_t launch_attn_decode(const DecodeArgs &a, int cd, hipStream_t s);
 
 bool attn_prefill_supported(const AttnFwdArgs &f, int cd);
 hipError_t launch_attn_prefill(const AttnFwdArgs &a, int cd, hipStream_t s);
 
 bool attn_decode_q8_supported(const AttnFwdArgs &f, int q_dtype);
+int attn_decode_q8_splits(const AttnFwdArgs &f);
 hipError_t launch_attn_decode_q8(const DecodeArgs &a, hipStream_t s);
 hipError_t launch_attn_decode_merge(const DecodeArgs &a, int out_dtype, hipStream_t s);
 

@@ -6,18 +6,24 @@
 // kept: scale, additive/bool mask, top-left causal (only key 0 when L = 1), empty rows -> 0.
 //
 // Work decomposition (HBM-bound; bytes per launch = K + V + Q + O):
-//   workgroup = (kv head of one sequence, chunk of kChunk keys), 256 threads;
-//   a key row of D values is read by D/8 lanes with one 16-byte load each, so a wave reads
-//   64*16 bytes of consecutive rows per load instruction (fully coalesced);
-//   every lane issues all of its row loads for the chunk before using any of them;
-//   scores use v_dot2_f32_{f16,bf16}: products exact, fp32 sums; the chunk softmax runs in the
-//   log2 domain (exp2); P.V accumulates in fp32.
+//   workgroup = (kv head of one sequence, chunk of kChunk keys), 256 threads; every lane
+//   issues all of its K and V loads for the chunk before using any of them.
+//   D = 64, 128: the scores S^T (keys x heads) = K . Q^T run on v_mfma_f32_16x16x32_{f16,bf16}
+//   with the G query heads as MFMA columns: lane l holds K[key l%16][32t + 8(l/16) .. +7] as the
+//   A operand straight from memory (4 lanes read 64 consecutive bytes of a row), so no
+//   cross-lane reduction is needed for a dot product.  D = 256: a key row is split over D/8
+//   lanes, dot products with v_dot2_f32_{f16,bf16} summed across those lanes.
+//   The chunk softmax runs in the log2 domain (exp2); P.V is a VALU fp32 accumulation over
+//   coalesced V rows (D/8 lanes per row, 16-byte loads), reduced across lanes once per chunk.
 // A second kernel merges the per-chunk (max, sum, unnormalised O) partials of each row.
 
 #include "attn_common.h"
 #include "gt_internal.h"
 
+#include <algorithm>
 #include <cmath>
+#include <map>
+#include <mutex>
 
 namespace {
 
@@ -28,6 +34,9 @@ constexpr float kLn2 = 0.6931471805599453f;
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 typedef __bf16 bf162_t __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+__device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 template <typename T>
 struct Pack;
@@ -74,8 +83,248 @@ __device__ inline float finish_score(const AttnFwdArgs &f, float dot, int64_t b,
     return s;
 }
 
+template <typename T>
+struct Mfma16;
+template <>
+struct Mfma16<_Float16> {
+    typedef _Float16 V8 __attribute__((ext_vector_type(8)));
+    static __device__ inline f32x4 mma(V8 a, V8 b, f32x4 c) { return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0); }
+};
+template <>
+struct Mfma16<__bf16> {
+    typedef __bf16 V8 __attribute__((ext_vector_type(8)));
+    static __device__ inline f32x4 mma(V8 a, V8 b, f32x4 c) { return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0); }
+};
+
+template <typename T>
+__device__ inline void store_t(void *o, int64_t i, float v);
+template <>
+__device__ inline void store_t<_Float16>(void *o, int64_t i, float v) {
+    ((_Float16 *)o)[i] = (_Float16)v;
+}
+template <>
+__device__ inline void store_t<__bf16>(void *o, int64_t i, float v) {
+    ((__bf16 *)o)[i] = (__bf16)v;
+}
+template <>
+__device__ inline void store_t<float>(void *o, int64_t i, float v) {
+    ((float *)o)[i] = v;
+}
+
+// D = 64, 128: streaming kernel.  Workgroup = (kv head of one sequence, split); the split's
+// keys are walked in steps of kStep = 128 keys, the loads of step s+1 in flight while step s is
+// computed.  Wave w owns keys [32w, 32w + 32) of every step end to end (scores, softmax, P.V)
+// and keeps its own online-softmax state, so steps need no workgroup barrier; the four waves
+// are combined once at the end.  With a single split the kernel writes the output itself.
+// v_mfma_f32_16x16x32 layouts (lane l): A[m = l%16][k = 8(l/16) + 0..7], B[k = 8(l/16) + 0..7][n = l%16],
+// C[m = 4(l/16) + i][n = l%16], i = 0..3.
+constexpr int kStep = 128;  // keys per step of a workgroup (32 per wave)
+
+// MASK: 0 = none, 1 = bool bytes, 2 = additive float.
+template <typename T, int D, int G, int MASK>
+__global__ __launch_bounds__(256, 2) void decode_stream_kernel(DecodeArgs a) {
+    using P = Pack<T>;
+    using MM = Mfma16<T>;
+    using V8 = typename MM::V8;
+    constexpr int NT = D / 32;     // k-steps of the score MFMA
+    constexpr int LPR = D / 8;     // lanes per V row (16 bytes each)
+    constexpr int RPW = 64 / LPR;  // V rows per wave load
+    constexpr int NV = 32 / RPW;   // V loads per lane and step
+    __shared__ __attribute__((aligned(16))) float s_p[4][32][G];  // per-wave probabilities
+    __shared__ float s_m[4][G], s_l[4][G];
+    __shared__ float s_o[4][G][D];
+
+    const AttnFwdArgs &f = a.f;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int l16 = lane & 15, q4 = lane >> 4;
+    const int sub = lane % LPR, vrow = lane / LPR;
+    const int split = blockIdx.x;
+    const int64_t bk = blockIdx.y, b = bk / f.Hkv, hk = bk % f.Hkv;
+    const int S = (int)f.S;
+    const int span = ((S + kStep - 1) / kStep + a.nsplit - 1) / a.nsplit * kStep;  // keys per split
+    const int kbeg = split * span, kend = min(S, kbeg + span);
+    const int nsteps = kend > kbeg ? (kend - kbeg + kStep - 1) / kStep : 0;
+
+    // B operand (Q^T): lane holds Q[head l16][32t + 8 q4 + 0..7]; columns l16 >= G repeat head
+    // G-1 and are discarded
+    V8 qb[NT];
+    {
+        const T *qr = (const T *)f.q + b * f.q_sb + (hk * G + min(l16, G - 1)) * f.q_sh + 8 * q4;
+#pragma unroll
+        for (int t = 0; t < NT; ++t) qb[t] = __builtin_bit_cast(V8, *(const u32x4 *)(qr + 32 * t));
+    }
+    // K/V rows of a step; keys past S read row S-1 (finite; masked to -inf / weight 0).  Byte
+    // offsets from the (b, kv head) bases fit 32 bits (checked by the launcher).  Every byte is
+    // read once: nontemporal loads keep it from displacing useful lines in the caches.
+    const char *kbase = (const char *)((const T *)f.k + b * f.k_sb + hk * f.k_sh);
+    const char *vbase = (const char *)((const T *)f.v + b * f.v_sb + hk * f.v_sh);
+    const uint32_t krow = (uint32_t)f.k_ss * (uint32_t)sizeof(T), vrowb = (uint32_t)f.v_ss * (uint32_t)sizeof(T);
+    struct Tile {
+        V8 k[2][NT];   // A operands: block kb = keys 16kb + l16 of the wave's 32
+        u32x4 v[NV];   // V rows RPW*i + vrow of the wave's 32, dims 8 sub .. +7
+    };
+    auto load = [&](int step, Tile &tl) {
+        const int k0 = kbeg + step * kStep + 32 * w;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+            const uint32_t off = (uint32_t)min(k0 + 16 * kb + l16, S - 1) * krow + 16u * q4;
+#pragma unroll
+            for (int t = 0; t < NT; ++t) tl.k[kb][t] = __builtin_bit_cast(V8, __builtin_nontemporal_load((const u32x4 *)(kbase + off + 64 * t)));
+        }
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            const uint32_t off = (uint32_t)min(k0 + RPW * i + vrow, S - 1) * vrowb + 16u * sub;
+            tl.v[i] = __builtin_nontemporal_load((const u32x4 *)(vbase + off));
+        }
+    };
+
+    const float cs = f.scale * kLog2e;
+    const int64_t mrow = b * f.m_sb + (hk * G + min(l16, G - 1)) * f.m_sh;
+    float m = -INFINITY;  // running max of head l16 (log2 domain), same in the 4 lanes of a head
+    float lsum = 0.0f;    // running sum of head l16
+    float acc[G][8];      // unnormalised O of every head, dims 8 sub .. +7, this lane's rows
+#pragma unroll
+    for (int h = 0; h < G; ++h)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[h][j] = 0.0f;
+
+    auto compute = [&](int step, const Tile &tl) {
+        const int k0 = kbeg + step * kStep + 32 * w;
+        float sc[2][4];
+        float cm = -INFINITY;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+            f32x4 c4 = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int t = 0; t < NT; ++t) c4 = MM::mma(tl.k[kb][t], qb[t], c4);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int key = k0 + 16 * kb + 4 * q4 + i;
+                float x = c4[i] * cs;
+                bool blocked = key >= kend || (f.causal && key > 0) || l16 >= G;
+                if (MASK != 0) {
+                    const int64_t mi = mrow + (int64_t)min(key, S - 1) * f.m_ss;
+                    if (MASK == 1) blocked = blocked || !((const uint8_t *)f.mask)[mi];
+                    else x = fmaf(((const float *)f.mask)[mi], kLog2e, x);
+                }
+                x = blocked ? -INFINITY : x;
+                sc[kb][i] = x;
+                cm = fmaxf(cm, x);
+            }
+        }
+        cm = fmaxf(cm, __shfl_xor(cm, 16, 64));
+        cm = fmaxf(cm, __shfl_xor(cm, 32, 64));
+        const float mnew = fmaxf(m, cm);
+        const float msub = mnew == -INFINITY ? 0.0f : mnew;
+        const float alpha = mnew == -INFINITY ? 1.0f : fast_exp2(m - mnew);  // m = -inf: 0
+        m = mnew;
+        float ps = 0.0f;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                sc[kb][i] = fast_exp2(sc[kb][i] - msub);  // -inf -> 0
+                ps += sc[kb][i];
+            }
+        ps += __shfl_xor(ps, 16, 64);
+        ps += __shfl_xor(ps, 32, 64);
+        lsum = fmaf(lsum, alpha, ps);
+        if (l16 < G) {
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) s_p[w][16 * kb + 4 * q4 + i][l16] = sc[kb][i];
+        }
+        // the head-h rescale factor sits in lane h
+        float al[G];
+#pragma unroll
+        for (int h = 0; h < G; ++h) al[h] = __shfl(alpha, h, 64);
+        __builtin_amdgcn_wave_barrier();  // s_p written by this wave before it is read
+#pragma unroll
+        for (int h = 0; h < G; ++h)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) acc[h][j] *= al[h];
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            const int r = RPW * i + vrow;
+            float vf[8];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                vf[2 * j] = P::lo(tl.v[i][j]);
+                vf[2 * j + 1] = P::hi(tl.v[i][j]);
+            }
+#pragma unroll
+            for (int h = 0; h < G; ++h) {
+                const float p = s_p[w][r][h];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) acc[h][j] = fmaf(p, vf[j], acc[h][j]);
+            }
+        }
+        __builtin_amdgcn_wave_barrier();  // s_p read before the next step overwrites it
+    };
+
+    // two tiles in flight, unrolled by two so they swap roles without copies
+    Tile ta, tb;
+    if (nsteps > 0) load(0, ta);
+    for (int st = 0; st < nsteps; st += 2) {
+        if (st + 1 < nsteps) load(st + 1, tb);
+        __builtin_amdgcn_sched_barrier(0);
+        compute(st, ta);
+        if (st + 1 < nsteps) {
+            if (st + 2 < nsteps) load(st + 2, ta);
+            __builtin_amdgcn_sched_barrier(0);
+            compute(st + 1, tb);
+        }
+    }
+
+    // ---- combine the four waves ----
+#pragma unroll
+    for (int h = 0; h < G; ++h)
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+#pragma unroll
+            for (int mm = LPR; mm < 64; mm <<= 1) acc[h][j] += __shfl_xor(acc[h][j], mm, 64);
+    if (lane < G) {
+        s_m[w][lane] = m;
+        s_l[w][lane] = lsum;
+    }
+    if (lane < LPR) {
+#pragma unroll
+        for (int h = 0; h < G; ++h)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) s_o[w][h][8 * sub + j] = acc[h][j];
+    }
+    __syncthreads();
+    for (int e = tid; e < G * D; e += 256) {
+        const int h = e / D, d = e % D;
+        const float M = fmaxf(fmaxf(s_m[0][h], s_m[1][h]), fmaxf(s_m[2][h], s_m[3][h]));
+        float o = 0.0f, L = 0.0f;
+#pragma unroll
+        for (int ww = 0; ww < 4; ++ww) {
+            const float wg = s_m[ww][h] == -INFINITY ? 0.0f : fast_exp2(s_m[ww][h] - M);
+            o = fmaf(wg, s_o[ww][h][d], o);
+            L = fmaf(wg, s_l[ww][h], L);
+        }
+        const int64_t row = b * f.H + hk * G + h;
+        if (a.nsplit == 1) {
+            // the whole key range: normalise and store
+            store_t<T>(f.o, row * D + d, L > 0.0f ? o / L : 0.0f);
+            if (f.lse && d == 0) ((float *)f.lse)[row] = L > 0.0f ? (M + log2f(L)) * kLn2 : INFINITY;
+        } else {
+            const int64_t pr = row * a.nsplit + split;
+            a.part_o[pr * D + d] = o;
+            if (d == 0) {
+                a.part_ml[pr * 2 + 0] = M;
+                a.part_ml[pr * 2 + 1] = L;
+            }
+        }
+    }
+}
+
+// D = 256: a key row is split over D/8 lanes (16-byte loads), dot products reduced across lanes.
 template <typename T, int D, int G>
-__global__ __launch_bounds__(256) void decode_split_kernel(DecodeArgs a) {
+__global__ __launch_bounds__(256) void decode_rows_kernel(DecodeArgs a) {
     using P = Pack<T>;
     constexpr int LPR = D / 8;        // lanes per key row
     constexpr int RPW = 64 / LPR;     // rows per wave per load
@@ -223,53 +472,54 @@ __global__ __launch_bounds__(256) void decode_split_kernel(DecodeArgs a) {
     }
 }
 
-template <typename T>
-__device__ inline void store_t(void *o, int64_t i, float v);
-template <>
-__device__ inline void store_t<_Float16>(void *o, int64_t i, float v) {
-    ((_Float16 *)o)[i] = (_Float16)v;
-}
-template <>
-__device__ inline void store_t<__bf16>(void *o, int64_t i, float v) {
-    ((__bf16 *)o)[i] = (__bf16)v;
-}
-template <>
-__device__ inline void store_t<float>(void *o, int64_t i, float v) {
-    ((float *)o)[i] = v;
-}
-
-// One wave per (b, h) row: out = sum_i 2^(m_i - M) O_i / sum_i 2^(m_i - M) l_i.
+// One wave per (b, h) row: out = sum_i 2^(m_i - M) O_i / sum_i 2^(m_i - M) l_i.  A split's
+// partial O row is read as 16-byte pieces by D/4 lanes, 64/(D/4) splits per wave load, eight
+// independent loads per lane in flight.
 template <typename TO, int D>
 __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a) {
+    constexpr int LPS = D / 4;     // lanes per partial row
+    constexpr int SPW = 64 / LPS;  // partial rows per wave load
+    constexpr int U = 8;           // loads in flight per lane
     const AttnFwdArgs &f = a.f;
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int64_t row = (int64_t)blockIdx.x * 4 + w;
     if (row >= f.B * f.H) return;
-    const float *ml = a.part_ml + row * a.nsplit * 2;
+    const int ns = a.nsplit;
+    const float *ml = a.part_ml + row * ns * 2;
     float M = -INFINITY;
-    for (int i = lane; i < a.nsplit; i += 64) M = fmaxf(M, ml[2 * i]);
+    for (int i = lane; i < ns; i += 64) M = fmaxf(M, ml[2 * i]);
     M = wave_max(M);
-    constexpr int NJ = (D + 63) / 64;
-    float o[NJ];
-#pragma unroll
-    for (int j = 0; j < NJ; ++j) o[j] = 0.0f;
     float L = 0.0f;
-    for (int i = 0; i < a.nsplit; ++i) {
+    for (int i = lane; i < ns; i += 64) {
         const float m = ml[2 * i];
-        const float wgt = (m == -INFINITY) ? 0.0f : exp2f(m - M);
-        L = fmaf(wgt, ml[2 * i + 1], L);
-        const float *po = a.part_o + (row * a.nsplit + i) * D;
+        L += m == -INFINITY ? 0.0f : fast_exp2(m - M) * ml[2 * i + 1];
+    }
+    L = wave_sum(L);
+    const int sub = lane % LPS, sp = lane / LPS;
+    const float *po = a.part_o + row * ns * D + 4 * sub;
+    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int i0 = 0; i0 < ns; i0 += SPW * U) {
+        f32x4 x[U];
+        float wgt[U];
 #pragma unroll
-        for (int j = 0; j < NJ; ++j) {
-            const int d = lane + 64 * j;
-            if (d < D) o[j] = fmaf(wgt, po[d], o[j]);
+        for (int u = 0; u < U; ++u) {
+            const int i = min(i0 + SPW * u + sp, ns - 1);
+            x[u] = *(const f32x4 *)(po + (int64_t)i * D);
+            const float m = ml[2 * i];
+            wgt[u] = (i0 + SPW * u + sp >= ns || m == -INFINITY) ? 0.0f : fast_exp2(m - M);
         }
+#pragma unroll
+        for (int u = 0; u < U; ++u) acc += wgt[u] * x[u];
+    }
+#pragma unroll
+    for (int m = LPS; m < 64; m <<= 1) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[j] += __shfl_xor(acc[j], m, 64);
     }
     const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+    if (lane < LPS) {
 #pragma unroll
-    for (int j = 0; j < NJ; ++j) {
-        const int d = lane + 64 * j;
-        if (d < D) store_t<TO>(f.o, row * D + d, o[j] * inv);
+        for (int j = 0; j < 4; ++j) store_t<TO>(f.o, row * D + 4 * sub + j, acc[j] * inv);
     }
     if (f.lse && lane == 0) ((float *)f.lse)[row] = L > 0.0f ? (M + log2f(L)) * kLn2 : INFINITY;
 }
@@ -277,9 +527,17 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a) {
 template <typename T, int D, int G>
 hipError_t launch_typed(const DecodeArgs &a, hipStream_t s) {
     dim3 grid((unsigned)a.nsplit, (unsigned)(a.f.B * a.f.Hkv));
-    hipLaunchKernelGGL((decode_split_kernel<T, D, G>), grid, dim3(256), 0, s, a);
+    if constexpr (D <= 128) {
+        const int mode = !a.f.mask ? 0 : (a.f.mask_bool ? 1 : 2);
+        if (mode == 0) hipLaunchKernelGGL((decode_stream_kernel<T, D, G, 0>), grid, dim3(256), 0, s, a);
+        else if (mode == 1) hipLaunchKernelGGL((decode_stream_kernel<T, D, G, 1>), grid, dim3(256), 0, s, a);
+        else hipLaunchKernelGGL((decode_stream_kernel<T, D, G, 2>), grid, dim3(256), 0, s, a);
+    } else {
+        hipLaunchKernelGGL((decode_rows_kernel<T, D, G>), grid, dim3(256), 0, s, a);
+    }
     hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
+    // one split of the streaming kernel: it wrote the output itself
+    if (e != hipSuccess || (D <= 128 && a.nsplit == 1)) return e;
     const int64_t rows = a.f.B * a.f.H;
     hipLaunchKernelGGL((decode_merge_kernel<T, D>), dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, s, a);
     return hipGetLastError();
@@ -328,11 +586,76 @@ hipError_t launch_attn_decode_merge(const DecodeArgs &a, int out_dtype, hipStrea
     return hipErrorInvalidValue;
 }
 
-int attn_decode_splits(int64_t S) { return (int)((S + kChunk - 1) / kChunk); }
+namespace {
+
+// The streaming kernel instance a launch of `f` uses (compute dtype cd).
+template <typename T, int D>
+const void *stream_kernel_d(const AttnFwdArgs &f, int G) {
+    const int mode = !f.mask ? 0 : (f.mask_bool ? 1 : 2);
+#define GT_SK(GG) \
+    (mode == 0 ? (const void *)decode_stream_kernel<T, D, GG, 0> \
+               : mode == 1 ? (const void *)decode_stream_kernel<T, D, GG, 1> : (const void *)decode_stream_kernel<T, D, GG, 2>)
+    switch (G) {
+        case 1: return GT_SK(1);
+        case 2: return GT_SK(2);
+        case 4: return GT_SK(4);
+        case 8: return GT_SK(8);
+        default: return nullptr;
+    }
+#undef GT_SK
+}
+
+const void *stream_kernel(const AttnFwdArgs &f, int cd) {
+    const int G = (int)(f.H / f.Hkv);
+    if (cd == GT_F16) return f.D == 128 ? stream_kernel_d<_Float16, 128>(f, G) : stream_kernel_d<_Float16, 64>(f, G);
+    return f.D == 128 ? stream_kernel_d<__bf16, 128>(f, G) : stream_kernel_d<__bf16, 64>(f, G);
+}
+
+// Workgroups of `kernel` the device runs at once (CUs x resident workgroups per CU), cached.
+int64_t resident_slots(const void *kernel) {
+    static std::mutex mu;
+    static std::map<std::pair<int, const void *>, int64_t> cache;
+    int dev = 0;
+    (void)hipGetDevice(&dev);
+    std::lock_guard<std::mutex> lock(mu);
+    auto it = cache.find({dev, kernel});
+    if (it != cache.end()) return it->second;
+    int cus = 0, per = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, kernel, 256, 0) != hipSuccess || per <= 0) per = 2;
+    const int64_t slots = (int64_t)cus * per;
+    cache[{dev, kernel}] = slots;
+    return slots;
+}
+
+}  // namespace
+
+int attn_decode_splits(const AttnFwdArgs &f, int cd) {
+    if (f.D > 128) return (int)((f.S + kChunk - 1) / kChunk);  // one 256-key chunk per workgroup
+    // Streaming kernel: workgroups of equal length, as many splits as keep every CU busy
+    // without a partial last round; each extra split costs a little merge work.
+    const void *kernel = stream_kernel(f, cd);
+    const int64_t slots = kernel ? resident_slots(kernel) : 512;
+    const int64_t wgs = f.B * f.Hkv;
+    const int64_t maxs = std::min<int64_t>(64, (f.S + kStep - 1) / kStep);
+    int best = 1;
+    double best_cost = 1e30;
+    for (int64_t n = 1; n <= maxs; ++n) {
+        const double cost = (double)((wgs * n + slots - 1) / slots) / (double)n + (n > 1 ? 0.02 * (double)n : 0.0);
+        if (cost < best_cost - 1e-9) {
+            best_cost = cost;
+            best = (int)n;
+        }
+    }
+    return best;
+}
 
 bool attn_decode_supported(const AttnFwdArgs &f, int cd) {
     if (cd != GT_F16 && cd != GT_BF16) return false;
     if (f.L != 1 || f.S <= 0 || f.D != f.Dv) return false;
+    if (f.S >= (1LL << 30)) return false;  // 32-bit key indices
+    // 32-bit byte offsets of K/V rows from the (batch, kv head) base
+    if ((f.S - 1) * f.k_ss * 2 + f.D * 2 > 0xffffffffLL || (f.S - 1) * f.v_ss * 2 + f.D * 2 > 0xffffffffLL) return false;
     if (f.D != 64 && f.D != 128 && f.D != 256) return false;
     const int64_t G = f.H / f.Hkv;
     if (G != 1 && G != 2 && G != 4 && G != 8) return false;

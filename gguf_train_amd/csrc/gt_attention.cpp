@@ -166,7 +166,7 @@ bool dispatch_forward(const AttnFwdArgs &a, int cd, int dev) {
     if (a.out_dtype == cd && !a.o32 && attn_decode_supported(a, cd)) {
         DecodeArgs da{};
         da.f = a;
-        da.nsplit = attn_decode_splits(a.S);
+        da.nsplit = attn_decode_splits(a, cd);
         const size_t rows = (size_t)(a.B * a.H) * (size_t)da.nsplit;
         gt_scratch ws;
         if (!gt_scratch_alloc(ws, rows * (size_t)(a.D + 2) * sizeof(float), dev)) return false;
@@ -210,7 +210,7 @@ int run_q8_decode(const gt_tensor *q, const gt_tensor *k, const gt_tensor *v, co
     if (!stage_mask(mask, dev, GT_F16, a, tmp)) return -1;
     DecodeArgs da{};
     da.f = a;
-    da.nsplit = attn_decode_splits(a.S);
+    da.nsplit = attn_decode_q8_splits(a);
     const size_t rows = (size_t)(a.B * a.H) * (size_t)da.nsplit;
     gt_scratch ws;
     if (!gt_scratch_alloc(ws, rows * (size_t)(a.D + 2) * sizeof(float), dev)) return -1;
