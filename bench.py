@@ -81,6 +81,9 @@ class Runner:
         return [self.bridge.borrow(t) if t is not None else None for t in ts]
 
     def time_steps(self, step, steps, warmup):
+        """Mean over exactly `steps` steps bracketed by synchronisations (events on the current
+        stream, which the native calls are bound to), then the median of a second pass timed
+        step by step."""
         torch = self.torch
         for _ in range(warmup):
             step(0)
@@ -93,7 +96,14 @@ class Runner:
         e1.record()
         torch.cuda.synchronize()
         wall = time.perf_counter() - t0
-        return e0.elapsed_time(e1) / steps, wall * 1e3 / steps
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+        for i, (a, b) in enumerate(ev):
+            a.record()
+            step(i)
+            b.record()
+        torch.cuda.synchronize()
+        per = sorted(a.elapsed_time(b) for a, b in ev)
+        return e0.elapsed_time(e1) / steps, wall * 1e3 / steps, per[len(per) // 2]
 
 
 def bench_forward(r: Runner, name, cfg, steps, warmup):
@@ -125,8 +135,8 @@ def bench_forward(r: Runner, name, cfg, steps, warmup):
             raise RuntimeError(r.C.last_error())
         lib.gt_tensor_free(p)
 
-    ms, wall_ms = r.time_steps(step, steps, warmup)
-    out = {"ms_per_step": ms, "wall_ms_per_step": wall_ms}
+    ms, wall_ms, med_ms = r.time_steps(step, steps, warmup)
+    out = {"ms_per_step": ms, "wall_ms_per_step": wall_ms, "median_ms": med_ms}
     es = 2 if dt != torch.float32 else 4
     if "decode" in name:
         if cfg.get("q8_0"):
@@ -173,10 +183,11 @@ def bench_train(r: Runner, cfg, steps, warmup):
         for p in (po, pl, p32, dq, dk, dv):
             lib.gt_tensor_free(p)
 
-    ms, wall_ms = r.time_steps(step, steps, warmup)
+    ms, wall_ms, med_ms = r.time_steps(step, steps, warmup)
     fwd = sum(4 * D * causal_pairs(L, int(n)) * H for n in lens)
     flops = int(fwd * 3.5)
-    return {"ms_per_step": ms, "wall_ms_per_step": wall_ms, "flop_per_step": flops, "forward_flop": fwd,
+    return {"ms_per_step": ms, "wall_ms_per_step": wall_ms, "median_ms": med_ms, "flop_per_step": flops,
+            "forward_flop": fwd,
             "value": flops / (ms * 1e-3) / 1e12, "unit": "TFLOP/s",
             "frac_of_peak": flops / (ms * 1e-3) / 1e12 / PEAK_FP16_TFLOPS, "valid_lengths": [int(x) for x in lens]}
 
@@ -191,9 +202,9 @@ def bench_copy(r: Runner, steps, warmup):
     def step(i):
         y.copy_(x)
 
-    ms, wall_ms = r.time_steps(step, steps, warmup)
+    ms, wall_ms, med_ms = r.time_steps(step, steps, warmup)
     nbytes = 2 * x.numel() * x.element_size()
-    return {"ms_per_step": ms, "wall_ms_per_step": wall_ms, "bytes_per_step": nbytes, "read_bytes": nbytes // 2,
+    return {"ms_per_step": ms, "wall_ms_per_step": wall_ms, "median_ms": med_ms, "bytes_per_step": nbytes, "read_bytes": nbytes // 2,
             "write_bytes": nbytes // 2, "value": nbytes / (ms * 1e-3) / 1e9, "unit": "GB/s",
             "frac_of_peak": nbytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS}
 
@@ -221,8 +232,8 @@ def cpu_baseline(heads: int):
 # Dominant kernel of each configuration (substring of its symbol) for the HBM byte counters.
 TRAFFIC_KERNELS = {
     "prefill": "prefill_fwd_kernelIDF16_Li128ELb1ELi0E",
-    "decode": "decode_split_kernelIDF16_Li128ELi4E",
-    "decode_q8_0": "decode_q8_split_kernel<128, 4>",
+    "decode": "decode_stream_kernelIDF16_Li128ELi4ELi0E",
+    "decode_q8_0": "decode_q8_stream_kernel<128, 4, 0>",
 }
 TRAFFIC_FILE = ROOT / "profiles" / "hbm_traffic_prefill_decode.md"
 
@@ -292,7 +303,7 @@ def committed_traffic(config):
 
 CONFIGS = {
     "prefill": dict(B=4, H=32, Hkv=32, L=2048, S=2048, D=128, dtype="float16", causal=True, amp=0.5),
-    "decode": dict(B=32, H=32, Hkv=8, L=1, S=4096, D=128, dtype="float16", rotate=2),
+    "decode": dict(B=32, H=32, Hkv=8, L=1, S=4096, D=128, dtype="float16", rotate=3),
     "decode_q8_0": dict(B=16, H=32, Hkv=8, L=1, S=8192, D=128, dtype="float16", q8_0=True, rotate=3),
     "train": dict(B=8, H=16, L=1024, D=64, dtype="bfloat16"),
     "fp32": dict(B=1, H=4, Hkv=4, L=128, S=128, D=64, dtype="float32", causal=True),
