@@ -5,7 +5,7 @@ restypes declared up front, `check_ptr` / `check_rc` turning a NULL / non-zero n
 into a Python exception built from the thread-local `gt_last_error()`, and the
 "IndexError: " message prefix mapping to IndexError (gguf_train/_C.py:680-710).
 
-The library is built in-tree (python -m gguf_train_amd._build).  Importing this module never
+The library is built in-tree (python gguf_train_amd/_build.py).  Importing this module never
 builds, downloads or falls back to anything: a missing library is an ImportError.
 """
 
@@ -29,7 +29,7 @@ GT_DEV_CPU, GT_DEV_CUDA = 0, 1
 def _load_native() -> ctypes.CDLL:
     if not LIB_PATH.exists():
         raise ImportError(
-            f"{LIB_PATH} is not built; build it with `python -m gguf_train_amd._build --lib` "
+            f"{LIB_PATH} is not built; build it with `python gguf_train_amd/_build.py --lib` "
             "(hipcc, gfx950). There is no CPU fallback."
         )
     return ctypes.CDLL(str(LIB_PATH))

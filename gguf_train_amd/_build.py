@@ -1,7 +1,7 @@
 """In-tree build of libgt_attn.so (hipcc, gfx950) and of the CPU oracle (gcc).
 
-    python -m gguf_train_amd._build            # both
-    python -m gguf_train_amd._build --lib      # only the HIP library
+    python gguf_train_amd/_build.py            # both (a script: the package needs the library)
+    python gguf_train_amd/_build.py --lib      # only the HIP library
 
 Objects go to gguf_train_amd/_build/ (ignored by git); the shared library is written next to
 this file so that it travels with the source tree.
