@@ -83,6 +83,14 @@ __device__ inline void wait_vm() {
     __builtin_amdgcn_s_waitcnt(0x0f70 | N);
 }
 
+// max of three floats in one v_max3_f32 (fmaxf would first quiet each MFMA result with a
+// v_max_f32 x, x, x; the scores are never signalling NaNs)
+__device__ inline float max3(float a, float b, float c) {
+    float r;
+    asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+    return r;
+}
+
 // Keys covered by query tile qt: all of them, or up to the tile's last row (causal, top-left).
 template <bool CAUSAL>
 __device__ inline int key_tiles(int qt, int S) {
@@ -147,18 +155,55 @@ __global__ __launch_bounds__(64 * NW, 1) void prefill_fwd_kernel(AttnFwdArgs a, 
         lrow_n[n] = slot / CH;
         lcol_n[n] = 16u * (uint32_t)((slot % CH) ^ swz<D>(slot / CH));
     }
+    uint32_t kofs_n[NPW], vofs_n[NPW];  // lane offsets within a full tile
+#pragma unroll
+    for (int n = 0; n < NPW; ++n) {
+        kofs_n[n] = (uint32_t)lrow_n[n] * k_row + lcol_n[n];
+        vofs_n[n] = (uint32_t)lrow_n[n] * v_row + lcol_n[n];
+    }
     auto issue = [&](int step) {
         const int kt = step < na ? step : step - na;
         const int st = step % NST;
         const uint32_t dk = lds_addr(&sK[st][0]) + w * NPW * 1024;
         const uint32_t dv = lds_addr(&sV[st][0]) + w * NPW * 1024;
+        if (kt * BN + BN <= S) {
+            // a full tile: its offset goes into the scalar base, the lane offsets are fixed
+            const char *kb = (const char *)kbase + (uint64_t)(kt * BN) * k_row;
+            const char *vb = (const char *)vbase + (uint64_t)(kt * BN) * v_row;
 #pragma unroll
-        for (int n = 0; n < NPW; ++n) {
-            const uint32_t key = (uint32_t)min(kt * BN + lrow_n[n], S - 1);
-            lds_dma16(dk + n * 1024, kbase, key * k_row + lcol_n[n]);
-            lds_dma16(dv + n * 1024, vbase, key * v_row + lcol_n[n]);
+            for (int n = 0; n < NPW; ++n) {
+                lds_dma16(dk + n * 1024, kb, kofs_n[n]);
+                lds_dma16(dv + n * 1024, vb, vofs_n[n]);
+            }
+        } else {
+#pragma unroll
+            for (int n = 0; n < NPW; ++n) {
+                const uint32_t key = (uint32_t)min(kt * BN + lrow_n[n], S - 1);
+                lds_dma16(dk + n * 1024, kbase, key * k_row + lcol_n[n]);
+                lds_dma16(dv + n * 1024, vbase, key * v_row + lcol_n[n]);
+            }
         }
     };
+
+    // LDS element offsets of this lane's fragments within a tile, fixed for the whole kernel:
+    //   K, k-step t: row lrow (+32 kb), 16-byte chunk 2t + half (the swizzle of row r only
+    //   depends on r mod 32 for both D)
+    //   V^T, (kb, hs, db): rows (keys) 32kb + 16hs + 4(g16/2) + i16/4 and +8, column
+    //   32db + 16(g16%2) + 4(i16%4); with D = 128 the swizzle only depends on row mod 16, so
+    //   (kb, hs) is a constant 16(2kb + hs) rows further.
+    constexpr int NV = D == 128 ? DB : 4 * DB;
+    int kofs[DT], vofs0[NV], vofs1[NV];
+#pragma unroll
+    for (int t = 0; t < DT; ++t) kofs[t] = lrow * D + 8 * ((2 * t + half) ^ swz<D>(lrow));
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        const int db = i % DB, g = i / DB;  // g = 2kb + hs (D = 64)
+        const int row = 16 * g + 4 * (g16 >> 1) + (i16 >> 2);
+        const int col = 32 * db + 16 * (g16 & 1) + 4 * (i16 & 3);
+        const int chunk = col >> 3, within = col & 7;
+        vofs0[i] = row * D + 8 * (chunk ^ swz<D>(row)) + within;
+        vofs1[i] = (row + 8) * D + 8 * (chunk ^ swz<D>(row + 8)) + within;
+    }
 
 #pragma unroll
     for (int st = 0; st < NST - 1; ++st)
@@ -178,6 +223,10 @@ __global__ __launch_bounds__(64 * NW, 1) void prefill_fwd_kernel(AttnFwdArgs a, 
             const T *qr = (const T *)a.q + b * a.q_sb + h * a.q_sh + (int64_t)min(lq, L - 1) * a.q_sl + 8 * half;
 #pragma unroll
             for (int t = 0; t < DT; ++t) qf[t] = __builtin_bit_cast(V8, *(const u32x4 *)(qr + 16 * t));
+            // Wait for Q here: otherwise the compiler's wait for these loads lands inside the tile
+            // loop, where it also waits for every K/V tile prefetch issued since.
+#pragma unroll
+            for (int t = 0; t < DT; ++t) asm volatile("" ::"v"(qf[t]));
         }
 
         f32x16 o[DB];
@@ -208,10 +257,9 @@ __global__ __launch_bounds__(64 * NW, 1) void prefill_fwd_kernel(AttnFwdArgs a, 
             f32x16 s[2];
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb) {
-                const int row = 32 * kb + lrow;
                 V8 kf[DT];
 #pragma unroll
-                for (int t = 0; t < DT; ++t) kf[t] = *(const V8 *)&cK[row * D + 8 * ((2 * t + half) ^ swz<D>(row))];
+                for (int t = 0; t < DT; ++t) kf[t] = *(const V8 *)&cK[kofs[t] + 32 * kb * D];
 #pragma unroll
                 for (int i = 0; i < 16; ++i) s[kb][i] = 0.0f;
 #pragma unroll
@@ -243,11 +291,10 @@ __global__ __launch_bounds__(64 * NW, 1) void prefill_fwd_kernel(AttnFwdArgs a, 
             }
 
             // ---- online softmax ----
-            float tmax = -INFINITY;
+            float tmax = max3(s[0][0], s[0][1], s[0][2]);
 #pragma unroll
-            for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-                for (int i = 0; i < 16; ++i) tmax = fmaxf(tmax, s[kb][i]);
+            for (int i = 3; i < 31; i += 2) tmax = max3(tmax, s[i / 16][i % 16], s[(i + 1) / 16][(i + 1) % 16]);
+            tmax = max3(tmax, s[1][15], s[1][15]);
             tmax = xhalf_max(tmax);
             // Lazy rescaling: the reference point m of a row only moves when the tile's max
             // exceeds it by more than kLazy, so p = 2^(s c - m) stays below 2^kLazy.  A row with
@@ -288,13 +335,9 @@ __global__ __launch_bounds__(64 * NW, 1) void prefill_fwd_kernel(AttnFwdArgs a, 
                 for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
                     for (int hs = 0; hs < 2; ++hs) {
-                        // rows (keys) 32kb + 16hs + 4(g16/2) + i16/4 (+8), column 32db + 16(g16%2) + 4(i16%4)
-                        const int row = 32 * kb + 16 * hs + 4 * (g16 >> 1) + (i16 >> 2);
-                        const int col = 32 * db + 16 * (g16 & 1) + 4 * (i16 & 3);
-                        const int chunk = col >> 3, within = col & 7;
-                        const T *p0 = &cV[row * D + 8 * (chunk ^ swz<D>(row)) + within];
-                        const T *p1 = &cV[(row + 8) * D + 8 * (chunk ^ swz<D>(row + 8)) + within];
-                        const V8 av = read_tr8<T>(p0, p1);
+                        const int g = 2 * kb + hs;
+                        const V8 av = D == 128 ? read_tr8<T>(&cV[vofs0[db] + 16 * g * D], &cV[vofs1[db] + 16 * g * D])
+                                               : read_tr8<T>(&cV[vofs0[g * DB + db]], &cV[vofs1[g * DB + db]]);
                         o[db] = M::mma(av, pb[kb][hs], o[db]);
                         if constexpr (M::kSplit) o[db] = M::mma(av, pl[kb][hs], o[db]);
                     }
