@@ -14,7 +14,9 @@
 //             S^T = K.Q^T, dP^T = V.dO^T, dS^T as above, dQ^T += K^T.dS^T
 // dK and dV of a GQA group are summed in registers (no atomics).  bf16 P and dS are split
 // into hi + lo bf16 operands so the products keep ~16 bits.  Masks: top-left causal,
-// bool / additive (read per element), keys >= S and queries >= L contribute nothing.
+// bool / additive (read per element; an additive mask that does not depend on the query row is
+// read once per key: per head in dK/dV, staged with the K/V tile in dQ), keys >= S and
+// queries >= L contribute nothing.
 
 #include "attn_common.h"
 #include "gt_internal.h"
@@ -155,12 +157,15 @@ __global__ __launch_bounds__(256) void bwd_dkdv_kernel(AttnBwdArgs a, int nkt) {
         if (nsteps > 1) load_step(1);
     }
     __syncthreads();
+    float madd = 0.0f;  // MASK 4: mask value of this lane's key for the current head (raw units)
     for (int st = 0; st < nsteps; ++st) {
         const int buf = st & 1;
         const int hh = st / nqs, qs0 = qstart + (st % nqs) * BQ;
         const int64_t h = hk * G + hh;
         const T *cQ = sQ[buf];
         const T *cG = sG[buf];
+        if (MASK == 4 && st % nqs == 0)
+            madd = ((const float *)f.mask)[b * f.m_sb + h * f.m_sh + (int64_t)min(key, S - 1) * f.m_ss] * inv_scale;
 #pragma unroll
         for (int qb = 0; qb < 2; ++qb) {
             const int q0 = qs0 + 32 * qb;
@@ -187,7 +192,8 @@ __global__ __launch_bounds__(256) void bwd_dkdv_kernel(AttnBwdArgs a, int nkt) {
                     const int i = 4 * g + e, q = qs0 + qi + e;
                     float add;
                     bool ok = key < S && q < L && (!CAUSAL || key <= q);
-                    if (MASK != 0) ok = ok && mask_at<MASK>(f, b, h, min(q, L - 1), min(key, S - 1), inv_scale, add);
+                    if (MASK == 4) add = madd;
+                    else if (MASK != 0) ok = ok && mask_at<MASK>(f, b, h, min(q, L - 1), min(key, S - 1), inv_scale, add);
                     else add = 0.0f;
                     const float pv = ok ? fast_exp2(fmaf(s[i] + add, c, -l4[e])) : 0.0f;
                     p[i] = pv;
@@ -252,6 +258,7 @@ __global__ __launch_bounds__(256) void bwd_dq_kernel(AttnBwdArgs a, int nq) {
     constexpr int NLD = BNK * CH / 256;
     __shared__ __attribute__((aligned(16))) T sK[2][BNK * KP];
     __shared__ __attribute__((aligned(16))) T sV[2][BNK * VP];
+    __shared__ __attribute__((aligned(16))) float sMk[MASK == 4 ? 2 : 1][BNK];  // MASK 4: the tile's mask row
 
     const AttnFwdArgs &f = a.f;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
@@ -290,7 +297,10 @@ __global__ __launch_bounds__(256) void bwd_dq_kernel(AttnBwdArgs a, int nq) {
     const int kv_end = CAUSAL ? min(q0 + BMQ, S) : S;
     const int ntiles = (kv_end + BNK - 1) / BNK;
     u32x4 kreg[NLD], vreg[NLD];
+    float mreg = 0.0f;
+    const float *mrow = MASK == 4 ? (const float *)f.mask + b * f.m_sb + h * f.m_sh : nullptr;
     auto load_tile = [&](int j) {
+        if (MASK == 4 && tid < BNK) mreg = mrow[(int64_t)min(j * BNK + tid, S - 1) * f.m_ss] * inv_scale;
 #pragma unroll
         for (int i = 0; i < NLD; ++i) {
             const int cidx = tid + 256 * i, row = cidx / CH, col = cidx % CH;
@@ -300,6 +310,7 @@ __global__ __launch_bounds__(256) void bwd_dq_kernel(AttnBwdArgs a, int nq) {
         }
     };
     auto store_tile = [&](int buf) {
+        if (MASK == 4 && tid < BNK) sMk[buf][tid] = mreg;
 #pragma unroll
         for (int i = 0; i < NLD; ++i) {
             const int cidx = tid + 256 * i, row = cidx / CH, col = cidx % CH;
@@ -337,12 +348,18 @@ __global__ __launch_bounds__(256) void bwd_dq_kernel(AttnBwdArgs a, int nq) {
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb) {
                 float ds[16];
+                f32x4 mv[4];
+                if (MASK == 4) {
+#pragma unroll
+                    for (int g = 0; g < 4; ++g) mv[g] = *(const f32x4 *)&sMk[buf][32 * kb + 8 * g + 4 * half];
+                }
 #pragma unroll
                 for (int i = 0; i < 16; ++i) {
                     const int kk = k0 + 32 * kb + 8 * (i / 4) + 4 * half + (i % 4);
                     float add;
                     bool ok = kk < S && lq < L && (!CAUSAL || kk <= lq);
-                    if (MASK != 0) ok = ok && mask_at<MASK>(f, b, h, lqc, min(kk, S - 1), inv_scale, add);
+                    if (MASK == 4) add = mv[i / 4][i % 4];
+                    else if (MASK != 0) ok = ok && mask_at<MASK>(f, b, h, lqc, min(kk, S - 1), inv_scale, add);
                     else add = 0.0f;
                     const float pv = ok ? fast_exp2(fmaf(s[kb][i] + add, c, -lse2)) : 0.0f;
                     ds[i] = pv * (dp[kb][i] - dlt);
@@ -410,14 +427,17 @@ hipError_t launch_bwd_typed(const AttnBwdArgs &a, hipStream_t s) {
 
 template <typename T, int D>
 hipError_t launch_bwd_d(const AttnBwdArgs &a, hipStream_t s) {
-    const int mode = !a.f.mask ? 0 : (a.f.mask_bool ? 1 : 2);
+    // mode 4: a float mask that does not depend on the query row (key padding)
+    const int mode = !a.f.mask ? 0 : (a.f.mask_bool ? 1 : (a.f.m_sl == 0 ? 4 : 2));
     if (a.f.causal) {
         if (mode == 0) return launch_bwd_typed<T, D, true, 0>(a, s);
         if (mode == 1) return launch_bwd_typed<T, D, true, 1>(a, s);
+        if (mode == 4) return launch_bwd_typed<T, D, true, 4>(a, s);
         return launch_bwd_typed<T, D, true, 2>(a, s);
     }
     if (mode == 0) return launch_bwd_typed<T, D, false, 0>(a, s);
     if (mode == 1) return launch_bwd_typed<T, D, false, 1>(a, s);
+    if (mode == 4) return launch_bwd_typed<T, D, false, 4>(a, s);
     return launch_bwd_typed<T, D, false, 2>(a, s);
 }
 

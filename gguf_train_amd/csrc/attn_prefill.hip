@@ -72,6 +72,20 @@ __device__ inline void lds_dma16(uint32_t lds, const void *gbase, uint32_t voff)
         : "memory");
 }
 
+// One global_load_lds_dword: lane l copies 4 bytes from gbase + voff to LDS byte address
+// lds + 4 l.
+__device__ inline void lds_dma4(uint32_t lds, const void *gbase, uint32_t voff) {
+    uint32_t save;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %1\n\t"
+        "global_load_lds_dword %2, %3\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(save)
+        : "s"(lds), "v"(voff), "s"(gbase)
+        : "memory");
+}
+
 __device__ inline uint32_t lds_addr(const void *p) {
     return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
 }
@@ -98,7 +112,8 @@ __device__ inline int key_tiles(int qt, int S) {
     return (kv_end + BN - 1) / BN;
 }
 
-// MASK: 0 = none, 1 = bool bytes, 2 = additive float.
+// MASK: 0 = none, 1 = bool bytes, 2 = additive float, 4 = additive float that does not depend
+// on the query row (key padding: the tile's mask row travels to LDS with the K/V tile).
 template <typename T, int D, bool CAUSAL, int MASK>
 __global__ __launch_bounds__(64 * NW, 1) void prefill_fwd_kernel(AttnFwdArgs a, int nq, int npairs) {
     using M = Mfma<T>;
@@ -108,10 +123,13 @@ __global__ __launch_bounds__(64 * NW, 1) void prefill_fwd_kernel(AttnFwdArgs a, 
     constexpr int CH = D / 8;              // 16-byte chunks per row
     constexpr int TILE = BN * D;           // elements per tile
     constexpr int NPW = BN * CH / 64 / NW; // 1 KB wave loads per operand, wave and tile
-    constexpr int PER = 2 * NPW;           // loads per wave and tile (K and V)
+    constexpr bool MROW = MASK == 4;
+    constexpr int PER = 2 * NPW + (MROW ? 1 : 0);  // loads per wave and tile (K, V, mask row)
     static_assert(NPW >= 1 && PER * (NST - 2) < 16, "tile split");
+    static_assert(BN == 64, "mask row: one key per lane");
     __shared__ __attribute__((aligned(1024))) T sK[NST][TILE];
     __shared__ __attribute__((aligned(1024))) T sV[NST][TILE];
+    __shared__ __attribute__((aligned(16))) float sMk[MROW ? NST : 1][BN];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wavefront index, uniform
@@ -161,9 +179,15 @@ __global__ __launch_bounds__(64 * NW, 1) void prefill_fwd_kernel(AttnFwdArgs a, 
         kofs_n[n] = (uint32_t)lrow_n[n] * k_row + lcol_n[n];
         vofs_n[n] = (uint32_t)lrow_n[n] * v_row + lcol_n[n];
     }
+    const float *mrow = MROW ? (const float *)a.mask + b * a.m_sb + h * a.m_sh : nullptr;
     auto issue = [&](int step) {
         const int kt = step < na ? step : step - na;
         const int st = step % NST;
+        if constexpr (MROW) {
+            // the mask values of keys kt*BN .. +63 (keys past S repeat key S-1); every wave writes
+            // the same row, which keeps the loads per wave and tile uniform and needs no exec mask
+            lds_dma4(lds_addr(&sMk[st][0]), mrow, (uint32_t)min(kt * BN + lane, S - 1) * (uint32_t)a.m_ss * 4u);
+        }
         const uint32_t dk = lds_addr(&sK[st][0]) + w * NPW * 1024;
         const uint32_t dv = lds_addr(&sV[st][0]) + w * NPW * 1024;
         if (kt * BN + BN <= S) {
@@ -269,13 +293,22 @@ __global__ __launch_bounds__(64 * NW, 1) void prefill_fwd_kernel(AttnFwdArgs a, 
             // ---- masks: s[kb][i] is (key = k0 + 32kb + 8(i/4) + 4half + i%4, query = lq) ----
             const bool edge = k0 + BN > S || (CAUSAL && k0 + BN - 1 > wq0);
             if (MASK != 0 || edge) {
+                f32x4 mv[2][4];  // MROW: the mask values of this lane's keys, from LDS
+                if constexpr (MROW) {
+#pragma unroll
+                    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                        for (int g = 0; g < 4; ++g) mv[kb][g] = *(const f32x4 *)&sMk[step % NST][32 * kb + 8 * g + 4 * half];
+                }
 #pragma unroll
                 for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
                     for (int i = 0; i < 16; ++i) {
                         const int key = k0 + 32 * kb + 8 * (i / 4) + 4 * half + (i % 4);
                         float x = s[kb][i];
-                        if (MASK != 0) {
+                        if constexpr (MROW) {
+                            x = fmaf(mv[kb][i / 4][i % 4], 1.0f / a.scale, x);
+                        } else if (MASK != 0) {
                             const int64_t mi = b * a.m_sb + h * a.m_sh + (int64_t)min(lq, L - 1) * a.m_sl +
                                                (int64_t)min(key, S - 1) * a.m_ss;
                             if (MASK == 1) {
@@ -375,16 +408,18 @@ __global__ __launch_bounds__(64 * NW, 1) void prefill_fwd_kernel(AttnFwdArgs a, 
 
 template <typename T, int D>
 hipError_t launch_variant(const AttnFwdArgs &a, int nq, int npairs, int64_t grid, hipStream_t s) {
-    const int mode = !a.mask ? 0 : (a.mask_bool ? 1 : 2);
+    const int mode = !a.mask ? 0 : (a.mask_bool ? 1 : (a.m_sl == 0 ? 4 : 2));
 #define GT_PREFILL_LAUNCH(C, MK) \
     hipLaunchKernelGGL((prefill_fwd_kernel<T, D, C, MK>), dim3((unsigned)grid), dim3(64 * NW), 0, s, a, nq, npairs)
     if (a.causal) {
         if (mode == 0) GT_PREFILL_LAUNCH(true, 0);
         else if (mode == 1) GT_PREFILL_LAUNCH(true, 1);
+        else if (mode == 4) GT_PREFILL_LAUNCH(true, 4);
         else GT_PREFILL_LAUNCH(true, 2);
     } else {
         if (mode == 0) GT_PREFILL_LAUNCH(false, 0);
         else if (mode == 1) GT_PREFILL_LAUNCH(false, 1);
+        else if (mode == 4) GT_PREFILL_LAUNCH(false, 4);
         else GT_PREFILL_LAUNCH(false, 2);
     }
 #undef GT_PREFILL_LAUNCH
@@ -404,6 +439,8 @@ bool attn_prefill_supported(const AttnFwdArgs &f, int cd) {
     // K/V tiles are addressed by 32-bit byte offsets from the (batch, kv head) base
     if ((f.S - 1) * f.k_ss * 2 + f.D * 2 > 0xffffffffLL) return false;
     if ((f.S - 1) * f.v_ss * 2 + f.Dv * 2 > 0xffffffffLL) return false;
+    // a query-independent float mask row is addressed the same way
+    if (f.mask && !f.mask_bool && f.m_sl == 0 && (f.m_ss < 0 || (f.S - 1) * f.m_ss * 4 + 4 > 0xffffffffLL)) return false;
     return true;
 }
 

@@ -111,6 +111,21 @@ bool stage_mask(const gt_tensor *mask, int dev, int cd, AttnFwdArgs &a, Temps &t
         m = tmp.keep(gt_to_device_dense(mask, dev, want));
         if (!m) return false;
     }
+    // A bool mask that does not depend on the query row (key padding, (L, S) with L == 1 or a
+    // broadcast query dimension) becomes the equivalent additive mask (0 / -inf): x + 0 = x and
+    // x + -inf = -inf, so the scores, the blocked positions and the all-blocked rows are the same,
+    // and the kernels read it once per key instead of once per (query, key).
+    const bool row_bcast = m->ndim < 2 || m->shape[m->ndim - 2] == 1;
+    if (want == GT_BOOL && cd != GT_F64 && row_bcast) {
+        const gt_tensor *dense = gt_is_dense(m) && m->offset == 0 ? m : tmp.keep(gt_to_device_dense(m, dev, GT_BOOL));
+        if (!dense) return false;
+        gt_tensor *bias = tmp.keep(gt_new_tensor(dense->ndim, dense->shape, GT_F32, GT_DEV_CUDA, dev));
+        if (!bias) return false;
+        if (!gt_hip_check(gt_launch_bool_to_bias(gt_data(dense), (float *)gt_data(bias), dense->numel, gt_stream()),
+                          "flash_attention: mask conversion"))
+            return false;
+        m = bias;
+    }
     int64_t st[4] = {0, 0, 0, 0}, sh[4] = {1, 1, 1, 1};
     for (int i = 0; i < m->ndim; ++i) {
         sh[4 - m->ndim + i] = m->shape[i];
@@ -118,7 +133,7 @@ bool stage_mask(const gt_tensor *mask, int dev, int cd, AttnFwdArgs &a, Temps &t
     }
     for (int i = 0; i < 4; ++i) if (sh[i] == 1) st[i] = 0;
     a.mask = gt_data(m);
-    a.mask_bool = want == GT_BOOL;
+    a.mask_bool = m->dtype == GT_BOOL;
     a.m_sb = st[0];
     a.m_sh = st[1];
     a.m_sl = st[2];

@@ -205,6 +205,13 @@ __global__ void q8_0_dequantize_kernel(const uint8_t *__restrict__ in, void *__r
     }
 }
 
+// Bool mask bytes -> additive float mask: 0 (attend) or -inf (blocked).
+__global__ void bool_to_bias_kernel(const uint8_t *__restrict__ src, float *__restrict__ dst, int64_t n) {
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
+        dst[i] = src[i] ? 0.0f : -INFINITY;
+}
+
 inline unsigned grid_for(int64_t n, int block) {
     const int64_t g = (n + block - 1) / block;
     return (unsigned)(g < 65536 * 16 ? (g > 0 ? g : 1) : 65536 * 16);
@@ -234,5 +241,11 @@ hipError_t gt_launch_q8_0_dequantize(const void *src, void *dst, int dst_dtype, 
     const int64_t waves = (nblocks + 1) / 2;
     hipLaunchKernelGGL(q8_0_dequantize_kernel, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, stream,
                        (const uint8_t *)src, dst, dst_dtype, nblocks);
+    return hipGetLastError();
+}
+
+hipError_t gt_launch_bool_to_bias(const void *src, float *dst, int64_t n, hipStream_t stream) {
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(bool_to_bias_kernel, dim3(grid_for(n, 256)), dim3(256), 0, stream, (const uint8_t *)src, dst, n);
     return hipGetLastError();
 }

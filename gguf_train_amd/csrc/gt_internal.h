@@ -100,6 +100,8 @@ struct gt_layout {
 // supported dtype): dst[dst_layout(i)] = convert(src[src_layout(i)]) for i < numel.
 hipError_t gt_launch_convert(const void *src, int src_dtype, const gt_layout &src_layout, void *dst, int dst_dtype,
                              const gt_layout &dst_layout, int64_t numel, hipStream_t stream);
+// Dense bool bytes -> dense float additive mask (0 where true, -inf where false).
+hipError_t gt_launch_bool_to_bias(const void *src, float *dst, int64_t n, hipStream_t stream);
 // Q8_0 (ggml block_q8_0) quantize `nrows` rows of `row_len` floats (row_len % 32 == 0).
 hipError_t gt_launch_q8_0_quantize(const float *src, void *dst, int64_t nblocks, hipStream_t stream);
 // Q8_0 dequantize into `dst_dtype` (f32/f16/bf16/f64).
