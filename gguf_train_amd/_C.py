@@ -135,6 +135,27 @@ def _configure(lib: ctypes.CDLL) -> ctypes.CDLL:
     lib.gt_dequantize.argtypes = [c_void_p, c_int]
     lib.gt_dequantize.restype = c_void_p
 
+    # KV cache (no counterpart in the reference ABI; behaviour of LlamaContext's cache,
+    # csrc/llama_bridge.cpp:245-296)
+    lib.gt_kv_cache_create.argtypes = [c_int64, c_int64, c_int64, c_int64, c_int, c_int]
+    lib.gt_kv_cache_create.restype = c_void_p
+    lib.gt_kv_cache_free.argtypes = [c_void_p]
+    lib.gt_kv_cache_free.restype = None
+    lib.gt_kv_cache_clear.argtypes = [c_void_p, c_int64]
+    lib.gt_kv_cache_clear.restype = c_int
+    lib.gt_kv_cache_length.argtypes = [c_void_p, c_int64]
+    lib.gt_kv_cache_length.restype = c_int64
+    lib.gt_kv_cache_capacity.argtypes = [c_void_p]
+    lib.gt_kv_cache_capacity.restype = c_int64
+    lib.gt_kv_cache_keys.argtypes = [c_void_p]
+    lib.gt_kv_cache_keys.restype = c_void_p
+    lib.gt_kv_cache_values.argtypes = [c_void_p]
+    lib.gt_kv_cache_values.restype = c_void_p
+    lib.gt_kv_cache_append.argtypes = [c_void_p, c_void_p, c_void_p, c_int64]
+    lib.gt_kv_cache_append.restype = c_int
+    lib.gt_kv_cache_attention.argtypes = [c_void_p, c_void_p, c_float, c_int]
+    lib.gt_kv_cache_attention.restype = c_void_p
+
     lib.gt_init()
     return lib
 

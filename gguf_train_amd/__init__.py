@@ -12,6 +12,7 @@ from ._functions import FlashAttentionFn
 from ._ops import (dequantize, flash_attention, flash_attention_backward, flash_attention_lse, flash_attention_train,
                    quantize)
 from . import nn
+from .kv_cache import KVCache
 
 __all__ = [
     "_C",
@@ -24,4 +25,5 @@ __all__ = [
     "quantize",
     "dequantize",
     "nn",
+    "KVCache",
 ]

@@ -34,7 +34,20 @@ struct AttnFwdArgs {
     int causal;
     int mask_bool;
     int out_dtype;  // gt_dtype of o
+    // Per-sequence key lengths and query positions (a KV cache; both null for the reference
+    // operator): key s of batch b is present when s < kv_len[b], and the causal test is
+    // s <= q_pos[b] + l (null: s < S, and q_pos = 0, the reference's top-left alignment).
+    const int32_t *kv_len;
+    const int32_t *q_pos;
 };
+
+__device__ inline int attn_kv_len(const AttnFwdArgs &a, int64_t b) { return a.kv_len ? a.kv_len[b] : (int)a.S; }
+__device__ inline int attn_q_pos(const AttnFwdArgs &a, int64_t b) { return a.q_pos ? a.q_pos[b] : 0; }
+// Keys [0, end) are visible to a single query row (L == 1) of batch b.
+__device__ inline int attn_decode_end(const AttnFwdArgs &a, int64_t b) {
+    const int n = attn_kv_len(a, b);
+    return a.causal ? min(n, attn_q_pos(a, b) + 1) : n;
+}
 
 struct AttnBwdArgs {
     AttnFwdArgs f;         // q/k/v/mask/o/lse as in the forward (o and lse are inputs here)

@@ -70,7 +70,7 @@ __device__ inline float wave_sum(float v) {
 
 // Score of key `key` for query head `h` after scale and mask, in the log2 domain.
 __device__ inline float finish_score(const AttnFwdArgs &f, float dot, int64_t b, int64_t h, int64_t key) {
-    if (key >= f.S || (f.causal && key > 0)) return -INFINITY;
+    if (key >= attn_decode_end(f, b)) return -INFINITY;
     float s = dot * (f.scale * kLog2e);
     if (f.mask) {
         const int64_t mi = b * f.m_sb + h * f.m_sh + key * f.m_ss;
@@ -143,7 +143,7 @@ __global__ __launch_bounds__(256, 2) void decode_stream_kernel(DecodeArgs a) {
     const int64_t bk = blockIdx.y, b = bk / f.Hkv, hk = bk % f.Hkv;
     const int S = (int)f.S;
     const int span = ((S + kStep - 1) / kStep + a.nsplit - 1) / a.nsplit * kStep;  // keys per split
-    const int kbeg = split * span, kend = min(S, kbeg + span);
+    const int kbeg = split * span, kend = min(attn_decode_end(f, b), kbeg + span);
     const int nsteps = kend > kbeg ? (kend - kbeg + kStep - 1) / kStep : 0;
 
     // B operand (Q^T): lane holds Q[head l16][32t + 8 q4 + 0..7]; columns l16 >= G repeat head
@@ -202,7 +202,7 @@ __global__ __launch_bounds__(256, 2) void decode_stream_kernel(DecodeArgs a) {
             for (int i = 0; i < 4; ++i) {
                 const int key = k0 + 16 * kb + 4 * q4 + i;
                 float x = c4[i] * cs;
-                bool blocked = key >= kend || (f.causal && key > 0) || l16 >= G;
+                bool blocked = key >= kend || l16 >= G;
                 if (MASK != 0) {
                     const int64_t mi = mrow + (int64_t)min(key, S - 1) * f.m_ss;
                     if (MASK == 1) blocked = blocked || !((const uint8_t *)f.mask)[mi];

@@ -102,7 +102,7 @@ __global__ __launch_bounds__(256, 2) void decode_q8_stream_kernel(DecodeArgs a) 
     const int64_t bk = blockIdx.y, b = bk / f.Hkv, hk = bk % f.Hkv;
     const int S = (int)f.S;
     const int span = ((S + kStep - 1) / kStep + a.nsplit - 1) / a.nsplit * kStep;
-    const int kbeg = split * span, kend = min(S, kbeg + span);
+    const int kbeg = split * span, kend = min(attn_decode_end(f, b), kbeg + span);
     const int nsteps = kend > kbeg ? (kend - kbeg + kStep - 1) / kStep : 0;
 
     // B operand (Q^T, fp16): lane holds Q[head l16][32t + 8 q4 + 0..7]; columns l16 >= G repeat
@@ -206,7 +206,7 @@ __global__ __launch_bounds__(256, 2) void decode_q8_stream_kernel(DecodeArgs a) 
             for (int i = 0; i < 4; ++i) {
                 const int key = k0 + 16 * kb + 4 * q4 + i;
                 float x = sum4[i] * cs;
-                bool blocked = key >= kend || (f.causal && key > 0) || l16 >= G;
+                bool blocked = key >= kend || l16 >= G;
                 if (MASK != 0) {
                     const int64_t mi = mrow + (int64_t)min(key, S - 1) * f.m_ss;
                     if (MASK == 1) blocked = blocked || !((const uint8_t *)f.mask)[mi];

@@ -76,7 +76,7 @@ __device__ inline void store_out(void *o, int dtype, int64_t i, A v) {
 template <typename T, typename A>
 __device__ inline A score_of(const AttnFwdArgs &a, const T *qr, const T *kb, int64_t b, int64_t h, int64_t l,
                              int64_t s) {
-    if (a.causal && s > l) return neg_inf<A>();
+    if (s >= attn_kv_len(a, b) || (a.causal && s > l + attn_q_pos(a, b))) return neg_inf<A>();
     const T *kr = kb + s * a.k_ss;
     A dot = 0;
     for (int64_t d = 0; d < a.D; ++d) dot += to_acc(qr[d], A()) * to_acc(kr[d], A());

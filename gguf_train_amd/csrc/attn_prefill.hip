@@ -105,11 +105,12 @@ __device__ inline float max3(float a, float b, float c) {
     return r;
 }
 
-// Keys covered by query tile qt: all of them, or up to the tile's last row (causal, top-left).
+// Keys covered by query tile qt: the sequence's keys, or (causal) up to the tile's last row,
+// whose position is qpos + qt*BM + BM-1.
 template <bool CAUSAL>
-__device__ inline int key_tiles(int qt, int S) {
-    const int kv_end = CAUSAL ? min(qt * BM + BM, S) : S;
-    return (kv_end + BN - 1) / BN;
+__device__ inline int key_tiles(int qt, int nkv, int qpos) {
+    const int kv_end = CAUSAL ? min(qt * BM + BM + qpos, nkv) : nkv;
+    return kv_end > 0 ? (kv_end + BN - 1) / BN : 0;
 }
 
 // MASK: 0 = none, 1 = bool bytes, 2 = additive float, 4 = additive float that does not depend
@@ -150,10 +151,13 @@ __global__ __launch_bounds__(64 * NW, 1) void prefill_fwd_kernel(AttnFwdArgs a, 
     }
     const int64_t b = bh / a.H, h = bh % a.H, hk = h / (a.H / a.Hkv);
     const int L = (int)a.L, S = (int)a.S;
+    // keys present for this sequence and the position of its query row 0 (KV cache; the
+    // reference operator: S and 0)
+    const int nkv = attn_kv_len(a, b), qpos = attn_q_pos(a, b);
     const int qa = nq - 1 - pair, qb = pair;  // the heavier tile first
     const int nparts = qa == qb ? 1 : 2;
-    const int na = key_tiles<CAUSAL>(qa, S);
-    const int total = na + (nparts == 2 ? key_tiles<CAUSAL>(qb, S) : 0);
+    const int na = key_tiles<CAUSAL>(qa, nkv, qpos);
+    const int total = na + (nparts == 2 ? key_tiles<CAUSAL>(qb, nkv, qpos) : 0);
 
     const T *kbase = (const T *)a.k + b * a.k_sb + hk * a.k_sh;
     const T *vbase = (const T *)a.v + b * a.v_sb + hk * a.v_sh;
@@ -291,7 +295,7 @@ __global__ __launch_bounds__(64 * NW, 1) void prefill_fwd_kernel(AttnFwdArgs a, 
             }
 
             // ---- masks: s[kb][i] is (key = k0 + 32kb + 8(i/4) + 4half + i%4, query = lq) ----
-            const bool edge = k0 + BN > S || (CAUSAL && k0 + BN - 1 > wq0);
+            const bool edge = k0 + BN > nkv || (CAUSAL && k0 + BN - 1 > wq0 + qpos);
             if (MASK != 0 || edge) {
                 f32x4 mv[2][4];  // MROW: the mask values of this lane's keys, from LDS
                 if constexpr (MROW) {
@@ -317,7 +321,7 @@ __global__ __launch_bounds__(64 * NW, 1) void prefill_fwd_kernel(AttnFwdArgs a, 
                                 x = fmaf(((const float *)a.mask)[mi], 1.0f / a.scale, x);
                             }
                         }
-                        const bool blocked = key >= S || (CAUSAL && key > lq);
+                        const bool blocked = key >= nkv || (CAUSAL && key > lq + qpos);
                         s[kb][i] = blocked ? -INFINITY : x;
                     }
                 }

@@ -8,6 +8,7 @@
 #include "attn_common.h"
 #include "gt_internal.h"
 
+#include <algorithm>
 #include <cmath>
 #include <string>
 #include <vector>
@@ -209,7 +210,8 @@ gt_tensor *deliver(gt_tensor *dev_t, bool to_host) {
 // Single-query attention straight from Q8_0 K/V blocks.  Returns 1 when it ran, 0 when the
 // shapes do not suit the kernel (the caller then dequantizes), -1 on error.
 int run_q8_decode(const gt_tensor *q, const gt_tensor *k, const gt_tensor *v, const gt_tensor *mask, float scale,
-                  int is_causal, int dev, gt_tensor *o, gt_tensor *lse, Temps &tmp) {
+                  int is_causal, int dev, gt_tensor *o, gt_tensor *lse, Temps &tmp, const int32_t *kv_len = nullptr,
+                  const int32_t *q_pos = nullptr) {
     const gt_tensor *qs = stage(q, dev, GT_F16, tmp);
     const gt_tensor *ks = k->device_type == GT_DEV_CUDA && k->device_index == dev ? k : tmp.keep(gt_to_device_dense(k, dev, -1));
     const gt_tensor *vs = v->device_type == GT_DEV_CUDA && v->device_index == dev ? v : tmp.keep(gt_to_device_dense(v, dev, -1));
@@ -221,6 +223,8 @@ int run_q8_decode(const gt_tensor *q, const gt_tensor *k, const gt_tensor *v, co
     a.scale = scale;
     a.causal = is_causal ? 1 : 0;
     a.out_dtype = GT_F16;
+    a.kv_len = kv_len;
+    a.q_pos = q_pos;
     if (!attn_decode_q8_supported(a, GT_F16)) return 0;
     if (!stage_mask(mask, dev, GT_F16, a, tmp)) return -1;
     DecodeArgs da{};
@@ -510,4 +514,291 @@ extern "C" gt_tensor *gt_dequantize(const gt_tensor *t, int out_dtype) {
         return nullptr;
     }
     return deliver(out, t->device_type != GT_DEV_CUDA);
+}
+
+// ---- KV cache --------------------------------------------------------------------------------
+// The per-sequence K/V store of a decoding loop.  In the reference it is llama.cpp's cache
+// behind LlamaContext.forward_logits (csrc/llama_bridge.cpp:245-296, gguf_train/llama/__init__.py:
+// 174-190): tokens are appended at the positions that continue what a sequence holds
+// (pos_offset), the context has a fixed capacity (n_ctx), clear_kv() empties it, and a query
+// attends to its own position and everything before it.  Here the cache lives in HBM as dense
+// (B, Hkv, capacity, D) tensors, float16/bfloat16/float32 or GGUF Q8_0 (quantized on append
+// with the same steps as gt_quantize), with per-sequence lengths; attention over it runs the
+// same kernels as gt_flash_attention, given each sequence's length and query position.
+
+struct gt_kv_cache {
+    int64_t B = 0, Hkv = 0, cap = 0, D = 0;
+    int dtype = GT_F16;
+    int dev = 0;
+    gt_tensor *k = nullptr, *v = nullptr;  // (B, Hkv, cap, D), zero-filled at creation
+    std::vector<int32_t> len;              // tokens held per sequence (the authoritative copy)
+    gt_tensor *len_dev = nullptr;          // device copy of len (int32, B)
+    gt_tensor *pos_dev = nullptr;          // position of query row 0 per sequence (int32, B)
+};
+
+namespace {
+
+bool kv_upload(gt_tensor *dst, const std::vector<int32_t> &src) {
+    // pageable source: returns once the bytes are staged, so `src` may change afterwards
+    return gt_hip_check(hipMemcpyAsync(gt_data(dst), src.data(), src.size() * sizeof(int32_t), hipMemcpyHostToDevice,
+                                       gt_stream()),
+                        "kv cache: length upload");
+}
+
+bool kv_zero(gt_tensor *t) {
+    return gt_hip_check(hipMemsetAsync(gt_data(t), 0, gt_dtype_nbytes(t->dtype, t->numel), gt_stream()),
+                        "kv cache: zero fill");
+}
+
+bool kv_check_rows(const char *who, const gt_kv_cache *c, const gt_tensor *t, const char *name) {
+    if (!t || t->ndim != 4) {
+        gt_set_error(std::string(who) + ": " + name + " must be a 4-D tensor (B, Hkv, T, D)");
+        return false;
+    }
+    if (t->shape[0] != c->B || t->shape[1] != c->Hkv || t->shape[3] != c->D || t->shape[2] < 1) {
+        gt_set_error(std::string(who) + ": " + name + " of shape [" + std::to_string(t->shape[0]) + ", " +
+                     std::to_string(t->shape[1]) + ", " + std::to_string(t->shape[2]) + ", " +
+                     std::to_string(t->shape[3]) + "] does not match the cache [" + std::to_string(c->B) + ", " +
+                     std::to_string(c->Hkv) + ", T, " + std::to_string(c->D) + "]");
+        return false;
+    }
+    if (!gt_is_float(t->dtype)) {
+        gt_set_error(std::string(who) + ": " + name + " must be float32, float16, bfloat16 or float64, got " +
+                     gt_dtype_name(t->dtype));
+        return false;
+    }
+    return true;
+}
+
+}  // namespace
+
+extern "C" gt_kv_cache *gt_kv_cache_create(int64_t batch, int64_t n_head_kv, int64_t capacity, int64_t head_dim,
+                                           int dtype, int device_index) {
+    gt_init();
+    if (batch < 1 || n_head_kv < 1 || capacity < 1 || head_dim < 1) {
+        gt_set_error("kv_cache_create: batch, n_head_kv, capacity and head_dim must be positive");
+        return nullptr;
+    }
+    if (dtype != GT_F32 && dtype != GT_F16 && dtype != GT_BF16 && dtype != GT_Q8_0) {
+        gt_set_error(std::string("kv_cache_create: dtype must be float32, float16, bfloat16 or q8_0, got ") +
+                     gt_dtype_name(dtype));
+        return nullptr;
+    }
+    if (dtype == GT_Q8_0 && head_dim % 32 != 0) {
+        gt_set_error("kv_cache_create: a q8_0 cache needs a head_dim that is a multiple of 32, got " +
+                     std::to_string(head_dim));
+        return nullptr;
+    }
+    if (capacity >= (1LL << 30)) {
+        gt_set_error("kv_cache_create: capacity must be below 2^30");
+        return nullptr;
+    }
+    if (!gt_device_ok(device_index)) return nullptr;
+    auto *c = new gt_kv_cache();
+    c->B = batch;
+    c->Hkv = n_head_kv;
+    c->cap = capacity;
+    c->D = head_dim;
+    c->dtype = dtype;
+    c->dev = device_index;
+    c->len.assign((size_t)batch, 0);
+    const int64_t sh[4] = {batch, n_head_kv, capacity, head_dim}, lsh[1] = {batch};
+    c->k = gt_new_tensor(4, sh, dtype, GT_DEV_CUDA, device_index);
+    c->v = c->k ? gt_new_tensor(4, sh, dtype, GT_DEV_CUDA, device_index) : nullptr;
+    c->len_dev = c->v ? gt_new_tensor(1, lsh, GT_I32, GT_DEV_CUDA, device_index) : nullptr;
+    c->pos_dev = c->len_dev ? gt_new_tensor(1, lsh, GT_I32, GT_DEV_CUDA, device_index) : nullptr;
+    // rows past a sequence's length are read (and weighted 0) by the kernels: keep them finite
+    if (!c->pos_dev || !kv_zero(c->k) || !kv_zero(c->v) || !kv_upload(c->len_dev, c->len) ||
+        !kv_upload(c->pos_dev, c->len)) {
+        gt_kv_cache_free(c);
+        return nullptr;
+    }
+    return c;
+}
+
+extern "C" void gt_kv_cache_free(gt_kv_cache *c) {
+    if (!c) return;
+    gt_tensor_free(c->k);
+    gt_tensor_free(c->v);
+    gt_tensor_free(c->len_dev);
+    gt_tensor_free(c->pos_dev);
+    delete c;
+}
+
+extern "C" int gt_kv_cache_clear(gt_kv_cache *c, int64_t seq) {
+    if (!c) {
+        gt_set_error("kv_cache_clear: NULL cache");
+        return -1;
+    }
+    if (seq >= c->B) {
+        gt_set_error("kv_cache_clear: sequence " + std::to_string(seq) + " out of range for " + std::to_string(c->B) +
+                     " sequences");
+        return -1;
+    }
+    if (seq < 0) std::fill(c->len.begin(), c->len.end(), 0);
+    else c->len[(size_t)seq] = 0;
+    return kv_upload(c->len_dev, c->len) ? 0 : -1;
+}
+
+extern "C" int64_t gt_kv_cache_length(const gt_kv_cache *c, int64_t seq) {
+    if (!c || seq < 0 || seq >= c->B) {
+        gt_set_error("kv_cache_length: invalid cache or sequence");
+        return -1;
+    }
+    return c->len[(size_t)seq];
+}
+
+extern "C" int64_t gt_kv_cache_capacity(const gt_kv_cache *c) { return c ? c->cap : -1; }
+
+extern "C" gt_tensor *gt_kv_cache_keys(const gt_kv_cache *c) {
+    if (!c) {
+        gt_set_error("kv_cache_keys: NULL cache");
+        return nullptr;
+    }
+    auto *t = new gt_tensor(*c->k);  // shares the storage
+    return t;
+}
+
+extern "C" gt_tensor *gt_kv_cache_values(const gt_kv_cache *c) {
+    if (!c) {
+        gt_set_error("kv_cache_values: NULL cache");
+        return nullptr;
+    }
+    auto *t = new gt_tensor(*c->v);
+    return t;
+}
+
+extern "C" int gt_kv_cache_append(gt_kv_cache *c, const gt_tensor *k, const gt_tensor *v, int64_t pos_offset) {
+    const char *who = "kv_cache_append";
+    if (!c) {
+        gt_set_error("kv_cache_append: NULL cache");
+        return -1;
+    }
+    if (!kv_check_rows(who, c, k, "k") || !kv_check_rows(who, c, v, "v")) return -1;
+    const int64_t T = k->shape[2];
+    if (v->shape[2] != T) {
+        gt_set_error("kv_cache_append: k and v hold different numbers of tokens (" + std::to_string(T) + " and " +
+                     std::to_string(v->shape[2]) + ")");
+        return -1;
+    }
+    for (int64_t b = 0; b < c->B; ++b) {
+        const int64_t n = c->len[(size_t)b];
+        const int64_t p0 = pos_offset < 0 ? n : pos_offset;
+        if (pos_offset >= 0 && pos_offset != n) {
+            gt_set_error("kv_cache_append: positions " + std::to_string(p0) + ".." + std::to_string(p0 + T - 1) +
+                         " do not continue what sequence " + std::to_string(b) + " holds (" + std::to_string(n) +
+                         " tokens; see kv_cache_clear)");
+            return -1;
+        }
+        if (p0 + T > c->cap) {
+            gt_set_error("kv_cache_append: positions " + std::to_string(p0) + ".." + std::to_string(p0 + T - 1) +
+                         " of sequence " + std::to_string(b) + " do not fit the cache (capacity = " +
+                         std::to_string(c->cap) + ")");
+            return -1;
+        }
+    }
+    if (!gt_device_ok(c->dev)) return -1;
+    Temps tmp;
+    for (const gt_tensor *src : {k, v}) {
+        const gt_tensor *s = src->device_type == GT_DEV_CUDA && src->device_index == c->dev
+                                 ? src
+                                 : tmp.keep(gt_to_device_dense(src, c->dev, -1));
+        if (!s) return -1;
+        gt_tensor *dst = src == k ? c->k : c->v;
+        // the rows go to each sequence's current length (len_dev), before it is advanced
+        if (!gt_hip_check(gt_launch_kv_append(gt_data(s), s->dtype, s->strides, gt_data(dst), c->dtype,
+                                              (const int32_t *)gt_data(c->len_dev), c->B, c->Hkv, T, c->D, c->cap,
+                                              gt_stream()),
+                          "kv cache append kernel"))
+            return -1;
+    }
+    for (auto &n : c->len) n += (int32_t)T;
+    return kv_upload(c->len_dev, c->len) ? 0 : -1;
+}
+
+extern "C" gt_tensor *gt_kv_cache_attention(gt_kv_cache *c, const gt_tensor *q, float scale, int is_causal) {
+    if (!c) {
+        gt_set_error("kv_cache_attention: NULL cache");
+        return nullptr;
+    }
+    if (!q || q->ndim != 4 || q->shape[0] != c->B || q->shape[3] != c->D || q->shape[1] < 1 ||
+        q->shape[1] % c->Hkv != 0) {
+        gt_set_error("kv_cache_attention: q must be (B, H, L, D) with B = " + std::to_string(c->B) + ", D = " +
+                     std::to_string(c->D) + " and H a multiple of " + std::to_string(c->Hkv));
+        return nullptr;
+    }
+    if (!gt_is_float(q->dtype)) {
+        gt_set_error(std::string("kv_cache_attention: q must be a float tensor, got ") + gt_dtype_name(q->dtype));
+        return nullptr;
+    }
+    const int64_t B = c->B, H = q->shape[1], L = q->shape[2], D = c->D;
+    // query row l of sequence b is token len[b] - L + l
+    std::vector<int32_t> pos((size_t)B);
+    int64_t maxlen = 0;
+    for (int64_t b = 0; b < B; ++b) {
+        const int64_t n = c->len[(size_t)b];
+        if (n < L) {
+            gt_set_error("kv_cache_attention: sequence " + std::to_string(b) + " holds " + std::to_string(n) +
+                         " tokens, fewer than the " + std::to_string(L) + " query rows (append them first)");
+            return nullptr;
+        }
+        pos[(size_t)b] = (int32_t)(n - L);
+        maxlen = std::max<int64_t>(maxlen, n);
+    }
+    if (scale <= 0.0f) scale = 1.0f / std::sqrt((float)D);
+    const int dev = c->dev;
+    if (!gt_device_ok(dev) || !kv_upload(c->pos_dev, pos)) return nullptr;
+    const int32_t *kv_len = (const int32_t *)gt_data(c->len_dev), *q_pos = (const int32_t *)gt_data(c->pos_dev);
+    const bool host_io = q->device_type != GT_DEV_CUDA;
+    const int64_t osh[4] = {B, H, L, D};
+    gt_tensor *o = gt_new_tensor(4, osh, q->dtype, GT_DEV_CUDA, dev);
+    if (!o) return nullptr;
+    Temps tmp;
+    bool ok = true;
+    int q8 = 0;
+    if (o->numel > 0 && c->dtype == GT_Q8_0 && q->dtype == GT_F16 && L == 1) {
+        q8 = run_q8_decode(q, c->k, c->v, nullptr, scale, is_causal, dev, o, nullptr, tmp, kv_len, q_pos);
+        ok = q8 >= 0;
+    }
+    if (ok && q8 == 0 && o->numel > 0) {
+        // the float cache is read in place through a view of its first maxlen rows; a Q8_0
+        // cache is dequantized to float32 (exact values) first
+        const gt_tensor *kc = c->k, *vc = c->v;
+        if (c->dtype == GT_Q8_0) {
+            const int kd = q->dtype == GT_F64 ? GT_F64 : GT_F32;  // exact, as gt_flash_attention does
+            kc = tmp.keep(gt_dequantize(c->k, kd));
+            vc = kc ? tmp.keep(gt_dequantize(c->v, kd)) : nullptr;
+        }
+        const gt_tensor *kv_views[2] = {nullptr, nullptr};
+        if (kc && vc) {
+            const int64_t vsh[4] = {B, c->Hkv, maxlen, D};
+            for (int i = 0; i < 2; ++i) {
+                const gt_tensor *base = i == 0 ? kc : vc;
+                kv_views[i] = tmp.keep(gt_tensor_view(base, 4, vsh, base->strides, base->offset));
+            }
+        }
+        const gt_tensor *kv = kv_views[0], *vv = kv_views[1];
+        ok = kv && vv;
+        const int cd = ok ? compute_dtype(q, kv, vv) : GT_F32;
+        const gt_tensor *qs = ok ? stage(q, dev, cd, tmp) : nullptr;
+        const gt_tensor *ks = ok ? stage(kv, dev, cd, tmp) : nullptr;
+        const gt_tensor *vs = ok ? stage(vv, dev, cd, tmp) : nullptr;
+        ok = qs && ks && vs;
+        if (ok) {
+            AttnFwdArgs a{};
+            fill_qkv(a, qs, ks, vs);
+            a.o = gt_data(o);
+            a.scale = scale;
+            a.causal = is_causal ? 1 : 0;
+            a.out_dtype = q->dtype;
+            a.kv_len = kv_len;
+            a.q_pos = q_pos;
+            ok = dispatch_forward(a, cd, dev);
+        }
+    }
+    if (!ok) {
+        gt_tensor_free(o);
+        return nullptr;
+    }
+    return deliver(o, host_io);
 }

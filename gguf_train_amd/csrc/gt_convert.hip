@@ -161,6 +161,25 @@ __global__ void convert_kernel(const void *__restrict__ src, int sdt, gt_layout 
     }
 }
 
+// One Q8_0 block, one lane per value: value j (= lane % 32) of the block at `b`, quantized
+// with the other 31 lanes of its wave half.  Every lane of the wave calls it (the max is a
+// cross-lane exchange); `live` lanes write.
+__device__ inline void q8_0_quantize_lane(float v, bool live, uint8_t *b, int j) {
+    float amax = fabsf(v);
+    // max over the 32 lanes of this half (xor offsets < 32 stay inside the half)
+    for (int off = 16; off >= 1; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+    const float d = __fdiv_rn(amax, 127.0f);
+    const float id = d != 0.0f ? __fdiv_rn(1.0f, d) : 0.0f;
+    if (!live) return;
+    const float x0 = v * id;
+    b[2 + j] = (uint8_t)(int8_t)roundf(x0);
+    if (j == 0) {
+        const uint16_t h = d_f32_to_f16(d);
+        b[0] = (uint8_t)(h & 0xff);
+        b[1] = (uint8_t)(h >> 8);
+    }
+}
+
 // 64 lanes = two blocks of 32 values; lane j of a half handles value j of its block.
 __global__ void q8_0_quantize_kernel(const float *__restrict__ x, uint8_t *__restrict__ out, int64_t nblocks) {
     const int lane = threadIdx.x & 63;
@@ -169,19 +188,26 @@ __global__ void q8_0_quantize_kernel(const float *__restrict__ x, uint8_t *__res
     const int j = lane & 31;
     const bool live = blk < nblocks;
     const float v = live ? x[blk * 32 + j] : 0.0f;
-    float amax = fabsf(v);
-    // max over the 32 lanes of this half (xor offsets < 32 stay inside the half)
-    for (int off = 16; off >= 1; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
-    const float d = __fdiv_rn(amax, 127.0f);
-    const float id = d != 0.0f ? __fdiv_rn(1.0f, d) : 0.0f;
-    if (!live) return;
-    uint8_t *b = out + blk * 34;
-    const float x0 = v * id;
-    b[2 + j] = (uint8_t)(int8_t)roundf(x0);
-    if (j == 0) {
-        const uint16_t h = d_f32_to_f16(d);
-        b[0] = (uint8_t)(h & 0xff);
-        b[1] = (uint8_t)(h >> 8);
+    q8_0_quantize_lane(v, live, out + (live ? blk : 0) * 34, j);
+}
+
+// KV-cache append: row (b, h, t) of src (B, Hkv, T, D), any strides, goes to row pos[b] + t of
+// the cache (B, Hkv, cap, D).  A float cache receives converted elements (one thread each); a
+// Q8_0 cache receives the row quantized block by block (two blocks per wave, as above).
+__global__ void kv_append_kernel(const void *__restrict__ src, int sdt, int64_t s_sb, int64_t s_sh, int64_t s_st,
+                                 int64_t s_sd, void *__restrict__ dst, int ddt, const int32_t *__restrict__ pos,
+                                 int64_t Hkv, int64_t T, int64_t D, int64_t cap, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;  // value index (b, h, t, d)
+    const bool live = i < n;
+    const int64_t ic = live ? i : 0;
+    const int64_t d = ic % D, t = (ic / D) % T, h = (ic / (D * T)) % Hkv, b = ic / (D * T * Hkv);
+    const double x = read_elem(src, sdt, b * s_sb + h * s_sh + t * s_st + d * s_sd);
+    const int64_t row = (b * Hkv + h) * cap + pos[b] + t;
+    if (ddt == GT_Q8_0) {
+        // D % 32 == 0 and n % 32 == 0, so a wave half is one whole block of one row
+        q8_0_quantize_lane((float)x, live, (uint8_t *)dst + (row * (D / 32) + d / 32) * 34, (int)(d % 32));
+    } else if (live) {
+        write_elem(dst, ddt, row * D + d, x);
     }
 }
 
@@ -247,5 +273,17 @@ hipError_t gt_launch_q8_0_dequantize(const void *src, void *dst, int dst_dtype, 
 hipError_t gt_launch_bool_to_bias(const void *src, float *dst, int64_t n, hipStream_t stream) {
     if (n <= 0) return hipSuccess;
     hipLaunchKernelGGL(bool_to_bias_kernel, dim3(grid_for(n, 256)), dim3(256), 0, stream, (const uint8_t *)src, dst, n);
+    return hipGetLastError();
+}
+
+hipError_t gt_launch_kv_append(const void *src, int src_dtype, const int64_t *src_strides, void *dst, int dst_dtype,
+                               const int32_t *pos, int64_t B, int64_t Hkv, int64_t T, int64_t D, int64_t cap,
+                               hipStream_t stream) {
+    const int64_t n = B * Hkv * T * D;
+    if (n <= 0) return hipSuccess;
+    const int64_t blocks = (n + 255) / 256;
+    if (blocks > 0x7fffffffLL) return hipErrorInvalidConfiguration;
+    hipLaunchKernelGGL(kv_append_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, src, src_dtype, src_strides[0],
+                       src_strides[1], src_strides[2], src_strides[3], dst, dst_dtype, pos, Hkv, T, D, cap, n);
     return hipGetLastError();
 }

@@ -100,6 +100,12 @@ struct gt_layout {
 // supported dtype): dst[dst_layout(i)] = convert(src[src_layout(i)]) for i < numel.
 hipError_t gt_launch_convert(const void *src, int src_dtype, const gt_layout &src_layout, void *dst, int dst_dtype,
                              const gt_layout &dst_layout, int64_t numel, hipStream_t stream);
+// KV-cache append: rows (b, h, t) of the 4-D src (element strides src_strides) are written at
+// row pos[b] + t (pos: device int32 per batch) of the dense (B, Hkv, cap, D) cache of dtype
+// dst_dtype (float32/float16/bfloat16, or GT_Q8_0 quantized row by row; D % 32 == 0 then).
+hipError_t gt_launch_kv_append(const void *src, int src_dtype, const int64_t *src_strides, void *dst, int dst_dtype,
+                               const int32_t *pos, int64_t B, int64_t Hkv, int64_t T, int64_t D, int64_t cap,
+                               hipStream_t stream);
 // Dense bool bytes -> dense float additive mask (0 where true, -inf where false).
 hipError_t gt_launch_bool_to_bias(const void *src, float *dst, int64_t n, hipStream_t stream);
 // Q8_0 (ggml block_q8_0) quantize `nrows` rows of `row_len` floats (row_len % 32 == 0).

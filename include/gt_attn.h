@@ -185,6 +185,39 @@ GT_API gt_tensor *gt_quantize(const gt_tensor *t, int ggml_type_id);
 /* csrc/gguf_train.h:377: y = float(qs[j]) * float(d), then converted to out_dtype. */
 GT_API gt_tensor *gt_dequantize(const gt_tensor *t, int out_dtype);
 
+/* ---- KV cache ------------------------------------------------------------------------- */
+
+/* No counterpart in the reference ABI: the reference's decode cache is llama.cpp's, reached
+ * through LlamaContext (gt_llama_forward_logits, csrc/llama_bridge.cpp:245-296; clear_kv,
+ * gguf_train/llama/__init__.py:174-190).  This is the same behaviour for attention on the
+ * device: a cache of `batch` sequences with n_head_kv heads of head_dim values and room for
+ * `capacity` tokens each, stored as GT_F32, GT_F16, GT_BF16 or GT_Q8_0 (rows quantized on
+ * append exactly as gt_quantize does; head_dim % 32 == 0).  Returns NULL on failure. */
+typedef struct gt_kv_cache gt_kv_cache;
+GT_API gt_kv_cache *gt_kv_cache_create(int64_t batch, int64_t n_head_kv, int64_t capacity, int64_t head_dim,
+                                       int dtype, int device_index);
+GT_API void gt_kv_cache_free(gt_kv_cache *c);
+/* Empties sequence `seq`, or every sequence when seq < 0 (LlamaContext.clear_kv). */
+GT_API int gt_kv_cache_clear(gt_kv_cache *c, int64_t seq);
+/* Tokens held by sequence `seq` (-1 on error). */
+GT_API int64_t gt_kv_cache_length(const gt_kv_cache *c, int64_t seq);
+GT_API int64_t gt_kv_cache_capacity(const gt_kv_cache *c);
+/* New handles sharing the cache's K / V storage, (batch, n_head_kv, capacity, head_dim). */
+GT_API gt_tensor *gt_kv_cache_keys(const gt_kv_cache *c);
+GT_API gt_tensor *gt_kv_cache_values(const gt_kv_cache *c);
+/* Appends T tokens to every sequence: k, v (batch, n_head_kv, T, head_dim), any float dtype
+ * and strides, host or device.  pos_offset < 0 appends after what each sequence holds;
+ * otherwise it must equal every sequence's length (positions continue the cache, as
+ * gt_llama_forward_logits requires).  Fails without writing when a sequence would pass the
+ * capacity.  Returns 0 on success. */
+GT_API int gt_kv_cache_append(gt_kv_cache *c, const gt_tensor *k, const gt_tensor *v, int64_t pos_offset);
+/* Attention of q (batch, H, L, head_dim), H % n_head_kv == 0, over each sequence's cached
+ * tokens, query row l of sequence b being its token len_b - L + l (the last L appended).
+ * is_causal: a query attends to its own position and the ones before it; otherwise to every
+ * cached token.  scale <= 0 means 1/sqrt(head_dim).  Output (batch, H, L, head_dim), dtype
+ * and device of q. */
+GT_API gt_tensor *gt_kv_cache_attention(gt_kv_cache *c, const gt_tensor *q, float scale, int is_causal);
+
 #ifdef __cplusplus
 }
 #endif
