@@ -129,6 +129,9 @@ def _configure(lib: ctypes.CDLL) -> ctypes.CDLL:
                                                 c_void_p, c_float, c_int, p_vp, p_vp, p_vp]
     lib.gt_flash_attention_backward.restype = c_int
 
+    lib.gt_attention_weights.argtypes = [c_void_p, c_void_p, c_void_p, c_void_p, c_float, c_int, c_int]
+    lib.gt_attention_weights.restype = c_void_p
+
     # Q8_0 (csrc/gguf_train.h:376-377)
     lib.gt_quantize.argtypes = [c_void_p, c_int]
     lib.gt_quantize.restype = c_void_p

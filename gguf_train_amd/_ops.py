@@ -73,6 +73,17 @@ def flash_attention_backward(dout, q, k, v, mask, out, lse, scale: float, is_cau
             adopt(pv.value, "flash_attention_backward"))
 
 
+def attention_weights(q, k, mask, lse, scale: float = 0.0, is_causal: bool = False, average_heads: bool = False):
+    """gt_attention_weights: softmax(q.k^T*scale + mask) (causal-masked), recomputed from the
+    forward's log-sum-exp `lse`; (B,H,L,S), or (B,L,S) averaged over the heads."""
+    bind_stream(_device_of(q))
+    hq, hk, hl = borrow(q), borrow(k), borrow(lse)
+    hm = borrow(mask) if mask is not None else None
+    ptr = _C.lib.gt_attention_weights(hq.ptr, hk.ptr, hm.ptr if hm else None, hl.ptr, ctypes.c_float(scale),
+                                      1 if is_causal else 0, 1 if average_heads else 0)
+    return adopt(ptr, "attention_weights")
+
+
 def quantize(t: torch.Tensor, qtype: str = "q8_0") -> QuantizedTensor:
     """gt_quantize (csrc/gguf_train.h:376); rows of last-dim length, GGUF Q8_0 blocks."""
     if qtype != "q8_0":

@@ -83,5 +83,9 @@ int attn_decode_q8_splits(const AttnFwdArgs &f);
 hipError_t launch_attn_decode_q8(const DecodeArgs &a, hipStream_t s);
 hipError_t launch_attn_decode_merge(const DecodeArgs &a, int out_dtype, hipStream_t s);
 
+// Explicit attention weights from the forward's log-sum-exp: (B,H,L,S), or (B,L,S) averaged
+// over the heads, in f.out_dtype.
+hipError_t launch_attn_weights(const AttnFwdArgs &f, int cd, void *w, bool average, hipStream_t s);
+
 bool attn_bwd_mfma_supported(const AttnBwdArgs &a, int cd);
 hipError_t launch_attn_bwd_mfma(const AttnBwdArgs &a, int cd, hipStream_t s);

@@ -1,0 +1,213 @@
+// Explicit attention weights (MultiheadAttention with need_weights=True).
+//
+// The reference materialises them with ggml ops (gguf_train/nn/modules/transformer.py:153-166:
+// scores = q.k^T * scale (+ causal, + mask), weights = softmax(scores), optionally averaged over
+// the heads).  Here they are recomputed from the log-sum-exp of the fused forward, which has
+// already produced the attention output: P[l, s] = exp(scores[l, s] - lse[l]), written in the
+// dtype of q.  Causally excluded and masked-out positions get weight 0, a row with nothing to
+// attend to is all zeros (as the fused forward's output row).
+//
+// float16 / bfloat16, head size 64 or 128: S = Q.K^T on v_mfma_f32_32x32x16, a wavefront owns 32
+// query rows (Q in registers as the A operand) and walks the key tiles of 32; K rows are the B
+// operand straight from memory (each 16-byte piece feeds one MFMA).  The accumulator holds
+// S[query = 8(i/4) + 4half + i%4][key = lane % 32], so the 32 lanes of a half store 32
+// consecutive keys of one query row.  HBM-bound: the weights written dominate the traffic.
+// Averaged weights: a workgroup walks all H heads of its rows and writes the mean once.
+// Other dtypes / head sizes: one thread per (query, key) in the compute precision.
+
+#include "attn_common.h"
+#include "gt_internal.h"
+#include "mfma_util.h"
+
+#include <cmath>
+
+namespace {
+
+using namespace gtmfma;
+
+constexpr int WQ = 4;  // wavefronts per workgroup: 128 query rows
+
+template <typename T>
+__device__ inline void store1(void *o, int64_t i, float v) {
+    ((T *)o)[i] = (T)v;
+}
+
+template <int MASK>
+__device__ inline float mask_term(const AttnFwdArgs &f, int64_t b, int64_t h, int64_t q, int64_t s, bool &blocked) {
+    if (MASK == 0) return 0.0f;
+    const int64_t mi = b * f.m_sb + h * f.m_sh + q * f.m_sl + s * f.m_ss;
+    if (MASK == 1) {
+        blocked = blocked || !((const uint8_t *)f.mask)[mi];
+        return 0.0f;
+    }
+    return ((const float *)f.mask)[mi];
+}
+
+// grid: (row blocks of 128 queries) x (B*H, or B when averaging)
+template <typename T, int D, bool CAUSAL, int MASK, bool AVG>
+__global__ __launch_bounds__(64 * WQ) void attn_weights_kernel(AttnFwdArgs f, void *wout, int64_t nrb) {
+    using M = Mfma<T>;
+    using V8 = typename M::V8;
+    constexpr int DT = D / 16;
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int lrow = lane & 31, half = lane >> 5;
+    const int64_t rb = blockIdx.x % nrb, g = blockIdx.x / nrb;
+    const int64_t b = AVG ? g : g / f.H;
+    const int L = (int)f.L, S = (int)f.S;
+    const int q0 = (int)rb * 32 * WQ + 32 * w;  // first query row of this wavefront
+    const float c = f.scale * kLog2e;
+    const int nh = AVG ? (int)f.H : 1;
+    const float inv_h = 1.0f / (float)nh;
+    const int kv_end = CAUSAL ? min(q0 + 32, S) : S;  // keys any of the wave's rows can see
+    const int nkt = (S + 31) / 32;
+    // log2(e) * lse of this lane's 16 rows (one head: loaded once)
+    float lsv[16];
+    if (!AVG) {
+        const float *lse = (const float *)f.lse + g * f.L;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) lsv[i] = lse[min(q0 + 8 * (i / 4) + 4 * half + (i % 4), L - 1)] * kLog2e;
+    }
+    for (int kt = 0; kt < nkt; ++kt) {
+        const int k0 = kt * 32;
+        f32x16 acc;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc[i] = 0.0f;
+        if (k0 < kv_end) {
+            for (int hh = 0; hh < nh; ++hh) {
+                const int64_t h = AVG ? hh : g % f.H;
+                const int64_t hk = h / (f.H / f.Hkv);
+                // A = Q rows (query lrow of the wave, d = 16t + 8half + 0..7); B = K rows
+                const T *qr = (const T *)f.q + b * f.q_sb + h * f.q_sh + (int64_t)min(q0 + lrow, L - 1) * f.q_sl + 8 * half;
+                const T *kr = (const T *)f.k + b * f.k_sb + hk * f.k_sh + (int64_t)min(k0 + lrow, S - 1) * f.k_ss + 8 * half;
+                f32x16 s;
+#pragma unroll
+                for (int i = 0; i < 16; ++i) s[i] = 0.0f;
+#pragma unroll
+                for (int t = 0; t < DT; ++t) {
+                    const V8 qa = __builtin_bit_cast(V8, *(const u32x4 *)(qr + 16 * t));
+                    const V8 kb = __builtin_bit_cast(V8, *(const u32x4 *)(kr + 16 * t));
+                    s = M::mma(qa, kb, s);
+                }
+                // s[i]: query q0 + 8(i/4) + 4half + i%4, key k0 + lrow
+                const int key = k0 + lrow;
+                const float *lse = (const float *)f.lse + (b * f.H + h) * f.L;
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    const int q = q0 + 8 * (i / 4) + 4 * half + (i % 4);
+                    bool blocked = key >= S || q >= L || (CAUSAL && key > q);
+                    const float add = mask_term<MASK>(f, b, h, min(q, L - 1), min(key, S - 1), blocked);
+                    const float ls = AVG ? lse[min(q, L - 1)] * kLog2e : lsv[i];
+                    // lse = +inf (nothing visible): weight 0
+                    const float p = blocked ? 0.0f : exp2f(fmaf(s[i], c, add * kLog2e - ls));
+                    acc[i] += AVG ? p * inv_h : p;
+                }
+            }
+        }
+        // store: for fixed i, the 32 lanes of a half write 32 consecutive keys of one row
+        const int key = k0 + lrow;
+        if (key < S) {
+            const int64_t base = AVG ? b * f.L : g * f.L;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int q = q0 + 8 * (i / 4) + 4 * half + (i % 4);
+                if (q < L) store1<T>(wout, (base + q) * f.S + key, acc[i]);
+            }
+        }
+    }
+}
+
+// Generic: one thread per (query, key), any float dtype, accumulation in A (double for float64).
+template <typename T, typename A, bool AVG>
+__global__ __launch_bounds__(256) void attn_weights_generic_kernel(AttnFwdArgs f, void *wout) {
+    const int64_t nrow = AVG ? f.B * f.L : f.B * f.H * f.L;
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= nrow * f.S) return;
+    const int64_t s = i % f.S, r = i / f.S;
+    const int64_t l = r % f.L, g = r / f.L;
+    const int64_t b = AVG ? g : g / f.H;
+    const int nh = AVG ? (int)f.H : 1;
+    A sum = 0;
+    for (int hh = 0; hh < nh; ++hh) {
+        const int64_t h = AVG ? hh : g % f.H, hk = h / (f.H / f.Hkv);
+        if (s >= attn_kv_len(f, b) || (f.causal && s > l + attn_q_pos(f, b))) continue;
+        const T *qr = (const T *)f.q + b * f.q_sb + h * f.q_sh + l * f.q_sl;
+        const T *kr = (const T *)f.k + b * f.k_sb + hk * f.k_sh + s * f.k_ss;
+        A dot = 0;
+        for (int64_t d = 0; d < f.D; ++d) dot += (A)(float)qr[d] * (A)(float)kr[d];
+        A x = dot * (A)f.scale;
+        if (f.mask) {
+            const int64_t mi = b * f.m_sb + h * f.m_sh + l * f.m_sl + s * f.m_ss;
+            if (f.mask_bool) {
+                if (!((const uint8_t *)f.mask)[mi]) continue;
+            } else {
+                x += sizeof(A) == 8 ? (A)((const double *)f.mask)[mi] : (A)((const float *)f.mask)[mi];
+            }
+        }
+        const A ls = sizeof(A) == 8 ? (A)((const double *)f.lse)[(b * f.H + h) * f.L + l]
+                                    : (A)((const float *)f.lse)[(b * f.H + h) * f.L + l];
+        sum += sizeof(A) == 8 ? (A)exp((double)(x - ls)) : (A)expf((float)(x - ls));
+    }
+    if (AVG) sum /= (A)nh;
+    switch (f.out_dtype) {
+        case GT_F64: ((double *)wout)[i] = (double)sum; break;
+        case GT_F32: ((float *)wout)[i] = (float)sum; break;
+        case GT_F16: ((_Float16 *)wout)[i] = (_Float16)(float)sum; break;
+        case GT_BF16: ((__bf16 *)wout)[i] = (__bf16)(float)sum; break;
+        default: break;
+    }
+}
+
+template <typename T, int D, bool AVG>
+hipError_t launch_mfma(const AttnFwdArgs &f, void *w, hipStream_t st) {
+    const int64_t nrb = (f.L + 32 * WQ - 1) / (32 * WQ);
+    const int64_t grid = nrb * (AVG ? f.B : f.B * f.H);
+    if (grid > 0x7fffffffLL) return hipErrorInvalidConfiguration;
+    const int mode = !f.mask ? 0 : (f.mask_bool ? 1 : 2);
+#define GT_W(C, MK) hipLaunchKernelGGL((attn_weights_kernel<T, D, C, MK, AVG>), dim3((unsigned)grid), dim3(64 * WQ), 0, st, f, w, nrb)
+    if (f.causal) {
+        if (mode == 0) GT_W(true, 0);
+        else if (mode == 1) GT_W(true, 1);
+        else GT_W(true, 2);
+    } else {
+        if (mode == 0) GT_W(false, 0);
+        else if (mode == 1) GT_W(false, 1);
+        else GT_W(false, 2);
+    }
+#undef GT_W
+    return hipGetLastError();
+}
+
+template <typename T, typename A>
+hipError_t launch_generic(const AttnFwdArgs &f, void *w, bool avg, hipStream_t st) {
+    const int64_t n = (avg ? f.B * f.L : f.B * f.H * f.L) * f.S;
+    const int64_t blocks = (n + 255) / 256;
+    if (blocks > 0x7fffffffLL) return hipErrorInvalidConfiguration;
+    if (avg) hipLaunchKernelGGL((attn_weights_generic_kernel<T, A, true>), dim3((unsigned)blocks), dim3(256), 0, st, f, w);
+    else hipLaunchKernelGGL((attn_weights_generic_kernel<T, A, false>), dim3((unsigned)blocks), dim3(256), 0, st, f, w);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+// `f` as for the forward (q, k, mask, lse of the same call; out_dtype = dtype of the weights);
+// `w` receives (B,H,L,S), or (B,L,S) when averaging over the heads.
+hipError_t launch_attn_weights(const AttnFwdArgs &f, int cd, void *w, bool average, hipStream_t st) {
+    if (f.B * f.L * f.S == 0 || f.H == 0) return hipSuccess;
+    bool mfma = (cd == GT_F16 || cd == GT_BF16) && (f.D == 64 || f.D == 128) && f.out_dtype == cd && !f.kv_len &&
+                !f.q_pos && (uintptr_t)f.q % 16 == 0 && (uintptr_t)f.k % 16 == 0;
+    for (int64_t st8 : {f.q_sb, f.q_sh, f.q_sl, f.k_sb, f.k_sh, f.k_ss}) mfma = mfma && st8 % 8 == 0;
+    if (mfma) {
+        if (cd == GT_F16) {
+            if (f.D == 128) return average ? launch_mfma<_Float16, 128, true>(f, w, st) : launch_mfma<_Float16, 128, false>(f, w, st);
+            return average ? launch_mfma<_Float16, 64, true>(f, w, st) : launch_mfma<_Float16, 64, false>(f, w, st);
+        }
+        if (f.D == 128) return average ? launch_mfma<__bf16, 128, true>(f, w, st) : launch_mfma<__bf16, 128, false>(f, w, st);
+        return average ? launch_mfma<__bf16, 64, true>(f, w, st) : launch_mfma<__bf16, 64, false>(f, w, st);
+    }
+    switch (cd) {
+        case GT_F64: return launch_generic<double, double>(f, w, average, st);
+        case GT_F16: return launch_generic<_Float16, float>(f, w, average, st);
+        case GT_BF16: return launch_generic<__bf16, float>(f, w, average, st);
+        default: return launch_generic<float, float>(f, w, average, st);
+    }
+}

@@ -516,6 +516,55 @@ extern "C" gt_tensor *gt_dequantize(const gt_tensor *t, int out_dtype) {
     return deliver(out, t->device_type != GT_DEV_CUDA);
 }
 
+// ---- explicit attention weights ----------------------------------------------------------------
+// MultiheadAttention(need_weights=True) in the reference materialises softmax(q.k^T*scale +
+// masks) with ggml ops (gguf_train/nn/modules/transformer.py:153-166).  Here the fused forward
+// gives the output and the log-sum-exp; this entry point recomputes the weights from them.
+
+extern "C" gt_tensor *gt_attention_weights(const gt_tensor *q, const gt_tensor *k, const gt_tensor *mask,
+                                           const gt_tensor *lse, float scale, int is_causal, int average_heads) {
+    if (!validate("attention_weights", q, k, k, mask)) return nullptr;
+    if (!lse || lse->ndim != 3 || lse->shape[0] != q->shape[0] || lse->shape[1] != q->shape[1] ||
+        lse->shape[2] != q->shape[2]) {
+        gt_set_error("attention_weights: lse must be (B, H, L), the log-sum-exp of the same forward");
+        return nullptr;
+    }
+    if (k->dtype == GT_Q8_0) {
+        gt_set_error("attention_weights: q8_0 keys are not supported (dequantize them first)");
+        return nullptr;
+    }
+    const int dev = q->device_type == GT_DEV_CUDA ? q->device_index : 0;
+    if (!gt_device_ok(dev)) return nullptr;
+    const int64_t B = q->shape[0], H = q->shape[1], L = q->shape[2], D = q->shape[3], S = k->shape[2];
+    if (scale <= 0.0f) scale = 1.0f / std::sqrt((float)D);
+    const int cd = compute_dtype(q, k, k);
+    Temps tmp;
+    const gt_tensor *qs = stage(q, dev, cd, tmp), *ks = stage(k, dev, cd, tmp);
+    const int ld = cd == GT_F64 ? GT_F64 : GT_F32;
+    const gt_tensor *ls = lse->device_type == GT_DEV_CUDA && lse->device_index == dev && lse->dtype == ld && gt_is_dense(lse) &&
+                                  lse->offset == 0
+                              ? lse
+                              : tmp.keep(gt_to_device_dense(lse, dev, ld));
+    if (!qs || !ks || !ls) return nullptr;
+    AttnFwdArgs a{};
+    fill_qkv(a, qs, ks, ks);
+    if (!stage_mask(mask, dev, cd, a, tmp)) return nullptr;
+    a.lse = gt_data(ls);
+    a.scale = scale;
+    a.causal = is_causal ? 1 : 0;
+    a.out_dtype = q->dtype;
+    const int64_t wsh4[4] = {B, H, L, S}, wsh3[3] = {B, L, S};
+    gt_tensor *w = average_heads ? gt_new_tensor(3, wsh3, q->dtype, GT_DEV_CUDA, dev)
+                                 : gt_new_tensor(4, wsh4, q->dtype, GT_DEV_CUDA, dev);
+    if (!w) return nullptr;
+    if (!gt_hip_check(launch_attn_weights(a, cd, gt_data(w), average_heads != 0, gt_stream()),
+                      "attention weights kernel")) {
+        gt_tensor_free(w);
+        return nullptr;
+    }
+    return deliver(w, q->device_type != GT_DEV_CUDA);
+}
+
 // ---- KV cache --------------------------------------------------------------------------------
 // The per-sequence K/V store of a decoding loop.  In the reference it is llama.cpp's cache
 // behind LlamaContext.forward_logits (csrc/llama_bridge.cpp:245-296, gguf_train/llama/__init__.py:

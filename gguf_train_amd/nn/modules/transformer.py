@@ -7,8 +7,12 @@
 - boolean attn_mask / key_padding_mask: True marks a position that must NOT be attended to and
   becomes -1e9; float masks are added; a 2-D attn_mask is (L, S), a 3-D one (B*H, L, S);
 - need_weights=False runs the fused attention kernel (scaled_dot_product_attention);
-  need_weights=True returns the softmax weights too (averaged over heads by default), computed
-  by the reference's explicit composition.
+  need_weights=True returns the softmax weights too (averaged over heads by default): the fused
+  kernel gives the output and its log-sum-exp, the native gt_attention_weights recomputes the
+  weights from them (the reference composes them with ggml ops, transformer.py:153-166).  The
+  causal mask excludes future keys rather than adding -1e9 (the same weights unless every
+  visible key of a row is masked out); gradients flow through the output, not the returned
+  weights; with dropout in training the reference's composition runs.
 
 The projections are plain GEMMs (torch.nn.functional.linear); the attention itself is the
 native kernel.
@@ -21,6 +25,8 @@ import math
 import torch
 from torch import nn
 
+from ... import _ops
+from ..._functions import FlashAttentionFn
 from .. import functional as F
 
 
@@ -154,19 +160,26 @@ class MultiheadAttention(nn.Module):
                 scale=scale,
             )
             attn_weights = None
-        else:
+        elif self.dropout > 0.0 and self.training:
+            # dropout on the explicit weights: the reference's composition (transformer.py:153-166)
             scores = q.matmul(k.transpose(-2, -1).contiguous()) * scale
             if is_causal:
                 cm = torch.ones((L, S), dtype=q.dtype, device=q.device).triu(diagonal=1) * (-1e9)
                 scores = scores + cm
             if mask is not None:
                 scores = scores + mask
-            attn_weights = torch.softmax(scores, dim=-1)
-            if self.dropout > 0.0 and self.training:
-                attn_weights = torch.nn.functional.dropout(attn_weights, p=self.dropout, training=True)
+            attn_weights = torch.nn.functional.dropout(torch.softmax(scores, dim=-1), p=self.dropout, training=True)
             attn_out = attn_weights.matmul(v)
             if average_attn_weights:
                 attn_weights = attn_weights.mean(dim=1)
+        else:
+            # native: the fused forward gives the output and the log-sum-exp, from which the
+            # weights are recomputed (gt_attention_weights); gradients flow through the output
+            needs_grad = torch.is_grad_enabled() and any(t.requires_grad for t in (q, k, v))
+            with torch.no_grad():
+                out_nat, lse = _ops.flash_attention_lse(q, k, v, mask, scale, is_causal)
+                attn_weights = _ops.attention_weights(q, k, mask, lse, scale, is_causal, average_attn_weights)
+            attn_out = FlashAttentionFn.apply(q, k, v, mask, scale, is_causal) if needs_grad else out_nat
 
         out = attn_out.transpose(1, 2).reshape(B, L, E)
         out = self.out_proj(out)

@@ -176,6 +176,15 @@ GT_API int gt_flash_attention_backward(const gt_tensor *grad_out, const gt_tenso
 /* (out may be NULL together with lse: the forward is then recomputed.  A float32 out, from
  * gt_flash_attention_train, is used as is.) */
 
+/* Replaces the explicit weights of MultiheadAttention(need_weights=True), which the reference
+ * computes with ggml ops (gguf_train/nn/modules/transformer.py:153-166): softmax(q.k^T*scale +
+ * mask) with the causal mask, recomputed from `lse`, the (B,H,L) log-sum-exp of the forward of
+ * the same q, k, mask, scale, is_causal (gt_flash_attention_lse).  Returns (B,H,L,S), or
+ * (B,L,S) averaged over the heads when average_heads != 0, dtype and device of q.  Positions
+ * that are causally or mask-blocked weigh 0; a row with nothing to attend to is all zeros. */
+GT_API gt_tensor *gt_attention_weights(const gt_tensor *q, const gt_tensor *k, const gt_tensor *mask,
+                                       const gt_tensor *lse, float scale, int is_causal, int average_heads);
+
 /* ---- GGUF Q8_0 ------------------------------------------------------------------------ */
 
 /* csrc/gguf_train.h:376 (gt_tensor_to_dtype, csrc/gt_core.cpp:784-847): quantizes rows of
