@@ -159,6 +159,36 @@ def _configure(lib: ctypes.CDLL) -> ctypes.CDLL:
     lib.gt_kv_cache_attention.argtypes = [c_void_p, c_void_p, c_float, c_int]
     lib.gt_kv_cache_attention.restype = c_void_p
 
+    # GGUF read side (csrc/gguf_train.h:363-379; gguf_train/_C.py:527-560)
+    lib.gt_gguf_open.argtypes = [c_char_p]
+    lib.gt_gguf_open.restype = c_void_p
+    lib.gt_gguf_close.argtypes = [c_void_p]
+    lib.gt_gguf_close.restype = None
+    lib.gt_gguf_n_tensors.argtypes = [c_void_p]
+    lib.gt_gguf_n_tensors.restype = c_int64
+    lib.gt_gguf_tensor_name.argtypes = [c_void_p, c_int64]
+    lib.gt_gguf_tensor_name.restype = c_char_p
+    lib.gt_gguf_get_tensor.argtypes = [c_void_p, c_char_p, c_int]
+    lib.gt_gguf_get_tensor.restype = c_void_p
+    lib.gt_gguf_get_tensor_device.argtypes = [c_void_p, c_char_p, c_int, c_int]
+    lib.gt_gguf_get_tensor_device.restype = c_void_p
+    lib.gt_gguf_n_kv.argtypes = [c_void_p]
+    lib.gt_gguf_n_kv.restype = c_int64
+    lib.gt_gguf_kv_key.argtypes = [c_void_p, c_int64]
+    lib.gt_gguf_kv_key.restype = c_char_p
+    lib.gt_gguf_kv_type.argtypes = [c_void_p, c_int64]
+    lib.gt_gguf_kv_type.restype = c_int
+    lib.gt_gguf_kv_val_str.argtypes = [c_void_p, c_int64, c_char_p, c_int]
+    lib.gt_gguf_kv_val_str.restype = c_int
+    lib.gt_gguf_kv_arr_type.argtypes = [c_void_p, c_int64]
+    lib.gt_gguf_kv_arr_type.restype = c_int
+    lib.gt_gguf_kv_arr_n.argtypes = [c_void_p, c_int64]
+    lib.gt_gguf_kv_arr_n.restype = c_int64
+    lib.gt_gguf_kv_arr_data.argtypes = [c_void_p, c_int64]
+    lib.gt_gguf_kv_arr_data.restype = c_void_p
+    lib.gt_gguf_kv_arr_str.argtypes = [c_void_p, c_int64, c_int64]
+    lib.gt_gguf_kv_arr_str.restype = c_char_p
+
     lib.gt_init()
     return lib
 

@@ -611,8 +611,16 @@ bool kv_check_rows(const char *who, const gt_kv_cache *c, const gt_tensor *t, co
                      std::to_string(c->Hkv) + ", T, " + std::to_string(c->D) + "]");
         return false;
     }
+    if (t->dtype == GT_Q8_0) {
+        // Q8_0 rows (e.g. read from a GGUF file): whole blocks along head_dim
+        if (c->D % 32 != 0 || !gt_is_dense(t) || t->offset != 0) {
+            gt_set_error(std::string(who) + ": a q8_0 " + name + " must be dense with head_dim a multiple of 32");
+            return false;
+        }
+        return true;
+    }
     if (!gt_is_float(t->dtype)) {
-        gt_set_error(std::string(who) + ": " + name + " must be float32, float16, bfloat16 or float64, got " +
+        gt_set_error(std::string(who) + ": " + name + " must be float32, float16, bfloat16, float64 or q8_0, got " +
                      gt_dtype_name(t->dtype));
         return false;
     }
@@ -753,13 +761,17 @@ extern "C" int gt_kv_cache_append(gt_kv_cache *c, const gt_tensor *k, const gt_t
                                  ? src
                                  : tmp.keep(gt_to_device_dense(src, c->dev, -1));
         if (!s) return -1;
+        // Q8_0 rows go into a Q8_0 cache unchanged; a float cache takes their dequantized values
+        if (s->dtype == GT_Q8_0 && c->dtype != GT_Q8_0 && !(s = tmp.keep(gt_dequantize(s, GT_F32)))) return -1;
         gt_tensor *dst = src == k ? c->k : c->v;
+        const int32_t *pos = (const int32_t *)gt_data(c->len_dev);
         // the rows go to each sequence's current length (len_dev), before it is advanced
-        if (!gt_hip_check(gt_launch_kv_append(gt_data(s), s->dtype, s->strides, gt_data(dst), c->dtype,
-                                              (const int32_t *)gt_data(c->len_dev), c->B, c->Hkv, T, c->D, c->cap,
-                                              gt_stream()),
-                          "kv cache append kernel"))
-            return -1;
+        const hipError_t e =
+            s->dtype == GT_Q8_0
+                ? gt_launch_kv_append_blocks(gt_data(s), gt_data(dst), pos, c->B, c->Hkv, T, c->D, c->cap, gt_stream())
+                : gt_launch_kv_append(gt_data(s), s->dtype, s->strides, gt_data(dst), c->dtype, pos, c->B, c->Hkv, T,
+                                      c->D, c->cap, gt_stream());
+        if (!gt_hip_check(e, "kv cache append kernel")) return -1;
     }
     for (auto &n : c->len) n += (int32_t)T;
     return kv_upload(c->len_dev, c->len) ? 0 : -1;

@@ -211,6 +211,19 @@ __global__ void kv_append_kernel(const void *__restrict__ src, int sdt, int64_t 
     }
 }
 
+// KV-cache append of rows that are already Q8_0: row (b, h, t) of the dense Q8_0 src
+// (B, Hkv, T, D) is copied, block bytes unchanged, to row pos[b] + t of the Q8_0 cache.  A row is
+// D / 32 blocks of 34 bytes; one thread moves one 16-bit half-word of it.
+__global__ void kv_append_blocks_kernel(const uint16_t *__restrict__ src, uint16_t *__restrict__ dst,
+                                        const int32_t *__restrict__ pos, int64_t Hkv, int64_t T, int64_t hpr,
+                                        int64_t cap, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const int64_t r = i / hpr, j = i % hpr;  // source row (b, h, t) and half-word in it
+    const int64_t t = r % T, bh = r / T, b = bh / Hkv;
+    dst[(bh * cap + pos[b] + t) * hpr + j] = src[i];
+}
+
 __global__ void q8_0_dequantize_kernel(const uint8_t *__restrict__ in, void *__restrict__ out, int dst_dtype,
                                        int64_t nblocks) {
     const int lane = threadIdx.x & 63;
@@ -285,5 +298,17 @@ hipError_t gt_launch_kv_append(const void *src, int src_dtype, const int64_t *sr
     if (blocks > 0x7fffffffLL) return hipErrorInvalidConfiguration;
     hipLaunchKernelGGL(kv_append_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, src, src_dtype, src_strides[0],
                        src_strides[1], src_strides[2], src_strides[3], dst, dst_dtype, pos, Hkv, T, D, cap, n);
+    return hipGetLastError();
+}
+
+hipError_t gt_launch_kv_append_blocks(const void *src, void *dst, const int32_t *pos, int64_t B, int64_t Hkv,
+                                      int64_t T, int64_t D, int64_t cap, hipStream_t stream) {
+    const int64_t hpr = D / 32 * 17;  // half-words per row
+    const int64_t n = B * Hkv * T * hpr;
+    if (n <= 0) return hipSuccess;
+    const int64_t blocks = (n + 255) / 256;
+    if (D % 32 != 0 || blocks > 0x7fffffffLL) return hipErrorInvalidConfiguration;
+    hipLaunchKernelGGL(kv_append_blocks_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, (const uint16_t *)src,
+                       (uint16_t *)dst, pos, Hkv, T, hpr, cap, n);
     return hipGetLastError();
 }

@@ -106,6 +106,10 @@ hipError_t gt_launch_convert(const void *src, int src_dtype, const gt_layout &sr
 hipError_t gt_launch_kv_append(const void *src, int src_dtype, const int64_t *src_strides, void *dst, int dst_dtype,
                                const int32_t *pos, int64_t B, int64_t Hkv, int64_t T, int64_t D, int64_t cap,
                                hipStream_t stream);
+// KV-cache append of Q8_0 rows: the dense Q8_0 src (B, Hkv, T, D), D % 32 == 0, copied block by
+// block (bytes unchanged) to rows pos[b] + t of the Q8_0 cache (B, Hkv, cap, D).
+hipError_t gt_launch_kv_append_blocks(const void *src, void *dst, const int32_t *pos, int64_t B, int64_t Hkv,
+                                      int64_t T, int64_t D, int64_t cap, hipStream_t stream);
 // Dense bool bytes -> dense float additive mask (0 where true, -inf where false).
 hipError_t gt_launch_bool_to_bias(const void *src, float *dst, int64_t n, hipStream_t stream);
 // Q8_0 (ggml block_q8_0) quantize `nrows` rows of `row_len` floats (row_len % 32 == 0).

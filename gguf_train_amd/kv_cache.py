@@ -70,8 +70,10 @@ class KVCache:
     clear_kv = clear
 
     def append(self, k: torch.Tensor, v: torch.Tensor, pos_offset: int | None = None) -> None:
-        """Appends k, v (batch, n_head_kv, T, head_dim) to every sequence.  With pos_offset the
-        positions must continue what each sequence holds, as forward_logits(pos_offset=...)."""
+        """Appends k, v (batch, n_head_kv, T, head_dim) to every sequence: float tensors, or Q8_0
+        `QuantizedTensor`s (e.g. read from a GGUF file), whose blocks a Q8_0 cache stores as they
+        are.  With pos_offset the positions must continue what each sequence holds, as
+        forward_logits(pos_offset=...)."""
         bind_stream(self.device)
         hk, hv = borrow(k), borrow(v)
         rc = _C.lib.gt_kv_cache_append(self._ptr, hk.ptr, hv.ptr, -1 if pos_offset is None else int(pos_offset))

@@ -194,6 +194,43 @@ GT_API gt_tensor *gt_quantize(const gt_tensor *t, int ggml_type_id);
 /* csrc/gguf_train.h:377: y = float(qs[j]) * float(d), then converted to out_dtype. */
 GT_API gt_tensor *gt_dequantize(const gt_tensor *t, int out_dtype);
 
+/* ---- GGUF files ----------------------------------------------------------------------- */
+
+/* csrc/gguf_train.h:363-379 (csrc/gt_ops_extra.cpp:1811-1990), read side.  The reader parses the
+ * file itself (no ggml); a file ggml would refuse fails with "Failed to open GGUF file: <why>".
+ * Tensors come back with the reference's dtype and shape rules, including the recorded
+ * "gguf_train.shape.<name>" / "gguf_train.dtype.<name>" keys.  Stored types: f32, f16, bf16,
+ * f64, i8, i16, i32, i64 and q8_0; other quantized types and complex tensors are refused by
+ * gt_gguf_get_tensor with a message naming the tensor.  The file stays open (and must not
+ * change) until gt_gguf_close; tensor bytes are read when a tensor is asked for. */
+typedef struct gt_gguf_file gt_gguf_file;
+GT_API gt_gguf_file *gt_gguf_open(const char *path);
+GT_API void gt_gguf_close(gt_gguf_file *f);
+GT_API int64_t gt_gguf_n_tensors(const gt_gguf_file *f);
+GT_API const char *gt_gguf_tensor_name(const gt_gguf_file *f, int64_t idx);
+/* A new host tensor; dequantize_f32 turns a q8_0 tensor into float32. */
+GT_API gt_tensor *gt_gguf_get_tensor(const gt_gguf_file *f, const char *name, int dequantize_f32);
+/* No counterpart in the reference ABI (there, gt_gguf_get_tensor then gt_tensor_to_device): the
+ * same tensor streamed from the file into memory of HIP device `device_index` through pinned
+ * staging, on the calling thread's stream, complete on return.  A q8_0 tensor stays in its
+ * 34-byte blocks (ready for gt_flash_attention as k / v) unless dequantize_f32 asks for float32,
+ * which is done on the device. */
+GT_API gt_tensor *gt_gguf_get_tensor_device(const gt_gguf_file *f, const char *name, int dequantize_f32,
+                                            int device_index);
+GT_API int64_t gt_gguf_n_kv(const gt_gguf_file *f);
+GT_API const char *gt_gguf_kv_key(const gt_gguf_file *f, int64_t idx);
+/* A gguf_type (0 u8 .. 12 f64; 8 string, 9 array), -1 for a bad index. */
+GT_API int gt_gguf_kv_type(const gt_gguf_file *f, int64_t idx);
+/* The value as text; returns its full length (as snprintf does), so a result >= buf_len means it
+ * was cut short.  A null buffer asks for the length. */
+GT_API int gt_gguf_kv_val_str(const gt_gguf_file *f, int64_t idx, char *buf, int buf_len);
+/* Arrays: element gguf_type (-1 when the value is not an array), element count, packed
+ * elements (null for string arrays; bools one byte each), and the i-th string of a string array. */
+GT_API int gt_gguf_kv_arr_type(const gt_gguf_file *f, int64_t idx);
+GT_API int64_t gt_gguf_kv_arr_n(const gt_gguf_file *f, int64_t idx);
+GT_API const void *gt_gguf_kv_arr_data(const gt_gguf_file *f, int64_t idx);
+GT_API const char *gt_gguf_kv_arr_str(const gt_gguf_file *f, int64_t idx, int64_t i);
+
 /* ---- KV cache ------------------------------------------------------------------------- */
 
 /* No counterpart in the reference ABI: the reference's decode cache is llama.cpp's, reached
@@ -215,7 +252,8 @@ GT_API int64_t gt_kv_cache_capacity(const gt_kv_cache *c);
 GT_API gt_tensor *gt_kv_cache_keys(const gt_kv_cache *c);
 GT_API gt_tensor *gt_kv_cache_values(const gt_kv_cache *c);
 /* Appends T tokens to every sequence: k, v (batch, n_head_kv, T, head_dim), any float dtype
- * and strides, host or device.  pos_offset < 0 appends after what each sequence holds;
+ * and strides, or dense q8_0 (e.g. from gt_gguf_get_tensor_device; copied block for block into a
+ * q8_0 cache, dequantized into a float one), host or device.  pos_offset < 0 appends after what each sequence holds;
  * otherwise it must equal every sequence's length (positions continue the cache, as
  * gt_llama_forward_logits requires).  Fails without writing when a sequence would pass the
  * capacity.  Returns 0 on success. */
