@@ -132,6 +132,12 @@ def _configure(lib: ctypes.CDLL) -> ctypes.CDLL:
     lib.gt_attention_weights.argtypes = [c_void_p, c_void_p, c_void_p, c_void_p, c_float, c_int, c_int]
     lib.gt_attention_weights.restype = c_void_p
 
+    # RoPE (csrc/gguf_train.h:309-310; gguf_train/_C.py binds them with the same types)
+    lib.gt_rope.argtypes = [c_void_p, c_void_p, c_int, c_int, c_int, c_float, c_float]
+    lib.gt_rope.restype = c_void_p
+    lib.gt_rope_backward.argtypes = [c_void_p, c_void_p, c_int, c_int, c_int, c_float, c_float]
+    lib.gt_rope_backward.restype = c_void_p
+
     # Q8_0 (csrc/gguf_train.h:376-377)
     lib.gt_quantize.argtypes = [c_void_p, c_int]
     lib.gt_quantize.restype = c_void_p
@@ -156,6 +162,8 @@ def _configure(lib: ctypes.CDLL) -> ctypes.CDLL:
     lib.gt_kv_cache_values.restype = c_void_p
     lib.gt_kv_cache_append.argtypes = [c_void_p, c_void_p, c_void_p, c_int64]
     lib.gt_kv_cache_append.restype = c_int
+    lib.gt_kv_cache_append_rope.argtypes = [c_void_p, c_void_p, c_void_p, c_int64, c_int, c_int, c_float, c_float]
+    lib.gt_kv_cache_append_rope.restype = c_int
     lib.gt_kv_cache_attention.argtypes = [c_void_p, c_void_p, c_float, c_int]
     lib.gt_kv_cache_attention.restype = c_void_p
 

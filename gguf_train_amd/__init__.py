@@ -8,9 +8,9 @@ MultiheadAttention with the reference's signatures, and the GGUF Q8_0 codec.
 
 from . import _C
 from ._bridge import QuantizedTensor
-from ._functions import FlashAttentionFn
+from ._functions import FlashAttentionFn, RoPEFn
 from ._ops import (dequantize, flash_attention, flash_attention_backward, flash_attention_lse, flash_attention_train,
-                   quantize)
+                   quantize, rope)
 from . import nn
 from .kv_cache import KVCache
 
@@ -18,6 +18,8 @@ __all__ = [
     "_C",
     "QuantizedTensor",
     "FlashAttentionFn",
+    "RoPEFn",
+    "rope",
     "flash_attention",
     "flash_attention_lse",
     "flash_attention_train",

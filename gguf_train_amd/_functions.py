@@ -1,5 +1,9 @@
 """Autograd Functions of the attention path.
 
+`RoPEFn` keeps the reference's RoPEFn (gguf_train/_functions.py:1906-1919): forward(ctx, x,
+pos, n_dims, mode, n_ctx_orig, freq_base, freq_scale) saves the positions and calls the native
+gt_rope; the backward calls gt_rope_backward (the inverse rotation) and returns (gx, None x 6).
+
 `FlashAttentionFn` keeps the reference's signature and behaviour
 (gguf_train/_functions.py:1922-1965): forward(ctx, q, k, v, mask, scale, is_causal) saves
 its inputs, sets ctx.scale (1/sqrt(D) when None) and ctx.is_causal, and calls the native
@@ -19,6 +23,22 @@ import math
 import torch
 
 from . import _ops
+
+
+class RoPEFn(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, pos, n_dims, mode, n_ctx_orig, freq_base, freq_scale):
+        ctx.args = (int(n_dims), int(mode), int(n_ctx_orig), float(freq_base), float(freq_scale))
+        ctx.save_for_backward(pos)
+        return _ops.rope(x, pos, *ctx.args)
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        if grad_out is None:
+            return (None,) * 7
+        (pos,) = ctx.saved_tensors
+        gx = _ops.rope(grad_out, pos, *ctx.args, backward=True)
+        return (gx, None, None, None, None, None, None)
 
 
 class FlashAttentionFn(torch.autograd.Function):

@@ -84,6 +84,17 @@ def attention_weights(q, k, mask, lse, scale: float = 0.0, is_causal: bool = Fal
     return adopt(ptr, "attention_weights")
 
 
+def rope(x, pos, n_dims: int, mode: int = 0, n_ctx_orig: int = 0, freq_base: float = 10000.0,
+         freq_scale: float = 1.0, backward: bool = False) -> torch.Tensor:
+    """gt_rope / gt_rope_backward (csrc/gguf_train.h:309-310) on PyTorch tensors."""
+    bind_stream(_device_of(x))
+    hx, hp = borrow(x), borrow(pos)
+    fn = _C.lib.gt_rope_backward if backward else _C.lib.gt_rope
+    ptr = fn(hx.ptr, hp.ptr, int(n_dims), int(mode), int(n_ctx_orig), ctypes.c_float(freq_base),
+             ctypes.c_float(freq_scale))
+    return adopt(ptr, "rope")
+
+
 def quantize(t: torch.Tensor, qtype: str = "q8_0") -> QuantizedTensor:
     """gt_quantize (csrc/gguf_train.h:376); rows of last-dim length, GGUF Q8_0 blocks."""
     if qtype != "q8_0":

@@ -196,16 +196,7 @@ bool dispatch_forward(const AttnFwdArgs &a, int cd, int dev) {
 }
 
 // Moves a device result into a new host tensor when the caller's q lives on the host.
-gt_tensor *deliver(gt_tensor *dev_t, bool to_host) {
-    if (!dev_t || !to_host) return dev_t;
-    gt_tensor *h = gt_new_tensor(dev_t->ndim, dev_t->shape, dev_t->dtype, GT_DEV_CPU, 0);
-    if (h && !gt_copy_device_to_host(h, dev_t)) {
-        gt_tensor_free(h);
-        h = nullptr;
-    }
-    gt_tensor_free(dev_t);
-    return h;
-}
+gt_tensor *deliver(gt_tensor *dev_t, bool to_host) { return gt_deliver(dev_t, to_host); }
 
 // Single-query attention straight from Q8_0 K/V blocks.  Returns 1 when it ran, 0 when the
 // shapes do not suit the kernel (the caller then dequantizes), -1 on error.
@@ -725,13 +716,23 @@ extern "C" gt_tensor *gt_kv_cache_values(const gt_kv_cache *c) {
     return t;
 }
 
-extern "C" int gt_kv_cache_append(gt_kv_cache *c, const gt_tensor *k, const gt_tensor *v, int64_t pos_offset) {
-    const char *who = "kv_cache_append";
+namespace {
+
+struct KvRope {
+    int n_dims, mode;
+    float freq_base, freq_scale;
+};
+
+// Appends k/v rows at each sequence's length; with `rope` the key rows are rotated at their cache
+// positions (length + t) on the way in.
+int kv_append(const char *who, gt_kv_cache *c, const gt_tensor *k, const gt_tensor *v, int64_t pos_offset,
+              const KvRope *rope) {
     if (!c) {
-        gt_set_error("kv_cache_append: NULL cache");
+        gt_set_error(std::string(who) + ": NULL cache");
         return -1;
     }
     if (!kv_check_rows(who, c, k, "k") || !kv_check_rows(who, c, v, "v")) return -1;
+    if (rope && !gt_rope_check_args(who, c->D, rope->n_dims, rope->mode, rope->freq_base, rope->freq_scale)) return -1;
     const int64_t T = k->shape[2];
     if (v->shape[2] != T) {
         gt_set_error("kv_cache_append: k and v hold different numbers of tokens (" + std::to_string(T) + " and " +
@@ -756,25 +757,54 @@ extern "C" int gt_kv_cache_append(gt_kv_cache *c, const gt_tensor *k, const gt_t
     }
     if (!gt_device_ok(c->dev)) return -1;
     Temps tmp;
+    const int32_t *pos = (const int32_t *)gt_data(c->len_dev);
+    gt_scratch table;
+    gt_rope_apply ra{};
+    if (rope && T > 0) {
+        // (cos, sin) of table row b * T + t at position len[b] + t
+        if (!gt_scratch_alloc(table, (size_t)(c->B * T) * (size_t)(rope->n_dims / 2) * 2 * sizeof(float), c->dev) ||
+            !gt_hip_check(gt_launch_rope_table(nullptr, pos, T, c->B * T, rope->n_dims,
+                                               gt_rope_theta_scale(rope->freq_base, rope->n_dims), rope->freq_scale, 0,
+                                               table.ptr(), gt_stream()),
+                          "rope table kernel"))
+            return -1;
+        ra.table = table.ptr();
+        ra.n_dims = rope->n_dims;
+        ra.neox = rope->mode == 2;
+    }
     for (const gt_tensor *src : {k, v}) {
+        const bool rotate = rope && src == k;
         const gt_tensor *s = src->device_type == GT_DEV_CUDA && src->device_index == c->dev
                                  ? src
                                  : tmp.keep(gt_to_device_dense(src, c->dev, -1));
         if (!s) return -1;
-        // Q8_0 rows go into a Q8_0 cache unchanged; a float cache takes their dequantized values
-        if (s->dtype == GT_Q8_0 && c->dtype != GT_Q8_0 && !(s = tmp.keep(gt_dequantize(s, GT_F32)))) return -1;
+        // Q8_0 rows go into a Q8_0 cache unchanged; a float cache takes their dequantized values,
+        // and so do rotated keys (rotated, then quantized again for a Q8_0 cache)
+        if (s->dtype == GT_Q8_0 && (c->dtype != GT_Q8_0 || rotate) && !(s = tmp.keep(gt_dequantize(s, GT_F32))))
+            return -1;
         gt_tensor *dst = src == k ? c->k : c->v;
-        const int32_t *pos = (const int32_t *)gt_data(c->len_dev);
         // the rows go to each sequence's current length (len_dev), before it is advanced
         const hipError_t e =
             s->dtype == GT_Q8_0
                 ? gt_launch_kv_append_blocks(gt_data(s), gt_data(dst), pos, c->B, c->Hkv, T, c->D, c->cap, gt_stream())
                 : gt_launch_kv_append(gt_data(s), s->dtype, s->strides, gt_data(dst), c->dtype, pos, c->B, c->Hkv, T,
-                                      c->D, c->cap, gt_stream());
+                                      c->D, c->cap, rotate && T > 0 ? &ra : nullptr, gt_stream());
         if (!gt_hip_check(e, "kv cache append kernel")) return -1;
     }
     for (auto &n : c->len) n += (int32_t)T;
     return kv_upload(c->len_dev, c->len) ? 0 : -1;
+}
+
+}  // namespace
+
+extern "C" int gt_kv_cache_append(gt_kv_cache *c, const gt_tensor *k, const gt_tensor *v, int64_t pos_offset) {
+    return kv_append("kv_cache_append", c, k, v, pos_offset, nullptr);
+}
+
+extern "C" int gt_kv_cache_append_rope(gt_kv_cache *c, const gt_tensor *k, const gt_tensor *v, int64_t pos_offset,
+                                       int n_dims, int mode, float freq_base, float freq_scale) {
+    const KvRope r{n_dims, mode, freq_base, freq_scale};
+    return kv_append("kv_cache_append_rope", c, k, v, pos_offset, &r);
 }
 
 extern "C" gt_tensor *gt_kv_cache_attention(gt_kv_cache *c, const gt_tensor *q, float scale, int is_causal) {

@@ -13,6 +13,7 @@
 // stores are coalesced; no LDS is needed.
 
 #include "gt_internal.h"
+#include "gt_rope_math.h"
 
 #include <cmath>
 
@@ -194,14 +195,31 @@ __global__ void q8_0_quantize_kernel(const float *__restrict__ x, uint8_t *__res
 // KV-cache append: row (b, h, t) of src (B, Hkv, T, D), any strides, goes to row pos[b] + t of
 // the cache (B, Hkv, cap, D).  A float cache receives converted elements (one thread each); a
 // Q8_0 cache receives the row quantized block by block (two blocks per wave, as above).
+// With a RoPE table (gt_rope_apply), element d < n_dims is first rotated with its partner (d ^ 1,
+// or d -/+ n_dims/2 for NeoX) read from the same source row, in float32 as gt_rope does, and
+// rounded to the source dtype, so the cache holds what gt_rope followed by the append stores.
 __global__ void kv_append_kernel(const void *__restrict__ src, int sdt, int64_t s_sb, int64_t s_sh, int64_t s_st,
                                  int64_t s_sd, void *__restrict__ dst, int ddt, const int32_t *__restrict__ pos,
-                                 int64_t Hkv, int64_t T, int64_t D, int64_t cap, int64_t n) {
+                                 int64_t Hkv, int64_t T, int64_t D, int64_t cap, int64_t n,
+                                 const float2 *__restrict__ rope_table, int n_dims, int neox) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;  // value index (b, h, t, d)
     const bool live = i < n;
     const int64_t ic = live ? i : 0;
     const int64_t d = ic % D, t = (ic / D) % T, h = (ic / (D * T)) % Hkv, b = ic / (D * T * Hkv);
-    const double x = read_elem(src, sdt, b * s_sb + h * s_sh + t * s_st + d * s_sd);
+    const int64_t src_row = b * s_sb + h * s_sh + t * s_st;
+    double x = read_elem(src, sdt, src_row + d * s_sd);
+    if (rope_table && d < n_dims) {
+        const int half = n_dims / 2;
+        const bool lo = neox ? d < half : (d & 1) == 0;
+        const int64_t pd = neox ? (lo ? d + half : d - half) : (d ^ 1);
+        const int pair = neox ? (int)(lo ? d : pd) : (int)(d >> 1);
+        const float v = (float)x, w = (float)read_elem(src, sdt, src_row + pd * s_sd);
+        const float2 cs = rope_table[(b * T + t) * half + pair];
+        float r = lo ? rope_rot_lo(v, w, cs) : rope_rot_hi(w, v, cs);
+        if (sdt == GT_F16) r = d_f16_to_f32(d_f32_to_f16(r));
+        else if (sdt == GT_BF16) r = u2f((uint32_t)d_f32_to_bf16(r) << 16);
+        x = r;
+    }
     const int64_t row = (b * Hkv + h) * cap + pos[b] + t;
     if (ddt == GT_Q8_0) {
         // D % 32 == 0 and n % 32 == 0, so a wave half is one whole block of one row
@@ -291,13 +309,15 @@ hipError_t gt_launch_bool_to_bias(const void *src, float *dst, int64_t n, hipStr
 
 hipError_t gt_launch_kv_append(const void *src, int src_dtype, const int64_t *src_strides, void *dst, int dst_dtype,
                                const int32_t *pos, int64_t B, int64_t Hkv, int64_t T, int64_t D, int64_t cap,
-                               hipStream_t stream) {
+                               const gt_rope_apply *rope, hipStream_t stream) {
     const int64_t n = B * Hkv * T * D;
     if (n <= 0) return hipSuccess;
     const int64_t blocks = (n + 255) / 256;
     if (blocks > 0x7fffffffLL) return hipErrorInvalidConfiguration;
+    if (rope && (rope->n_dims < 2 || rope->n_dims % 2 != 0 || rope->n_dims > D)) return hipErrorInvalidValue;
     hipLaunchKernelGGL(kv_append_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, src, src_dtype, src_strides[0],
-                       src_strides[1], src_strides[2], src_strides[3], dst, dst_dtype, pos, Hkv, T, D, cap, n);
+                       src_strides[1], src_strides[2], src_strides[3], dst, dst_dtype, pos, Hkv, T, D, cap, n,
+                       rope ? (const float2 *)rope->table : nullptr, rope ? rope->n_dims : 0, rope ? rope->neox : 0);
     return hipGetLastError();
 }
 

@@ -83,6 +83,9 @@ gt_tensor *gt_to_device_dense(const gt_tensor *t, int dev, int dtype);
 // Copies the device tensor `src` into host tensor `dst` (same shape, dense), waiting for it.
 bool gt_copy_device_to_host(gt_tensor *dst, const gt_tensor *src);
 
+// `dev_t` itself, or (to_host) a new host tensor with its contents, `dev_t` freed; NULL on error.
+gt_tensor *gt_deliver(gt_tensor *dev_t, bool to_host);
+
 // Stream-ordered scratch memory from the pool (freed back to the pool in stream order).
 struct gt_scratch {
     std::shared_ptr<gt_storage> st;
@@ -103,13 +106,36 @@ hipError_t gt_launch_convert(const void *src, int src_dtype, const gt_layout &sr
 // KV-cache append: rows (b, h, t) of the 4-D src (element strides src_strides) are written at
 // row pos[b] + t (pos: device int32 per batch) of the dense (B, Hkv, cap, D) cache of dtype
 // dst_dtype (float32/float16/bfloat16, or GT_Q8_0 quantized row by row; D % 32 == 0 then).
+// With `rope` (non-null) the rows are rotated on the way in: element d of row (b, h, t) becomes
+// RoPE(src row)[d] with the angles of table row b * T + t (positions pos[b] + t), rounded to
+// src_dtype first, so the cache holds exactly what gt_rope followed by the append would store.
+struct gt_rope_apply {
+    const void *table;  // float2 (cos, sin) per (row, pair), from gt_launch_rope_table
+    int n_dims;
+    int neox;
+};
 hipError_t gt_launch_kv_append(const void *src, int src_dtype, const int64_t *src_strides, void *dst, int dst_dtype,
                                const int32_t *pos, int64_t B, int64_t Hkv, int64_t T, int64_t D, int64_t cap,
-                               hipStream_t stream);
+                               const gt_rope_apply *rope, hipStream_t stream);
 // KV-cache append of Q8_0 rows: the dense Q8_0 src (B, Hkv, T, D), D % 32 == 0, copied block by
 // block (bytes unchanged) to rows pos[b] + t of the Q8_0 cache (B, Hkv, cap, D).
 hipError_t gt_launch_kv_append_blocks(const void *src, void *dst, const int32_t *pos, int64_t B, int64_t Hkv,
                                       int64_t T, int64_t D, int64_t cap, hipStream_t stream);
+// RoPE angle table: (cos, sin) of pair i < n_dims/2 for `rows` positions, row r at position pos[r],
+// or base[r / T] + r % T when base is non-null; float2 per entry, sin negated when backward.
+hipError_t gt_launch_rope_table(const int32_t *pos, const int32_t *base, int64_t T, int64_t rows, int n_dims,
+                                float theta_scale, float freq_scale, int backward, void *table, hipStream_t stream);
+// RoPE rotation of x (B, H, S, D; element strides) into the dense y of the same float dtype, with
+// the angles of table row b * table_b_stride + s; mode 0 NORMAL, 2 NEOX.
+hipError_t gt_launch_rope(const void *x, int dtype, const int64_t *strides, void *y, const void *table,
+                          int64_t table_b_stride, int64_t B, int64_t H, int64_t S, int64_t D, int n_dims, int mode,
+                          hipStream_t stream);
+// ---- RoPE argument checks (gt_rope_ops.cpp) ----------------------------------------------------
+// mode 0/2, even n_dims in [2, head_dim], positive finite freq_base, finite freq_scale; the
+// reference's messages prefixed with `who`.
+bool gt_rope_check_args(const char *who, int64_t head_dim, int n_dims, int mode, float freq_base, float freq_scale);
+// powf(freq_base, -2 / n_dims), as ggml computes it.
+float gt_rope_theta_scale(float freq_base, int n_dims);
 // Dense bool bytes -> dense float additive mask (0 where true, -inf where false).
 hipError_t gt_launch_bool_to_bias(const void *src, float *dst, int64_t n, hipStream_t stream);
 // Q8_0 (ggml block_q8_0) quantize `nrows` rows of `row_len` floats (row_len % 32 == 0).

@@ -760,6 +760,17 @@ bool gt_copy_device_to_host(gt_tensor *dst, const gt_tensor *src) {
            gt_hip_check(hipStreamSynchronize(gt_stream()), "hipStreamSynchronize");
 }
 
+gt_tensor *gt_deliver(gt_tensor *dev_t, bool to_host) {
+    if (!dev_t || !to_host) return dev_t;
+    gt_tensor *h = gt_new_tensor(dev_t->ndim, dev_t->shape, dev_t->dtype, GT_DEV_CPU, 0);
+    if (h && !gt_copy_device_to_host(h, dev_t)) {
+        gt_tensor_free(h);
+        h = nullptr;
+    }
+    gt_tensor_free(dev_t);
+    return h;
+}
+
 extern "C" int gt_tensor_copy_to_host(const gt_tensor *t, void *dst, size_t dst_bytes) {
     if (!t || !dst) {
         gt_set_error("copy_to_host: NULL argument");

@@ -69,14 +69,26 @@ class KVCache:
 
     clear_kv = clear
 
-    def append(self, k: torch.Tensor, v: torch.Tensor, pos_offset: int | None = None) -> None:
+    def append(self, k: torch.Tensor, v: torch.Tensor, pos_offset: int | None = None, rope: dict | None = None) -> None:
         """Appends k, v (batch, n_head_kv, T, head_dim) to every sequence: float tensors, or Q8_0
         `QuantizedTensor`s (e.g. read from a GGUF file), whose blocks a Q8_0 cache stores as they
         are.  With pos_offset the positions must continue what each sequence holds, as
-        forward_logits(pos_offset=...)."""
+        forward_logits(pos_offset=...).  `rope` (keys n_dims, mode, freq_base, freq_scale, as
+        nn.functional.rope) rotates each key row at its cache position on the way in; the cache
+        then holds what rope() of the keys followed by append() would store."""
         bind_stream(self.device)
         hk, hv = borrow(k), borrow(v)
-        rc = _C.lib.gt_kv_cache_append(self._ptr, hk.ptr, hv.ptr, -1 if pos_offset is None else int(pos_offset))
+        off = -1 if pos_offset is None else int(pos_offset)
+        if rope is None:
+            rc = _C.lib.gt_kv_cache_append(self._ptr, hk.ptr, hv.ptr, off)
+        else:
+            r = dict(rope)
+            unknown = set(r) - {"n_dims", "mode", "freq_base", "freq_scale"}
+            if unknown:
+                raise TypeError(f"unknown rope arguments {sorted(unknown)}")
+            rc = _C.lib.gt_kv_cache_append_rope(self._ptr, hk.ptr, hv.ptr, off, int(r.get("n_dims", self.head_dim)),
+                                                int(r.get("mode", 0)), ctypes.c_float(r.get("freq_base", 10000.0)),
+                                                ctypes.c_float(r.get("freq_scale", 1.0)))
         _C.check_rc(rc, "kv_cache")
 
     def attention(self, q: torch.Tensor, scale: float | None = None, is_causal: bool = True) -> torch.Tensor:

@@ -20,7 +20,7 @@ import math
 import torch
 
 from .._bridge import QuantizedTensor
-from .._functions import FlashAttentionFn
+from .._functions import FlashAttentionFn, RoPEFn
 from .. import _ops
 
 
@@ -86,3 +86,12 @@ def scaled_dot_product_attention(
         probs = torch.softmax(scores, dim=-1)
         probs = torch.nn.functional.dropout(probs, p=dropout_p, training=True)
         return probs.matmul(v_u)
+
+
+def rope(input, positions, n_dims: int | None = None, mode: int = 0, n_ctx_orig: int = 0, freq_base: float = 10000.0,
+         freq_scale: float = 1.0):
+    """Rotary position embedding with the reference's signature (gguf_train/nn/functional.py:770-772):
+    input (batch, heads, seq_len, head_dim) or (heads, seq_len, head_dim), positions 1-D (the first
+    seq_len are used); n_dims defaults to head_dim; mode 0 NORMAL, 2 NeoX."""
+    nd = input.shape[-1] if n_dims is None else int(n_dims)
+    return RoPEFn.apply(input, positions, nd, int(mode), int(n_ctx_orig), float(freq_base), float(freq_scale))

@@ -185,6 +185,24 @@ GT_API int gt_flash_attention_backward(const gt_tensor *grad_out, const gt_tenso
 GT_API gt_tensor *gt_attention_weights(const gt_tensor *q, const gt_tensor *k, const gt_tensor *mask,
                                        const gt_tensor *lse, float scale, int is_causal, int average_heads);
 
+/* ---- RoPE ------------------------------------------------------------------------------ */
+
+/* csrc/gguf_train.h:309-310 (implementation csrc/gt_ops_nn.cpp:2298-2421, ggml_rope_ext /
+ * ggml_rope_ext_back with ext_factor 0, attn_factor 1).  x (batch, heads, seq_len, head_dim) or
+ * (heads, seq_len, head_dim), any float dtype and strides; pos 1-D with at least seq_len
+ * positions (the first seq_len are used), any integer or float dtype, read as int32.  mode 0
+ * (NORMAL: pairs (2i, 2i+1)) or 2 (NeoX: pairs (i, i + n_dims/2)); n_dims even in
+ * [2, head_dim]; elements from n_dims on pass through.  Angle of pair i at position p:
+ * freq_scale * p * theta_scale^i in float32 (theta_scale = powf(freq_base, -2/n_dims), the
+ * power taken by repeated float32 products), rotation in float32, result rounded to x's dtype.
+ * The backward rotates by the negated angle.  n_ctx_orig is accepted and unused (YaRN only).
+ * Result: a new dense tensor of x's shape, dtype and device; NULL with the reference's message
+ * on bad arguments. */
+GT_API gt_tensor *gt_rope(const gt_tensor *x, const gt_tensor *pos, int n_dims, int mode, int n_ctx_orig,
+                          float freq_base, float freq_scale);
+GT_API gt_tensor *gt_rope_backward(const gt_tensor *grad_out, const gt_tensor *pos, int n_dims, int mode,
+                                   int n_ctx_orig, float freq_base, float freq_scale);
+
 /* ---- GGUF Q8_0 ------------------------------------------------------------------------ */
 
 /* csrc/gguf_train.h:376 (gt_tensor_to_dtype, csrc/gt_core.cpp:784-847): quantizes rows of
@@ -258,6 +276,13 @@ GT_API gt_tensor *gt_kv_cache_values(const gt_kv_cache *c);
  * gt_llama_forward_logits requires).  Fails without writing when a sequence would pass the
  * capacity.  Returns 0 on success. */
 GT_API int gt_kv_cache_append(gt_kv_cache *c, const gt_tensor *k, const gt_tensor *v, int64_t pos_offset);
+/* No counterpart in the reference ABI (there, gt_rope of the keys, then the cache write inside
+ * llama.cpp): gt_kv_cache_append with the keys rotated on the way in, each key row at its cache
+ * position (the sequence's length + t), with gt_rope's arguments and arithmetic; the cache then
+ * holds exactly what gt_rope followed by gt_kv_cache_append would store.  Values are not
+ * rotated.  q8_0 keys are dequantized, rotated and quantized again. */
+GT_API int gt_kv_cache_append_rope(gt_kv_cache *c, const gt_tensor *k, const gt_tensor *v, int64_t pos_offset,
+                                   int n_dims, int mode, float freq_base, float freq_scale);
 /* Attention of q (batch, H, L, head_dim), H % n_head_kv == 0, over each sequence's cached
  * tokens, query row l of sequence b being its token len_b - L + l (the last L appended).
  * is_causal: a query attends to its own position and the ones before it; otherwise to every

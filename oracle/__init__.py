@@ -2,7 +2,8 @@
 
 numpy front end of oracle/oracle_attn.c (a float64 C restatement of the reference's
 gt_flash_attention, csrc/gt_ops_nn.cpp:2423-2525, of FlashAttentionFn.backward,
-gguf_train/_functions.py:1933-1965, and of the GGUF Q8_0 codec, csrc/gt_core.cpp:800-832).
+gguf_train/_functions.py:1933-1965, of the GGUF Q8_0 codec, csrc/gt_core.cpp:800-832, and of
+gt_rope / gt_rope_backward, csrc/gt_ops_nn.cpp:2298-2421).
 Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg import this package, as
 the checker; the product (gguf_train_amd) never does.
 
@@ -48,6 +49,9 @@ def lib() -> ctypes.CDLL:
         L.oracle_q8_0_quantize.argtypes = [vp, vp, i64]
         L.oracle_q8_0_dequantize.argtypes = [vp, vp, i64]
         L.oracle_max_threads.restype = c_int
+        L.oracle_rope.argtypes = [vp, c_int, i64, i64, i64, i64, vp, c_int, c_int, ctypes.c_float, ctypes.c_float,
+                                  c_int, vp]
+        L.oracle_rope.restype = c_int
         _lib = L
     return _lib
 
@@ -190,6 +194,30 @@ def q8_0_dequantize(blocks) -> np.ndarray:
     y = np.empty(n * 32, dtype=np.float32)
     lib().oracle_q8_0_dequantize(_ptr(b), _ptr(y), n)
     return y
+
+
+# ---- RoPE ----------------------------------------------------------------------------------
+
+def rope(x, pos, n_dims=None, mode: int = 0, freq_base: float = 10000.0, freq_scale: float = 1.0,
+         backward: bool = False):
+    """gt_rope / gt_rope_backward on a dense (B, H, S, D) or (H, S, D) array: the result has x's
+    dtype (float16/bfloat16 as uint16 bit patterns, BF16 in -> BF16 out)."""
+    xa, xc = _code(x)
+    shape = xa.shape
+    if xa.ndim == 3:
+        xa = xa.reshape((1,) + shape)
+    B, H, S, D = xa.shape
+    nd = D if n_dims is None else int(n_dims)
+    p = np.ascontiguousarray(np.asarray(pos)[:S], dtype=np.int32)
+    if p.size < S:
+        raise ValueError("oracle rope: fewer positions than sequence elements")
+    y = np.empty_like(xa)
+    rc = lib().oracle_rope(_ptr(xa), xc, B, H, S, D, _ptr(p), nd, int(mode), float(freq_base), float(freq_scale),
+                           int(bool(backward)), _ptr(y))
+    if rc != 0:
+        raise ValueError("oracle rope: bad n_dims or mode")
+    y = y.reshape(shape)
+    return BF16(y) if isinstance(x, BF16) else y
 
 
 def max_threads() -> int:

@@ -17,6 +17,8 @@
  *   oracle_q8_0_quantize / _dequantize   csrc/gt_core.cpp:800-832 -> ggml quantize_row_q8_0_ref
  *                                        and dequantize_row_q8_0 (ggml @ f3b407ca, tag b12283,
  *                                        not vendored: restated from its published algorithm)
+ *   oracle_rope                          csrc/gt_ops_nn.cpp:2298-2421 -> ggml_rope_ext(_back)
+ *                                        (same ggml, restated from its published algorithm)
  *
  * How each is pinned (tests/test_oracle.py): the converters against numpy float16 and torch
  * bfloat16 over every 16-bit pattern and edge values; the forward against the closed form
@@ -24,7 +26,11 @@
  * fully-masked-row and causal rules, GQA = explicit head repetition; the backward against
  * central finite differences of the forward and against torch.autograd in float64; the Q8_0
  * codec against hand-computed blocks (amax = 127 gives exact integers, d = 0, ties away from
- * zero) and the reference's own accuracy checks (tests/test_numpy_interop.py:443-454).
+ * zero) and the reference's own accuracy checks (tests/test_numpy_interop.py:443-454); RoPE
+ * against the reference's own known-answer test (tests/test_losses_and_rope.py:254-291, the
+ * closed form in float64), the closed form at large positions within the float32 angle
+ * chain's error bound, position 0 = identity, backward = inverse and adjoint, norm kept, NeoX =
+ * NORMAL under the pair permutation, pass-through beyond n_dims (tests/test_oracle_rope.py).
  * Parity unpinned: the byte output of ggml_quantize_chunk itself (ggml cannot be built here),
  * bfloat16 results whose magnitude is below 2^-126 (ggml versions differ on flushing them).
  */
@@ -375,6 +381,51 @@ void oracle_q8_0_dequantize(const uint8_t *in, float *y, int64_t nblocks) {
         const float d = oracle_f16_to_f32((uint16_t)(b[0] | (b[1] << 8)));
         for (int j = 0; j < 32; ++j) y[i * 32 + j] = (float)(int8_t)b[2 + j] * d;
     }
+}
+
+/* RoPE: csrc/gt_ops_nn.cpp:2298-2421 (gt_rope / gt_rope_backward) -> ggml_rope_ext /
+ * ggml_rope_ext_back with ext_factor 0, attn_factor 1, no frequency factors (ggml @ f3b407ca, not
+ * vendored; restated from its published CPU algorithm, ggml_rope_cache_init + rope_yarn):
+ *   theta_scale = powf(freq_base, -2/n_dims); for position p: theta = (float)p, and for pair i
+ *   (i < n_dims/2) angle_i = freq_scale * theta then theta *= theta_scale (float32 each step);
+ *   (c, s) = (cosf, sinf)(angle_i), s negated for the backward.
+ *   NORMAL (mode 0) rotates (x[2i], x[2i+1]), NEOX (mode 2) rotates (x[i], x[i + n_dims/2]):
+ *   y_lo = x_lo*c - x_hi*s, y_hi = x_lo*s + x_hi*c; elements from n_dims on are copied.
+ * x is read as float32 (the reference converts its input to float32) and the result written in
+ * x's dtype.  The two products of each output are formed in double and rounded once to float
+ * (ggml's float32 expression differs from this by at most an ulp of its terms).
+ * x (B, H, S, D) dense; pos[s] is the position of sequence element s. */
+int oracle_rope(const void *x, int x_dtype, int64_t B, int64_t H, int64_t S, int64_t D, const int32_t *pos,
+                int n_dims, int mode, float freq_base, float freq_scale, int backward, void *y) {
+    if (n_dims < 2 || n_dims % 2 || n_dims > D || (mode != 0 && mode != 2)) return -1;
+    const int half = n_dims / 2;
+    const float theta_scale = powf(freq_base, -2.0f / (float)n_dims);
+    float *cs = (float *)malloc(sizeof(float) * 2 * (size_t)(half > 0 ? half : 1));
+    if (!cs) return -1;
+    for (int64_t si = 0; si < S; ++si) {
+        float theta = (float)pos[si];
+        for (int i = 0; i < half; ++i) {
+            const float angle = freq_scale * theta;
+            cs[2 * i] = cosf(angle);
+            cs[2 * i + 1] = backward ? -sinf(angle) : sinf(angle);
+            theta *= theta_scale;
+        }
+        for (int64_t bh = 0; bh < B * H; ++bh) {
+            const int64_t row = (bh * S + si) * D;
+            for (int64_t d = n_dims; d < D; ++d)
+                oracle_write_f64(y, x_dtype, row + d, (double)(float)oracle_read_f64(x, x_dtype, row + d));
+            for (int i = 0; i < half; ++i) {
+                const int64_t a = mode == 2 ? i : 2 * i, b = mode == 2 ? i + half : 2 * i + 1;
+                const double xa = (float)oracle_read_f64(x, x_dtype, row + a);
+                const double xb = (float)oracle_read_f64(x, x_dtype, row + b);
+                const double c = cs[2 * i], sn = cs[2 * i + 1];
+                oracle_write_f64(y, x_dtype, row + a, (double)(float)(xa * c - xb * sn));
+                oracle_write_f64(y, x_dtype, row + b, (double)(float)(xa * sn + xb * c));
+            }
+        }
+    }
+    free(cs);
+    return 0;
 }
 
 int oracle_max_threads(void) {
