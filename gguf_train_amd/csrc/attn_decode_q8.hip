@@ -53,17 +53,9 @@ __device__ inline float hlo(uint32_t a) { return (float)__builtin_bit_cast(half2
 __device__ inline float hhi(uint32_t a) { return (float)__builtin_bit_cast(half2_t, a)[1]; }
 __device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
-// Two int8 values -> packed fp16 (qs + 1152): bytes selected by `sel` from x into the low byte
-// of each half, then the 0x64 exponent and the sign flip.
-__device__ inline uint32_t magic2(uint32_t x, uint32_t sel) { return __builtin_amdgcn_perm(0u, x, sel) ^ 0x64806480u; }
-// selectors: bytes (b0,b1) and (b2,b3) of x into the two halves (0x0c = zero byte)
-constexpr uint32_t kSelLo = 0x0c010c00u;
-constexpr uint32_t kSelHi = 0x0c030c02u;
-
-// 12 loaded bytes -> the 8 quantized values as 4 packed fp16 (qs + 1152) and the raw scale
-// bits (meaningful in the block's first lane).  `odd`: block index odd (see the header).
-__device__ inline void unpack12(u32x3 w, bool odd, u32x4 &mag, uint32_t &dbits) {
-    uint32_t q0, q1;
+// Eight qs bytes of a loaded 12-byte group (`odd`: block index odd, see the header), and the
+// raw fp16 scale bits (meaningful in the block's first lane).
+__device__ inline void extract12(u32x3 w, bool odd, uint32_t &q0, uint32_t &q1, uint32_t &dbits) {
     if (odd) {
         q0 = w[1];
         q1 = w[2];
@@ -73,22 +65,57 @@ __device__ inline void unpack12(u32x3 w, bool odd, u32x4 &mag, uint32_t &dbits) 
         q1 = __builtin_amdgcn_alignbyte(w[2], w[1], 2);
         dbits = w[0] & 0xffffu;
     }
-    mag[0] = magic2(q0, kSelLo);
-    mag[1] = magic2(q0, kSelHi);
-    mag[2] = magic2(q1, kSelLo);
-    mag[3] = magic2(q1, kSelHi);
+}
+
+// Four bytes u = qs + 128 (the sign bit flipped) -> two packed fp16 0x64uu = 1024 + u = qs + 1152:
+// one v_perm_b32 puts two bytes under 0x64 exponent bytes taken from the constant.
+constexpr uint32_t kExp64 = 0x64646464u;
+constexpr uint32_t kSelLo = 0x04010400u;  // (u.b0, 0x64, u.b1, 0x64)
+constexpr uint32_t kSelHi = 0x04030402u;  // (u.b2, 0x64, u.b3, 0x64)
+__device__ inline u32x2 magic4(uint32_t u) {
+    return u32x2{__builtin_amdgcn_perm(kExp64, u, kSelLo), __builtin_amdgcn_perm(kExp64, u, kSelHi)};
+}
+constexpr uint32_t kFlip = 0x80808080u;
+
+typedef int i32x2 __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) i32x2 lds_i32x2;
+__device__ inline u32x2 read_tr8(const uint8_t *p) {
+    return __builtin_bit_cast(
+        u32x2, __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_i32x2 *)(__attribute__((address_space(3))) char *)p));
+}
+
+__device__ inline uint32_t pack_h2(float x, float y) {
+    const half2_t v = {(_Float16)x, (_Float16)y};  // round to nearest even
+    return __builtin_bit_cast(uint32_t, v);
 }
 
 // MASK: 0 = none, 1 = bool bytes, 2 = additive float.
+//
+// Per wave and step of 32 keys (v_mfma_f32_16x16x32_f16 layouts, lane l: A[m = l%16][k = 8(l/16)
+// + 0..7], B[k = 8(l/16) + 0..7][n = l%16], C[m = 4(l/16) + i][n = l%16]):
+//   scores S^T = K . Q^T: A = key rows 16kb + l%16 straight from the loaded blocks, B = Q^T (the
+//     G heads as columns), one MFMA per Q8_0 block; lane l ends with the scores of keys
+//     16kb + 4(l/16) + i of head l%16, and the softmax runs on those in registers.
+//   O^T += V^T . P'^T per Q8_0 block: A = V^T, 16 dims x 32 keys, read from the wave's LDS copy
+//     of its 32 V rows with ds_read_b64_tr_b8 (lane i of a 16-lane group receives byte i of 8
+//     consecutive rows); B = P'^T with P'[key][head] = p * d_v[key][block] rounded to fp16, the
+//     block's scale folded into the probabilities.  The k order of both operands is fixed by
+//     storing key r of the step in LDS row 8((r%16)/4) + 4(r/16) + r%4, so that k-slot e of lane
+//     group g is key 16(e/4) + 4g + e%4: the probabilities a lane already holds.  The bytes are
+//     stored as u = qs + 128, read as fp16 (qs + 1152), and the offset is removed by one more MFMA
+//     per accumulator, -1152 x P'^T.
+//   The rescale of the accumulators by exp2(m_old - m_new) is skipped when no lane's max moved.
 template <int D, int G, int MASK>
-__global__ __launch_bounds__(256, 2) void decode_q8_stream_kernel(DecodeArgs a) {
+__global__ __launch_bounds__(256, 2) void decode_q8_mfma_kernel(DecodeArgs a) {
     constexpr int NB = D / 32;     // Q8_0 blocks per row = k-steps of the score MFMA
     constexpr int RB = NB * 34;    // bytes per row
     constexpr int LPR = D / 8;     // lanes per V row (8 values each)
     constexpr int RPW = 64 / LPR;  // V rows per wave load
     constexpr int NV = 32 / RPW;   // V loads per lane and step
-    __shared__ __attribute__((aligned(16))) float s_p[4][32][G];   // per-wave probabilities
-    __shared__ __attribute__((aligned(16))) float s_d[4][32][NB];  // per-wave K block scales
+    constexpr int VP = D + 16;     // LDS pitch of a staged V row: 16 consecutive rows hit distinct banks
+    __shared__ __attribute__((aligned(16))) uint8_t s_v[4][32 * VP];  // per-wave V bytes u = qs + 128
+    __shared__ __attribute__((aligned(16))) float s_dv[4][NB][32];    // per-wave V block scales (k-slot rows)
+    __shared__ __attribute__((aligned(16))) float s_d[4][32][NB];     // per-wave K block scales
     __shared__ float s_m[4][G], s_l[4][G];
     __shared__ float s_o[4][G][D];
 
@@ -106,7 +133,7 @@ __global__ __launch_bounds__(256, 2) void decode_q8_stream_kernel(DecodeArgs a) 
     const int nsteps = kend > kbeg ? (kend - kbeg + kStep - 1) / kStep : 0;
 
     // B operand (Q^T, fp16): lane holds Q[head l16][32t + 8 q4 + 0..7]; columns l16 >= G repeat
-    // head G-1 and are discarded.  cq[t]: sum of block t of head l16's query.
+    // head G-1 and are discarded.  cq[t]: 1152 x the sum of block t of head l16's query.
     half8_t qb[NB];
     float cq[NB];
     {
@@ -157,30 +184,38 @@ __global__ __launch_bounds__(256, 2) void decode_q8_stream_kernel(DecodeArgs a) 
 
     const float cs = f.scale * kLog2e;
     const int64_t mrow = b * f.m_sb + (hk * G + min(l16, G - 1)) * f.m_sh;
+    const half8_t neg_magic = {(_Float16)-kMagic, (_Float16)-kMagic, (_Float16)-kMagic, (_Float16)-kMagic,
+                               (_Float16)-kMagic, (_Float16)-kMagic, (_Float16)-kMagic, (_Float16)-kMagic};
     float m = -INFINITY;  // running max of head l16 (log2 domain)
     float lsum = 0.0f;    // running sum of head l16
-    float acc[G][8];      // unnormalised sum of p d (qs + 1152), dims 8 sub .. +7, this lane's rows
-    float csum[G];        // sum of p d over this lane's rows (the offset to remove)
+    f32x4 acc[NB][2];     // O^T[32 blk + 16 h + 4 q4 + i][head l16], unnormalised
 #pragma unroll
-    for (int h = 0; h < G; ++h) {
-        csum[h] = 0.0f;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) acc[h][j] = 0.0f;
-    }
+    for (int t = 0; t < NB; ++t) acc[t][0] = acc[t][1] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    uint8_t *vt = s_v[w];
 
     auto compute = [&](int step, const Tile &tl) {
         const int k0 = kbeg + step * kStep + 32 * w;
-        // K operands and scales
+        // ---- V rows of the step into LDS (k-slot order) with their scales ----
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            const int r = RPW * i + vrow;
+            const int rho = 8 * ((r & 15) >> 2) + 4 * (r >> 4) + (r & 3);
+            uint32_t q0, q1, db;
+            extract12(tl.v[i], vblk & 1, q0, q1, db);
+            *(u32x2 *)(vt + rho * VP + 8 * sub) = u32x2{q0 ^ kFlip, q1 ^ kFlip};
+            if (vpart == 0) s_dv[w][vblk][rho] = h2f(db);
+        }
+        // ---- scores ----
         half8_t ka[2][NB];
         float dk[2][NB];
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
             for (int t = 0; t < NB; ++t) {
-                u32x4 mag;
-                uint32_t db;
-                unpack12(tl.k[kb][t], t & 1, mag, db);
-                ka[kb][t] = __builtin_bit_cast(half8_t, mag);
+                uint32_t q0, q1, db;
+                extract12(tl.k[kb][t], t & 1, q0, q1, db);
+                const u32x2 lo = magic4(q0 ^ kFlip), hi = magic4(q1 ^ kFlip);
+                ka[kb][t] = __builtin_bit_cast(half8_t, u32x4{lo[0], lo[1], hi[0], hi[1]});
                 dk[kb][t] = h2f(db);
             }
         if (q4 == 0) {
@@ -189,7 +224,259 @@ __global__ __launch_bounds__(256, 2) void decode_q8_stream_kernel(DecodeArgs a) 
 #pragma unroll
                 for (int t = 0; t < NB; ++t) s_d[w][16 * kb + l16][t] = dk[kb][t];
         }
-        __builtin_amdgcn_wave_barrier();  // s_d written by this wave before it is read
+        __builtin_amdgcn_wave_barrier();  // LDS written by this wave before it is read
+        float sc[2][4];
+        float cm = -INFINITY;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+            f32x4 sum4 = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int t = 0; t < NB; ++t) {
+                const f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
+                const f32x4 c4 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[kb][t], qb[t], z, 0, 0, 0);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) sum4[i] = fmaf(s_d[w][16 * kb + 4 * q4 + i][t], c4[i] - cq[t], sum4[i]);
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int key = k0 + 16 * kb + 4 * q4 + i;
+                float x = sum4[i] * cs;
+                bool blocked = key >= kend || l16 >= G;
+                if (MASK != 0) {
+                    const int64_t mi = mrow + (int64_t)min(key, S - 1) * f.m_ss;
+                    if (MASK == 1) blocked = blocked || !((const uint8_t *)f.mask)[mi];
+                    else x = fmaf(((const float *)f.mask)[mi], kLog2e, x);
+                }
+                x = blocked ? -INFINITY : x;
+                sc[kb][i] = x;
+                cm = fmaxf(cm, x);
+            }
+        }
+        // ---- online softmax of head l16 over the step ----
+        cm = fmaxf(cm, __shfl_xor(cm, 16, 64));
+        cm = fmaxf(cm, __shfl_xor(cm, 32, 64));
+        const float mnew = fmaxf(m, cm);
+        const float msub = mnew == -INFINITY ? 0.0f : mnew;
+        const float alpha = mnew == -INFINITY ? 1.0f : fast_exp2(m - mnew);  // m = -inf: 0
+        m = mnew;
+        float ps = 0.0f;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                sc[kb][i] = fast_exp2(sc[kb][i] - msub);  // -inf -> 0
+                ps += sc[kb][i];
+            }
+        ps += __shfl_xor(ps, 16, 64);
+        ps += __shfl_xor(ps, 32, 64);
+        lsum = fmaf(lsum, alpha, ps);
+        if (__builtin_amdgcn_ballot_w64(alpha != 1.0f) != 0) {
+#pragma unroll
+            for (int t = 0; t < NB; ++t) {
+                acc[t][0] *= alpha;
+                acc[t][1] *= alpha;
+            }
+        }
+        // ---- P.V on MFMA ----
+#pragma unroll
+        for (int t = 0; t < NB; ++t) {
+            const f32x4 dv0 = *(const f32x4 *)&s_dv[w][t][8 * q4], dv1 = *(const f32x4 *)&s_dv[w][t][8 * q4 + 4];
+            u32x4 pw;  // k-slot e = 4 kb + i: key 16 kb + 4 q4 + i, scale of k-slot row 8 q4 + e
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                pw[j] = pack_h2(sc[0][2 * j] * dv0[2 * j], sc[0][2 * j + 1] * dv0[2 * j + 1]);
+                pw[j + 2] = pack_h2(sc[1][2 * j] * dv1[2 * j], sc[1][2 * j + 1] * dv1[2 * j + 1]);
+            }
+            const half8_t bp = __builtin_bit_cast(half8_t, pw);
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const u32x2 raw = read_tr8(vt + (8 * q4 + (l16 >> 1)) * VP + 32 * t + 16 * h + 8 * (l16 & 1));
+                const uint32_t r0 = raw[0], r1 = raw[1];  // through scalars (see extract12's caller)
+                const u32x2 lo = magic4(r0), hi = magic4(r1);
+                const half8_t av = __builtin_bit_cast(half8_t, u32x4{lo[0], lo[1], hi[0], hi[1]});
+                acc[t][h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bp, acc[t][h], 0, 0, 0);
+            }
+#pragma unroll
+            for (int h = 0; h < 2; ++h) acc[t][h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(neg_magic, bp, acc[t][h], 0, 0, 0);
+        }
+        __builtin_amdgcn_wave_barrier();  // LDS read before the next step overwrites it
+    };
+
+    // The loads are unconditional (rows past the split are clamped reads of valid rows): with a
+    // branch around them the compiler's load counters cannot tell which loads are in flight and
+    // would wait for the prefetched step too.
+    Tile ta, tb;
+    load(0, ta);
+    for (int st = 0; st < nsteps; st += 2) {
+        load(st + 1, tb);
+        __builtin_amdgcn_sched_barrier(0);
+        compute(st, ta);
+        load(st + 2, ta);
+        __builtin_amdgcn_sched_barrier(0);
+        if (st + 1 < nsteps) compute(st + 1, tb);
+    }
+
+    // ---- combine the four waves ----
+    if (lane < G) {
+        s_m[w][lane] = m;
+        s_l[w][lane] = lsum;
+    }
+    if (l16 < G) {
+#pragma unroll
+        for (int t = 0; t < NB; ++t)
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) s_o[w][l16][32 * t + 16 * h + 4 * q4 + i] = acc[t][h][i];
+    }
+    __syncthreads();
+    for (int e = tid; e < G * D; e += 256) {
+        const int h = e / D, d = e % D;
+        const float M = fmaxf(fmaxf(s_m[0][h], s_m[1][h]), fmaxf(s_m[2][h], s_m[3][h]));
+        float o = 0.0f, L = 0.0f;
+#pragma unroll
+        for (int ww = 0; ww < 4; ++ww) {
+            const float wg = s_m[ww][h] == -INFINITY ? 0.0f : fast_exp2(s_m[ww][h] - M);
+            o = fmaf(wg, s_o[ww][h][d], o);
+            L = fmaf(wg, s_l[ww][h], L);
+        }
+        const int64_t row = b * f.H + hk * G + h;
+        if (a.nsplit == 1) {
+            ((_Float16 *)f.o)[row * D + d] = (_Float16)(L > 0.0f ? o / L : 0.0f);
+            if (f.lse && d == 0) ((float *)f.lse)[row] = L > 0.0f ? (M + log2f(L)) * kLn2 : INFINITY;
+        } else {
+            const int64_t pr = row * a.nsplit + split;
+            a.part_o[pr * D + d] = o;
+            if (d == 0) {
+                a.part_ml[pr * 2 + 0] = M;
+                a.part_ml[pr * 2 + 1] = L;
+            }
+        }
+    }
+}
+
+// Streaming variant: each wavefront's 32 K rows and 32 V rows of a step (34 D / 32 bytes each,
+// so a step's rows are one contiguous span per tensor) are read with 16-byte loads, 1 KiB per
+// instruction, so every request the memory pipeline sees is a whole run of cache lines, and
+// written raw into the wave's LDS tile; the next step's loads are in flight in registers while
+// this step is computed from LDS.  Operands come from the raw rows:
+//   K (scores): the 12-byte windows of the register variant, read as dwords from LDS;
+//   V^T (P.V MFMA A operand): byte e of lane (g = l/16, m = l%16) is row key(g, e) of dim
+//     32 blk + 16 h + m, one ds_read_u8 each, packed as fp16 (qs + 1152);
+//   the V block scales are read once per (row, block) into a small table, zero for keys past
+//     the end (their rows may be clamped copies).
+// Needs 16-byte aligned K/V bases and (b, kv head) slices of a multiple of 16 bytes.
+template <int D, int G, int MASK>
+__global__ __launch_bounds__(256, 2) void decode_q8_lds_kernel(DecodeArgs a) {
+    constexpr int NB = D / 32;                // Q8_0 blocks per row
+    constexpr int RB = NB * 34;               // bytes per row
+    constexpr int TB = 32 * RB;               // bytes of a wave's 32 rows (a multiple of 16)
+    constexpr int NL = (TB + 1023) / 1024;    // 16-byte loads per lane and tile
+    constexpr int SV = NB * 32 / 64;          // V scales read per lane and step
+    __shared__ __attribute__((aligned(16))) uint8_t s_raw[4][2][NL * 1024];  // [wave][K, V]
+    __shared__ __attribute__((aligned(16))) float s_dv[4][NB][32];       // V scales by row
+    __shared__ __attribute__((aligned(16))) float s_d[4][32][NB];        // K scales by row
+    __shared__ float s_m[4][G], s_l[4][G];
+    static_assert(G * D * 4 <= 2 * NL * 1024, "s_o alias");
+
+    const AttnFwdArgs &f = a.f;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int l16 = lane & 15, q4 = lane >> 4;
+    const int split = blockIdx.x;
+    const int64_t bk = blockIdx.y, b = bk / f.Hkv, hk = bk % f.Hkv;
+    const int S = (int)f.S;
+    const int span = ((S + kStep - 1) / kStep + a.nsplit - 1) / a.nsplit * kStep;
+    const int kbeg = split * span, kend = min(attn_decode_end(f, b), kbeg + span);
+    const int nsteps = kend > kbeg ? (kend - kbeg + kStep - 1) / kStep : 0;
+
+    half8_t qb[NB];
+    float cq[NB];
+    {
+        const _Float16 *qr = (const _Float16 *)f.q + b * f.q_sb + (hk * G + min(l16, G - 1)) * f.q_sh + 8 * q4;
+#pragma unroll
+        for (int t = 0; t < NB; ++t) {
+            const u32x4 x = *(const u32x4 *)(qr + 32 * t);
+            qb[t] = __builtin_bit_cast(half8_t, x);
+            float c = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const uint32_t xe = x[e];  // through a scalar: bit-casting a vector element reads element 0
+                c += hlo(xe) + hhi(xe);
+            }
+            c += __shfl_xor(c, 16, 64);
+            c += __shfl_xor(c, 32, 64);
+            cq[t] = kMagic * c;
+        }
+    }
+
+    const int64_t slice = (b * f.Hkv + hk) * (int64_t)S * RB;
+    const uint8_t *kbase = (const uint8_t *)f.k + slice;
+    const uint8_t *vbase = (const uint8_t *)f.v + slice;
+    const uint32_t last16 = (uint32_t)S * RB - 16;  // last 16-byte piece of the slice
+    // the lane's pieces of the wave's K and V tiles of `step` (pieces past the slice read its last
+    // piece; pieces past the tile land in the LDS tile's slack and are never read)
+    u32x4 rk[NL], rv[NL];
+    auto load = [&](int step) {
+        const uint32_t t0 = (uint32_t)(kbeg + step * kStep + 32 * w) * RB;
+#pragma unroll
+        for (int j = 0; j < NL; ++j) {
+            const uint32_t off = min(t0 + 1024u * j + 16u * lane, last16);
+            rk[j] = __builtin_nontemporal_load((const u32x4 *)(kbase + off));
+            rv[j] = __builtin_nontemporal_load((const u32x4 *)(vbase + off));
+        }
+    };
+    auto stage = [&]() {
+#pragma unroll
+        for (int j = 0; j < NL; ++j) {
+            *(u32x4 *)&s_raw[w][0][1024 * j + 16 * lane] = rk[j];
+            *(u32x4 *)&s_raw[w][1][1024 * j + 16 * lane] = rv[j];
+        }
+    };
+
+    auto in_row = [](int blk, int part) { return 34 * blk + 8 * part - ((blk & 1) ? 2 : 0); };
+    const float cs = f.scale * kLog2e;
+    const int64_t mrow = b * f.m_sb + (hk * G + min(l16, G - 1)) * f.m_sh;
+    const half8_t neg_magic = {(_Float16)-kMagic, (_Float16)-kMagic, (_Float16)-kMagic, (_Float16)-kMagic,
+                               (_Float16)-kMagic, (_Float16)-kMagic, (_Float16)-kMagic, (_Float16)-kMagic};
+    float m = -INFINITY, lsum = 0.0f;
+    f32x4 acc[NB][2];
+#pragma unroll
+    for (int t = 0; t < NB; ++t) acc[t][0] = acc[t][1] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    auto compute = [&](int step) {
+        const int k0 = kbeg + step * kStep + 32 * w;
+        const uint8_t *kt = s_raw[w][0];
+        const uint8_t *vt = s_raw[w][1];
+        // ---- V block scales of the step (zero past the end: those rows may be clamped copies) ----
+#pragma unroll
+        for (int j = 0; j < SV; ++j) {
+            const int idx = lane + 64 * j, r = idx & 31, t = idx >> 5;
+            const float d = h2f(*(const uint16_t *)(vt + r * RB + 34 * t));
+            s_dv[w][t][r] = k0 + r < kend ? d : 0.0f;
+        }
+        // ---- scores ----
+        half8_t ka[2][NB];
+        float dk[2][NB];
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int t = 0; t < NB; ++t) {
+                const uint32_t *p = (const uint32_t *)(kt + (16 * kb + l16) * RB + in_row(t, q4));
+                const u32x3 win = {p[0], p[1], p[2]};
+                uint32_t q0, q1, db;
+                extract12(win, t & 1, q0, q1, db);
+                const u32x2 lo = magic4(q0 ^ kFlip), hi = magic4(q1 ^ kFlip);
+                ka[kb][t] = __builtin_bit_cast(half8_t, u32x4{lo[0], lo[1], hi[0], hi[1]});
+                dk[kb][t] = h2f(db);
+            }
+        if (q4 == 0) {
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                for (int t = 0; t < NB; ++t) s_d[w][16 * kb + l16][t] = dk[kb][t];
+        }
+        __builtin_amdgcn_wave_barrier();
         float sc[2][4];
         float cm = -INFINITY;
 #pragma unroll
@@ -221,91 +508,85 @@ __global__ __launch_bounds__(256, 2) void decode_q8_stream_kernel(DecodeArgs a) 
         cm = fmaxf(cm, __shfl_xor(cm, 32, 64));
         const float mnew = fmaxf(m, cm);
         const float msub = mnew == -INFINITY ? 0.0f : mnew;
-        const float alpha = mnew == -INFINITY ? 1.0f : fast_exp2(m - mnew);  // m = -inf: 0
+        const float alpha = mnew == -INFINITY ? 1.0f : fast_exp2(m - mnew);
         m = mnew;
         float ps = 0.0f;
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                sc[kb][i] = fast_exp2(sc[kb][i] - msub);  // -inf -> 0
+                sc[kb][i] = fast_exp2(sc[kb][i] - msub);
                 ps += sc[kb][i];
             }
         ps += __shfl_xor(ps, 16, 64);
         ps += __shfl_xor(ps, 32, 64);
         lsum = fmaf(lsum, alpha, ps);
-        if (l16 < G) {
+        if (__builtin_amdgcn_ballot_w64(alpha != 1.0f) != 0) {
 #pragma unroll
-            for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) s_p[w][16 * kb + 4 * q4 + i][l16] = sc[kb][i];
-        }
-        float al[G];
-#pragma unroll
-        for (int h = 0; h < G; ++h) al[h] = __shfl(alpha, h, 64);
-        __builtin_amdgcn_wave_barrier();  // s_p written by this wave before it is read
-#pragma unroll
-        for (int h = 0; h < G; ++h) {
-            csum[h] *= al[h];
-#pragma unroll
-            for (int j = 0; j < 8; ++j) acc[h][j] *= al[h];
-        }
-#pragma unroll
-        for (int i = 0; i < NV; ++i) {
-            const int r = RPW * i + vrow;
-            u32x4 mag;
-            uint32_t db;
-            unpack12(tl.v[i], vblk & 1, mag, db);
-            // the block's scale sits in the first lane of each group of 4 (quad broadcast)
-            const float dv = h2f((uint32_t)__builtin_amdgcn_mov_dpp((int)db, 0x00, 0xf, 0xf, false));
-#pragma unroll
-            for (int h = 0; h < G; ++h) {
-                const float pd = s_p[w][r][h] * dv;
-                csum[h] += pd;
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const uint32_t mj = mag[j];
-                    acc[h][2 * j] = fmaf(pd, hlo(mj), acc[h][2 * j]);
-                    acc[h][2 * j + 1] = fmaf(pd, hhi(mj), acc[h][2 * j + 1]);
-                }
+            for (int t = 0; t < NB; ++t) {
+                acc[t][0] *= alpha;
+                acc[t][1] *= alpha;
             }
         }
-        __builtin_amdgcn_wave_barrier();  // s_p / s_d read before the next step overwrites them
+        // ---- P.V: k-slot e of lane group q4 is key 16(e/4) + 4 q4 + e%4 ----
+#pragma unroll
+        for (int t = 0; t < NB; ++t) {
+            const f32x4 dv0 = *(const f32x4 *)&s_dv[w][t][4 * q4], dv1 = *(const f32x4 *)&s_dv[w][t][16 + 4 * q4];
+            u32x4 pw;
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                pw[j] = pack_h2(sc[0][2 * j] * dv0[2 * j], sc[0][2 * j + 1] * dv0[2 * j + 1]);
+                pw[j + 2] = pack_h2(sc[1][2 * j] * dv1[2 * j], sc[1][2 * j + 1] * dv1[2 * j + 1]);
+            }
+            const half8_t bp = __builtin_bit_cast(half8_t, pw);
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const uint8_t *col = vt + 34 * t + 2 + 16 * h + l16;
+                uint32_t by[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) by[e] = col[(16 * (e >> 2) + 4 * q4 + (e & 3)) * RB];
+                u32x4 av;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) av[j] = (by[2 * j] | (by[2 * j + 1] << 16)) ^ 0x64806480u;
+                acc[t][h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, av), bp, acc[t][h], 0,
+                                                                   0, 0);
+            }
+#pragma unroll
+            for (int h = 0; h < 2; ++h) acc[t][h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(neg_magic, bp, acc[t][h], 0, 0, 0);
+        }
     };
 
-    Tile ta, tb;
-    if (nsteps > 0) load(0, ta);
-    for (int st = 0; st < nsteps; st += 2) {
-        if (st + 1 < nsteps) load(st + 1, tb);
+    // The wave's LDS tile holds the step being computed; the registers hold the next one in
+    // flight.  Loads are unconditional (clamped) so the compiler's load counters stay exact.
+    load(0);
+    for (int st = 0; st < nsteps; ++st) {
+        __builtin_amdgcn_wave_barrier();  // the previous step's LDS reads come before the overwrite
+        stage();
         __builtin_amdgcn_sched_barrier(0);
-        compute(st, ta);
-        if (st + 1 < nsteps) {
-            if (st + 2 < nsteps) load(st + 2, ta);
-            __builtin_amdgcn_sched_barrier(0);
-            compute(st + 1, tb);
-        }
+        load(st + 1);
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_wave_barrier();
+        compute(st);
     }
 
-    // ---- remove the offset, combine the four waves ----
-#pragma unroll
-    for (int h = 0; h < G; ++h)
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            acc[h][j] = fmaf(-kMagic, csum[h], acc[h][j]);
-#pragma unroll
-            for (int mm = LPR; mm < 64; mm <<= 1) acc[h][j] += __shfl_xor(acc[h][j], mm, 64);
-        }
+    // ---- combine the four waves (each wave's partial O goes into its own LDS tile) ----
+    constexpr int WSTRIDE = 2 * NL * 1024 / 4;  // floats per wave region
+    float *my_o = reinterpret_cast<float *>(&s_raw[w][0][0]);
+    __builtin_amdgcn_wave_barrier();
     if (lane < G) {
         s_m[w][lane] = m;
         s_l[w][lane] = lsum;
     }
-    if (lane < LPR) {
+    if (l16 < G) {
 #pragma unroll
-        for (int h = 0; h < G; ++h)
+        for (int t = 0; t < NB; ++t)
 #pragma unroll
-            for (int j = 0; j < 8; ++j) s_o[w][h][8 * sub + j] = acc[h][j];
+            for (int h = 0; h < 2; ++h)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) my_o[l16 * D + 32 * t + 16 * h + 4 * q4 + i] = acc[t][h][i];
     }
     __syncthreads();
+    const float *o_all = reinterpret_cast<const float *>(&s_raw[0][0][0]);
     for (int e = tid; e < G * D; e += 256) {
         const int h = e / D, d = e % D;
         const float M = fmaxf(fmaxf(s_m[0][h], s_m[1][h]), fmaxf(s_m[2][h], s_m[3][h]));
@@ -313,7 +594,7 @@ __global__ __launch_bounds__(256, 2) void decode_q8_stream_kernel(DecodeArgs a) 
 #pragma unroll
         for (int ww = 0; ww < 4; ++ww) {
             const float wg = s_m[ww][h] == -INFINITY ? 0.0f : fast_exp2(s_m[ww][h] - M);
-            o = fmaf(wg, s_o[ww][h][d], o);
+            o = fmaf(wg, o_all[ww * WSTRIDE + h * D + d], o);
             L = fmaf(wg, s_l[ww][h], L);
         }
         const int64_t row = b * f.H + hk * G + h;
@@ -331,25 +612,34 @@ __global__ __launch_bounds__(256, 2) void decode_q8_stream_kernel(DecodeArgs a) 
     }
 }
 
-template <int D>
+template <int D, bool LDS>
 const void *q8_kernel_d(const AttnFwdArgs &f, int G) {
     const int mode = !f.mask ? 0 : (f.mask_bool ? 1 : 2);
-#define GT_QK(GG) \
-    (mode == 0 ? (const void *)decode_q8_stream_kernel<D, GG, 0> \
-               : mode == 1 ? (const void *)decode_q8_stream_kernel<D, GG, 1> : (const void *)decode_q8_stream_kernel<D, GG, 2>)
+#define GT_QK(K, GG) \
+    (mode == 0 ? (const void *)K<D, GG, 0> : mode == 1 ? (const void *)K<D, GG, 1> : (const void *)K<D, GG, 2>)
+#define GT_QG(GG) (LDS ? GT_QK(decode_q8_lds_kernel, GG) : GT_QK(decode_q8_mfma_kernel, GG))
     switch (G) {
-        case 1: return GT_QK(1);
-        case 2: return GT_QK(2);
-        case 4: return GT_QK(4);
-        case 8: return GT_QK(8);
+        case 1: return GT_QG(1);
+        case 2: return GT_QG(2);
+        case 4: return GT_QG(4);
+        case 8: return GT_QG(8);
         default: return nullptr;
     }
+#undef GT_QG
 #undef GT_QK
+}
+
+// The streaming kernel reads 16-byte pieces of each (b, kv head) slice: bases 16-byte aligned and
+// slices a multiple of 16 bytes.
+bool q8_stream_ok(const AttnFwdArgs &f) {
+    const int64_t slice = f.S * (f.D / 32 * 34);
+    return slice % 16 == 0 && (uintptr_t)f.k % 16 == 0 && (uintptr_t)f.v % 16 == 0;
 }
 
 const void *q8_kernel(const AttnFwdArgs &f) {
     const int G = (int)(f.H / f.Hkv);
-    return f.D == 128 ? q8_kernel_d<128>(f, G) : q8_kernel_d<64>(f, G);
+    if (q8_stream_ok(f)) return f.D == 128 ? q8_kernel_d<128, true>(f, G) : q8_kernel_d<64, true>(f, G);
+    return f.D == 128 ? q8_kernel_d<128, false>(f, G) : q8_kernel_d<64, false>(f, G);
 }
 
 // Workgroups of `kernel` the device runs at once (CUs x resident workgroups per CU), cached.
