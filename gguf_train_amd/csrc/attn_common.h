@@ -65,7 +65,10 @@ struct DecodeArgs {
     float *part_o;   // (B*H, nsplit, D) unnormalised chunk outputs
     float *part_ml;  // (B*H, nsplit, 2) chunk max (log2 domain) and sum of exp2
     int nsplit;
+    int *counters;   // (B*Hkv) zeroed arrival counters in uncached memory (part_o / part_ml then too):
+                     // the last split merges in the kernel; null: a merge launch
 };
+
 
 // Launchers.  `cd` is the compute dtype of q/k/v (GT_F32/GT_F16/GT_BF16/GT_F64).
 hipError_t launch_attn_generic_fwd(const AttnFwdArgs &a, int cd, hipStream_t s);

@@ -18,6 +18,7 @@
 // A second kernel merges the per-chunk (max, sum, unnormalised O) partials of each row.
 
 #include "attn_common.h"
+#include "decode_merge.h"
 #include "gt_internal.h"
 
 #include <algorithm>
@@ -264,7 +265,9 @@ __global__ __launch_bounds__(256, 2) void decode_stream_kernel(DecodeArgs a) {
         __builtin_amdgcn_wave_barrier();  // s_p read before the next step overwrites it
     };
 
-    // two tiles in flight, unrolled by two so they swap roles without copies
+    // two tiles in flight, unrolled by two so they swap roles without copies.  (Measured: issuing
+    // the prefetch under these branches, which makes the compiler wait for it as well, is faster
+    // on this kernel than keeping it in flight across the compute.)
     Tile ta, tb;
     if (nsteps > 0) load(0, ta);
     for (int st = 0; st < nsteps; st += 2) {
@@ -320,6 +323,7 @@ __global__ __launch_bounds__(256, 2) void decode_stream_kernel(DecodeArgs a) {
             }
         }
     }
+    if (a.nsplit > 1 && a.counters) gtdecode::finish_split<T, D>(a, bk, b * f.H + hk * G, G);
 }
 
 // D = 256: a key row is split over D/8 lanes (16-byte loads), dot products reduced across lanes.
@@ -536,8 +540,8 @@ hipError_t launch_typed(const DecodeArgs &a, hipStream_t s) {
         hipLaunchKernelGGL((decode_rows_kernel<T, D, G>), grid, dim3(256), 0, s, a);
     }
     hipError_t e = hipGetLastError();
-    // one split of the streaming kernel: it wrote the output itself
-    if (e != hipSuccess || (D <= 128 && a.nsplit == 1)) return e;
+    // one split of the streaming kernel, or its last split merged in the kernel: it wrote the output
+    if (e != hipSuccess || (D <= 128 && (a.nsplit == 1 || a.counters))) return e;
     const int64_t rows = a.f.B * a.f.H;
     hipLaunchKernelGGL((decode_merge_kernel<T, D>), dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, s, a);
     return hipGetLastError();

@@ -27,6 +27,7 @@
 //           offset 1152 sum (p d) is subtracted once at the end.
 
 #include "attn_common.h"
+#include "decode_merge.h"
 #include "gt_internal.h"
 
 #include <algorithm>
@@ -166,7 +167,8 @@ __global__ __launch_bounds__(256, 2) void decode_q8_mfma_kernel(DecodeArgs a) {
         u32x3 v[NV];     // V row RPW*i + vrow of the wave's 32, block vblk, part vpart
     };
     auto load = [&](int step, Tile &tl) {
-        const int k0 = kbeg + step * kStep + 32 * w;
+        // steps past the split re-read its last step (cache hits) instead of new lines
+        const int k0 = kbeg + min(step, max(nsteps - 1, 0)) * kStep + 32 * w;
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb) {
             const uint32_t row = (uint32_t)min(k0 + 16 * kb + l16, S - 1) * RB;
@@ -353,6 +355,25 @@ __global__ __launch_bounds__(256, 2) void decode_q8_mfma_kernel(DecodeArgs a) {
             }
         }
     }
+    if (a.nsplit > 1 && a.counters) gtdecode::finish_split<_Float16, D>(a, bk, b * f.H + hk * G, G);
+}
+
+// Reductions over lanes l, l ^ 16 and l, l ^ 32 with v_permlane16/32_swap (VALU, no LDS).
+__device__ inline float max_x16(float v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ inline float max_x32(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ inline float sum_x16(float v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ inline float sum_x32(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
 // Streaming variant: each wavefront's 32 K rows and 32 V rows of a step (34 D / 32 bytes each,
@@ -375,7 +396,6 @@ __global__ __launch_bounds__(256, 2) void decode_q8_lds_kernel(DecodeArgs a) {
     constexpr int SV = NB * 32 / 64;          // V scales read per lane and step
     __shared__ __attribute__((aligned(16))) uint8_t s_raw[4][2][NL * 1024];  // [wave][K, V]
     __shared__ __attribute__((aligned(16))) float s_dv[4][NB][32];       // V scales by row
-    __shared__ __attribute__((aligned(16))) float s_d[4][32][NB];        // K scales by row
     __shared__ float s_m[4][G], s_l[4][G];
     static_assert(G * D * 4 <= 2 * NL * 1024, "s_o alias");
 
@@ -391,24 +411,20 @@ __global__ __launch_bounds__(256, 2) void decode_q8_lds_kernel(DecodeArgs a) {
     const int nsteps = kend > kbeg ? (kend - kbeg + kStep - 1) / kStep : 0;
 
     half8_t qb[NB];
-    float cq[NB];
+    f32x4 c0[NB];  // -1152 x the block sums of each head's query: the score MFMA's initial value
     {
         const _Float16 *qr = (const _Float16 *)f.q + b * f.q_sb + (hk * G + min(l16, G - 1)) * f.q_sh + 8 * q4;
 #pragma unroll
         for (int t = 0; t < NB; ++t) {
             const u32x4 x = *(const u32x4 *)(qr + 32 * t);
             qb[t] = __builtin_bit_cast(half8_t, x);
-            float c = 0.0f;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const uint32_t xe = x[e];  // through a scalar: bit-casting a vector element reads element 0
-                c += hlo(xe) + hhi(xe);
-            }
-            c += __shfl_xor(c, 16, 64);
-            c += __shfl_xor(c, 32, 64);
-            cq[t] = kMagic * c;
         }
     }
+    const half8_t neg_magic = {(_Float16)-kMagic, (_Float16)-kMagic, (_Float16)-kMagic, (_Float16)-kMagic,
+                               (_Float16)-kMagic, (_Float16)-kMagic, (_Float16)-kMagic, (_Float16)-kMagic};
+#pragma unroll
+    for (int t = 0; t < NB; ++t)
+        c0[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(neg_magic, qb[t], f32x4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
 
     const int64_t slice = (b * f.Hkv + hk) * (int64_t)S * RB;
     const uint8_t *kbase = (const uint8_t *)f.k + slice;
@@ -437,8 +453,6 @@ __global__ __launch_bounds__(256, 2) void decode_q8_lds_kernel(DecodeArgs a) {
     auto in_row = [](int blk, int part) { return 34 * blk + 8 * part - ((blk & 1) ? 2 : 0); };
     const float cs = f.scale * kLog2e;
     const int64_t mrow = b * f.m_sb + (hk * G + min(l16, G - 1)) * f.m_sh;
-    const half8_t neg_magic = {(_Float16)-kMagic, (_Float16)-kMagic, (_Float16)-kMagic, (_Float16)-kMagic,
-                               (_Float16)-kMagic, (_Float16)-kMagic, (_Float16)-kMagic, (_Float16)-kMagic};
     float m = -INFINITY, lsum = 0.0f;
     f32x4 acc[NB][2];
 #pragma unroll
@@ -456,8 +470,21 @@ __global__ __launch_bounds__(256, 2) void decode_q8_lds_kernel(DecodeArgs a) {
             s_dv[w][t][r] = k0 + r < kend ? d : 0.0f;
         }
         // ---- scores ----
+        // K block scales of the C rows (keys 16 kb + 4 q4 + i): d of block 2p is the low half of the
+        // dword at 68 p of the row, d of block 2p + 1 the high half of the dword 32 bytes later
+        float dk[2][4][NB];
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t *row = (const uint32_t *)(kt + (16 * kb + 4 * q4 + i) * RB);
+#pragma unroll
+                for (int p2 = 0; p2 < NB / 2; ++p2) {
+                    dk[kb][i][2 * p2] = h2f(row[17 * p2] & 0xffffu);
+                    dk[kb][i][2 * p2 + 1] = h2f(row[17 * p2 + 8] >> 16);
+                }
+            }
         half8_t ka[2][NB];
-        float dk[2][NB];
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
@@ -468,15 +495,7 @@ __global__ __launch_bounds__(256, 2) void decode_q8_lds_kernel(DecodeArgs a) {
                 extract12(win, t & 1, q0, q1, db);
                 const u32x2 lo = magic4(q0 ^ kFlip), hi = magic4(q1 ^ kFlip);
                 ka[kb][t] = __builtin_bit_cast(half8_t, u32x4{lo[0], lo[1], hi[0], hi[1]});
-                dk[kb][t] = h2f(db);
             }
-        if (q4 == 0) {
-#pragma unroll
-            for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-                for (int t = 0; t < NB; ++t) s_d[w][16 * kb + l16][t] = dk[kb][t];
-        }
-        __builtin_amdgcn_wave_barrier();
         float sc[2][4];
         float cm = -INFINITY;
 #pragma unroll
@@ -484,10 +503,9 @@ __global__ __launch_bounds__(256, 2) void decode_q8_lds_kernel(DecodeArgs a) {
             f32x4 sum4 = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (int t = 0; t < NB; ++t) {
-                const f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
-                const f32x4 c4 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[kb][t], qb[t], z, 0, 0, 0);
+                const f32x4 c4 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[kb][t], qb[t], c0[t], 0, 0, 0);
 #pragma unroll
-                for (int i = 0; i < 4; ++i) sum4[i] = fmaf(s_d[w][16 * kb + 4 * q4 + i][t], c4[i] - cq[t], sum4[i]);
+                for (int i = 0; i < 4; ++i) sum4[i] = fmaf(dk[kb][i][t], c4[i], sum4[i]);
             }
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
@@ -504,8 +522,8 @@ __global__ __launch_bounds__(256, 2) void decode_q8_lds_kernel(DecodeArgs a) {
                 cm = fmaxf(cm, x);
             }
         }
-        cm = fmaxf(cm, __shfl_xor(cm, 16, 64));
-        cm = fmaxf(cm, __shfl_xor(cm, 32, 64));
+        cm = max_x16(cm);
+        cm = max_x32(cm);
         const float mnew = fmaxf(m, cm);
         const float msub = mnew == -INFINITY ? 0.0f : mnew;
         const float alpha = mnew == -INFINITY ? 1.0f : fast_exp2(m - mnew);
@@ -518,8 +536,8 @@ __global__ __launch_bounds__(256, 2) void decode_q8_lds_kernel(DecodeArgs a) {
                 sc[kb][i] = fast_exp2(sc[kb][i] - msub);
                 ps += sc[kb][i];
             }
-        ps += __shfl_xor(ps, 16, 64);
-        ps += __shfl_xor(ps, 32, 64);
+        ps = sum_x16(ps);
+        ps = sum_x32(ps);
         lsum = fmaf(lsum, alpha, ps);
         if (__builtin_amdgcn_ballot_w64(alpha != 1.0f) != 0) {
 #pragma unroll
@@ -610,6 +628,7 @@ __global__ __launch_bounds__(256, 2) void decode_q8_lds_kernel(DecodeArgs a) {
             }
         }
     }
+    if (a.nsplit > 1 && a.counters) gtdecode::finish_split<_Float16, D>(a, bk, b * f.H + hk * G, G);
 }
 
 template <int D, bool LDS>
@@ -699,6 +718,7 @@ hipError_t launch_attn_decode_q8(const DecodeArgs &a, hipStream_t s) {
     dim3 grid((unsigned)a.nsplit, (unsigned)(a.f.B * a.f.Hkv));
     void *args[] = {(void *)&a};
     hipError_t e = hipLaunchKernel(kernel, grid, dim3(256), args, 0, s);
-    if (e != hipSuccess || a.nsplit == 1) return e;  // one split: the kernel wrote the output
+    // one split, or the last split merged in the kernel: the kernel wrote the output
+    if (e != hipSuccess || a.nsplit == 1 || a.counters) return e;
     return launch_attn_decode_merge(a, GT_F16, s);
 }

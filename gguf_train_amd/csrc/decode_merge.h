@@ -1,0 +1,94 @@
+// Split-K finish for the single-query (decode) kernels, done inside the split kernel instead of
+// a second launch: every workgroup of a (sequence, kv head) writes its partial (max, sum,
+// unnormalised O) rows, then counts itself in; the last one to arrive merges the partials of
+// that kv head's G query rows and resets the counter to zero for the next launch.
+//
+// The partials and the counters live in uncached device memory (a persistent per-stream
+// workspace), which every XCD reads and writes at the memory itself: no L2 write-back or
+// invalidation is needed, only the order of each workgroup's own accesses.  A workgroup waits
+// for its partial stores to complete (vmcnt(0)) before it counts itself in, and the counters are
+// relaxed device-scope atomics.  Launches on one stream run one after another, so they never
+// share a workspace while running.
+#pragma once
+
+#include "attn_common.h"
+
+#include <hip/hip_runtime.h>
+
+namespace gtdecode {
+
+template <typename TO>
+__device__ inline void store_out(void *o, int64_t i, float v) {
+    if constexpr (sizeof(TO) == 4) ((float *)o)[i] = v;
+    else ((TO *)o)[i] = (TO)v;  // float16 / bfloat16: round to nearest even
+}
+
+__device__ inline float wmax(float v) {
+    for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
+    return v;
+}
+__device__ inline float wsum(float v) {
+    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+    return v;
+}
+
+// Merges the nsplit partials of output rows row0 .. row0 + nrows - 1 (one wavefront per row).
+template <typename TO, int D>
+__device__ inline void merge_rows(const DecodeArgs &a, int64_t row0, int nrows) {
+    typedef float f32x4 __attribute__((ext_vector_type(4)));
+    constexpr int LPS = D / 4;     // lanes per partial row
+    constexpr int SPW = 64 / LPS;  // partial rows per wave load
+    const AttnFwdArgs &f = a.f;
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    const int ns = a.nsplit;
+    for (int r = w; r < nrows; r += nw) {
+        const int64_t row = row0 + r;
+        const float *ml = a.part_ml + row * ns * 2;
+        float M = -INFINITY;
+        for (int i = lane; i < ns; i += 64) M = fmaxf(M, ml[2 * i]);
+        M = wmax(M);
+        float L = 0.0f;
+        for (int i = lane; i < ns; i += 64) {
+            const float m = ml[2 * i];
+            L += m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m - M) * ml[2 * i + 1];
+        }
+        L = wsum(L);
+        const int sub = lane % LPS, sp = lane / LPS;
+        const float *po = a.part_o + row * ns * D + 4 * sub;
+        f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (int i = sp; i < ns; i += SPW) {
+            const float m = ml[2 * i];
+            const float wgt = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m - M);
+            acc += wgt * *(const f32x4 *)(po + (int64_t)i * D);
+        }
+#pragma unroll
+        for (int m = LPS; m < 64; m <<= 1) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[j] += __shfl_xor(acc[j], m, 64);
+        }
+        const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+        if (lane < LPS) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) store_out<TO>(f.o, row * D + 4 * sub + j, acc[j] * inv);
+        }
+        if (f.lse && lane == 0) ((float *)f.lse)[row] = L > 0.0f ? (M + log2f(L)) * 0.6931471805599453f : INFINITY;
+    }
+}
+
+// Called by every thread of a split workgroup after its partial stores (nsplit > 1, counters
+// set).  `bk` is the (sequence, kv head) index, rows row0 .. row0 + nrows - 1 its query rows.
+template <typename TO, int D>
+__device__ inline void finish_split(const DecodeArgs &a, int64_t bk, int64_t row0, int nrows) {
+    __shared__ int s_last;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this thread's partial stores have completed
+    __syncthreads();
+    if (threadIdx.x == 0)
+        s_last = __hip_atomic_fetch_add(&a.counters[bk], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                 a.nsplit - 1;
+    __syncthreads();
+    if (!s_last) return;
+    merge_rows<TO, D>(a, row0, nrows);
+    if (threadIdx.x == 0) __hip_atomic_store(&a.counters[bk], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+}  // namespace gtdecode

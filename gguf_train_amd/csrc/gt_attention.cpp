@@ -177,17 +177,33 @@ void fill_qkv(AttnFwdArgs &a, const gt_tensor *q, const gt_tensor *k, const gt_t
 }
 
 // Picks the kernel for a staged forward: split-K decode for single-query rows, the MFMA
+// Memory for the split partials of a decode launch (da.nsplit set): with several splits, the
+// per-stream uncached workspace whose counters let the last split merge in the kernel; otherwise
+// (or when that workspace is unavailable) stream-ordered scratch, merged by a second launch.
+bool decode_partials(DecodeArgs &da, int dev, gt_scratch &scratch) {
+    const AttnFwdArgs &a = da.f;
+    const size_t rows = (size_t)(a.B * a.H) * (size_t)da.nsplit;
+    const size_t bytes = rows * (size_t)(a.D + 2) * sizeof(float);
+    gt_decode_ws ws{};
+    if (da.nsplit > 1 && gt_decode_workspace(dev, gt_stream(), a.B * a.Hkv, bytes, ws)) {
+        da.counters = ws.counters;
+        da.part_o = (float *)ws.parts;
+    } else {
+        if (!gt_scratch_alloc(scratch, bytes, dev)) return false;
+        da.part_o = (float *)scratch.ptr();
+    }
+    da.part_ml = da.part_o + rows * (size_t)a.D;
+    return true;
+}
+
 // prefill kernel for fp16/bf16 with head size 64/128, the generic kernel otherwise.
 bool dispatch_forward(const AttnFwdArgs &a, int cd, int dev) {
     if (a.out_dtype == cd && !a.o32 && attn_decode_supported(a, cd)) {
         DecodeArgs da{};
         da.f = a;
         da.nsplit = attn_decode_splits(a, cd);
-        const size_t rows = (size_t)(a.B * a.H) * (size_t)da.nsplit;
         gt_scratch ws;
-        if (!gt_scratch_alloc(ws, rows * (size_t)(a.D + 2) * sizeof(float), dev)) return false;
-        da.part_o = (float *)ws.ptr();
-        da.part_ml = da.part_o + rows * (size_t)a.D;
+        if (!decode_partials(da, dev, ws)) return false;
         return gt_hip_check(launch_attn_decode(da, cd, gt_stream()), "flash_attention decode kernel");
     }
     if (attn_prefill_supported(a, cd))
@@ -221,11 +237,8 @@ int run_q8_decode(const gt_tensor *q, const gt_tensor *k, const gt_tensor *v, co
     DecodeArgs da{};
     da.f = a;
     da.nsplit = attn_decode_q8_splits(a);
-    const size_t rows = (size_t)(a.B * a.H) * (size_t)da.nsplit;
     gt_scratch ws;
-    if (!gt_scratch_alloc(ws, rows * (size_t)(a.D + 2) * sizeof(float), dev)) return -1;
-    da.part_o = (float *)ws.ptr();
-    da.part_ml = da.part_o + rows * (size_t)a.D;
+    if (!decode_partials(da, dev, ws)) return -1;
     return gt_hip_check(launch_attn_decode_q8(da, gt_stream()), "flash_attention q8_0 decode kernel") ? 1 : -1;
 }
 

@@ -86,6 +86,16 @@ bool gt_copy_device_to_host(gt_tensor *dst, const gt_tensor *src);
 // `dev_t` itself, or (to_host) a new host tensor with its contents, `dev_t` freed; NULL on error.
 gt_tensor *gt_deliver(gt_tensor *dev_t, bool to_host);
 
+// Workspace of the decode kernels' in-kernel split merge on stream `s` of device `dev`, in
+// uncached device memory: `n_counters` zeroed arrival counters (the kernels leave them zero),
+// then at least `part_bytes` bytes for the partials, 256-byte aligned.  Cached per stream and
+// never freed (uncached memory a kernel has read is kept until the process ends); null on failure.
+struct gt_decode_ws {
+    int *counters;
+    void *parts;
+};
+bool gt_decode_workspace(int dev, hipStream_t s, int64_t n_counters, size_t part_bytes, gt_decode_ws &ws);
+
 // Stream-ordered scratch memory from the pool (freed back to the pool in stream order).
 struct gt_scratch {
     std::shared_ptr<gt_storage> st;

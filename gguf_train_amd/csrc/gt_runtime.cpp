@@ -72,6 +72,42 @@ hipStream_t gt_stream() { return t_stream; }
 extern "C" void gt_set_stream(void *stream) { t_stream = (hipStream_t)stream; }
 extern "C" void *gt_get_stream(void) { return (void *)t_stream; }
 
+// One uncached buffer per (device, stream), grown on demand.  The kernels leave every counter at
+// zero, so a buffer is zeroed only when it is created; a buffer replaced by a larger one is kept
+// (launches in flight may use it, and uncached memory is not freed while the process runs).
+bool gt_decode_workspace(int dev, hipStream_t s, int64_t n_counters, size_t part_bytes, gt_decode_ws &ws) {
+    static std::mutex mu;
+    struct Buf {
+        char *p = nullptr;
+        int64_t counters = 0;
+        size_t parts = 0;
+    };
+    static std::map<std::pair<int, hipStream_t>, Buf> bufs;
+    std::lock_guard<std::mutex> lock(mu);
+    Buf &e = bufs[{dev, s}];
+    const size_t cbytes_of = 256;  // granule of the counter area
+    auto cbytes = [&](int64_t n) { return ((size_t)n * sizeof(int) + cbytes_of - 1) / cbytes_of * cbytes_of; };
+    if (!e.p || e.counters < n_counters || e.parts < part_bytes) {
+        Buf nb;
+        nb.counters = std::max<int64_t>({n_counters, e.counters, 4096});
+        nb.parts = std::max<size_t>({part_bytes, e.parts, (size_t)1 << 20});
+        if (hipExtMallocWithFlags((void **)&nb.p, cbytes(nb.counters) + nb.parts, hipDeviceMallocUncached) !=
+                hipSuccess ||
+            !nb.p) {
+            (void)hipGetLastError();
+            return false;
+        }
+        if (hipMemsetAsync(nb.p, 0, cbytes(nb.counters), s) != hipSuccess) {
+            (void)hipGetLastError();
+            return false;  // the buffer is kept (never freed), unused
+        }
+        e = nb;
+    }
+    ws.counters = (int *)e.p;
+    ws.parts = e.p + cbytes(e.counters);
+    return true;
+}
+
 extern "C" int gt_device_count(int device_type) {
     gt_init();
     if (device_type == GT_DEV_CPU) return 1;
