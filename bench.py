@@ -233,7 +233,7 @@ def cpu_baseline(heads: int):
 TRAFFIC_KERNELS = {
     "prefill": "prefill_fwd_kernelIDF16_Li128ELb1ELi0E",
     "decode": "decode_stream_kernelIDF16_Li128ELi4ELi0E",
-    "decode_q8_0": "decode_q8_stream_kernel<128, 4, 0>",
+    "decode_q8_0": "decode_q8_lds_kernel<128, 4, 0>",
 }
 TRAFFIC_FILE = ROOT / "profiles" / "hbm_traffic_prefill_decode.md"
 

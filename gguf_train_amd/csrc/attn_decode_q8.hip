@@ -393,6 +393,7 @@ __global__ __launch_bounds__(256, 2) void decode_q8_lds_kernel(DecodeArgs a) {
     constexpr int RB = NB * 34;               // bytes per row
     constexpr int TB = 32 * RB;               // bytes of a wave's 32 rows (a multiple of 16)
     constexpr int NL = (TB + 1023) / 1024;    // 16-byte loads per lane and tile
+    constexpr int TAIL = (TB % 1024) / 16;    // lanes of the last load that fall inside the tile (0: all)
     constexpr int SV = NB * 32 / 64;          // V scales read per lane and step
     __shared__ __attribute__((aligned(16))) uint8_t s_raw[4][2][NL * 1024];  // [wave][K, V]
     __shared__ __attribute__((aligned(16))) float s_dv[4][NB][32];       // V scales by row
@@ -431,13 +432,15 @@ __global__ __launch_bounds__(256, 2) void decode_q8_lds_kernel(DecodeArgs a) {
     const uint8_t *vbase = (const uint8_t *)f.v + slice;
     const uint32_t last16 = (uint32_t)S * RB - 16;  // last 16-byte piece of the slice
     // the lane's pieces of the wave's K and V tiles of `step` (pieces past the slice read its last
-    // piece; pieces past the tile land in the LDS tile's slack and are never read)
+    // piece; lanes of the last load past the tile re-read lane 0's line, adding no requests, and land
+    // in the LDS tile's slack, never read)
     u32x4 rk[NL], rv[NL];
     auto load = [&](int step) {
         const uint32_t t0 = (uint32_t)(kbeg + step * kStep + 32 * w) * RB;
 #pragma unroll
         for (int j = 0; j < NL; ++j) {
-            const uint32_t off = min(t0 + 1024u * j + 16u * lane, last16);
+            const bool spare = TAIL != 0 && j == NL - 1 && lane >= TAIL;
+            const uint32_t off = min(t0 + 1024u * j + (spare ? 0u : 16u * lane), last16);
             rk[j] = __builtin_nontemporal_load((const u32x4 *)(kbase + off));
             rv[j] = __builtin_nontemporal_load((const u32x4 *)(vbase + off));
         }
