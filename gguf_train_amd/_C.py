@@ -137,6 +137,9 @@ def _configure(lib: ctypes.CDLL) -> ctypes.CDLL:
     lib.gt_rope.restype = c_void_p
     lib.gt_rope_backward.argtypes = [c_void_p, c_void_p, c_int, c_int, c_int, c_float, c_float]
     lib.gt_rope_backward.restype = c_void_p
+    lib.gt_flash_attention_rope.argtypes = [c_void_p, c_void_p, c_void_p, c_void_p, c_float, c_int, c_void_p, c_int,
+                                            c_int, c_float, c_float]
+    lib.gt_flash_attention_rope.restype = c_void_p
 
     # Q8_0 (csrc/gguf_train.h:376-377)
     lib.gt_quantize.argtypes = [c_void_p, c_int]

@@ -9,8 +9,8 @@ MultiheadAttention with the reference's signatures, and the GGUF Q8_0 codec.
 from . import _C
 from ._bridge import QuantizedTensor
 from ._functions import FlashAttentionFn, RoPEFn
-from ._ops import (dequantize, flash_attention, flash_attention_backward, flash_attention_lse, flash_attention_train,
-                   quantize, rope)
+from ._ops import (dequantize, flash_attention, flash_attention_backward, flash_attention_lse, flash_attention_rope,
+                   flash_attention_train, quantize, rope)
 from . import nn
 from .kv_cache import KVCache
 
@@ -23,6 +23,7 @@ __all__ = [
     "flash_attention",
     "flash_attention_lse",
     "flash_attention_train",
+    "flash_attention_rope",
     "flash_attention_backward",
     "quantize",
     "dequantize",

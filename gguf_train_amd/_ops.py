@@ -95,6 +95,20 @@ def rope(x, pos, n_dims: int, mode: int = 0, n_ctx_orig: int = 0, freq_base: flo
     return adopt(ptr, "rope")
 
 
+def flash_attention_rope(q, k, v, pos, mask=None, scale: float = 0.0, is_causal: bool = False, n_dims=None,
+                         mode: int = 0, freq_base: float = 10000.0, freq_scale: float = 1.0) -> torch.Tensor:
+    """gt_flash_attention_rope: attention of rope(q, pos) and rope(k, pos), the query rotation fused
+    into the prefill kernel where it runs (no autograd; forward only)."""
+    bind_stream(_device_of(q))
+    hq, hk, hv, hp = borrow(q), borrow(k), borrow(v), borrow(pos)
+    hm = borrow(mask) if mask is not None else None
+    nd = q.shape[-1] if n_dims is None else int(n_dims)
+    ptr = _C.lib.gt_flash_attention_rope(hq.ptr, hk.ptr, hv.ptr, hm.ptr if hm else None, ctypes.c_float(scale),
+                                         1 if is_causal else 0, hp.ptr, nd, int(mode), ctypes.c_float(freq_base),
+                                         ctypes.c_float(freq_scale))
+    return adopt(ptr, "flash_attention_rope")
+
+
 def quantize(t: torch.Tensor, qtype: str = "q8_0") -> QuantizedTensor:
     """gt_quantize (csrc/gguf_train.h:376); rows of last-dim length, GGUF Q8_0 blocks."""
     if qtype != "q8_0":

@@ -39,6 +39,10 @@ struct AttnFwdArgs {
     // s <= q_pos[b] + l (null: s < S, and q_pos = 0, the reference's top-left alignment).
     const int32_t *kv_len;
     const int32_t *q_pos;
+    // RoPE of the queries (all D dims) applied as the prefill kernel loads them (null: none):
+    // (cos, sin) of pair i of query row l at rope_q[l * D / 2 + i]; rope_neox: NeoX pairing.
+    const void *rope_q;  // float2
+    int rope_neox;
 };
 
 __device__ inline int attn_kv_len(const AttnFwdArgs &a, int64_t b) { return a.kv_len ? a.kv_len[b] : (int)a.S; }

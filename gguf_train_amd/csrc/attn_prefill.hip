@@ -31,6 +31,7 @@
 #include "attn_common.h"
 #include "gt_internal.h"
 #include "mfma_util.h"
+#include "gt_rope_math.h"
 
 #include <cmath>
 
@@ -105,6 +106,36 @@ __device__ inline float max3(float a, float b, float c) {
     return r;
 }
 
+// RoPE of the lane's query row as it is loaded (all D dims rotated): q[t] holds dims
+// 16t + 8 half + 0..7.  The same float32 rotation and rounding as the rope kernel (gt_rope), so
+// the result equals attention of gt_rope's output.  NORMAL pairs (2i, 2i+1) lie inside one
+// 8-dim group; NeoX pairs (i, i + D/2) lie D/32 groups apart in the same lane.
+template <typename T, int D>
+__device__ inline void rope_rows(typename Mfma<T>::V8 *q, const float2 *tab, int neox, int half) {
+    constexpr int DT = D / 16, TP = D / 32;
+    if (!neox) {
+#pragma unroll
+        for (int t = 0; t < DT; ++t)
+#pragma unroll
+            for (int e = 0; e < 8; e += 2) {
+                const float2 cs = tab[(16 * t + 8 * half + e) >> 1];
+                const float lo = (float)q[t][e], hi = (float)q[t][e + 1];
+                q[t][e] = (T)rope_rot_lo(lo, hi, cs);
+                q[t][e + 1] = (T)rope_rot_hi(lo, hi, cs);
+            }
+    } else {
+#pragma unroll
+        for (int t = 0; t < TP; ++t)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float2 cs = tab[16 * t + 8 * half + e];
+                const float lo = (float)q[t][e], hi = (float)q[t + TP][e];
+                q[t][e] = (T)rope_rot_lo(lo, hi, cs);
+                q[t + TP][e] = (T)rope_rot_hi(lo, hi, cs);
+            }
+    }
+}
+
 // Keys covered by query tile qt: the sequence's keys, or (causal) up to the tile's last row,
 // whose position is qpos + qt*BM + BM-1.
 template <bool CAUSAL>
@@ -115,7 +146,7 @@ __device__ inline int key_tiles(int qt, int nkv, int qpos) {
 
 // MASK: 0 = none, 1 = bool bytes, 2 = additive float, 4 = additive float that does not depend
 // on the query row (key padding: the tile's mask row travels to LDS with the K/V tile).
-template <typename T, int D, bool CAUSAL, int MASK>
+template <typename T, int D, bool CAUSAL, int MASK, bool ROPE = false>
 __global__ __launch_bounds__(64 * NW, 1) void prefill_fwd_kernel(AttnFwdArgs a, int nq, int npairs) {
     using M = Mfma<T>;
     using V8 = typename M::V8;
@@ -251,6 +282,8 @@ __global__ __launch_bounds__(64 * NW, 1) void prefill_fwd_kernel(AttnFwdArgs a, 
             const T *qr = (const T *)a.q + b * a.q_sb + h * a.q_sh + (int64_t)min(lq, L - 1) * a.q_sl + 8 * half;
 #pragma unroll
             for (int t = 0; t < DT; ++t) qf[t] = __builtin_bit_cast(V8, *(const u32x4 *)(qr + 16 * t));
+            if constexpr (ROPE)
+                rope_rows<T, D>(qf, (const float2 *)a.rope_q + (int64_t)min(lq, L - 1) * (D / 2), a.rope_neox, half);
             // Wait for Q here: otherwise the compiler's wait for these loads lands inside the tile
             // loop, where it also waits for every K/V tile prefetch issued since.
 #pragma unroll
@@ -415,7 +448,19 @@ hipError_t launch_variant(const AttnFwdArgs &a, int nq, int npairs, int64_t grid
     const int mode = !a.mask ? 0 : (a.mask_bool ? 1 : (a.m_sl == 0 ? 4 : 2));
 #define GT_PREFILL_LAUNCH(C, MK) \
     hipLaunchKernelGGL((prefill_fwd_kernel<T, D, C, MK>), dim3((unsigned)grid), dim3(64 * NW), 0, s, a, nq, npairs)
-    if (a.causal) {
+#define GT_PREFILL_LAUNCH_R(C, MK) \
+    hipLaunchKernelGGL((prefill_fwd_kernel<T, D, C, MK, true>), dim3((unsigned)grid), dim3(64 * NW), 0, s, a, nq, npairs)
+    if (a.rope_q) {
+        // fused query RoPE: no mask or a key-padding row (the host rotates q itself otherwise)
+        if (mode != 0 && mode != 4) return hipErrorInvalidValue;
+        if (a.causal) {
+            if (mode == 0) GT_PREFILL_LAUNCH_R(true, 0);
+            else GT_PREFILL_LAUNCH_R(true, 4);
+        } else {
+            if (mode == 0) GT_PREFILL_LAUNCH_R(false, 0);
+            else GT_PREFILL_LAUNCH_R(false, 4);
+        }
+    } else if (a.causal) {
         if (mode == 0) GT_PREFILL_LAUNCH(true, 0);
         else if (mode == 1) GT_PREFILL_LAUNCH(true, 1);
         else if (mode == 4) GT_PREFILL_LAUNCH(true, 4);
@@ -427,6 +472,7 @@ hipError_t launch_variant(const AttnFwdArgs &a, int nq, int npairs, int64_t grid
         else GT_PREFILL_LAUNCH(false, 2);
     }
 #undef GT_PREFILL_LAUNCH
+#undef GT_PREFILL_LAUNCH_R
     return hipGetLastError();
 }
 
@@ -434,6 +480,7 @@ hipError_t launch_variant(const AttnFwdArgs &a, int nq, int npairs, int64_t grid
 
 bool attn_prefill_supported(const AttnFwdArgs &f, int cd) {
     if (cd != GT_F16 && cd != GT_BF16) return false;
+    if (f.rope_q && f.mask && (f.mask_bool || f.m_sl != 0)) return false;  // fused RoPE: no mask or key padding
     if (f.out_dtype != cd || f.D != f.Dv || (f.D != 64 && f.D != 128)) return false;
     if (f.L < 1 || f.S < 1 || !(f.scale > 0.0f)) return false;
     if (f.L >= (1LL << 30) || f.S >= (1LL << 30)) return false;  // 32-bit row indices

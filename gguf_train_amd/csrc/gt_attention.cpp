@@ -242,9 +242,15 @@ int run_q8_decode(const gt_tensor *q, const gt_tensor *k, const gt_tensor *v, co
     return gt_hip_check(launch_attn_decode_q8(da, gt_stream()), "flash_attention q8_0 decode kernel") ? 1 : -1;
 }
 
+// RoPE of the queries fused into the prefill kernel: the (cos, sin) table of the L query rows.
+struct QRope {
+    const void *table;  // float2 (L, D/2) on the device
+    int neox;
+};
+
 int attention_forward(const char *who, const gt_tensor *q, const gt_tensor *k, const gt_tensor *v,
                       const gt_tensor *mask, float scale, int is_causal, gt_tensor **out_o, gt_tensor **out_lse,
-                      gt_tensor **out_o32 = nullptr) {
+                      gt_tensor **out_o32 = nullptr, const QRope *qrope = nullptr) {
     if (out_o) *out_o = nullptr;
     if (out_lse) *out_lse = nullptr;
     if (out_o32) *out_o32 = nullptr;
@@ -298,7 +304,18 @@ int attention_forward(const char *who, const gt_tensor *q, const gt_tensor *k, c
             a.scale = scale;
             a.causal = is_causal ? 1 : 0;
             a.out_dtype = q->dtype;
-            ok = dispatch_forward(a, cd, dev);
+            if (qrope) {
+                a.rope_q = qrope->table;
+                a.rope_neox = qrope->neox;
+                if (!attn_prefill_supported(a, cd)) {
+                    // only the prefill kernel applies the rotation: the caller rotates q itself
+                    gt_tensor_free(o);
+                    gt_tensor_free(lse);
+                    gt_tensor_free(o32);
+                    return 1;
+                }
+            }
+            ok = ok && dispatch_forward(a, cd, dev);
         }
     }
     if (!ok) {
@@ -328,6 +345,60 @@ extern "C" gt_tensor *gt_flash_attention(const gt_tensor *q, const gt_tensor *k,
                                          const gt_tensor *mask, float scale, int is_causal) {
     gt_tensor *o = nullptr;
     if (attention_forward("flash_attention", q, k, v, mask, scale, is_causal, &o, nullptr) != 0) return nullptr;
+    return o;
+}
+
+// Attention of RoPE-rotated queries and keys: gt_rope(q, pos) and gt_rope(k, pos) (first L / S
+// positions) followed by gt_flash_attention.  The keys are rotated in one pass (each is read by
+// every query tile); the queries are rotated by the prefill kernel as it loads them when it runs
+// (float16/bfloat16 q, k, v of one dtype, n_dims = D, L > 1, no mask or a key-padding row),
+// otherwise in a pass of their own.
+extern "C" gt_tensor *gt_flash_attention_rope(const gt_tensor *q, const gt_tensor *k, const gt_tensor *v,
+                                              const gt_tensor *mask, float scale, int is_causal, const gt_tensor *pos,
+                                              int n_dims, int mode, float freq_base, float freq_scale) {
+    const char *who = "flash_attention_rope";
+    if (!validate(who, q, k, v, mask)) return nullptr;
+    const int64_t L = q->shape[2], S = k->shape[2], D = q->shape[3];
+    if (!gt_rope_check_args(who, D, n_dims, mode, freq_base, freq_scale)) return nullptr;
+    const int64_t need = std::max(L, S);
+    if (!pos || pos->ndim != 1 || pos->shape[0] < need || gt_is_quantized(pos->dtype)) {
+        gt_set_error(std::string(who) + ": pos must be a 1-D tensor with a position for each of the " +
+                     std::to_string(need) + " sequence elements");
+        return nullptr;
+    }
+    if (k->dtype == GT_Q8_0) {
+        gt_set_error(std::string(who) + ": k must be a floating point tensor (RoPE of q8_0 keys: dequantize first)");
+        return nullptr;
+    }
+    const int dev = q->device_type == GT_DEV_CUDA ? q->device_index : 0;
+    if (!gt_device_ok(dev)) return nullptr;
+    Temps tmp;
+    const gt_tensor *kd =
+        k->device_type == GT_DEV_CUDA && k->device_index == dev ? k : tmp.keep(gt_to_device_dense(k, dev, -1));
+    const gt_tensor *kr = kd ? tmp.keep(gt_rope(kd, pos, n_dims, mode, 0, freq_base, freq_scale)) : nullptr;
+    if (!kr) return nullptr;
+    gt_tensor *o = nullptr;
+    const bool key_padding = !mask || (mask->dtype != GT_BOOL && mask->shape[mask->ndim - 2] == 1);
+    if ((q->dtype == GT_F16 || q->dtype == GT_BF16) && k->dtype == q->dtype && v->dtype == q->dtype &&
+        q->device_type == GT_DEV_CUDA && n_dims == D && (D == 64 || D == 128) && L > 1 && key_padding) {
+        const gt_tensor *pd = (pos->device_type == GT_DEV_CUDA && pos->device_index == dev && pos->dtype == GT_I32 &&
+                               gt_is_dense(pos))
+                                  ? pos
+                                  : tmp.keep(gt_to_device_dense(pos, dev, GT_I32));
+        gt_scratch table;
+        if (!pd || !gt_scratch_alloc(table, (size_t)L * (size_t)(D / 2) * 2 * sizeof(float), dev) ||
+            !gt_hip_check(gt_launch_rope_table((const int32_t *)gt_data(pd), nullptr, 1, L, n_dims,
+                                               gt_rope_theta_scale(freq_base, n_dims), freq_scale, 0, table.ptr(),
+                                               gt_stream()),
+                          "rope table kernel"))
+            return nullptr;
+        const QRope qr{table.ptr(), mode == 2 ? 1 : 0};
+        const int rc = attention_forward(who, q, kr, v, mask, scale, is_causal, &o, nullptr, nullptr, &qr);
+        if (rc < 0) return nullptr;
+        if (rc == 0) return o;
+    }
+    const gt_tensor *qr = tmp.keep(gt_rope(q, pos, n_dims, mode, 0, freq_base, freq_scale));
+    if (!qr || attention_forward(who, qr, kr, v, mask, scale, is_causal, &o, nullptr) != 0) return nullptr;
     return o;
 }
 

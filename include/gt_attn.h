@@ -203,6 +203,17 @@ GT_API gt_tensor *gt_rope(const gt_tensor *x, const gt_tensor *pos, int n_dims, 
 GT_API gt_tensor *gt_rope_backward(const gt_tensor *grad_out, const gt_tensor *pos, int n_dims, int mode,
                                    int n_ctx_orig, float freq_base, float freq_scale);
 
+/* No counterpart in the reference (there: gt_rope of q and of k, then gt_flash_attention, the
+ * composition of csrc/gt_ops_nn.cpp:2298-2525): attention of gt_rope(q, pos) and gt_rope(k, pos)
+ * (q rows at the first L positions, k rows at the first S), gt_flash_attention's other arguments
+ * and semantics, gt_rope's checks and arithmetic; pos needs max(L, S) positions.  The keys are
+ * rotated in one pass; for float16/bfloat16 q, k, v of one dtype with n_dims = D (64 or 128),
+ * L > 1 and no mask or a key-padding mask, the prefill kernel rotates each query row as it loads
+ * it (the same bits as gt_rope).  Output as gt_flash_attention. */
+GT_API gt_tensor *gt_flash_attention_rope(const gt_tensor *q, const gt_tensor *k, const gt_tensor *v,
+                                          const gt_tensor *mask, float scale, int is_causal, const gt_tensor *pos,
+                                          int n_dims, int mode, float freq_base, float freq_scale);
+
 /* ---- GGUF Q8_0 ------------------------------------------------------------------------ */
 
 /* csrc/gguf_train.h:376 (gt_tensor_to_dtype, csrc/gt_core.cpp:784-847): quantizes rows of

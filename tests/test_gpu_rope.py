@@ -261,3 +261,77 @@ def test_append_rope_errors(dev):
     with pytest.raises(TypeError):
         cache.append(k, k, rope={"theta": 1.0})
     assert cache.lengths == [0]
+
+
+# ---- attention of rotated queries and keys (gt_flash_attention_rope) ------------------------------
+
+FUSED_CASES = [
+    # (dtype, B, H, Hkv, L, S, D, mode, causal)  -- the prefill kernel rotates q as it loads it
+    (torch.float16, 2, 8, 2, 300, 300, 128, 2, True),
+    (torch.float16, 1, 4, 4, 256, 256, 128, 0, True),
+    (torch.bfloat16, 2, 4, 2, 200, 200, 64, 2, True),
+    (torch.bfloat16, 1, 4, 1, 130, 130, 64, 0, False),
+    (torch.float16, 1, 8, 8, 512, 512, 128, 2, False),
+]
+
+
+@pytest.mark.parametrize("case", FUSED_CASES)
+def test_fused_query_rope_equals_rope_then_attention(dev, case):
+    dtype, B, H, Hkv, L, S, D, mode, causal = case
+    q = randn((B, H, L, D), 51, dtype).to(dev)
+    k = randn((B, Hkv, S, D), 52, dtype).to(dev)
+    v = randn((B, Hkv, S, D), 53, dtype).to(dev)
+    pos = torch.from_numpy(np.random.default_rng(54).permutation(4 * max(L, S))[: max(L, S)]).to(dev)
+    got = g.flash_attention_rope(q, k, v, pos, None, 0.0, causal, None, mode)
+    qr, kr = F.rope(q, pos, mode=mode), F.rope(k, pos, mode=mode)
+    want = g.flash_attention(qr, kr, v, None, 0.0, causal)
+    # the same kernel on the same rotated values: bit for bit
+    assert torch.equal(got, want)
+    ref = oracle_forward(qr, kr, v, is_causal=causal)
+    assert_close(got, ref, dtype, "fused rope attention")
+
+
+def test_fused_query_rope_with_a_key_padding_mask(dev):
+    B, H, L, D = 2, 4, 257, 128
+    q, k, v = (randn((B, H, L, D), s, torch.float16).to(dev) for s in (61, 62, 63))
+    mask = torch.zeros(B, 1, 1, L, device=dev)
+    mask[0, ..., 200:] = float("-inf")
+    pos = torch.arange(L, device=dev) + 17
+    got = g.flash_attention_rope(q, k, v, pos, mask, 0.0, True, None, 2)
+    want = g.flash_attention(F.rope(q, pos, mode=2), F.rope(k, pos, mode=2), v, mask, 0.0, True)
+    assert torch.equal(got, want)
+
+
+@pytest.mark.parametrize("variant", ["float32", "partial_dims", "bool_mask", "decode", "host"])
+def test_unfused_shapes_rotate_q_first(dev, variant):
+    B, H, L, D = 1, 4, 96, 64
+    dtype = torch.float32 if variant == "float32" else torch.float16
+    q, k, v = (randn((B, H, L, D), s, dtype).to(dev) for s in (71, 72, 73))
+    pos = torch.arange(L, device=dev)
+    n_dims, mask, causal = None, None, True
+    if variant == "partial_dims":
+        n_dims = 32
+    if variant == "bool_mask":
+        mask = torch.rand(1, 1, L, L, generator=torch.Generator().manual_seed(3)).to(dev) > 0.3
+        mask[..., 0] = True
+        causal = False
+    if variant == "decode":
+        q = q[:, :, -1:].contiguous()
+        causal = False
+    if variant == "host":
+        q, k, v, pos = q.cpu(), k.cpu(), v.cpu(), pos.cpu()
+    nd = D if n_dims is None else n_dims
+    got = g.flash_attention_rope(q, k, v, pos, mask, 0.0, causal, n_dims, 0)
+    want = g.flash_attention(F.rope(q, pos, n_dims=nd), F.rope(k, pos, n_dims=nd), v, mask, 0.0, causal)
+    assert got.device == q.device
+    assert torch.equal(got, want)
+
+
+def test_fused_rope_errors(dev):
+    q = torch.zeros(1, 2, 8, 64, dtype=torch.float16, device=dev)
+    with pytest.raises(RuntimeError, match="a position for each of the 8 sequence elements"):
+        g.flash_attention_rope(q, q, q, torch.arange(4, device=dev))
+    with pytest.raises(RuntimeError, match="mode must be 0 \\(normal\\) or 2 \\(NeoX\\)"):
+        g.flash_attention_rope(q, q, q, torch.arange(8, device=dev), mode=1)
+    with pytest.raises(RuntimeError, match="n_dims must be an even number"):
+        g.flash_attention_rope(q, q, q, torch.arange(8, device=dev), n_dims=65)
