@@ -182,22 +182,41 @@ __global__ __launch_bounds__(256) void bwd_dkdv_kernel(AttnBwdArgs a, int nkt) {
             }
             // s[i], dp[i]: query q0 + 8(i/4) + 4half + i%4, key `key`
             float p[16], ds[16];
+            // every (query, key) of the block visible and no per-element mask: no tests
+            const bool interior = (MASK == 0 || MASK == 4) && wk0 + 31 < S && q0 + 31 < L && (!CAUSAL || q0 >= wk0 + 31);
+            if (interior) {
+                const float add = MASK == 4 ? madd : 0.0f;
 #pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                const int qi = 32 * qb + 8 * g + 4 * half;  // 4 consecutive queries
-                const f32x4 l4 = *(const f32x4 *)&sL[buf][qi];
-                const f32x4 d4 = *(const f32x4 *)&sD[buf][qi];
+                for (int g = 0; g < 4; ++g) {
+                    const int qi = 32 * qb + 8 * g + 4 * half;
+                    const f32x4 l4 = *(const f32x4 *)&sL[buf][qi];
+                    const f32x4 d4 = *(const f32x4 *)&sD[buf][qi];
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const int i = 4 * g + e, q = qs0 + qi + e;
-                    float add;
-                    bool ok = key < S && q < L && (!CAUSAL || key <= q);
-                    if (MASK == 4) add = madd;
-                    else if (MASK != 0) ok = ok && mask_at<MASK>(f, b, h, min(q, L - 1), min(key, S - 1), inv_scale, add);
-                    else add = 0.0f;
-                    const float pv = ok ? fast_exp2(fmaf(s[i] + add, c, -l4[e])) : 0.0f;
-                    p[i] = pv;
-                    ds[i] = pv * (dp[i] - d4[e]);
+                    for (int e = 0; e < 4; ++e) {
+                        const int i = 4 * g + e;
+                        const float pv = fast_exp2(fmaf(s[i] + add, c, -l4[e]));
+                        p[i] = pv;
+                        ds[i] = pv * (dp[i] - d4[e]);
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const int qi = 32 * qb + 8 * g + 4 * half;  // 4 consecutive queries
+                    const f32x4 l4 = *(const f32x4 *)&sL[buf][qi];
+                    const f32x4 d4 = *(const f32x4 *)&sD[buf][qi];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const int i = 4 * g + e, q = qs0 + qi + e;
+                        float add;
+                        bool ok = key < S && q < L && (!CAUSAL || key <= q);
+                        if (MASK == 4) add = madd;
+                        else if (MASK != 0) ok = ok && mask_at<MASK>(f, b, h, min(q, L - 1), min(key, S - 1), inv_scale, add);
+                        else add = 0.0f;
+                        const float pv = ok ? fast_exp2(fmaf(s[i] + add, c, -l4[e])) : 0.0f;
+                        p[i] = pv;
+                        ds[i] = pv * (dp[i] - d4[e]);
+                    }
                 }
             }
             V8 pa[2], pal[2], da[2], dal[2];
@@ -353,16 +372,28 @@ __global__ __launch_bounds__(256) void bwd_dq_kernel(AttnBwdArgs a, int nq) {
 #pragma unroll
                     for (int g = 0; g < 4; ++g) mv[g] = *(const f32x4 *)&sMk[buf][32 * kb + 8 * g + 4 * half];
                 }
+                // every (query, key) of the block visible and no per-element mask: no tests
+                const int kb0 = k0 + 32 * kb;
+                const bool interior =
+                    (MASK == 0 || MASK == 4) && kb0 + 31 < S && wq0 + 31 < L && (!CAUSAL || wq0 >= kb0 + 31);
+                if (interior) {
 #pragma unroll
-                for (int i = 0; i < 16; ++i) {
-                    const int kk = k0 + 32 * kb + 8 * (i / 4) + 4 * half + (i % 4);
-                    float add;
-                    bool ok = kk < S && lq < L && (!CAUSAL || kk <= lq);
-                    if (MASK == 4) add = mv[i / 4][i % 4];
-                    else if (MASK != 0) ok = ok && mask_at<MASK>(f, b, h, lqc, min(kk, S - 1), inv_scale, add);
-                    else add = 0.0f;
-                    const float pv = ok ? fast_exp2(fmaf(s[kb][i] + add, c, -lse2)) : 0.0f;
-                    ds[i] = pv * (dp[kb][i] - dlt);
+                    for (int i = 0; i < 16; ++i) {
+                        const float add = MASK == 4 ? mv[i / 4][i % 4] : 0.0f;
+                        ds[i] = fast_exp2(fmaf(s[kb][i] + add, c, -lse2)) * (dp[kb][i] - dlt);
+                    }
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) {
+                        const int kk = kb0 + 8 * (i / 4) + 4 * half + (i % 4);
+                        float add;
+                        bool ok = kk < S && lq < L && (!CAUSAL || kk <= lq);
+                        if (MASK == 4) add = mv[i / 4][i % 4];
+                        else if (MASK != 0) ok = ok && mask_at<MASK>(f, b, h, lqc, min(kk, S - 1), inv_scale, add);
+                        else add = 0.0f;
+                        const float pv = ok ? fast_exp2(fmaf(s[kb][i] + add, c, -lse2)) : 0.0f;
+                        ds[i] = pv * (dp[kb][i] - dlt);
+                    }
                 }
                 pack8<T>(ds, sb[kb][0], sl[kb][0]);
                 pack8<T>(ds + 8, sb[kb][1], sl[kb][1]);
