@@ -71,8 +71,10 @@ __device__ inline bool mask_at(const AttnFwdArgs &f, int64_t b, int64_t h, int q
 
 // ---- dK, dV ----------------------------------------------------------------------------------
 
+// D = 64 fits two wavefronts per SIMD without spills (with one, the compiler parks values in
+// AGPRs and moves them back and forth); D = 128 needs the whole register file.
 template <typename T, int D, bool CAUSAL, int MASK>
-__global__ __launch_bounds__(256) void bwd_dkdv_kernel(AttnBwdArgs a, int nkt) {
+__global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void bwd_dkdv_kernel(AttnBwdArgs a, int nkt) {
     using M = Mfma<T>;
     using V8 = typename M::V8;
     constexpr int DT = D / 16, DB = D / 32, CH = D / 8;
@@ -267,8 +269,9 @@ __global__ __launch_bounds__(256) void bwd_dkdv_kernel(AttnBwdArgs a, int nkt) {
 
 // ---- dQ --------------------------------------------------------------------------------------
 
+// (two per SIMD for D = 64 as in dK/dV, except with a per-element mask, which would spill)
 template <typename T, int D, bool CAUSAL, int MASK>
-__global__ __launch_bounds__(256) void bwd_dq_kernel(AttnBwdArgs a, int nq) {
+__global__ __launch_bounds__(256, D <= 64 && (MASK == 0 || MASK == 4) ? 2 : 1) void bwd_dq_kernel(AttnBwdArgs a, int nq) {
     using M = Mfma<T>;
     using V8 = typename M::V8;
     constexpr int DT = D / 16, DB = D / 32, CH = D / 8;
