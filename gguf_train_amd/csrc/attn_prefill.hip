@@ -329,7 +329,17 @@ __global__ __launch_bounds__(64 * NW, 1) void prefill_fwd_kernel(AttnFwdArgs a, 
 
             // ---- masks: s[kb][i] is (key = k0 + 32kb + 8(i/4) + 4half + i%4, query = lq) ----
             const bool edge = k0 + BN > nkv || (CAUSAL && k0 + BN - 1 > wq0 + qpos);
-            if (MASK != 0 || edge) {
+            if (MROW && !edge) {
+                // key padding away from the edges: the mask row is added, nothing is blocked
+#pragma unroll
+                for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                    for (int g = 0; g < 4; ++g) {
+                        const f32x4 mv4 = *(const f32x4 *)&sMk[step % NST][32 * kb + 8 * g + 4 * half];
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) s[kb][4 * g + e] = fmaf(mv4[e], 1.0f / a.scale, s[kb][4 * g + e]);
+                    }
+            } else if (MASK != 0 || edge) {
                 f32x4 mv[2][4];  // MROW: the mask values of this lane's keys, from LDS
                 if constexpr (MROW) {
 #pragma unroll
