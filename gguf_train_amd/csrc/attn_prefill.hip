@@ -4,8 +4,9 @@
 // the same semantics: scale, top-left causal mask, bool/additive mask, rows with nothing to
 // attend to -> 0, output rounded from fp32 to the input dtype.
 //
-// Workgroup: 8 wavefronts (two per SIMD), query tiles of BM = 256 rows (32 per wavefront), so
-// each K/V tile brought into LDS serves 256 queries.  A workgroup runs the query tiles p and
+// Workgroup (D = 128): 8 wavefronts (two per SIMD), query tiles of BM = 256 rows (32 per
+// wavefront), so each K/V tile brought into LDS serves 256 queries; D = 64: 4 wavefronts, 128
+// rows, two workgroups per CU.  A workgroup runs the query tiles p and
 // nq-1-p of one head one after the other: under the causal mask their key ranges add up to
 // the same length for every p, so all workgroups carry equal work.  K/V tiles of BN = 64 rows
 // stream through NST LDS stages: global_load_lds_dwordx4 writes tile s+NST-1 straight into LDS
@@ -37,8 +38,12 @@
 
 namespace {
 
-constexpr int NW = 8;           // wavefronts per workgroup
-constexpr int BM = 32 * NW;     // query rows per tile
+// wavefronts per workgroup: 8 for D = 128; 4 for D = 64, whose smaller tiles and per-tile work
+// would otherwise leave one workgroup per CU with all of its waves in the same phase
+template <int D>
+constexpr int nw_of() { return D == 64 ? 4 : 8; }
+template <int D>
+constexpr int bm_of() { return 32 * nw_of<D>(); }  // query rows per tile
 constexpr int BN = 64;          // keys per K/V tile
 constexpr int NST = 4;          // K/V tile stages in LDS
 constexpr float kLazy = 8.0f;   // rescale threshold, log2 domain: probabilities stay <= 256
@@ -138,7 +143,7 @@ __device__ inline void rope_rows(typename Mfma<T>::V8 *q, const float2 *tab, int
 
 // Keys covered by query tile qt: the sequence's keys, or (causal) up to the tile's last row,
 // whose position is qpos + qt*BM + BM-1.
-template <bool CAUSAL>
+template <bool CAUSAL, int BM>
 __device__ inline int key_tiles(int qt, int nkv, int qpos) {
     const int kv_end = CAUSAL ? min(qt * BM + BM + qpos, nkv) : nkv;
     return kv_end > 0 ? (kv_end + BN - 1) / BN : 0;
@@ -147,7 +152,8 @@ __device__ inline int key_tiles(int qt, int nkv, int qpos) {
 // MASK: 0 = none, 1 = bool bytes, 2 = additive float, 4 = additive float that does not depend
 // on the query row (key padding: the tile's mask row travels to LDS with the K/V tile).
 template <typename T, int D, bool CAUSAL, int MASK, bool ROPE = false>
-__global__ __launch_bounds__(64 * NW, 1) void prefill_fwd_kernel(AttnFwdArgs a, int nq, int npairs) {
+__global__ __launch_bounds__(64 * nw_of<D>(), 8 / nw_of<D>()) void prefill_fwd_kernel(AttnFwdArgs a, int nq, int npairs) {
+    constexpr int NW = nw_of<D>(), BM = bm_of<D>();
     using M = Mfma<T>;
     using V8 = typename M::V8;
     constexpr int DT = D / 16;             // k-steps of S^T = K.Q^T
@@ -187,8 +193,8 @@ __global__ __launch_bounds__(64 * NW, 1) void prefill_fwd_kernel(AttnFwdArgs a, 
     const int nkv = attn_kv_len(a, b), qpos = attn_q_pos(a, b);
     const int qa = nq - 1 - pair, qb = pair;  // the heavier tile first
     const int nparts = qa == qb ? 1 : 2;
-    const int na = key_tiles<CAUSAL>(qa, nkv, qpos);
-    const int total = na + (nparts == 2 ? key_tiles<CAUSAL>(qb, nkv, qpos) : 0);
+    const int na = key_tiles<CAUSAL, BM>(qa, nkv, qpos);
+    const int total = na + (nparts == 2 ? key_tiles<CAUSAL, BM>(qb, nkv, qpos) : 0);
 
     const T *kbase = (const T *)a.k + b * a.k_sb + hk * a.k_sh;
     const T *vbase = (const T *)a.v + b * a.v_sb + hk * a.v_sh;
@@ -457,9 +463,9 @@ template <typename T, int D>
 hipError_t launch_variant(const AttnFwdArgs &a, int nq, int npairs, int64_t grid, hipStream_t s) {
     const int mode = !a.mask ? 0 : (a.mask_bool ? 1 : (a.m_sl == 0 ? 4 : 2));
 #define GT_PREFILL_LAUNCH(C, MK) \
-    hipLaunchKernelGGL((prefill_fwd_kernel<T, D, C, MK>), dim3((unsigned)grid), dim3(64 * NW), 0, s, a, nq, npairs)
+    hipLaunchKernelGGL((prefill_fwd_kernel<T, D, C, MK>), dim3((unsigned)grid), dim3(64 * nw_of<D>()), 0, s, a, nq, npairs)
 #define GT_PREFILL_LAUNCH_R(C, MK) \
-    hipLaunchKernelGGL((prefill_fwd_kernel<T, D, C, MK, true>), dim3((unsigned)grid), dim3(64 * NW), 0, s, a, nq, npairs)
+    hipLaunchKernelGGL((prefill_fwd_kernel<T, D, C, MK, true>), dim3((unsigned)grid), dim3(64 * nw_of<D>()), 0, s, a, nq, npairs)
     if (a.rope_q) {
         // fused query RoPE: no mask or a key-padding row (the host rotates q itself otherwise)
         if (mode != 0 && mode != 4) return hipErrorInvalidValue;
@@ -506,6 +512,7 @@ bool attn_prefill_supported(const AttnFwdArgs &f, int cd) {
 }
 
 hipError_t launch_attn_prefill(const AttnFwdArgs &a, int cd, hipStream_t s) {
+    const int BM = a.D == 64 ? bm_of<64>() : bm_of<128>();
     const int nq = (int)((a.L + BM - 1) / BM);
     const int npairs = (nq + 1) / 2;  // query tiles p and nq-1-p share a workgroup
     const int64_t grid = (int64_t)npairs * a.B * a.H;
