@@ -419,12 +419,15 @@ __global__ __launch_bounds__(64 * nw_of<D>(), 8 / nw_of<D>()) void prefill_fwd_k
             }
 
             // ---- O^T += V^T . P^T ----
+            // d blocks innermost: consecutive MFMAs accumulate into different O blocks, so none
+            // waits for the previous one's result (a dependent 32x32x16 chain issues at ~44
+            // cycles per MFMA instead of 32)
 #pragma unroll
-            for (int db = 0; db < DB; ++db) {
+            for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
-                for (int kb = 0; kb < 2; ++kb) {
+                for (int hs = 0; hs < 2; ++hs) {
 #pragma unroll
-                    for (int hs = 0; hs < 2; ++hs) {
+                    for (int db = 0; db < DB; ++db) {
                         const int g = 2 * kb + hs;
                         const V8 av = D == 128 ? read_tr8<T>(&cV[vofs0[db] + 16 * g * D], &cV[vofs1[db] + 16 * g * D])
                                                : read_tr8<T>(&cV[vofs0[g * DB + db]], &cV[vofs1[g * DB + db]]);
