@@ -56,6 +56,9 @@ def parse_args():
     p.add_argument("--measure-traffic", action="store_true",
                    help="run rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes over the benchmark's kernels (child "
                         "processes), calibrate them against a plain copy and write the summary under profiles/")
+    p.add_argument("--measure-mfma", action="store_true",
+                   help="run one rocprofv3 --pmc pass of MFMA / VALU / LDS counters over the prefill and training "
+                        "configs (child processes) and write the summary under profiles/")
     return p.parse_args()
 
 
@@ -238,23 +241,73 @@ TRAFFIC_KERNELS = {
 TRAFFIC_FILE = ROOT / "profiles" / "hbm_traffic_prefill_decode.md"
 
 
-def _pmc_average(counter, config):
-    """Average per-dispatch value of `counter` (KiB for FETCH_SIZE / WRITE_SIZE) for every kernel
-    of `python bench.py --configs <config>`, from one rocprofv3 --pmc pass."""
+def _pmc_pass(counters, config, steps=3, warmup=1):
+    """Average per-dispatch value of each counter for every kernel of `python bench.py --configs
+    <config>`, from one rocprofv3 --pmc pass: {counter: {kernel: average}}."""
     with tempfile.TemporaryDirectory() as d:
-        cmd = ["rocprofv3", "--pmc", counter, "-d", d, "-o", "run", "--output-format", "csv", "--",
-               sys.executable, str(ROOT / "bench.py"), "--configs", config, "--no-cpu", "--steps", "3", "--warmup", "1"]
-        print("[traffic] " + " ".join(cmd[:4] + ["<tmp>"] + cmd[6:]), file=sys.stderr, flush=True)
+        cmd = ["rocprofv3", "--pmc", *counters, "-d", d, "-o", "run", "--output-format", "csv", "--",
+               sys.executable, str(ROOT / "bench.py"), "--configs", config, "--no-cpu", "--steps", str(steps),
+               "--warmup", str(warmup)]
+        n = len(counters)
+        print("[pmc] " + " ".join(cmd[:2 + n] + ["-d", "<tmp>"] + cmd[4 + n:]), file=sys.stderr, flush=True)
         subprocess.run(cmd, check=True, timeout=120, stdout=subprocess.DEVNULL, stderr=subprocess.DEVNULL)
         files = list(Path(d).rglob("*counter_collection.csv"))
         if not files:
-            raise RuntimeError(f"rocprofv3 wrote no counter file for {counter} / {config}")
+            raise RuntimeError(f"rocprofv3 wrote no counter file for {counters} / {config}")
         vals = {}
         with open(files[0]) as f:
             for row in csv.DictReader(f):
-                if row["Counter_Name"] == counter:
-                    vals.setdefault(row["Kernel_Name"], []).append(float(row["Counter_Value"]))
-    return {k: sum(v) / len(v) for k, v in vals.items()}
+                vals.setdefault(row["Counter_Name"], {}).setdefault(row["Kernel_Name"], []).append(
+                    float(row["Counter_Value"]))
+    return {c: {k: sum(v) / len(v) for k, v in per.items()} for c, per in vals.items()}
+
+
+def _pmc_average(counter, config):
+    """Average per-dispatch value of `counter` (KiB for FETCH_SIZE / WRITE_SIZE) for every kernel
+    of `python bench.py --configs <config>`, from one rocprofv3 --pmc pass."""
+    return _pmc_pass([counter], config).get(counter, {})
+
+
+# MFMA / VALU / LDS counters of the compute-bound kernels (one pass: 7 SQ counters and GRBM's
+# clock; MfmaUtil = MFMA-busy SIMD cycles / (GPU-active cycles x SIMDs), MfmaFlops* = MOPS x 512)
+MFMA_COUNTERS = ["MfmaUtil", "MfmaFlopsF16", "MfmaFlopsBF16", "SQ_INSTS_MFMA", "SQ_INSTS_VALU", "SQ_INSTS_LDS",
+                 "SQ_BUSY_CYCLES"]
+MFMA_KERNELS = {"prefill": ["prefill_fwd_kernel"], "train": ["prefill_fwd_kernel", "bwd_dkdv_kernel", "bwd_dq_kernel"]}
+MFMA_FILE = ROOT / "profiles" / "mfma_counters_prefill_train.md"
+
+
+def measure_mfma():
+    """MFMA utilisation and instruction mix of the prefill and training kernels."""
+    lines = ["# MFMA utilisation and instruction mix of the prefill and training kernels", "",
+             "Command: `python bench.py --measure-mfma` (per config: `rocprofv3 --pmc " + " ".join(MFMA_COUNTERS) +
+             " -d <tmp> -o run --output-format csv -- python bench.py --configs <config> --no-cpu --steps 3 "
+             "--warmup 1`). Values are per dispatch, averaged over the run's dispatches of each kernel.", "",
+             "- `MfmaUtil`: MFMA-busy SIMD cycles / (GPU-active cycles x SIMDs), in percent.",
+             "- MFMA GFLOP executed per dispatch: `MfmaFlopsF16 + MfmaFlopsBF16` (MOPS x 512): every MFMA the kernel "
+             "issues, including the masked work of diagonal tiles and the bf16 hi/lo split, so it exceeds the "
+             "algorithmic count.",
+             "- VALU and LDS instructions per MFMA: `SQ_INSTS_VALU / SQ_INSTS_MFMA`, `SQ_INSTS_LDS / SQ_INSTS_MFMA` "
+             "(`SQ_INSTS_VALU` counts the MFMAs too).", "",
+             "| config | kernel | MfmaUtil % | MFMA GFLOP executed | MFMA instructions | VALU per MFMA | LDS per MFMA |",
+             "|---|---|---|---|---|---|---|"]
+    for config, pats in MFMA_KERNELS.items():
+        r = _pmc_pass(MFMA_COUNTERS, config)
+        seen = set()
+        for kernel in sorted(r.get("SQ_INSTS_MFMA", {})):
+            if not any(p in kernel for p in pats) or kernel in seen:
+                continue
+            seen.add(kernel)
+            def g(c, default=float("nan")):
+                return r.get(c, {}).get(kernel, default)
+
+            mfma = g("SQ_INSTS_MFMA")
+            flops = g("MfmaFlopsF16", 0.0) + g("MfmaFlopsBF16", 0.0)
+            name = kernel.split("(")[0]
+            lines.append(f"| {config} | `{name}` | {g('MfmaUtil'):.1f} | {flops / 1e9:.1f} | {mfma:.4g} | "
+                         f"{g('SQ_INSTS_VALU') / mfma:.2f} | {g('SQ_INSTS_LDS') / mfma:.2f} |")
+    MFMA_FILE.parent.mkdir(exist_ok=True)
+    MFMA_FILE.write_text("\n".join(lines) + "\n")
+    print("\n".join(lines))
 
 
 def measure_traffic():
@@ -315,6 +368,9 @@ def main():
     args = parse_args()
     if args.measure_traffic:
         measure_traffic()
+        return 0
+    if args.measure_mfma:
+        measure_mfma()
         return 0
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
