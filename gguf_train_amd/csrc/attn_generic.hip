@@ -4,8 +4,10 @@
 // backward composition (gguf_train/_functions.py:1933-1965) for the shapes the MFMA kernels
 // do not take (tiny or odd head sizes, float32/float64, mixed dtypes).
 //
-// Forward: one wavefront per query row.  Keys are processed 64 at a time, one per lane, with
-// an online softmax; the P.V product runs with lanes over the value dimension.
+// Forward: one wavefront per query row.  Keys are processed in chunks, with an online softmax;
+// the P.V product runs with lanes over the value dimension.  When a chunk of K and V fits in
+// LDS (head sizes up to a few hundred), the 4 rows of a workgroup share chunks staged there
+// (generic_fwd_lds_kernel); otherwise each lane reads its key row from global memory.
 // Backward: a row kernel (dQ and delta = rowsum(P*dP)) and a column kernel (dK, dV) with one
 // wavefront per key; both recompute P from the saved log-sum-exp.
 
@@ -142,6 +144,205 @@ __global__ __launch_bounds__(256) void generic_fwd_kernel(AttnFwdArgs a, int64_t
         }
         if (dv0 + kDvChunk >= a.Dv) break;
     }
+}
+
+// Wave-wide max / sum whose result every lane holds: DPP within rows of 16 (quad swaps, then
+// the half-row and row mirrors), then the row and half swaps (v_permlane16/32_swap); all in
+// registers.  Max keeps generic_fwd_kernel's comparison (a NaN on the right is not taken).
+template <int CTRL>
+__device__ inline float dpp_mov(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+__device__ inline float max_by(float a, float b) { return b > a ? b : a; }
+__device__ inline float wave_max_reg(float v) {
+    v = max_by(v, dpp_mov<0xB1>(v));   // quad_perm [1,0,3,2]
+    v = max_by(v, dpp_mov<0x4E>(v));   // quad_perm [2,3,0,1]
+    v = max_by(v, dpp_mov<0x141>(v));  // row_half_mirror
+    v = max_by(v, dpp_mov<0x140>(v));  // row_mirror
+    auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = max_by(__uint_as_float(r[0]), __uint_as_float(r[1]));
+    r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return max_by(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ inline float wave_sum_reg(float v) {
+    v += dpp_mov<0xB1>(v);
+    v += dpp_mov<0x4E>(v);
+    v += dpp_mov<0x141>(v);
+    v += dpp_mov<0x140>(v);
+    auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ inline double wave_max_reg(double v) { return wave_max(v); }
+__device__ inline double wave_sum_reg(double v) { return wave_sum(v); }
+// v of lane t (t wave-uniform)
+__device__ inline float lane_value(float v, int t) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), t));
+}
+__device__ inline double lane_value(double v, int t) {
+    const int64_t x = __double_as_longlong(v);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)x, t);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(x >> 32), t);
+    return __longlong_as_double((int64_t)(((uint64_t)hi << 32) | lo));
+}
+
+// Copies rows [0, nk) of a row-major block (row r at base + r * rs, D values each) into LDS
+// through put(r, d, value), and zeros for rows nk .. NR - 1.  Thread t owns column t % D of
+// rows t / D, t / D + 256 / D, ... (D <= 256; columns t, t + 256, ... of every row otherwise):
+// the loads of 8 rows are issued before their stores, so their latencies overlap.
+template <int NR, typename T, typename A, typename F>
+__device__ inline void stage_rows(const T *base, int64_t rs, int nk, int D, int tid, F put) {
+    const bool narrow = D <= 256;
+    const int rstep = narrow ? 256 / D : 1;
+    const int r0 = narrow ? tid / D : 0;
+    if (r0 >= rstep) return;
+    for (int d = narrow ? tid % D : tid; d < D; d += narrow ? D : 256) {
+        for (int rb = r0; rb < NR; rb += 8 * rstep) {
+            A buf[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int r = rb + u * rstep;
+                buf[u] = r < nk ? to_acc(base[(int64_t)r * rs + d], A()) : (A)0;
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int r = rb + u * rstep;
+                if (r < NR) put(r, d, buf[u]);
+            }
+        }
+    }
+}
+
+// Forward with the key/value chunks staged in LDS: the 4 query rows of a workgroup share each
+// chunk of NK keys (64, 32 or 16, the largest whose K and V fit; LPK = 64 / NK lanes per key).
+// The chunk is read once, coalesced, converted to the accumulation type; K is stored transposed
+// (Kt[d][key], rows of NK + 1) so that the lanes of a key column read consecutive words and the
+// transposing stores of consecutive dims land in distinct banks.  Lane (key = lane % NK,
+// part = lane / NK) sums dims [part*DP, part*DP + DP) of its key's dot product; shuffles across
+// the parts complete it.  Then the same online softmax and P.V as generic_fwd_kernel (lanes over
+// the value dims, terms with p == 0 skipped), with register-only reductions and broadcasts.
+template <typename T, typename A, int NK, int NJ>
+__global__ __launch_bounds__(256) void generic_fwd_lds_kernel(AttnFwdArgs a, int64_t row_blocks) {
+    constexpr int LPK = 64 / NK, KT = NK + 1;
+    extern __shared__ __attribute__((aligned(16))) unsigned char g_lds[];
+    A *Kt = reinterpret_cast<A *>(g_lds);  // [D][KT]
+    A *Vs = Kt + a.D * KT;                 // [NK][Dv]
+    A *Qs = Vs + NK * a.Dv;                // [kRowsPerBlock][D]
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int key = lane % NK, part = lane / NK;
+    const int D = (int)a.D, Dv = (int)a.Dv;
+    const int DP = (D + LPK - 1) / LPK;
+    const int d_lo = min(part * DP, D), d_hi = min(d_lo + DP, D);
+    const int64_t bh = blockIdx.x / row_blocks;
+    const int64_t l0 = (blockIdx.x % row_blocks) * kRowsPerBlock;
+    const int64_t l = l0 + w;
+    const bool active = l < a.L;
+    const int64_t b = bh / a.H, h = bh % a.H, g = h / (a.H / a.Hkv);
+    const T *kb = (const T *)a.k + b * a.k_sb + g * a.k_sh;
+    const T *vb = (const T *)a.v + b * a.v_sb + g * a.v_sh;
+    const int64_t row = bh * a.L + l;
+    const A ninf = neg_inf<A>();
+    const int64_t kvn = attn_kv_len(a, b), qpos = attn_q_pos(a, b);
+    // keys this workgroup needs: its last row's causal limit
+    const int64_t l_last = min(l0 + kRowsPerBlock - 1, a.L - 1);
+    const int64_t kend = min(kvn, a.causal ? l_last + qpos + 1 : a.S);
+    const int64_t my_end = active ? min(kvn, a.causal ? l + qpos + 1 : a.S) : 0;
+
+    // the query rows (zeros past L: those wavefronts compute nothing)
+    stage_rows<kRowsPerBlock, T, A>((const T *)a.q + b * a.q_sb + h * a.q_sh + l0 * a.q_sl, a.q_sl,
+                                    (int)min((int64_t)kRowsPerBlock, a.L - l0), D, tid,
+                                    [&](int r, int d, A x) { Qs[r * D + d] = x; });
+    // value dims lane, lane + 64, ... (NJ blocks of 64 cover Dv; the last one's reads clamp to
+    // column Dv - 1 and its results past Dv are not stored)
+    int dcol[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) dcol[j] = min(lane + 64 * j, Dv - 1);
+    A m = ninf, lsum = 0;
+    A acc[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) acc[j] = 0;
+    // Chunk staging through registers: thread t holds column t % D of rows t / D + u * (256 / D)
+    // (at most PR of them: NK * D <= 256 * PR), likewise for V.  The next chunk's loads are
+    // issued before the current chunk is computed and stored to LDS after the next barrier.
+    constexpr int PR = 16;
+    const int kstep = 256 / D, kr0 = tid / D, kd = tid % D;
+    const int vstep = 256 / Dv, vr0 = tid / Dv, vd = tid % Dv;
+    A kreg[PR], vreg[PR];
+    auto load_chunk = [&](int64_t c0, int n) {
+#pragma unroll
+        for (int u = 0; u < PR; ++u) {
+            const int rk = kr0 + u * kstep, rv = vr0 + u * vstep;
+            kreg[u] = (kr0 < kstep && rk < n) ? to_acc(kb[(c0 + rk) * a.k_ss + kd], A()) : (A)0;
+            vreg[u] = (vr0 < vstep && rv < n) ? to_acc(vb[(c0 + rv) * a.v_ss + vd], A()) : (A)0;
+        }
+    };
+    auto store_chunk = [&]() {
+#pragma unroll
+        for (int u = 0; u < PR; ++u) {
+            const int rk = kr0 + u * kstep, rv = vr0 + u * vstep;
+            if (kr0 < kstep && rk < NK) Kt[kd * KT + rk] = kreg[u];
+            if (vr0 < vstep && rv < NK) Vs[rv * Dv + vd] = vreg[u];
+        }
+    };
+    if (kend > 0) load_chunk(0, (int)min((int64_t)NK, kend));
+    for (int64_t s0 = 0; s0 < kend; s0 += NK) {
+        const int nk = (int)min((int64_t)NK, kend - s0);
+        __syncthreads();  // the previous chunk is no longer read (and Qs is written)
+        store_chunk();
+        __syncthreads();
+        if (s0 + NK < kend) load_chunk(s0 + NK, (int)min((int64_t)NK, kend - s0 - NK));
+        if (s0 >= my_end) continue;  // this row sees none of the chunk (wave-uniform)
+        const int64_t s = s0 + key;
+        A dot = 0;
+        {
+            const A *kc = Kt + key;
+            const A *qr = Qs + w * D;
+#pragma unroll 8
+            for (int d = d_lo; d < d_hi; ++d) dot += qr[d] * kc[d * KT];
+        }
+#pragma unroll
+        for (int off = NK; off < 64; off <<= 1) dot += __shfl_xor(dot, off, 64);
+        A sc = ninf;
+        if (s < my_end) sc = apply_mask<A>(a, dot * (A)a.scale, b, h, l, s);
+        const A cm = wave_max_reg(sc);
+        if (!(cm > ninf)) continue;  // the whole chunk is blocked for this row
+        const A mn = cm > m ? cm : m;
+        const A corr = m > ninf ? acc_exp(m - mn) : (A)0;
+        lsum *= corr;
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) acc[j] *= corr;
+        m = mn;
+        const A p = sc > ninf ? acc_exp(sc - m) : (A)0;
+        lsum += wave_sum_reg(part == 0 ? p : (A)0);
+        // P.V over 8 keys at a time: their V words are read first; a key with p == 0 adds nothing
+        // (its V word is replaced by 0, so an inf / NaN there is never touched, as the reference
+        // skips such terms, gt_ops_nn.cpp:2515).  Keys past nk have p == 0 and zero rows.
+        for (int t0 = 0; t0 < nk; t0 += 8) {
+            A pp[8], vv[8][NJ];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                pp[u] = lane_value(p, t0 + u);  // lane t holds key t (part 0)
+#pragma unroll
+                for (int j = 0; j < NJ; ++j) vv[u][j] = Vs[(t0 + u) * Dv + dcol[j]];
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+#pragma unroll
+                for (int j = 0; j < NJ; ++j) acc[j] += pp[u] * (pp[u] != (A)0 ? vv[u][j] : (A)0);
+        }
+    }
+    if (!active) return;
+    const A inv = lsum > (A)0 ? (A)1 / lsum : (A)0;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+        const int64_t d = lane + 64 * j;
+        if (d < Dv) {
+            store_out<A>(a.o, a.out_dtype, row * Dv + d, acc[j] * inv);
+            if (a.o32) store_out<A>(a.o32, GT_F32, row * Dv + d, acc[j] * inv);
+        }
+    }
+    if (a.lse && lane == 0) ((A *)a.lse)[row] = lsum > (A)0 ? m + acc_log(lsum) : (A)__builtin_huge_val();
 }
 
 // dO . V[s] for lane-private use.
@@ -283,11 +484,38 @@ __global__ __launch_bounds__(256) void generic_bwd_cols_kernel(AttnBwdArgs a, in
     }
 }
 
+template <typename T, typename A, int NK>
+hipError_t launch_lds(int nj, int64_t grid, size_t bytes, const AttnFwdArgs &a, int64_t row_blocks, hipStream_t s) {
+    if (nj == 1)
+        hipLaunchKernelGGL((generic_fwd_lds_kernel<T, A, NK, 1>), dim3((unsigned)grid), dim3(256), bytes, s, a, row_blocks);
+    else if (nj == 2)
+        hipLaunchKernelGGL((generic_fwd_lds_kernel<T, A, NK, 2>), dim3((unsigned)grid), dim3(256), bytes, s, a, row_blocks);
+    else
+        hipLaunchKernelGGL((generic_fwd_lds_kernel<T, A, NK, 4>), dim3((unsigned)grid), dim3(256), bytes, s, a, row_blocks);
+    return hipGetLastError();
+}
+
 template <typename T, typename A>
 hipError_t launch_fwd(const AttnFwdArgs &a, hipStream_t s) {
     const int64_t row_blocks = (a.L + kRowsPerBlock - 1) / kRowsPerBlock;
     const int64_t grid = row_blocks * a.B * a.H;
     if (grid <= 0) return hipSuccess;
+    // LDS-staged chunks (head sizes up to 256): NK keys per chunk, the largest whose K and V fit
+    // in 48 KB of LDS and whose rows per staging thread (rows / (256 / D)) fit its 16 registers
+    if (a.Dv <= 256 && a.D <= 256 && a.D > 0 && a.Dv > 0) {
+        auto bytes = [&](int nk) { return (size_t)(a.D * (nk + 1) + nk * a.Dv + kRowsPerBlock * a.D) * sizeof(A); };
+        auto rows_per_thread = [](int nk, int64_t d) { return (nk + 256 / d - 1) / (256 / d); };
+        auto fits = [&](int nk) {
+            return bytes(nk) <= 48 * 1024 && rows_per_thread(nk, a.D) <= 16 && rows_per_thread(nk, a.Dv) <= 16;
+        };
+        const int nj = a.Dv <= 64 ? 1 : a.Dv <= 128 ? 2 : 4;
+        if (fits(64))
+            return launch_lds<T, A, 64>(nj, grid, bytes(64), a, row_blocks, s);
+        if (fits(32))
+            return launch_lds<T, A, 32>(nj, grid, bytes(32), a, row_blocks, s);
+        if (fits(16))
+            return launch_lds<T, A, 16>(nj, grid, bytes(16), a, row_blocks, s);
+    }
     hipLaunchKernelGGL((generic_fwd_kernel<T, A>), dim3((unsigned)grid), dim3(256), 0, s, a, row_blocks);
     return hipGetLastError();
 }
