@@ -103,6 +103,30 @@ def test_host_tensors_round_trip_through_the_device(dev):
     assert_close(got, oracle_forward(q, k, v, is_causal=True), torch.float32, "host io")
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64, torch.float16])
+@pytest.mark.parametrize("D,Dv", [(64, 96), (256, 256), (200, 160), (1, 1), (300, 40), (48, 130), (16, 8)])
+@pytest.mark.parametrize("causal", [False, True])
+def test_generic_kernel_chunk_and_value_shapes(dev, dtype, D, Dv, causal):
+    # head sizes that select each chunk size of the generic forward (64 / 32 / 16 keys staged per
+    # workgroup), 1, 2 or 4 value blocks of 64 with a partial last block, and the unstaged path
+    # (D > 256); 150 keys = several chunks with a partial last one, 37 rows = a partial row block
+    B, H, Hkv, L, S = 1, 4, 2, 37, 150
+    seed = D * 31 + Dv
+    q, k, v = randn((B, H, L, D), seed, dtype), randn((B, Hkv, S, D), seed + 1, dtype), randn((B, Hkv, S, Dv), seed + 2, dtype)
+    got = g.flash_attention(q.to(dev), k.to(dev), v.to(dev), None, 0.0, causal)
+    assert got.shape == (B, H, L, Dv) and got.dtype == dtype
+    want = oracle_forward(q, k, v, is_causal=causal)
+    assert_close(got, want, dtype, f"{dtype} D={D} Dv={Dv} causal={causal}")
+    # a float mask blocking scattered keys (and every key of row 5) on top
+    rng = np.random.default_rng(seed)
+    mask = torch.from_numpy(np.where(rng.random((L, S)) < 0.3, -np.inf, rng.standard_normal((L, S)))).to(dtype)
+    mask[5] = -math.inf
+    got = g.flash_attention(q.to(dev), k.to(dev), v.to(dev), mask.to(dev), 0.0, causal)
+    want = oracle_forward(q, k, v, mask=mask, is_causal=causal)
+    assert_close(got, want, dtype, f"{dtype} D={D} Dv={Dv} causal={causal} masked")
+    assert torch.equal(got[:, :, 5].cpu(), torch.zeros(B, H, Dv, dtype=dtype))
+
+
 def test_mixed_dtypes_compute_in_the_wider_type(dev):
     q = randn((1, 2, 9, 32), 40, torch.float16)
     k = randn((1, 2, 11, 32), 41, torch.float32)
