@@ -84,7 +84,7 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void bwd_dkdv_kernel(AttnBwdA
     __shared__ __attribute__((aligned(16))) T sQ[2][BQ * QP];
     __shared__ __attribute__((aligned(16))) T sG[2][BQ * QP];  // dO
     __shared__ __attribute__((aligned(16))) float sL[2][BQ];    // lse * log2(e)
-    __shared__ __attribute__((aligned(16))) float sD[2][BQ];    // delta
+    __shared__ __attribute__((aligned(16))) float sD[2][BQ];    // -delta
 
     const AttnFwdArgs &f = a.f;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
@@ -137,7 +137,7 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void bwd_dkdv_kernel(AttnBwdA
         if (tid < BQ) {
             const int64_t r = (b * f.H + h) * f.L + min(qs0 + tid, L - 1);
             lreg = ((const float *)f.lse)[r] * kLog2e;
-            dreg = ((const float *)a.delta)[r];
+            dreg = -((const float *)a.delta)[r];
         }
     };
     auto store_step = [&](int buf) {
@@ -159,46 +159,56 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void bwd_dkdv_kernel(AttnBwdA
         if (nsteps > 1) load_step(1);
     }
     __syncthreads();
-    float madd = 0.0f;  // MASK 4: mask value of this lane's key for the current head (raw units)
+    // The first S and dP products accumulate onto (the key's mask term, -delta of each query):
+    // S then holds QK^T + mask and dP holds dO.V^T - delta, with no per-element adds.
+    f32x16 sinit;  // MASK 4: the mask value of this lane's key for the current head (raw units)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) sinit[i] = 0.0f;
     for (int st = 0; st < nsteps; ++st) {
         const int buf = st & 1;
         const int hh = st / nqs, qs0 = qstart + (st % nqs) * BQ;
         const int64_t h = hk * G + hh;
         const T *cQ = sQ[buf];
         const T *cG = sG[buf];
-        if (MASK == 4 && st % nqs == 0)
-            madd = ((const float *)f.mask)[b * f.m_sb + h * f.m_sh + (int64_t)min(key, S - 1) * f.m_ss] * inv_scale;
+        if (MASK == 4 && st % nqs == 0) {
+            const float madd =
+                ((const float *)f.mask)[b * f.m_sb + h * f.m_sh + (int64_t)min(key, S - 1) * f.m_ss] * inv_scale;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) sinit[i] = madd;
+        }
 #pragma unroll
         for (int qb = 0; qb < 2; ++qb) {
             const int q0 = qs0 + 32 * qb;
             if (CAUSAL && q0 + 31 < wk0) continue;  // every query of the block precedes our keys
+            // s[i], dp[i]: query q0 + 8(i/4) + 4half + i%4, key `key`
             f32x16 s, dp;
 #pragma unroll
-            for (int i = 0; i < 16; ++i) s[i] = dp[i] = 0.0f;
+            for (int g = 0; g < 4; ++g) {
+                const f32x4 d4 = *(const f32x4 *)&sD[buf][32 * qb + 8 * g + 4 * half];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) dp[4 * g + e] = d4[e];
+            }
 #pragma unroll
             for (int t = 0; t < DT; ++t) {
                 const V8 qa = *(const V8 *)&cQ[(32 * qb + lrow) * QP + 16 * t + 8 * half];
                 const V8 ga = *(const V8 *)&cG[(32 * qb + lrow) * QP + 16 * t + 8 * half];
-                s = M::mma(qa, kf[t], s);
+                s = M::mma(qa, kf[t], t == 0 ? sinit : s);
                 dp = M::mma(ga, vf[t], dp);
             }
-            // s[i], dp[i]: query q0 + 8(i/4) + 4half + i%4, key `key`
             float p[16], ds[16];
             // every (query, key) of the block visible and no per-element mask: no tests
             const bool interior = (MASK == 0 || MASK == 4) && wk0 + 31 < S && q0 + 31 < L && (!CAUSAL || q0 >= wk0 + 31);
             if (interior) {
-                const float add = MASK == 4 ? madd : 0.0f;
 #pragma unroll
                 for (int g = 0; g < 4; ++g) {
                     const int qi = 32 * qb + 8 * g + 4 * half;
                     const f32x4 l4 = *(const f32x4 *)&sL[buf][qi];
-                    const f32x4 d4 = *(const f32x4 *)&sD[buf][qi];
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
                         const int i = 4 * g + e;
-                        const float pv = fast_exp2(fmaf(s[i] + add, c, -l4[e]));
+                        const float pv = fast_exp2(fmaf(s[i], c, -l4[e]));
                         p[i] = pv;
-                        ds[i] = pv * (dp[i] - d4[e]);
+                        ds[i] = pv * dp[i];
                     }
                 }
             } else {
@@ -206,18 +216,16 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void bwd_dkdv_kernel(AttnBwdA
                 for (int g = 0; g < 4; ++g) {
                     const int qi = 32 * qb + 8 * g + 4 * half;  // 4 consecutive queries
                     const f32x4 l4 = *(const f32x4 *)&sL[buf][qi];
-                    const f32x4 d4 = *(const f32x4 *)&sD[buf][qi];
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
                         const int i = 4 * g + e, q = qs0 + qi + e;
-                        float add;
+                        float add = 0.0f;  // MASK 4: already in s
                         bool ok = key < S && q < L && (!CAUSAL || key <= q);
-                        if (MASK == 4) add = madd;
-                        else if (MASK != 0) ok = ok && mask_at<MASK>(f, b, h, min(q, L - 1), min(key, S - 1), inv_scale, add);
-                        else add = 0.0f;
+                        if (MASK == 1 || MASK == 2)
+                            ok = ok && mask_at<MASK>(f, b, h, min(q, L - 1), min(key, S - 1), inv_scale, add);
                         const float pv = ok ? fast_exp2(fmaf(s[i] + add, c, -l4[e])) : 0.0f;
                         p[i] = pv;
-                        ds[i] = pv * (dp[i] - d4[e]);
+                        ds[i] = pv * dp[i];
                     }
                 }
             }
@@ -306,7 +314,13 @@ __global__ __launch_bounds__(256, D <= 64 && (MASK == 0 || MASK == 4) ? 2 : 1) v
         }
     }
     const float lse2 = ((const float *)f.lse)[bh * f.L + lqc] * kLog2e;
-    const float dlt = ((const float *)a.delta)[bh * f.L + lqc];
+    // dP accumulates onto -delta of this lane's query: dP - delta with no per-element subtract
+    f32x16 dinit;
+    {
+        const float dlt = ((const float *)a.delta)[bh * f.L + lqc];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) dinit[i] = -dlt;
+    }
 
     f32x16 dq[DB];
 #pragma unroll
@@ -352,50 +366,48 @@ __global__ __launch_bounds__(256, D <= 64 && (MASK == 0 || MASK == 4) ? 2 : 1) v
         const T *cK = sK[buf];
         const T *cV = sV[buf];
         if (!CAUSAL || k0 <= wq0 + 31) {
+            // s[kb][i]: key k0 + 32kb + 8(i/4) + 4half + i%4, query lq.  S accumulates onto the
+            // tile's mask row (MASK 4: the keys' additive terms), dP onto -delta.
             f32x16 s[2], dp[2];
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb) {
+                f32x16 sinit;
 #pragma unroll
-                for (int i = 0; i < 16; ++i) s[kb][i] = dp[kb][i] = 0.0f;
+                for (int g = 0; g < 4; ++g) {
+                    const f32x4 mv = MASK == 4 ? *(const f32x4 *)&sMk[buf][32 * kb + 8 * g + 4 * half]
+                                               : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) sinit[4 * g + e] = mv[e];
+                }
 #pragma unroll
                 for (int t = 0; t < DT; ++t) {
                     const V8 ka = *(const V8 *)&cK[(32 * kb + lrow) * KP + 16 * t + 8 * half];
                     const V8 va = *(const V8 *)&cV[(32 * kb + lrow) * VP + 16 * t + 8 * half];
-                    s[kb] = M::mma(ka, qf[t], s[kb]);
-                    dp[kb] = M::mma(va, gf[t], dp[kb]);
+                    s[kb] = M::mma(ka, qf[t], t == 0 ? sinit : s[kb]);
+                    dp[kb] = M::mma(va, gf[t], t == 0 ? dinit : dp[kb]);
                 }
             }
-            // s[kb][i]: key k0 + 32kb + 8(i/4) + 4half + i%4, query lq
             V8 sb[2][2], sl[2][2];
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb) {
                 float ds[16];
-                f32x4 mv[4];
-                if (MASK == 4) {
-#pragma unroll
-                    for (int g = 0; g < 4; ++g) mv[g] = *(const f32x4 *)&sMk[buf][32 * kb + 8 * g + 4 * half];
-                }
                 // every (query, key) of the block visible and no per-element mask: no tests
                 const int kb0 = k0 + 32 * kb;
                 const bool interior =
                     (MASK == 0 || MASK == 4) && kb0 + 31 < S && wq0 + 31 < L && (!CAUSAL || wq0 >= kb0 + 31);
                 if (interior) {
 #pragma unroll
-                    for (int i = 0; i < 16; ++i) {
-                        const float add = MASK == 4 ? mv[i / 4][i % 4] : 0.0f;
-                        ds[i] = fast_exp2(fmaf(s[kb][i] + add, c, -lse2)) * (dp[kb][i] - dlt);
-                    }
+                    for (int i = 0; i < 16; ++i) ds[i] = fast_exp2(fmaf(s[kb][i], c, -lse2)) * dp[kb][i];
                 } else {
 #pragma unroll
                     for (int i = 0; i < 16; ++i) {
                         const int kk = kb0 + 8 * (i / 4) + 4 * half + (i % 4);
-                        float add;
+                        float add = 0.0f;  // MASK 4: already in s
                         bool ok = kk < S && lq < L && (!CAUSAL || kk <= lq);
-                        if (MASK == 4) add = mv[i / 4][i % 4];
-                        else if (MASK != 0) ok = ok && mask_at<MASK>(f, b, h, lqc, min(kk, S - 1), inv_scale, add);
-                        else add = 0.0f;
+                        if (MASK == 1 || MASK == 2)
+                            ok = ok && mask_at<MASK>(f, b, h, lqc, min(kk, S - 1), inv_scale, add);
                         const float pv = ok ? fast_exp2(fmaf(s[kb][i] + add, c, -lse2)) : 0.0f;
-                        ds[i] = pv * (dp[kb][i] - dlt);
+                        ds[i] = pv * dp[kb][i];
                     }
                 }
                 pack8<T>(ds, sb[kb][0], sl[kb][0]);
