@@ -74,7 +74,7 @@ __device__ inline bool mask_at(const AttnFwdArgs &f, int64_t b, int64_t h, int q
 // D = 64 fits two wavefronts per SIMD without spills (with one, the compiler parks values in
 // AGPRs and moves them back and forth); D = 128 needs the whole register file.
 template <typename T, int D, bool CAUSAL, int MASK>
-__global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void bwd_dkdv_kernel(AttnBwdArgs a, int nkt) {
+__global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void bwd_dkdv_kernel(AttnBwdArgs a) {
     using M = Mfma<T>;
     using V8 = typename M::V8;
     constexpr int DT = D / 16, DB = D / 32, CH = D / 8;
@@ -90,8 +90,14 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void bwd_dkdv_kernel(AttnBwdA
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int lrow = lane & 31, half = lane >> 5;
     const int g16 = lane >> 4, i16 = lane & 15;
-    const int kt = (int)(blockIdx.x % nkt);
-    const int64_t bk = blockIdx.x / nkt, b = bk / f.Hkv, hk = bk % f.Hkv;
+    // Key tile major: all workgroups of key tile 0 first.  Under the causal mask tile kt walks
+    // the queries from k0 on, so the heaviest workgroups start first and the short ones fill
+    // the tail (list scheduling over two rounds of B*Hkv*nkt = 1024 workgroups on 512 slots:
+    // makespan 18 steps instead of 28 with key tiles interleaved).  The tiles of one (b, kv
+    // head) sit B*Hkv apart, on the same XCD when B*Hkv % 8 == 0.
+    const int64_t nbk = f.B * f.Hkv;
+    const int kt = (int)(blockIdx.x / nbk);
+    const int64_t bk = blockIdx.x % nbk, b = bk / f.Hkv, hk = bk % f.Hkv;
     const int G = (int)(f.H / f.Hkv);
     const int L = (int)f.L, S = (int)f.S;
     const int k0 = kt * BKV, wk0 = k0 + 32 * w, key = wk0 + lrow;  // this lane's key (n index)
@@ -462,8 +468,7 @@ hipError_t launch_bwd_typed(const AttnBwdArgs &a, hipStream_t s) {
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const int nkt = (int)((f.S + BKV - 1) / BKV);
-    hipLaunchKernelGGL((bwd_dkdv_kernel<T, D, CAUSAL, MASK>), dim3((unsigned)(nkt * f.B * f.Hkv)), dim3(256), 0, s, a,
-                       nkt);
+    hipLaunchKernelGGL((bwd_dkdv_kernel<T, D, CAUSAL, MASK>), dim3((unsigned)(nkt * f.B * f.Hkv)), dim3(256), 0, s, a);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
     const int nq = (int)((f.L + BMQ - 1) / BMQ);
