@@ -1,17 +1,18 @@
 // Recompute-based attention backward on gfx950 MFMA (fp16 / bf16 inputs, fp32 gradients).
 //
 // Replaces the reference's Python composition (gguf_train/_functions.py:1933-1965), which
-// materialises (B,H,L,S) scores, probabilities and their gradients, with three kernels that
+// materialises (B,H,L,S) scores, probabilities and their gradients, with two kernels that
 // keep everything in registers and LDS and recompute P from the forward's log-sum-exp:
-//   delta:  D_q = sum_d dO[q,d] * O[q,d]  (= sum_s P[q,s] dP[q,s], the rowsum in dS)
+//   dQ:     the forward's structure (a workgroup owns 128 query rows, loops over key tiles);
+//           each row first forms D_q = sum_d dO[q,d] * O[q,d] (= sum_s P[q,s] dP[q,s], the
+//           rowsum in dS) and writes it for dK/dV, which runs after it:
+//             S^T = K.Q^T, dP^T = V.dO^T, dS^T as below, dQ^T += K^T.dS^T
 //   dK/dV:  a workgroup owns 128 keys of one kv head (32 per wavefront, K and V rows held in
 //           registers) and walks over the query tiles of every query head of its GQA group:
 //             S = Q.K^T, dP = dO.V^T          (keys on lanes: the accumulator layout)
 //             P = exp2(S*scale*log2e - lse*log2e), dS = P * (dP - D_q)
 //             dV += P^T.dO, dK += dS^T.Q      (P, dS feed the MFMA A operand in place; dO and Q
 //                                              are read transposed from row-major LDS tiles)
-//   dQ:     the forward's structure (a workgroup owns 128 query rows, loops over key tiles):
-//             S^T = K.Q^T, dP^T = V.dO^T, dS^T as above, dQ^T += K^T.dS^T
 // dK and dV of a GQA group are summed in registers (no atomics).  bf16 P and dS are split
 // into hi + lo bf16 operands so the products keep ~16 bits.  Masks: top-left causal,
 // bool / additive (read per element; an additive mask that does not depend on the query row is
@@ -32,29 +33,6 @@ constexpr int BKV = 128;  // keys per dK/dV workgroup (32 per wavefront)
 constexpr int BQ = 64;    // query rows per dK/dV step
 constexpr int BMQ = 128;  // query rows per dQ workgroup (32 per wavefront)
 constexpr int BNK = 64;   // key rows per dQ step
-
-// ---- delta = rowsum(dO * O) ------------------------------------------------------------------
-
-template <typename T>
-__device__ inline float to_f(T x) { return (float)x; }
-
-template <typename T, typename TO, int D>
-__global__ __launch_bounds__(256) void bwd_delta_kernel(const T *__restrict__ dout, const TO *__restrict__ o,
-                                                        float *__restrict__ delta, int64_t rows) {
-    constexpr int PER = D / 16;  // values per lane, 16 lanes per row
-    const int64_t row = ((int64_t)blockIdx.x * 256 + threadIdx.x) / 16;
-    const int sub = threadIdx.x % 16;
-    float acc = 0.0f;
-    if (row < rows) {
-        const T *g = dout + row * D + sub * PER;
-        const TO *x = o + row * D + sub * PER;
-#pragma unroll
-        for (int e = 0; e < PER; ++e) acc = fmaf(to_f(g[e]), to_f(x[e]), acc);
-    }
-#pragma unroll
-    for (int m = 1; m < 16; m <<= 1) acc += __shfl_xor(acc, m, 64);
-    if (row < rows && sub == 0) delta[row] = acc;
-}
 
 // Mask value for (b, h, query, key) under the compile-time mask mode: returns false when the
 // position is blocked; `add` receives an additive term in raw-score units.
@@ -320,10 +298,34 @@ __global__ __launch_bounds__(256, D <= 64 && (MASK == 0 || MASK == 4) ? 2 : 1) v
         }
     }
     const float lse2 = ((const float *)f.lse)[bh * f.L + lqc] * kLog2e;
-    // dP accumulates onto -delta of this lane's query: dP - delta with no per-element subtract
+    // delta = rowsum(dO * O) of this lane's query (the two lanes of a row each hold half of it;
+    // O is the training forward's float32 output when given, else the rounded one), written for
+    // the dK/dV kernel that runs next; dP accumulates onto -delta (no per-element subtract)
     f32x16 dinit;
     {
-        const float dlt = ((const float *)a.delta)[bh * f.L + lqc];
+        float part = 0.0f;
+        if (a.o_f32) {
+            const float *orow = (const float *)f.o + (bh * f.L + lqc) * D + 8 * half;
+#pragma unroll
+            for (int t = 0; t < DT; ++t) {
+                const f32x4 o0 = *(const f32x4 *)(orow + 16 * t), o1 = *(const f32x4 *)(orow + 16 * t + 4);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    part = fmaf((float)gf[t][e], o0[e], part);
+                    part = fmaf((float)gf[t][e + 4], o1[e], part);
+                }
+            }
+        } else {
+            const T *orow = (const T *)f.o + (bh * f.L + lqc) * D + 8 * half;
+#pragma unroll
+            for (int t = 0; t < DT; ++t) {
+                const V8 ov = __builtin_bit_cast(V8, *(const u32x4 *)(orow + 16 * t));
+#pragma unroll
+                for (int e = 0; e < 8; ++e) part = fmaf((float)gf[t][e], (float)ov[e], part);
+            }
+        }
+        const float dlt = xhalf_sum(part);
+        if (half == 0 && lq < L) ((float *)a.delta)[bh * f.L + lq] = dlt;
 #pragma unroll
         for (int i = 0; i < 16; ++i) dinit[i] = -dlt;
     }
@@ -457,22 +459,13 @@ __global__ __launch_bounds__(256, D <= 64 && (MASK == 0 || MASK == 4) ? 2 : 1) v
 template <typename T, int D, bool CAUSAL, int MASK>
 hipError_t launch_bwd_typed(const AttnBwdArgs &a, hipStream_t s) {
     const AttnFwdArgs &f = a.f;
-    const int64_t rows = f.B * f.H * f.L;
-    const dim3 dgrid((unsigned)((rows * 16 + 255) / 256));
-    if (a.o_f32)
-        hipLaunchKernelGGL((bwd_delta_kernel<T, float, D>), dgrid, dim3(256), 0, s, (const T *)a.dout,
-                           (const float *)f.o, (float *)a.delta, rows);
-    else
-        hipLaunchKernelGGL((bwd_delta_kernel<T, T, D>), dgrid, dim3(256), 0, s, (const T *)a.dout, (const T *)f.o,
-                           (float *)a.delta, rows);
+    // dQ first: it computes delta = rowsum(dO * O) per query row, which dK/dV reads
+    const int nq = (int)((f.L + BMQ - 1) / BMQ);
+    hipLaunchKernelGGL((bwd_dq_kernel<T, D, CAUSAL, MASK>), dim3((unsigned)(nq * f.B * f.H)), dim3(256), 0, s, a, nq);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const int nkt = (int)((f.S + BKV - 1) / BKV);
     hipLaunchKernelGGL((bwd_dkdv_kernel<T, D, CAUSAL, MASK>), dim3((unsigned)(nkt * f.B * f.Hkv)), dim3(256), 0, s, a);
-    e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    const int nq = (int)((f.L + BMQ - 1) / BMQ);
-    hipLaunchKernelGGL((bwd_dq_kernel<T, D, CAUSAL, MASK>), dim3((unsigned)(nq * f.B * f.H)), dim3(256), 0, s, a, nq);
     return hipGetLastError();
 }
 
