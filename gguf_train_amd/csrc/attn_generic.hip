@@ -484,6 +484,228 @@ __global__ __launch_bounds__(256) void generic_bwd_cols_kernel(AttnBwdArgs a, in
     }
 }
 
+// Backward with LDS staging (head sizes up to 256), the structure of generic_fwd_lds_kernel:
+//   rows: the 4 query rows of a workgroup share chunks of NK keys (K and V transposed in LDS);
+//         one pass per row accumulates U = sum_s P dP K[s], W = sum_s P K[s] and
+//         delta = sum_s P dP, then dQ = scale (U - delta W) = scale sum_s P (dP - delta) K[s];
+//   cols: the 4 keys of a workgroup share chunks of NK query rows (Q and dO transposed, with
+//         their lse and delta) of every query head of the kv head's group:
+//         dV[s] = sum_l P dO[l], dK[s] = scale sum_l P (dP - delta[l]) Q[l].
+// Terms with P == 0 (dS == 0 for dK) are skipped, as the reference's loops skip them.  NJ
+// blocks of 64 output dims per lane.
+template <typename T, typename A, int NK, int NJ>
+__global__ __launch_bounds__(256) void generic_bwd_rows_lds_kernel(AttnBwdArgs a, int64_t row_blocks) {
+    constexpr int LPK = 64 / NK, KT = NK + 1;
+    const AttnFwdArgs &f = a.f;
+    extern __shared__ __attribute__((aligned(16))) unsigned char g_lds[];
+    const int D = (int)f.D, Dv = (int)f.Dv;
+    A *Kt = reinterpret_cast<A *>(g_lds);  // [D][KT]
+    A *Vt = Kt + D * KT;                   // [Dv][KT]
+    A *Qs = Vt + Dv * KT;                  // [kRowsPerBlock][D]
+    A *Gs = Qs + kRowsPerBlock * D;        // [kRowsPerBlock][Dv]: dO rows
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int key = lane % NK, part = lane / NK;
+    const int DPq = (D + LPK - 1) / LPK, DPv = (Dv + LPK - 1) / LPK;
+    const int q_lo = min(part * DPq, D), q_hi = min(q_lo + DPq, D);
+    const int v_lo = min(part * DPv, Dv), v_hi = min(v_lo + DPv, Dv);
+    const int64_t bh = blockIdx.x / row_blocks;
+    const int64_t l0 = (blockIdx.x % row_blocks) * kRowsPerBlock;
+    const int64_t l = l0 + w;
+    const bool active = l < f.L;
+    const int64_t b = bh / f.H, h = bh % f.H, g = h / (f.H / f.Hkv);
+    const T *kb = (const T *)f.k + b * f.k_sb + g * f.k_sh;
+    const T *vb = (const T *)f.v + b * f.v_sb + g * f.v_sh;
+    const int64_t row = bh * f.L + l;
+    const A ninf = neg_inf<A>();
+    const int64_t kvn = attn_kv_len(f, b), qpos = attn_q_pos(f, b);
+    const int64_t l_last = min(l0 + kRowsPerBlock - 1, f.L - 1);
+    const int64_t kend = min(kvn, f.causal ? l_last + qpos + 1 : f.S);
+    const int64_t my_end = active ? min(kvn, f.causal ? l + qpos + 1 : f.S) : 0;
+    const A lse = active ? ((const A *)f.lse)[row] : (A)0;
+
+    const int nrows = (int)min((int64_t)kRowsPerBlock, f.L - l0);
+    stage_rows<kRowsPerBlock, T, A>((const T *)f.q + b * f.q_sb + h * f.q_sh + l0 * f.q_sl, f.q_sl, nrows, D, tid,
+                                    [&](int r, int d, A x) { Qs[r * D + d] = x; });
+    stage_rows<kRowsPerBlock, T, A>((const T *)a.dout + (bh * f.L + l0) * Dv, Dv, nrows, Dv, tid,
+                                    [&](int r, int d, A x) { Gs[r * Dv + d] = x; });
+    int dcol[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) dcol[j] = min(lane + 64 * j, D - 1);
+    A U[NJ], W[NJ], delta = 0;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) U[j] = W[j] = 0;
+    for (int64_t s0 = 0; s0 < kend; s0 += NK) {
+        const int nk = (int)min((int64_t)NK, kend - s0);
+        __syncthreads();  // the previous chunk is no longer read (and Qs / Gs are written)
+        stage_rows<NK, T, A>(kb + s0 * f.k_ss, f.k_ss, nk, D, tid, [&](int r, int d, A x) { Kt[d * KT + r] = x; });
+        stage_rows<NK, T, A>(vb + s0 * f.v_ss, f.v_ss, nk, Dv, tid, [&](int r, int d, A x) { Vt[d * KT + r] = x; });
+        __syncthreads();
+        if (s0 >= my_end) continue;  // this row sees none of the chunk (wave-uniform)
+        const int64_t s = s0 + key;
+        A dot = 0, dpd = 0;
+        {
+            const A *qr = Qs + w * D;
+            const A *gr = Gs + w * Dv;
+#pragma unroll 8
+            for (int d = q_lo; d < q_hi; ++d) dot += qr[d] * Kt[d * KT + key];
+#pragma unroll 8
+            for (int d = v_lo; d < v_hi; ++d) dpd += gr[d] * Vt[d * KT + key];
+        }
+#pragma unroll
+        for (int off = NK; off < 64; off <<= 1) {
+            dot += __shfl_xor(dot, off, 64);
+            dpd += __shfl_xor(dpd, off, 64);
+        }
+        A p = 0;
+        if (s < my_end) {
+            const A sc = apply_mask<A>(f, dot * (A)f.scale, b, h, l, s);
+            if (sc > ninf) p = acc_exp(sc - lse);
+        }
+        const A pdp = p * dpd;
+        delta += wave_sum_reg(part == 0 ? pdp : (A)0);
+        for (int t0 = 0; t0 < nk; t0 += 8) {
+            A pp[8], qq[8], kv[8][NJ];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                pp[u] = lane_value(p, t0 + u);  // lane t holds key t (part 0)
+                qq[u] = lane_value(pdp, t0 + u);
+#pragma unroll
+                for (int j = 0; j < NJ; ++j) kv[u][j] = Kt[dcol[j] * KT + t0 + u];
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+#pragma unroll
+                for (int j = 0; j < NJ; ++j) {
+                    const A x = pp[u] != (A)0 ? kv[u][j] : (A)0;
+                    W[j] += pp[u] * x;
+                    U[j] += qq[u] * x;
+                }
+        }
+    }
+    if (!active) return;
+    if (lane == 0) ((A *)a.delta)[row] = delta;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+        const int d = lane + 64 * j;
+        if (d < D) ((A *)a.dq)[row * D + d] = (U[j] - delta * W[j]) * (A)f.scale;
+    }
+}
+
+template <typename T, typename A, int NQ, int NJ>
+__global__ __launch_bounds__(256) void generic_bwd_cols_lds_kernel(AttnBwdArgs a, int64_t col_blocks) {
+    constexpr int LPQ = 64 / NQ, QT = NQ + 1;
+    const AttnFwdArgs &f = a.f;
+    extern __shared__ __attribute__((aligned(16))) unsigned char g_lds[];
+    const int D = (int)f.D, Dv = (int)f.Dv;
+    A *Qt = reinterpret_cast<A *>(g_lds);  // [D][QT]
+    A *Gt = Qt + D * QT;                   // [Dv][QT]: dO rows, transposed
+    A *Ks = Gt + Dv * QT;                  // [kRowsPerBlock][D]
+    A *Vs = Ks + kRowsPerBlock * D;        // [kRowsPerBlock][Dv]
+    A *Ls = Vs + kRowsPerBlock * Dv;       // [NQ] lse of the chunk's rows
+    A *Ds = Ls + NQ;                       // [NQ] delta of the chunk's rows
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int r = lane % NQ, part = lane / NQ;
+    const int DPq = (D + LPQ - 1) / LPQ, DPv = (Dv + LPQ - 1) / LPQ;
+    const int q_lo = min(part * DPq, D), q_hi = min(q_lo + DPq, D);
+    const int v_lo = min(part * DPv, Dv), v_hi = min(v_lo + DPv, Dv);
+    const int64_t bg = blockIdx.x / col_blocks;
+    const int64_t k0 = (blockIdx.x % col_blocks) * kRowsPerBlock;
+    const int64_t s = k0 + w;
+    const bool active = s < f.S;
+    const int64_t b = bg / f.Hkv, g = bg % f.Hkv;
+    const int64_t group = f.H / f.Hkv;
+    const T *kb = (const T *)f.k + b * f.k_sb + g * f.k_sh;
+    const T *vb = (const T *)f.v + b * f.v_sb + g * f.v_sh;
+    const A ninf = neg_inf<A>();
+    const int64_t kvn = attn_kv_len(f, b), qpos = attn_q_pos(f, b);
+    const bool live = active && s < kvn;  // keys at or past the sequence's length are never seen
+
+    const int nkeys = (int)min((int64_t)kRowsPerBlock, f.S - k0);
+    stage_rows<kRowsPerBlock, T, A>(kb + k0 * f.k_ss, f.k_ss, nkeys, D, tid, [&](int rr, int d, A x) { Ks[rr * D + d] = x; });
+    stage_rows<kRowsPerBlock, T, A>(vb + k0 * f.v_ss, f.v_ss, nkeys, Dv, tid, [&](int rr, int d, A x) { Vs[rr * Dv + d] = x; });
+    int qcol[NJ], vcol[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+        qcol[j] = min(lane + 64 * j, D - 1);
+        vcol[j] = min(lane + 64 * j, Dv - 1);
+    }
+    A adk[NJ], adv[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) adk[j] = adv[j] = 0;
+    // (causal) rows l with l + qpos < k0 see none of the workgroup's keys
+    const int64_t lstart = f.causal ? max((int64_t)0, k0 - qpos) / NQ * NQ : 0;
+    const int64_t lfirst = k0 < kvn ? lstart : f.L;
+    for (int64_t hh = 0; hh < group; ++hh) {
+        const int64_t h = g * group + hh;
+        const int64_t bh = b * f.H + h;
+        for (int64_t c0 = lfirst; c0 < f.L; c0 += NQ) {
+            const int nq = (int)min((int64_t)NQ, f.L - c0);
+            __syncthreads();  // the previous chunk is no longer read (and Ks / Vs are written)
+            stage_rows<NQ, T, A>((const T *)f.q + b * f.q_sb + h * f.q_sh + c0 * f.q_sl, f.q_sl, nq, D, tid,
+                                 [&](int rr, int d, A x) { Qt[d * QT + rr] = x; });
+            stage_rows<NQ, T, A>((const T *)a.dout + (bh * f.L + c0) * Dv, Dv, nq, Dv, tid,
+                                 [&](int rr, int d, A x) { Gt[d * QT + rr] = x; });
+            if (tid < NQ) {
+                Ls[tid] = tid < nq ? ((const A *)f.lse)[bh * f.L + c0 + tid] : (A)0;
+                Ds[tid] = tid < nq ? ((const A *)a.delta)[bh * f.L + c0 + tid] : (A)0;
+            }
+            __syncthreads();
+            if (!live) continue;  // wave-uniform
+            const int64_t l = c0 + r;
+            A dot = 0, dpd = 0;
+            {
+                const A *kr = Ks + w * D;
+                const A *vr = Vs + w * Dv;
+#pragma unroll 8
+                for (int d = q_lo; d < q_hi; ++d) dot += kr[d] * Qt[d * QT + r];
+#pragma unroll 8
+                for (int d = v_lo; d < v_hi; ++d) dpd += vr[d] * Gt[d * QT + r];
+            }
+#pragma unroll
+            for (int off = NQ; off < 64; off <<= 1) {
+                dot += __shfl_xor(dot, off, 64);
+                dpd += __shfl_xor(dpd, off, 64);
+            }
+            A p = 0, ds = 0;
+            if (r < nq && (!f.causal || s <= l + qpos)) {
+                const A sc = apply_mask<A>(f, dot * (A)f.scale, b, h, l, s);
+                if (sc > ninf) {
+                    p = acc_exp(sc - Ls[r]);
+                    ds = p * (dpd - Ds[r]);
+                }
+            }
+            for (int t0 = 0; t0 < nq; t0 += 8) {
+                A pp[8], dd[8], gv[8][NJ], qv[8][NJ];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    pp[u] = lane_value(p, t0 + u);  // lane t holds row t (part 0)
+                    dd[u] = lane_value(ds, t0 + u);
+#pragma unroll
+                    for (int j = 0; j < NJ; ++j) {
+                        gv[u][j] = Gt[vcol[j] * QT + t0 + u];
+                        qv[u][j] = Qt[qcol[j] * QT + t0 + u];
+                    }
+                }
+#pragma unroll
+                for (int u = 0; u < 8; ++u)
+#pragma unroll
+                    for (int j = 0; j < NJ; ++j) {
+                        adv[j] += pp[u] * (pp[u] != (A)0 ? gv[u][j] : (A)0);
+                        adk[j] += dd[u] * (dd[u] != (A)0 ? qv[u][j] : (A)0);
+                    }
+            }
+        }
+    }
+    if (!active) return;
+    const int64_t col = bg * f.S + s;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+        const int d = lane + 64 * j;
+        if (d < Dv) ((A *)a.dv)[col * Dv + d] = adv[j];
+        if (d < D) ((A *)a.dk)[col * D + d] = adk[j] * (A)f.scale;
+    }
+}
+
 template <typename T, typename A, int NK>
 hipError_t launch_lds(int nj, int64_t grid, size_t bytes, const AttnFwdArgs &a, int64_t row_blocks, hipStream_t s) {
     if (nj == 1)
@@ -520,18 +742,53 @@ hipError_t launch_fwd(const AttnFwdArgs &a, hipStream_t s) {
     return hipGetLastError();
 }
 
+template <typename T, typename A, int NK, int NJ>
+void launch_bwd_lds(const AttnBwdArgs &a, int64_t rgrid, int64_t row_blocks, int64_t cgrid, int64_t col_blocks,
+                    size_t rbytes, size_t cbytes, hipStream_t s) {
+    if (rgrid > 0)
+        hipLaunchKernelGGL((generic_bwd_rows_lds_kernel<T, A, NK, NJ>), dim3((unsigned)rgrid), dim3(256), rbytes, s, a,
+                           row_blocks);
+    if (cgrid > 0)
+        hipLaunchKernelGGL((generic_bwd_cols_lds_kernel<T, A, NK, NJ>), dim3((unsigned)cgrid), dim3(256), cbytes, s, a,
+                           col_blocks);
+}
+
+template <typename T, typename A, int NK>
+void launch_bwd_lds_nj(int nj, const AttnBwdArgs &a, int64_t rgrid, int64_t row_blocks, int64_t cgrid,
+                       int64_t col_blocks, size_t rbytes, size_t cbytes, hipStream_t s) {
+    if (nj == 1) launch_bwd_lds<T, A, NK, 1>(a, rgrid, row_blocks, cgrid, col_blocks, rbytes, cbytes, s);
+    else if (nj == 2) launch_bwd_lds<T, A, NK, 2>(a, rgrid, row_blocks, cgrid, col_blocks, rbytes, cbytes, s);
+    else launch_bwd_lds<T, A, NK, 4>(a, rgrid, row_blocks, cgrid, col_blocks, rbytes, cbytes, s);
+}
+
 template <typename T, typename A>
 hipError_t launch_bwd(const AttnBwdArgs &a, hipStream_t s) {
     const AttnFwdArgs &f = a.f;
     const int64_t row_blocks = (f.L + kRowsPerBlock - 1) / kRowsPerBlock;
     const int64_t rgrid = row_blocks * f.B * f.H;
+    const int64_t col_blocks = (f.S + kRowsPerBlock - 1) / kRowsPerBlock;
+    const int64_t cgrid = col_blocks * f.B * f.Hkv;
+    // LDS-staged kernels (head sizes up to 256): chunks of 64, 32 or 16 keys (rows for dK/dV),
+    // the largest whose transposed K and V (Q and dO) fit in 48 KB
+    if (f.D <= 256 && f.Dv <= 256 && f.D > 0 && f.Dv > 0) {
+        const size_t dd = (size_t)(f.D + f.Dv);
+        auto rbytes = [&](int nk) { return (dd * (nk + 1) + kRowsPerBlock * dd) * sizeof(A); };
+        auto cbytes = [&](int nk) { return (dd * (nk + 1) + kRowsPerBlock * dd + 2 * (size_t)nk) * sizeof(A); };
+        const int64_t dm = f.D > f.Dv ? f.D : f.Dv;
+        const int nj = dm <= 64 ? 1 : dm <= 128 ? 2 : 4;
+        constexpr size_t kMax = 48 * 1024;
+        if (cbytes(64) <= kMax) launch_bwd_lds_nj<T, A, 64>(nj, a, rgrid, row_blocks, cgrid, col_blocks, rbytes(64), cbytes(64), s);
+        else if (cbytes(32) <= kMax) launch_bwd_lds_nj<T, A, 32>(nj, a, rgrid, row_blocks, cgrid, col_blocks, rbytes(32), cbytes(32), s);
+        else if (cbytes(16) <= kMax) launch_bwd_lds_nj<T, A, 16>(nj, a, rgrid, row_blocks, cgrid, col_blocks, rbytes(16), cbytes(16), s);
+        else goto unstaged;
+        return hipGetLastError();
+    }
+unstaged:
     if (rgrid > 0) {
         hipLaunchKernelGGL((generic_bwd_rows_kernel<T, A>), dim3((unsigned)rgrid), dim3(256), 0, s, a, row_blocks);
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
     }
-    const int64_t col_blocks = (f.S + kRowsPerBlock - 1) / kRowsPerBlock;
-    const int64_t cgrid = col_blocks * f.B * f.Hkv;
     if (cgrid > 0) {
         hipLaunchKernelGGL((generic_bwd_cols_kernel<T, A>), dim3((unsigned)cgrid), dim3(256), 0, s, a, col_blocks);
     }

@@ -47,6 +47,32 @@ def test_native_backward_matches_oracle(dev, dtype, B, H, Hkv, L, S, D, causal):
     assert_close(dv, wv, tol_dtype, "dv", out_dtype=torch.float32)
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+@pytest.mark.parametrize("D,Dv", [(64, 96), (256, 256), (200, 160), (16, 8), (300, 40), (1, 1)])
+@pytest.mark.parametrize("causal", [False, True])
+def test_generic_backward_chunk_and_value_shapes(dev, dtype, D, Dv, causal):
+    # the generic backward's chunk sizes (64 / 32 / 16 keys or query rows staged per workgroup),
+    # 1, 2 or 4 output blocks of 64 with a partial last one, the unstaged kernels (D > 256),
+    # GQA, 150 keys / 37 rows (partial chunks), key padding plus scattered float mask values
+    B, H, Hkv, L, S = 1, 4, 2, 37, 150
+    seed = D * 17 + Dv
+    q, k, v = randn((B, H, L, D), seed, dtype), randn((B, Hkv, S, D), seed + 1, dtype), randn((B, Hkv, S, Dv), seed + 2, dtype)
+    dout = randn((B, H, L, Dv), seed + 3, dtype)
+    rng = np.random.default_rng(seed)
+    mask = torch.from_numpy(rng.standard_normal((L, S)) * 0.5).to(dtype)
+    mask[:, 120:] = float("-inf")
+    out, lse, out32 = g.flash_attention_train(q.to(dev), k.to(dev), v.to(dev), mask.to(dev), 0.0, causal)
+    dq, dk, dv = g.flash_attention_backward(dout.to(dev), q.to(dev), k.to(dev), v.to(dev), mask.to(dev),
+                                            out if out32 is None else out32, lse, 0.0, causal)
+    assert dq.shape == q.shape and dk.shape == k.shape and dv.shape == v.shape
+    wq, wk, wv = oracle_grads(dout, q, k, v, mask=mask, is_causal=causal)
+    assert_close(dq, wq, dtype, f"dq D={D} Dv={Dv}")
+    assert_close(dk, wk, dtype, f"dk D={D} Dv={Dv}")
+    assert_close(dv, wv, dtype, f"dv D={D} Dv={Dv}")
+    # keys 120.. are never visible: their gradients are exactly zero
+    assert not dk[:, :, 120:].any() and not dv[:, :, 120:].any()
+
+
 def test_gradcheck_float64(dev):
     torch.manual_seed(0)
     q, k, v = (torch.randn(1, 2, 4, 8, dtype=torch.float64, device=dev, requires_grad=True) for _ in range(3))
