@@ -455,15 +455,22 @@ extern "C" int gt_flash_attention_backward(const gt_tensor *grad_out, const gt_t
     const int gd = cd == GT_F64 ? GT_F64 : GT_F32;
     Temps tmp;
 
-    // the forward's residuals (output and log-sum-exp): given, or recomputed by a forward pass
+    // the forward's residuals (output and log-sum-exp): given, or recomputed by a forward pass.
+    // The fp16/bf16 MFMA backward forms rowsum(dP * P) as rowsum(dO * O), exact with the float32
+    // output the training forward keeps; an output rounded to fp16/bf16 would carry its rounding
+    // into every dS, so that case recomputes the float32 output (the forward is deterministic:
+    // it is the training forward's copy bit for bit).
     const gt_tensor *lse_s = nullptr, *out_s = nullptr;
-    if (!lse || !out) {
-        gt_tensor *o2 = nullptr, *l2 = nullptr;
-        if (attention_forward(who, q, k, v, mask, scale, is_causal, &o2, &l2) != 0) return -1;
+    const bool mfma_shape = (cd == GT_F16 || cd == GT_BF16) && D == Dv && (D == 64 || D == 128);
+    if (!lse || !out || (mfma_shape && out->dtype != GT_F32)) {
+        gt_tensor *o2 = nullptr, *l2 = nullptr, *o32 = nullptr;
+        if (attention_forward(who, q, k, v, mask, scale, is_causal, &o2, &l2, mfma_shape ? &o32 : nullptr) != 0)
+            return -1;
         tmp.keep(o2);
         tmp.keep(l2);
-        lse = l2;
-        out = o2;
+        tmp.keep(o32);
+        if (!lse) lse = l2;
+        out = o32 ? o32 : o2;
     }
     lse_s = (lse->device_type == GT_DEV_CUDA && lse->device_index == dev && lse->dtype == gd && gt_is_dense(lse))
                 ? lse

@@ -160,15 +160,18 @@ GT_API int gt_flash_attention_lse(const gt_tensor *q, const gt_tensor *k, const 
 
 /* No counterpart in the reference: the training forward.  As gt_flash_attention_lse, plus
  * out32 = the float32 output before it is rounded to float16/bfloat16 (for float32/float64
- * inputs out32 is NULL and `out` itself is exact).  Passing out32 as the backward's `out`
- * makes its rowsum(dO * O) exact.  Returns 0 on success. */
+ * inputs out32 is NULL and `out` itself is exact).  Pass out32 as the backward's `out`: its
+ * rowsum(dO * O) is then exact without recomputing anything.  Returns 0 on success. */
 GT_API int gt_flash_attention_train(const gt_tensor *q, const gt_tensor *k, const gt_tensor *v, const gt_tensor *mask,
                                     float scale, int is_causal, gt_tensor **out, gt_tensor **lse, gt_tensor **out32);
 
 /* Replaces the Python composition FlashAttentionFn.backward (gguf_train/_functions.py:1933-1965)
  * with a native recompute-based backward.  dq (B,H,L,D), dk (B,Hkv,S,D), dv (B,Hkv,S,Dv) are
  * float32 for float16/bfloat16/float32 inputs and float64 for float64 inputs; gradients of
- * a GQA group are summed into its kv head.  Returns 0 on success. */
+ * a GQA group are summed into its kv head.  `out` (the forward's output) and `lse` may be NULL:
+ * they are recomputed; for float16/bfloat16 inputs an `out` that is not the float32 copy from
+ * gt_flash_attention_train also makes the backward recompute that copy (one forward pass), so
+ * the result does not depend on the output's rounding.  Returns 0 on success. */
 GT_API int gt_flash_attention_backward(const gt_tensor *grad_out, const gt_tensor *q, const gt_tensor *k,
                                        const gt_tensor *v, const gt_tensor *mask, const gt_tensor *out,
                                        const gt_tensor *lse, float scale, int is_causal, gt_tensor **dq,

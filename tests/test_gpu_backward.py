@@ -73,6 +73,28 @@ def test_generic_backward_chunk_and_value_shapes(dev, dtype, D, Dv, causal):
     assert not dk[:, :, 120:].any() and not dv[:, :, 120:].any()
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("given", ["rounded_out", "nothing", "rounded_out_no_lse"])
+def test_backward_from_the_rounded_output(dev, dtype, D, given):
+    # the C ABI also takes the forward's output in the input dtype (not the float32 copy the
+    # training forward keeps), or no output / log-sum-exp at all: the float32 output is then
+    # recomputed, so rowsum(dO * O) carries no output rounding
+    B, H, Hkv, L, S = 2, 4, 2, 70, 70
+    seed = D + (3 if dtype == torch.float16 else 5)
+    q, k, v = randn((B, H, L, D), seed, dtype), randn((B, Hkv, S, D), seed + 1, dtype), randn((B, Hkv, S, D), seed + 2, dtype)
+    dout = randn((B, H, L, D), seed + 3, dtype)
+    out, lse = g.flash_attention_lse(q.to(dev), k.to(dev), v.to(dev), None, 0.0, True)
+    assert out.dtype == dtype
+    o_arg = None if given == "nothing" else out
+    l_arg = lse if given == "rounded_out" else None
+    dq, dk, dv = g.flash_attention_backward(dout.to(dev), q.to(dev), k.to(dev), v.to(dev), None, o_arg, l_arg, 0.0, True)
+    wq, wk, wv = oracle_grads(dout, q, k, v, is_causal=True)
+    assert_close(dq, wq, torch.bfloat16, "dq", out_dtype=torch.float32)
+    assert_close(dk, wk, torch.bfloat16, "dk", out_dtype=torch.float32)
+    assert_close(dv, wv, torch.bfloat16, "dv", out_dtype=torch.float32)
+
+
 def test_gradcheck_float64(dev):
     torch.manual_seed(0)
     q, k, v = (torch.randn(1, 2, 4, 8, dtype=torch.float64, device=dev, requires_grad=True) for _ in range(3))
