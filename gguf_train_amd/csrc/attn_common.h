@@ -63,6 +63,27 @@ struct AttnBwdArgs {
     void *delta;           // (B,H,L) scratch: rowsum(P * dP)
 };
 
+// Split count of a split-K decode launch over `units` (sequence, kv head) pairs of `steps` key
+// steps each on `slots` resident workgroups: the n in 1 .. max_splits with the smallest time in
+// key steps, rounds(n) x (steps per split + 1, a workgroup's fixed cost: query load, first
+// load latency, epilogue) + n / 32 (each split's share of the merge).  A fixed per-split
+// penalty would starve short batches: one sequence of 8 kv heads and 32768 keys needs all 64
+// splits (512 workgroups) to cover the GPU.
+inline int decode_split_count(int64_t units, int64_t steps, int64_t slots, int64_t max_splits) {
+    int best = 1;
+    double best_cost = 1e300;
+    for (int64_t n = 1; n <= max_splits; ++n) {
+        const int64_t rounds = (units * n + slots - 1) / slots;
+        const int64_t per = (steps + n - 1) / n;
+        const double cost = (double)rounds * (double)(per + 1) + (double)n / 32.0;
+        if (cost < best_cost - 1e-9) {
+            best_cost = cost;
+            best = (int)n;
+        }
+    }
+    return best;
+}
+
 // Single-query (L == 1) split-K decode: per-chunk partials, then a merge.
 struct DecodeArgs {
     AttnFwdArgs f;

@@ -689,18 +689,8 @@ hipError_t launch_attn_decode_merge(const DecodeArgs &a, int out_dtype, hipStrea
 int attn_decode_q8_splits(const AttnFwdArgs &f) {
     const void *kernel = q8_kernel(f);
     const int64_t slots = kernel ? resident_slots(kernel) : 512;
-    const int64_t wgs = f.B * f.Hkv;
-    const int64_t maxs = std::min<int64_t>(64, (f.S + kStep - 1) / kStep);
-    int best = 1;
-    double best_cost = 1e30;
-    for (int64_t n = 1; n <= maxs; ++n) {
-        const double cost = (double)((wgs * n + slots - 1) / slots) / (double)n + (n > 1 ? 0.02 * (double)n : 0.0);
-        if (cost < best_cost - 1e-9) {
-            best_cost = cost;
-            best = (int)n;
-        }
-    }
-    return best;
+    const int64_t steps = (f.S + kStep - 1) / kStep;
+    return decode_split_count(f.B * f.Hkv, steps, slots, std::min<int64_t>(64, steps));
 }
 
 bool attn_decode_q8_supported(const AttnFwdArgs &f, int q_dtype) {
