@@ -63,7 +63,19 @@ struct AttnBwdArgs {
     void *delta;           // (B,H,L) scratch: rowsum(P * dP)
 };
 
-// Split count of a split-K decode launch over `units` (sequence, kv head) pairs of `steps` key
+// Query heads per decode workgroup: a kv head's gtot query heads (GQA / MQA) run in groups of
+// 1, 2, 4 or 8 heads, the 16 MFMA columns holding one group; more than 8 heads take several
+// workgroups over the same keys.
+inline int decode_head_tile(int64_t gtot) { return gtot > 4 ? 8 : gtot > 2 ? 4 : (int)gtot; }
+
+// Workgroups along blockIdx.y of a decode launch, (sequence, kv head, head group); also the
+// number of arrival counters its splits use.
+inline int64_t decode_units(int64_t B, int64_t H, int64_t Hkv) {
+    const int64_t gtot = H / Hkv, tile = decode_head_tile(gtot);
+    return B * Hkv * ((gtot + tile - 1) / tile);
+}
+
+// Split count of a split-K decode launch over `units` (sequence, kv head, head group) of `steps` key
 // steps each on `slots` resident workgroups: the n in 1 .. max_splits with the smallest time in
 // key steps, rounds(n) x (steps per split + 1, a workgroup's fixed cost: query load, first
 // load latency, epilogue) + n / 32 (each split's share of the merge).  A fixed per-split
@@ -90,7 +102,7 @@ struct DecodeArgs {
     float *part_o;   // (B*H, nsplit, D) unnormalised chunk outputs
     float *part_ml;  // (B*H, nsplit, 2) chunk max (log2 domain) and sum of exp2
     int nsplit;
-    int *counters;   // (B*Hkv) zeroed arrival counters in uncached memory (part_o / part_ml then too):
+    int *counters;   // (decode_units) zeroed arrival counters in uncached memory (part_o / part_ml too):
                      // the last split merges in the kernel; null: a merge launch
 };
 

@@ -141,17 +141,22 @@ __global__ __launch_bounds__(256, 2) void decode_stream_kernel(DecodeArgs a) {
     const int l16 = lane & 15, q4 = lane >> 4;
     const int sub = lane % LPR, vrow = lane / LPR;
     const int split = blockIdx.x;
-    const int64_t bk = blockIdx.y, b = bk / f.Hkv, hk = bk % f.Hkv;
+    // blockIdx.y = (sequence, kv head, head group): the kv head's gtot query heads run in
+    // groups of G (the last group may hold fewer, gv; its padding columns are blocked)
+    const int gtot = (int)(f.H / f.Hkv), ngrp = (gtot + G - 1) / G;
+    const int64_t bkg = blockIdx.y, bk = bkg / ngrp, b = bk / f.Hkv, hk = bk % f.Hkv;
+    const int hg = (int)(bkg % ngrp);
+    const int h0 = (int)hk * gtot + hg * G, gv = min(G, gtot - hg * G);
     const int S = (int)f.S;
     const int span = ((S + kStep - 1) / kStep + a.nsplit - 1) / a.nsplit * kStep;  // keys per split
     const int kbeg = split * span, kend = min(attn_decode_end(f, b), kbeg + span);
     const int nsteps = kend > kbeg ? (kend - kbeg + kStep - 1) / kStep : 0;
 
-    // B operand (Q^T): lane holds Q[head l16][32t + 8 q4 + 0..7]; columns l16 >= G repeat head
-    // G-1 and are discarded
+    // B operand (Q^T): lane holds Q[head h0 + l16][32t + 8 q4 + 0..7]; columns l16 >= gv repeat
+    // head h0 + gv - 1 and are discarded
     V8 qb[NT];
     {
-        const T *qr = (const T *)f.q + b * f.q_sb + (hk * G + min(l16, G - 1)) * f.q_sh + 8 * q4;
+        const T *qr = (const T *)f.q + b * f.q_sb + (h0 + min(l16, gv - 1)) * f.q_sh + 8 * q4;
 #pragma unroll
         for (int t = 0; t < NT; ++t) qb[t] = __builtin_bit_cast(V8, *(const u32x4 *)(qr + 32 * t));
     }
@@ -181,7 +186,7 @@ __global__ __launch_bounds__(256, 2) void decode_stream_kernel(DecodeArgs a) {
     };
 
     const float cs = f.scale * kLog2e;
-    const int64_t mrow = b * f.m_sb + (hk * G + min(l16, G - 1)) * f.m_sh;
+    const int64_t mrow = b * f.m_sb + (h0 + min(l16, gv - 1)) * f.m_sh;
     float m = -INFINITY;  // running max of head l16 (log2 domain), same in the 4 lanes of a head
     float lsum = 0.0f;    // running sum of head l16
     float acc[G][8];      // unnormalised O of every head, dims 8 sub .. +7, this lane's rows
@@ -203,7 +208,7 @@ __global__ __launch_bounds__(256, 2) void decode_stream_kernel(DecodeArgs a) {
             for (int i = 0; i < 4; ++i) {
                 const int key = k0 + 16 * kb + 4 * q4 + i;
                 float x = c4[i] * cs;
-                bool blocked = key >= kend || l16 >= G;
+                bool blocked = key >= kend || l16 >= gv;
                 if (MASK != 0) {
                     const int64_t mi = mrow + (int64_t)min(key, S - 1) * f.m_ss;
                     if (MASK == 1) blocked = blocked || !((const uint8_t *)f.mask)[mi];
@@ -299,7 +304,7 @@ __global__ __launch_bounds__(256, 2) void decode_stream_kernel(DecodeArgs a) {
             for (int j = 0; j < 8; ++j) s_o[w][h][8 * sub + j] = acc[h][j];
     }
     __syncthreads();
-    for (int e = tid; e < G * D; e += 256) {
+    for (int e = tid; e < gv * D; e += 256) {
         const int h = e / D, d = e % D;
         const float M = fmaxf(fmaxf(s_m[0][h], s_m[1][h]), fmaxf(s_m[2][h], s_m[3][h]));
         float o = 0.0f, L = 0.0f;
@@ -309,7 +314,7 @@ __global__ __launch_bounds__(256, 2) void decode_stream_kernel(DecodeArgs a) {
             o = fmaf(wg, s_o[ww][h][d], o);
             L = fmaf(wg, s_l[ww][h], L);
         }
-        const int64_t row = b * f.H + hk * G + h;
+        const int64_t row = b * f.H + h0 + h;
         if (a.nsplit == 1) {
             // the whole key range: normalise and store
             store_t<T>(f.o, row * D + d, L > 0.0f ? o / L : 0.0f);
@@ -323,7 +328,7 @@ __global__ __launch_bounds__(256, 2) void decode_stream_kernel(DecodeArgs a) {
             }
         }
     }
-    if (a.nsplit > 1 && a.counters) gtdecode::finish_split<T, D>(a, bk, b * f.H + hk * G, G);
+    if (a.nsplit > 1 && a.counters) gtdecode::finish_split<T, D>(a, bkg, b * f.H + h0, gv);
 }
 
 // D = 256: a key row is split over D/8 lanes (16-byte loads), dot products reduced across lanes.
@@ -530,7 +535,7 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a) {
 
 template <typename T, int D, int G>
 hipError_t launch_typed(const DecodeArgs &a, hipStream_t s) {
-    dim3 grid((unsigned)a.nsplit, (unsigned)(a.f.B * a.f.Hkv));
+    dim3 grid((unsigned)a.nsplit, (unsigned)decode_units(a.f.B, a.f.H, a.f.Hkv));
     if constexpr (D <= 128) {
         const int mode = !a.f.mask ? 0 : (a.f.mask_bool ? 1 : 2);
         if (mode == 0) hipLaunchKernelGGL((decode_stream_kernel<T, D, G, 0>), grid, dim3(256), 0, s, a);
@@ -610,7 +615,7 @@ const void *stream_kernel_d(const AttnFwdArgs &f, int G) {
 }
 
 const void *stream_kernel(const AttnFwdArgs &f, int cd) {
-    const int G = (int)(f.H / f.Hkv);
+    const int G = decode_head_tile(f.H / f.Hkv);
     if (cd == GT_F16) return f.D == 128 ? stream_kernel_d<_Float16, 128>(f, G) : stream_kernel_d<_Float16, 64>(f, G);
     return f.D == 128 ? stream_kernel_d<__bf16, 128>(f, G) : stream_kernel_d<__bf16, 64>(f, G);
 }
@@ -641,7 +646,7 @@ int attn_decode_splits(const AttnFwdArgs &f, int cd) {
     const void *kernel = stream_kernel(f, cd);
     const int64_t slots = kernel ? resident_slots(kernel) : 512;
     const int64_t steps = (f.S + kStep - 1) / kStep;
-    return decode_split_count(f.B * f.Hkv, steps, slots, std::min<int64_t>(64, steps));
+    return decode_split_count(decode_units(f.B, f.H, f.Hkv), steps, slots, std::min<int64_t>(64, steps));
 }
 
 bool attn_decode_supported(const AttnFwdArgs &f, int cd) {
@@ -651,9 +656,11 @@ bool attn_decode_supported(const AttnFwdArgs &f, int cd) {
     // 32-bit byte offsets of K/V rows from the (batch, kv head) base
     if ((f.S - 1) * f.k_ss * 2 + f.D * 2 > 0xffffffffLL || (f.S - 1) * f.v_ss * 2 + f.D * 2 > 0xffffffffLL) return false;
     if (f.D != 64 && f.D != 128 && f.D != 256) return false;
+    // any number of query heads per kv head on the streaming kernel (D <= 128), in groups of
+    // up to 8; the D = 256 kernel takes 1, 2, 4 or 8
     const int64_t G = f.H / f.Hkv;
-    if (G != 1 && G != 2 && G != 4 && G != 8) return false;
-    if (f.D / 8 < G) return false;
+    if (f.D == 256 && G != 1 && G != 2 && G != 4 && G != 8) return false;
+    if (decode_units(f.B, f.H, f.Hkv) > 65535) return false;  // grid.y
     // 16-byte row loads: every row start must be 16-byte aligned
     const int64_t strides[] = {f.q_sb, f.q_sh, f.k_sb, f.k_sh, f.k_ss, f.v_sb, f.v_sh, f.v_ss};
     for (int64_t st : strides) if (st % 8 != 0) return false;
@@ -662,7 +669,7 @@ bool attn_decode_supported(const AttnFwdArgs &f, int cd) {
 }
 
 hipError_t launch_attn_decode(const DecodeArgs &a, int cd, hipStream_t s) {
-    const int G = (int)(a.f.H / a.f.Hkv);
+    const int G = decode_head_tile(a.f.H / a.f.Hkv);
     if (cd == GT_F16) return launch_d<_Float16>(a, G, s);
     if (cd == GT_BF16) return launch_d<__bf16>(a, G, s);
     return hipErrorInvalidValue;

@@ -127,18 +127,23 @@ __global__ __launch_bounds__(256, 2) void decode_q8_mfma_kernel(DecodeArgs a) {
     const int sub = lane % LPR, vrow = lane / LPR;
     const int vblk = sub >> 2, vpart = sub & 3;  // V: block and 8-value part of this lane
     const int split = blockIdx.x;
-    const int64_t bk = blockIdx.y, b = bk / f.Hkv, hk = bk % f.Hkv;
+    // blockIdx.y = (sequence, kv head, head group): the kv head's gtot query heads run in
+    // groups of G (the last group may hold fewer, gv; its padding columns are blocked)
+    const int gtot = (int)(f.H / f.Hkv), ngrp = (gtot + G - 1) / G;
+    const int64_t bkg = blockIdx.y, bk = bkg / ngrp, b = bk / f.Hkv, hk = bk % f.Hkv;
+    const int hg = (int)(bkg % ngrp);
+    const int h0 = (int)hk * gtot + hg * G, gv = min(G, gtot - hg * G);
     const int S = (int)f.S;
     const int span = ((S + kStep - 1) / kStep + a.nsplit - 1) / a.nsplit * kStep;
     const int kbeg = split * span, kend = min(attn_decode_end(f, b), kbeg + span);
     const int nsteps = kend > kbeg ? (kend - kbeg + kStep - 1) / kStep : 0;
 
-    // B operand (Q^T, fp16): lane holds Q[head l16][32t + 8 q4 + 0..7]; columns l16 >= G repeat
-    // head G-1 and are discarded.  cq[t]: 1152 x the sum of block t of head l16's query.
+    // B operand (Q^T, fp16): lane holds Q[head h0 + l16][32t + 8 q4 + 0..7]; columns l16 >= gv
+    // repeat head h0 + gv - 1 and are discarded.  cq[t]: 1152 x the sum of block t of that query.
     half8_t qb[NB];
     float cq[NB];
     {
-        const _Float16 *qr = (const _Float16 *)f.q + b * f.q_sb + (hk * G + min(l16, G - 1)) * f.q_sh + 8 * q4;
+        const _Float16 *qr = (const _Float16 *)f.q + b * f.q_sb + (h0 + min(l16, gv - 1)) * f.q_sh + 8 * q4;
 #pragma unroll
         for (int t = 0; t < NB; ++t) {
             const u32x4 x = *(const u32x4 *)(qr + 32 * t);
@@ -185,7 +190,7 @@ __global__ __launch_bounds__(256, 2) void decode_q8_mfma_kernel(DecodeArgs a) {
     };
 
     const float cs = f.scale * kLog2e;
-    const int64_t mrow = b * f.m_sb + (hk * G + min(l16, G - 1)) * f.m_sh;
+    const int64_t mrow = b * f.m_sb + (h0 + min(l16, gv - 1)) * f.m_sh;
     const half8_t neg_magic = {(_Float16)-kMagic, (_Float16)-kMagic, (_Float16)-kMagic, (_Float16)-kMagic,
                                (_Float16)-kMagic, (_Float16)-kMagic, (_Float16)-kMagic, (_Float16)-kMagic};
     float m = -INFINITY;  // running max of head l16 (log2 domain)
@@ -243,7 +248,7 @@ __global__ __launch_bounds__(256, 2) void decode_q8_mfma_kernel(DecodeArgs a) {
             for (int i = 0; i < 4; ++i) {
                 const int key = k0 + 16 * kb + 4 * q4 + i;
                 float x = sum4[i] * cs;
-                bool blocked = key >= kend || l16 >= G;
+                bool blocked = key >= kend || l16 >= gv;
                 if (MASK != 0) {
                     const int64_t mi = mrow + (int64_t)min(key, S - 1) * f.m_ss;
                     if (MASK == 1) blocked = blocked || !((const uint8_t *)f.mask)[mi];
@@ -332,7 +337,7 @@ __global__ __launch_bounds__(256, 2) void decode_q8_mfma_kernel(DecodeArgs a) {
                 for (int i = 0; i < 4; ++i) s_o[w][l16][32 * t + 16 * h + 4 * q4 + i] = acc[t][h][i];
     }
     __syncthreads();
-    for (int e = tid; e < G * D; e += 256) {
+    for (int e = tid; e < gv * D; e += 256) {
         const int h = e / D, d = e % D;
         const float M = fmaxf(fmaxf(s_m[0][h], s_m[1][h]), fmaxf(s_m[2][h], s_m[3][h]));
         float o = 0.0f, L = 0.0f;
@@ -342,7 +347,7 @@ __global__ __launch_bounds__(256, 2) void decode_q8_mfma_kernel(DecodeArgs a) {
             o = fmaf(wg, s_o[ww][h][d], o);
             L = fmaf(wg, s_l[ww][h], L);
         }
-        const int64_t row = b * f.H + hk * G + h;
+        const int64_t row = b * f.H + h0 + h;
         if (a.nsplit == 1) {
             ((_Float16 *)f.o)[row * D + d] = (_Float16)(L > 0.0f ? o / L : 0.0f);
             if (f.lse && d == 0) ((float *)f.lse)[row] = L > 0.0f ? (M + log2f(L)) * kLn2 : INFINITY;
@@ -355,7 +360,7 @@ __global__ __launch_bounds__(256, 2) void decode_q8_mfma_kernel(DecodeArgs a) {
             }
         }
     }
-    if (a.nsplit > 1 && a.counters) gtdecode::finish_split<_Float16, D>(a, bk, b * f.H + hk * G, G);
+    if (a.nsplit > 1 && a.counters) gtdecode::finish_split<_Float16, D>(a, bkg, b * f.H + h0, gv);
 }
 
 // Reductions over lanes l, l ^ 16 and l, l ^ 32 with v_permlane16/32_swap (VALU, no LDS).
@@ -405,7 +410,12 @@ __global__ __launch_bounds__(256, 2) void decode_q8_lds_kernel(DecodeArgs a) {
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int l16 = lane & 15, q4 = lane >> 4;
     const int split = blockIdx.x;
-    const int64_t bk = blockIdx.y, b = bk / f.Hkv, hk = bk % f.Hkv;
+    // blockIdx.y = (sequence, kv head, head group): the kv head's gtot query heads run in
+    // groups of G (the last group may hold fewer, gv; its padding columns are blocked)
+    const int gtot = (int)(f.H / f.Hkv), ngrp = (gtot + G - 1) / G;
+    const int64_t bkg = blockIdx.y, bk = bkg / ngrp, b = bk / f.Hkv, hk = bk % f.Hkv;
+    const int hg = (int)(bkg % ngrp);
+    const int h0 = (int)hk * gtot + hg * G, gv = min(G, gtot - hg * G);
     const int S = (int)f.S;
     const int span = ((S + kStep - 1) / kStep + a.nsplit - 1) / a.nsplit * kStep;
     const int kbeg = split * span, kend = min(attn_decode_end(f, b), kbeg + span);
@@ -414,7 +424,7 @@ __global__ __launch_bounds__(256, 2) void decode_q8_lds_kernel(DecodeArgs a) {
     half8_t qb[NB];
     f32x4 c0[NB];  // -1152 x the block sums of each head's query: the score MFMA's initial value
     {
-        const _Float16 *qr = (const _Float16 *)f.q + b * f.q_sb + (hk * G + min(l16, G - 1)) * f.q_sh + 8 * q4;
+        const _Float16 *qr = (const _Float16 *)f.q + b * f.q_sb + (h0 + min(l16, gv - 1)) * f.q_sh + 8 * q4;
 #pragma unroll
         for (int t = 0; t < NB; ++t) {
             const u32x4 x = *(const u32x4 *)(qr + 32 * t);
@@ -455,7 +465,7 @@ __global__ __launch_bounds__(256, 2) void decode_q8_lds_kernel(DecodeArgs a) {
 
     auto in_row = [](int blk, int part) { return 34 * blk + 8 * part - ((blk & 1) ? 2 : 0); };
     const float cs = f.scale * kLog2e;
-    const int64_t mrow = b * f.m_sb + (hk * G + min(l16, G - 1)) * f.m_sh;
+    const int64_t mrow = b * f.m_sb + (h0 + min(l16, gv - 1)) * f.m_sh;
     float m = -INFINITY, lsum = 0.0f;
     f32x4 acc[NB][2];
 #pragma unroll
@@ -514,7 +524,7 @@ __global__ __launch_bounds__(256, 2) void decode_q8_lds_kernel(DecodeArgs a) {
             for (int i = 0; i < 4; ++i) {
                 const int key = k0 + 16 * kb + 4 * q4 + i;
                 float x = sum4[i] * cs;
-                bool blocked = key >= kend || l16 >= G;
+                bool blocked = key >= kend || l16 >= gv;
                 if (MASK != 0) {
                     const int64_t mi = mrow + (int64_t)min(key, S - 1) * f.m_ss;
                     if (MASK == 1) blocked = blocked || !((const uint8_t *)f.mask)[mi];
@@ -608,7 +618,7 @@ __global__ __launch_bounds__(256, 2) void decode_q8_lds_kernel(DecodeArgs a) {
     }
     __syncthreads();
     const float *o_all = reinterpret_cast<const float *>(&s_raw[0][0][0]);
-    for (int e = tid; e < G * D; e += 256) {
+    for (int e = tid; e < gv * D; e += 256) {
         const int h = e / D, d = e % D;
         const float M = fmaxf(fmaxf(s_m[0][h], s_m[1][h]), fmaxf(s_m[2][h], s_m[3][h]));
         float o = 0.0f, L = 0.0f;
@@ -618,7 +628,7 @@ __global__ __launch_bounds__(256, 2) void decode_q8_lds_kernel(DecodeArgs a) {
             o = fmaf(wg, o_all[ww * WSTRIDE + h * D + d], o);
             L = fmaf(wg, s_l[ww][h], L);
         }
-        const int64_t row = b * f.H + hk * G + h;
+        const int64_t row = b * f.H + h0 + h;
         if (a.nsplit == 1) {
             ((_Float16 *)f.o)[row * D + d] = (_Float16)(L > 0.0f ? o / L : 0.0f);
             if (f.lse && d == 0) ((float *)f.lse)[row] = L > 0.0f ? (M + log2f(L)) * kLn2 : INFINITY;
@@ -631,7 +641,7 @@ __global__ __launch_bounds__(256, 2) void decode_q8_lds_kernel(DecodeArgs a) {
             }
         }
     }
-    if (a.nsplit > 1 && a.counters) gtdecode::finish_split<_Float16, D>(a, bk, b * f.H + hk * G, G);
+    if (a.nsplit > 1 && a.counters) gtdecode::finish_split<_Float16, D>(a, bkg, b * f.H + h0, gv);
 }
 
 template <int D, bool LDS>
@@ -659,7 +669,7 @@ bool q8_stream_ok(const AttnFwdArgs &f) {
 }
 
 const void *q8_kernel(const AttnFwdArgs &f) {
-    const int G = (int)(f.H / f.Hkv);
+    const int G = decode_head_tile(f.H / f.Hkv);
     if (q8_stream_ok(f)) return f.D == 128 ? q8_kernel_d<128, true>(f, G) : q8_kernel_d<64, true>(f, G);
     return f.D == 128 ? q8_kernel_d<128, false>(f, G) : q8_kernel_d<64, false>(f, G);
 }
@@ -690,15 +700,15 @@ int attn_decode_q8_splits(const AttnFwdArgs &f) {
     const void *kernel = q8_kernel(f);
     const int64_t slots = kernel ? resident_slots(kernel) : 512;
     const int64_t steps = (f.S + kStep - 1) / kStep;
-    return decode_split_count(f.B * f.Hkv, steps, slots, std::min<int64_t>(64, steps));
+    return decode_split_count(decode_units(f.B, f.H, f.Hkv), steps, slots, std::min<int64_t>(64, steps));
 }
 
 bool attn_decode_q8_supported(const AttnFwdArgs &f, int q_dtype) {
     if (q_dtype != GT_F16 || f.out_dtype != GT_F16) return false;
     if (f.L != 1 || f.S <= 0 || f.D != f.Dv || (f.D != 64 && f.D != 128)) return false;
     if (f.S >= (1LL << 30) || f.S * (f.D / 32 * 34) > 0xffffffffLL) return false;  // 32-bit offsets
-    const int64_t G = f.H / f.Hkv;
-    if (G != 1 && G != 2 && G != 4 && G != 8) return false;
+    // any number of query heads per kv head, in groups of up to 8
+    if (decode_units(f.B, f.H, f.Hkv) > 65535) return false;  // grid.y
     if (f.q_sh % 8 != 0 || f.q_sb % 8 != 0 || (uintptr_t)f.q % 16 != 0) return false;
     // K/V are whole dense Q8_0 tensors; rows are 4-byte aligned when the base is
     for (const void *p : {f.k, f.v}) if ((uintptr_t)p % 8 != 0) return false;
@@ -708,7 +718,7 @@ bool attn_decode_q8_supported(const AttnFwdArgs &f, int q_dtype) {
 hipError_t launch_attn_decode_q8(const DecodeArgs &a, hipStream_t s) {
     const void *kernel = q8_kernel(a.f);
     if (!kernel) return hipErrorInvalidValue;
-    dim3 grid((unsigned)a.nsplit, (unsigned)(a.f.B * a.f.Hkv));
+    dim3 grid((unsigned)a.nsplit, (unsigned)decode_units(a.f.B, a.f.H, a.f.Hkv));
     void *args[] = {(void *)&a};
     hipError_t e = hipLaunchKernel(kernel, grid, dim3(256), args, 0, s);
     // one split, or the last split merged in the kernel: the kernel wrote the output

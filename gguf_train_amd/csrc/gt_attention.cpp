@@ -185,7 +185,7 @@ bool decode_partials(DecodeArgs &da, int dev, gt_scratch &scratch) {
     const size_t rows = (size_t)(a.B * a.H) * (size_t)da.nsplit;
     const size_t bytes = rows * (size_t)(a.D + 2) * sizeof(float);
     gt_decode_ws ws{};
-    if (da.nsplit > 1 && gt_decode_workspace(dev, gt_stream(), a.B * a.Hkv, bytes, ws)) {
+    if (da.nsplit > 1 && gt_decode_workspace(dev, gt_stream(), decode_units(a.B, a.H, a.Hkv), bytes, ws)) {
         da.counters = ws.counters;
         da.part_o = (float *)ws.parts;
     } else {

@@ -1,4 +1,4 @@
-"""Single-query (decode) attention, the split-K kernel: GQA group sizes, head sizes, KV lengths
+"""Single-query (decode) attention, the split-K kernel: GQA / MQA group sizes, head sizes, KV lengths
 that are not multiples of the chunk, key-padding masks, causal (top-left: key 0 only), and the
 invariant that decoding row t equals row t of a causal prefill (tests/test_llama_bridge.py:105-111)."""
 
@@ -23,6 +23,28 @@ def test_decode_matches_oracle(dev, dtype, G, D, S):
     k, v = randn((B, Hkv, S, D), seed + 1, dtype), randn((B, Hkv, S, D), seed + 2, dtype)
     got = g.flash_attention(q.to(dev), k.to(dev), v.to(dev))
     assert_close(got, oracle_forward(q, k, v), dtype, f"decode G={G} D={D} S={S}")
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("G,D", [(3, 128), (5, 64), (7, 128), (12, 128), (32, 128), (32, 64)])
+@pytest.mark.parametrize("S", [300, 4096])
+def test_decode_any_query_group(dev, dtype, G, D, S):
+    # GQA / MQA groups that are not 1, 2, 4 or 8 heads: the kv head's query heads run in groups
+    # of up to 8 over the same keys, the last group partial; a per-head mask checks that every
+    # group reads its own heads' query and mask rows and writes its own output rows
+    B, Hkv = 2, 2
+    seed = G * 10 + D + S
+    q = randn((B, Hkv * G, 1, D), seed, dtype)
+    k, v = randn((B, Hkv, S, D), seed + 1, dtype), randn((B, Hkv, S, D), seed + 2, dtype)
+    assert_close(g.flash_attention(q.to(dev), k.to(dev), v.to(dev)), oracle_forward(q, k, v), dtype,
+                 f"decode G={G} D={D} S={S}")
+    per_head = torch.from_numpy(np.random.default_rng(seed).random((B, Hkv * G, 1, S)) < 0.3)
+    per_head[:, ::3, :, S // 2:] = False
+    per_head[..., 0] = True
+    out, lse = g.flash_attention_lse(q.to(dev), k.to(dev), v.to(dev), per_head.to(dev))
+    want_o, want_l = oracle_forward(q, k, v, mask=per_head, return_lse=True)
+    assert_close(out, want_o, dtype, f"per-head mask G={G} D={D} S={S}")
+    assert np.abs(lse.cpu().numpy() - want_l).max() < 1e-4
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])

@@ -68,6 +68,29 @@ def test_q8_0_decode_kernel_shapes(dev, G, D, S):
     assert_close(got, oracle_forward(q, kd, vd), torch.float16, f"q8_0 G={G} D={D} S={S}")
 
 
+@pytest.mark.parametrize("G,D", [(3, 128), (7, 64), (12, 128), (32, 128)])
+@pytest.mark.parametrize("S", [300, 8192])
+def test_q8_0_decode_any_query_group(dev, G, D, S):
+    # query groups that are not 1, 2, 4 or 8 heads (groups of up to 8 over the same keys), with a
+    # per-head mask so that each group's query, mask and output rows are checked
+    B, Hkv = 2, 2
+    seed = G * 100 + D + S
+    q = randn((B, Hkv * G, 1, D), seed, torch.float16)
+    k, v = randn((B, Hkv, S, D), seed + 1), randn((B, Hkv, S, D), seed + 2)
+    kb, vb = oracle.q8_0_quantize(k.numpy()), oracle.q8_0_quantize(v.numpy())
+    kq = g.QuantizedTensor(torch.from_numpy(kb).to(dev), tuple(k.shape))
+    vq = g.QuantizedTensor(torch.from_numpy(vb).to(dev), tuple(v.shape))
+    kd = torch.from_numpy(oracle.q8_0_dequantize(kb).reshape(k.shape))
+    vd = torch.from_numpy(oracle.q8_0_dequantize(vb).reshape(v.shape))
+    assert_close(g.flash_attention(q.to(dev), kq, vq), oracle_forward(q, kd, vd), torch.float16,
+                 f"q8_0 G={G} D={D} S={S}")
+    per_head = torch.from_numpy(np.random.default_rng(seed).random((B, Hkv * G, 1, S)) < 0.3)
+    per_head[:, ::3, :, S // 2:] = False
+    per_head[..., 0] = True
+    assert_close(g.flash_attention(q.to(dev), kq, vq, per_head.to(dev)), oracle_forward(q, kd, vd, mask=per_head),
+                 torch.float16, f"q8_0 per-head mask G={G} D={D} S={S}")
+
+
 def test_q8_0_decode_masks_and_causal(dev):
     B, H, Hkv, S, D = 3, 8, 2, 600, 128
     q = randn((B, H, 1, D), 21, torch.float16)
