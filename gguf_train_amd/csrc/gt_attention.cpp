@@ -176,7 +176,6 @@ void fill_qkv(AttnFwdArgs &a, const gt_tensor *q, const gt_tensor *k, const gt_t
     }
 }
 
-// Picks the kernel for a staged forward: split-K decode for single-query rows, the MFMA
 // Memory for the split partials of a decode launch (da.nsplit set): with several splits, the
 // per-stream uncached workspace whose counters let the last split merge in the kernel; otherwise
 // (or when that workspace is unavailable) stream-ordered scratch, merged by a second launch.
@@ -196,6 +195,7 @@ bool decode_partials(DecodeArgs &da, int dev, gt_scratch &scratch) {
     return true;
 }
 
+// Picks the kernel for a staged forward: split-K decode for single-query rows, the MFMA
 // prefill kernel for fp16/bf16 with head size 64/128, the generic kernel otherwise.
 bool dispatch_forward(const AttnFwdArgs &a, int cd, int dev) {
     if (a.out_dtype == cd && !a.o32 && attn_decode_supported(a, cd)) {

@@ -68,7 +68,7 @@ def test_q8_0_decode_kernel_shapes(dev, G, D, S):
     assert_close(got, oracle_forward(q, kd, vd), torch.float16, f"q8_0 G={G} D={D} S={S}")
 
 
-@pytest.mark.parametrize("G,D", [(3, 128), (7, 64), (12, 128), (32, 128)])
+@pytest.mark.parametrize("G,D", [(3, 128), (7, 64), (12, 128), (16, 64), (20, 64), (32, 128)])
 @pytest.mark.parametrize("S", [300, 8192])
 def test_q8_0_decode_any_query_group(dev, G, D, S):
     # query groups that are not 1, 2, 4 or 8 heads (groups of up to 8 over the same keys), with a
