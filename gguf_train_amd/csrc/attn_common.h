@@ -64,14 +64,19 @@ struct AttnBwdArgs {
 };
 
 // Query heads per decode workgroup: a kv head's gtot query heads (GQA / MQA) run in groups of
-// 1, 2, 4 or 8 heads, the 16 MFMA columns holding one group; more than 8 heads take several
-// workgroups over the same keys.
-inline int decode_head_tile(int64_t gtot) { return gtot > 4 ? 8 : gtot > 2 ? 4 : (int)gtot; }
+// 1, 2, 4, 8 or 16 heads (at most max_tile), the 16 MFMA columns holding one group; more heads
+// take several workgroups over the same keys, each re-reading them.
+constexpr int kDecodeMaxTile = 16;   // fp16/bf16 streaming kernel (16 heads: P.V on MFMA)
+constexpr int kDecodeQ8MaxTile = 8;  // Q8_0 kernels (16 measured slower: half the workgroups)
+inline int decode_head_tile(int64_t gtot, int max_tile) {
+    const int t = gtot > 8 ? 16 : gtot > 4 ? 8 : gtot > 2 ? 4 : (int)gtot;
+    return t < max_tile ? t : max_tile;
+}
 
 // Workgroups along blockIdx.y of a decode launch, (sequence, kv head, head group); also the
 // number of arrival counters its splits use.
-inline int64_t decode_units(int64_t B, int64_t H, int64_t Hkv) {
-    const int64_t gtot = H / Hkv, tile = decode_head_tile(gtot);
+inline int64_t decode_units(int64_t B, int64_t H, int64_t Hkv, int max_tile) {
+    const int64_t gtot = H / Hkv, tile = decode_head_tile(gtot, max_tile);
     return B * Hkv * ((gtot + tile - 1) / tile);
 }
 

@@ -131,7 +131,13 @@ __global__ __launch_bounds__(256, 2) void decode_stream_kernel(DecodeArgs a) {
     constexpr int LPR = D / 8;     // lanes per V row (16 bytes each)
     constexpr int RPW = 64 / LPR;  // V rows per wave load
     constexpr int NV = 32 / RPW;   // V loads per lane and step
-    __shared__ __attribute__((aligned(16))) float s_p[4][32][G];  // per-wave probabilities
+    // G = 16 (query groups of more than 8 heads): P.V on MFMA with the heads as its columns,
+    // A = V^T gathered from the wave's V rows staged in LDS; otherwise P.V on VALU over the V
+    // rows in registers, the probabilities shared through LDS
+    constexpr bool PVM = G > 8;
+    constexpr int VS = D + 8;  // row stride (halfs) of the staged V rows
+    __shared__ __attribute__((aligned(16))) float s_p[4][PVM ? 1 : 32][G];  // per-wave probabilities
+    __shared__ __attribute__((aligned(16))) uint16_t s_v[PVM ? 4 : 1][32][PVM ? VS : 8];
     __shared__ float s_m[4][G], s_l[4][G];
     __shared__ float s_o[4][G][D];
 
@@ -170,18 +176,24 @@ __global__ __launch_bounds__(256, 2) void decode_stream_kernel(DecodeArgs a) {
         V8 k[2][NT];   // A operands: block kb = keys 16kb + l16 of the wave's 32
         u32x4 v[NV];   // V rows RPW*i + vrow of the wave's 32, dims 8 sub .. +7
     };
+    // (16-head groups: plain loads, so that the other head groups of the kv head, which run at the
+    // same time on the same XCD, find the lines in its L2)
+    auto ld = [](const char *p) -> u32x4 {
+        if constexpr (PVM) return *(const u32x4 *)p;
+        else return __builtin_nontemporal_load((const u32x4 *)p);
+    };
     auto load = [&](int step, Tile &tl) {
         const int k0 = kbeg + step * kStep + 32 * w;
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb) {
             const uint32_t off = (uint32_t)min(k0 + 16 * kb + l16, S - 1) * krow + 16u * q4;
 #pragma unroll
-            for (int t = 0; t < NT; ++t) tl.k[kb][t] = __builtin_bit_cast(V8, __builtin_nontemporal_load((const u32x4 *)(kbase + off + 64 * t)));
+            for (int t = 0; t < NT; ++t) tl.k[kb][t] = __builtin_bit_cast(V8, ld(kbase + off + 64 * t));
         }
 #pragma unroll
         for (int i = 0; i < NV; ++i) {
             const uint32_t off = (uint32_t)min(k0 + RPW * i + vrow, S - 1) * vrowb + 16u * sub;
-            tl.v[i] = __builtin_nontemporal_load((const u32x4 *)(vbase + off));
+            tl.v[i] = ld(vbase + off);
         }
     };
 
@@ -189,11 +201,14 @@ __global__ __launch_bounds__(256, 2) void decode_stream_kernel(DecodeArgs a) {
     const int64_t mrow = b * f.m_sb + (h0 + min(l16, gv - 1)) * f.m_sh;
     float m = -INFINITY;  // running max of head l16 (log2 domain), same in the 4 lanes of a head
     float lsum = 0.0f;    // running sum of head l16
-    float acc[G][8];      // unnormalised O of every head, dims 8 sub .. +7, this lane's rows
+    float acc[PVM ? 1 : G][8];  // VALU P.V: unnormalised O of every head, dims 8 sub .. +7, this lane's rows
 #pragma unroll
-    for (int h = 0; h < G; ++h)
+    for (int h = 0; h < (PVM ? 1 : G); ++h)
 #pragma unroll
         for (int j = 0; j < 8; ++j) acc[h][j] = 0.0f;
+    f32x4 accm[PVM ? D / 16 : 1];  // MFMA P.V: C[dim 16 blk + 4 q4 + i][head l16]
+#pragma unroll
+    for (int blk = 0; blk < (PVM ? D / 16 : 1); ++blk) accm[blk] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
     auto compute = [&](int step, const Tile &tl) {
         const int k0 = kbeg + step * kStep + 32 * w;
@@ -236,38 +251,66 @@ __global__ __launch_bounds__(256, 2) void decode_stream_kernel(DecodeArgs a) {
         ps += __shfl_xor(ps, 16, 64);
         ps += __shfl_xor(ps, 32, 64);
         lsum = fmaf(lsum, alpha, ps);
-        if (l16 < G) {
+        if constexpr (PVM) {
+            // the wave's 32 V rows into LDS, then per block of 16 dims one MFMA: A[dim][k-slot]
+            // = V^T, B[k-slot][head] = P, k-slot e of lane group q4 being key 16(e/4) + 4 q4 + e%4
+            // (this lane's sc[e/4][e%4])
 #pragma unroll
-            for (int kb = 0; kb < 2; ++kb)
+            for (int i = 0; i < NV; ++i) *(u32x4 *)&s_v[w][RPW * i + vrow][8 * sub] = tl.v[i];
+            if (__builtin_amdgcn_ballot_w64(alpha != 1.0f) != 0) {
 #pragma unroll
-                for (int i = 0; i < 4; ++i) s_p[w][16 * kb + 4 * q4 + i][l16] = sc[kb][i];
-        }
-        // the head-h rescale factor sits in lane h
-        float al[G];
-#pragma unroll
-        for (int h = 0; h < G; ++h) al[h] = __shfl(alpha, h, 64);
-        __builtin_amdgcn_wave_barrier();  // s_p written by this wave before it is read
-#pragma unroll
-        for (int h = 0; h < G; ++h)
-#pragma unroll
-            for (int j = 0; j < 8; ++j) acc[h][j] *= al[h];
-#pragma unroll
-        for (int i = 0; i < NV; ++i) {
-            const int r = RPW * i + vrow;
-            float vf[8];
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                vf[2 * j] = P::lo(tl.v[i][j]);
-                vf[2 * j + 1] = P::hi(tl.v[i][j]);
+                for (int blk = 0; blk < D / 16; ++blk) accm[blk] *= alpha;  // head l16's factor
             }
+            V8 bp;
 #pragma unroll
-            for (int h = 0; h < G; ++h) {
-                const float p = s_p[w][r][h];
+            for (int e = 0; e < 8; ++e) bp[e] = (T)sc[e >> 2][e & 3];
+            __builtin_amdgcn_wave_barrier();  // s_v written by this wave before it is read
 #pragma unroll
-                for (int j = 0; j < 8; ++j) acc[h][j] = fmaf(p, vf[j], acc[h][j]);
+            for (int blk = 0; blk < D / 16; ++blk) {
+                const uint16_t *col = &s_v[w][4 * q4][16 * blk + l16];
+                u32x4 av;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int r = 16 * (j >> 1) + 2 * (j & 1);  // k-slots 2j, 2j + 1: rows r, r + 1 past 4 q4
+                    av[j] = (uint32_t)col[r * VS] | ((uint32_t)col[(r + 1) * VS] << 16);
+                }
+                accm[blk] = MM::mma(__builtin_bit_cast(V8, av), bp, accm[blk]);
             }
+            __builtin_amdgcn_wave_barrier();  // s_v read before the next step overwrites it
+        } else {
+            if (l16 < G) {
+#pragma unroll
+                for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) s_p[w][16 * kb + 4 * q4 + i][l16] = sc[kb][i];
+            }
+            // the head-h rescale factor sits in lane h
+            float al[G];
+#pragma unroll
+            for (int h = 0; h < G; ++h) al[h] = __shfl(alpha, h, 64);
+            __builtin_amdgcn_wave_barrier();  // s_p written by this wave before it is read
+#pragma unroll
+            for (int h = 0; h < G; ++h)
+#pragma unroll
+                for (int j = 0; j < 8; ++j) acc[h][j] *= al[h];
+#pragma unroll
+            for (int i = 0; i < NV; ++i) {
+                const int r = RPW * i + vrow;
+                float vf[8];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    vf[2 * j] = P::lo(tl.v[i][j]);
+                    vf[2 * j + 1] = P::hi(tl.v[i][j]);
+                }
+#pragma unroll
+                for (int h = 0; h < G; ++h) {
+                    const float p = s_p[w][r][h];
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) acc[h][j] = fmaf(p, vf[j], acc[h][j]);
+                }
+            }
+            __builtin_amdgcn_wave_barrier();  // s_p read before the next step overwrites it
         }
-        __builtin_amdgcn_wave_barrier();  // s_p read before the next step overwrites it
     };
 
     // two tiles in flight, unrolled by two so they swap roles without copies.  (Measured: issuing
@@ -287,21 +330,28 @@ __global__ __launch_bounds__(256, 2) void decode_stream_kernel(DecodeArgs a) {
     }
 
     // ---- combine the four waves ----
-#pragma unroll
-    for (int h = 0; h < G; ++h)
-#pragma unroll
-        for (int j = 0; j < 8; ++j)
-#pragma unroll
-            for (int mm = LPR; mm < 64; mm <<= 1) acc[h][j] += __shfl_xor(acc[h][j], mm, 64);
     if (lane < G) {
         s_m[w][lane] = m;
         s_l[w][lane] = lsum;
     }
-    if (lane < LPR) {
+    if constexpr (PVM) {
+#pragma unroll
+        for (int blk = 0; blk < D / 16; ++blk)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) s_o[w][l16][16 * blk + 4 * q4 + i] = accm[blk][i];
+    } else {
 #pragma unroll
         for (int h = 0; h < G; ++h)
 #pragma unroll
-            for (int j = 0; j < 8; ++j) s_o[w][h][8 * sub + j] = acc[h][j];
+            for (int j = 0; j < 8; ++j)
+#pragma unroll
+                for (int mm = LPR; mm < 64; mm <<= 1) acc[h][j] += __shfl_xor(acc[h][j], mm, 64);
+        if (lane < LPR) {
+#pragma unroll
+            for (int h = 0; h < G; ++h)
+#pragma unroll
+                for (int j = 0; j < 8; ++j) s_o[w][h][8 * sub + j] = acc[h][j];
+        }
     }
     __syncthreads();
     for (int e = tid; e < gv * D; e += 256) {
@@ -535,7 +585,7 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a) {
 
 template <typename T, int D, int G>
 hipError_t launch_typed(const DecodeArgs &a, hipStream_t s) {
-    dim3 grid((unsigned)a.nsplit, (unsigned)decode_units(a.f.B, a.f.H, a.f.Hkv));
+    dim3 grid((unsigned)a.nsplit, (unsigned)decode_units(a.f.B, a.f.H, a.f.Hkv, kDecodeMaxTile));
     if constexpr (D <= 128) {
         const int mode = !a.f.mask ? 0 : (a.f.mask_bool ? 1 : 2);
         if (mode == 0) hipLaunchKernelGGL((decode_stream_kernel<T, D, G, 0>), grid, dim3(256), 0, s, a);
@@ -559,6 +609,9 @@ hipError_t launch_g(const DecodeArgs &a, int G, hipStream_t s) {
         case 2: return launch_typed<T, D, 2>(a, s);
         case 4: return launch_typed<T, D, 4>(a, s);
         case 8: return launch_typed<T, D, 8>(a, s);
+        case 16:
+            if constexpr (D <= 128) return launch_typed<T, D, 16>(a, s);
+            return hipErrorInvalidValue;
         default: return hipErrorInvalidValue;
     }
 }
@@ -609,13 +662,14 @@ const void *stream_kernel_d(const AttnFwdArgs &f, int G) {
         case 2: return GT_SK(2);
         case 4: return GT_SK(4);
         case 8: return GT_SK(8);
+        case 16: return GT_SK(16);
         default: return nullptr;
     }
 #undef GT_SK
 }
 
 const void *stream_kernel(const AttnFwdArgs &f, int cd) {
-    const int G = decode_head_tile(f.H / f.Hkv);
+    const int G = decode_head_tile(f.H / f.Hkv, kDecodeMaxTile);
     if (cd == GT_F16) return f.D == 128 ? stream_kernel_d<_Float16, 128>(f, G) : stream_kernel_d<_Float16, 64>(f, G);
     return f.D == 128 ? stream_kernel_d<__bf16, 128>(f, G) : stream_kernel_d<__bf16, 64>(f, G);
 }
@@ -646,7 +700,7 @@ int attn_decode_splits(const AttnFwdArgs &f, int cd) {
     const void *kernel = stream_kernel(f, cd);
     const int64_t slots = kernel ? resident_slots(kernel) : 512;
     const int64_t steps = (f.S + kStep - 1) / kStep;
-    return decode_split_count(decode_units(f.B, f.H, f.Hkv), steps, slots, std::min<int64_t>(64, steps));
+    return decode_split_count(decode_units(f.B, f.H, f.Hkv, kDecodeMaxTile), steps, slots, std::min<int64_t>(64, steps));
 }
 
 bool attn_decode_supported(const AttnFwdArgs &f, int cd) {
@@ -657,10 +711,10 @@ bool attn_decode_supported(const AttnFwdArgs &f, int cd) {
     if ((f.S - 1) * f.k_ss * 2 + f.D * 2 > 0xffffffffLL || (f.S - 1) * f.v_ss * 2 + f.D * 2 > 0xffffffffLL) return false;
     if (f.D != 64 && f.D != 128 && f.D != 256) return false;
     // any number of query heads per kv head on the streaming kernel (D <= 128), in groups of
-    // up to 8; the D = 256 kernel takes 1, 2, 4 or 8
+    // up to 16; the D = 256 kernel takes 1, 2, 4 or 8
     const int64_t G = f.H / f.Hkv;
     if (f.D == 256 && G != 1 && G != 2 && G != 4 && G != 8) return false;
-    if (decode_units(f.B, f.H, f.Hkv) > 65535) return false;  // grid.y
+    if (decode_units(f.B, f.H, f.Hkv, kDecodeMaxTile) > 65535) return false;  // grid.y
     // 16-byte row loads: every row start must be 16-byte aligned
     const int64_t strides[] = {f.q_sb, f.q_sh, f.k_sb, f.k_sh, f.k_ss, f.v_sb, f.v_sh, f.v_ss};
     for (int64_t st : strides) if (st % 8 != 0) return false;
@@ -669,7 +723,7 @@ bool attn_decode_supported(const AttnFwdArgs &f, int cd) {
 }
 
 hipError_t launch_attn_decode(const DecodeArgs &a, int cd, hipStream_t s) {
-    const int G = decode_head_tile(a.f.H / a.f.Hkv);
+    const int G = decode_head_tile(a.f.H / a.f.Hkv, kDecodeMaxTile);
     if (cd == GT_F16) return launch_d<_Float16>(a, G, s);
     if (cd == GT_BF16) return launch_d<__bf16>(a, G, s);
     return hipErrorInvalidValue;

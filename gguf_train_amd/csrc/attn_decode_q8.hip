@@ -669,7 +669,7 @@ bool q8_stream_ok(const AttnFwdArgs &f) {
 }
 
 const void *q8_kernel(const AttnFwdArgs &f) {
-    const int G = decode_head_tile(f.H / f.Hkv);
+    const int G = decode_head_tile(f.H / f.Hkv, kDecodeQ8MaxTile);
     if (q8_stream_ok(f)) return f.D == 128 ? q8_kernel_d<128, true>(f, G) : q8_kernel_d<64, true>(f, G);
     return f.D == 128 ? q8_kernel_d<128, false>(f, G) : q8_kernel_d<64, false>(f, G);
 }
@@ -700,7 +700,7 @@ int attn_decode_q8_splits(const AttnFwdArgs &f) {
     const void *kernel = q8_kernel(f);
     const int64_t slots = kernel ? resident_slots(kernel) : 512;
     const int64_t steps = (f.S + kStep - 1) / kStep;
-    return decode_split_count(decode_units(f.B, f.H, f.Hkv), steps, slots, std::min<int64_t>(64, steps));
+    return decode_split_count(decode_units(f.B, f.H, f.Hkv, kDecodeQ8MaxTile), steps, slots, std::min<int64_t>(64, steps));
 }
 
 bool attn_decode_q8_supported(const AttnFwdArgs &f, int q_dtype) {
@@ -708,7 +708,7 @@ bool attn_decode_q8_supported(const AttnFwdArgs &f, int q_dtype) {
     if (f.L != 1 || f.S <= 0 || f.D != f.Dv || (f.D != 64 && f.D != 128)) return false;
     if (f.S >= (1LL << 30) || f.S * (f.D / 32 * 34) > 0xffffffffLL) return false;  // 32-bit offsets
     // any number of query heads per kv head, in groups of up to 8
-    if (decode_units(f.B, f.H, f.Hkv) > 65535) return false;  // grid.y
+    if (decode_units(f.B, f.H, f.Hkv, kDecodeQ8MaxTile) > 65535) return false;  // grid.y
     if (f.q_sh % 8 != 0 || f.q_sb % 8 != 0 || (uintptr_t)f.q % 16 != 0) return false;
     // K/V are whole dense Q8_0 tensors; rows are 4-byte aligned when the base is
     for (const void *p : {f.k, f.v}) if ((uintptr_t)p % 8 != 0) return false;
@@ -718,7 +718,7 @@ bool attn_decode_q8_supported(const AttnFwdArgs &f, int q_dtype) {
 hipError_t launch_attn_decode_q8(const DecodeArgs &a, hipStream_t s) {
     const void *kernel = q8_kernel(a.f);
     if (!kernel) return hipErrorInvalidValue;
-    dim3 grid((unsigned)a.nsplit, (unsigned)decode_units(a.f.B, a.f.H, a.f.Hkv));
+    dim3 grid((unsigned)a.nsplit, (unsigned)decode_units(a.f.B, a.f.H, a.f.Hkv, kDecodeQ8MaxTile));
     void *args[] = {(void *)&a};
     hipError_t e = hipLaunchKernel(kernel, grid, dim3(256), args, 0, s);
     // one split, or the last split merged in the kernel: the kernel wrote the output

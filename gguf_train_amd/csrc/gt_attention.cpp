@@ -177,14 +177,15 @@ void fill_qkv(AttnFwdArgs &a, const gt_tensor *q, const gt_tensor *k, const gt_t
 }
 
 // Memory for the split partials of a decode launch (da.nsplit set): with several splits, the
-// per-stream uncached workspace whose counters let the last split merge in the kernel; otherwise
+// per-stream uncached workspace whose counters (`units`: one per blockIdx.y of the launch) let
+// the last split merge in the kernel; otherwise
 // (or when that workspace is unavailable) stream-ordered scratch, merged by a second launch.
-bool decode_partials(DecodeArgs &da, int dev, gt_scratch &scratch) {
+bool decode_partials(DecodeArgs &da, int64_t units, int dev, gt_scratch &scratch) {
     const AttnFwdArgs &a = da.f;
     const size_t rows = (size_t)(a.B * a.H) * (size_t)da.nsplit;
     const size_t bytes = rows * (size_t)(a.D + 2) * sizeof(float);
     gt_decode_ws ws{};
-    if (da.nsplit > 1 && gt_decode_workspace(dev, gt_stream(), decode_units(a.B, a.H, a.Hkv), bytes, ws)) {
+    if (da.nsplit > 1 && gt_decode_workspace(dev, gt_stream(), units, bytes, ws)) {
         da.counters = ws.counters;
         da.part_o = (float *)ws.parts;
     } else {
@@ -203,7 +204,7 @@ bool dispatch_forward(const AttnFwdArgs &a, int cd, int dev) {
         da.f = a;
         da.nsplit = attn_decode_splits(a, cd);
         gt_scratch ws;
-        if (!decode_partials(da, dev, ws)) return false;
+        if (!decode_partials(da, decode_units(a.B, a.H, a.Hkv, kDecodeMaxTile), dev, ws)) return false;
         return gt_hip_check(launch_attn_decode(da, cd, gt_stream()), "flash_attention decode kernel");
     }
     if (attn_prefill_supported(a, cd))
@@ -238,7 +239,7 @@ int run_q8_decode(const gt_tensor *q, const gt_tensor *k, const gt_tensor *v, co
     da.f = a;
     da.nsplit = attn_decode_q8_splits(a);
     gt_scratch ws;
-    if (!decode_partials(da, dev, ws)) return -1;
+    if (!decode_partials(da, decode_units(a.B, a.H, a.Hkv, kDecodeQ8MaxTile), dev, ws)) return -1;
     return gt_hip_check(launch_attn_decode_q8(da, gt_stream()), "flash_attention q8_0 decode kernel") ? 1 : -1;
 }
 

@@ -26,12 +26,12 @@ def test_decode_matches_oracle(dev, dtype, G, D, S):
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
-@pytest.mark.parametrize("G,D", [(3, 128), (5, 64), (7, 128), (12, 128), (32, 128), (32, 64)])
+@pytest.mark.parametrize("G,D", [(3, 128), (5, 64), (7, 128), (12, 128), (16, 64), (20, 128), (32, 128), (32, 64), (48, 64)])
 @pytest.mark.parametrize("S", [300, 4096])
 def test_decode_any_query_group(dev, dtype, G, D, S):
     # GQA / MQA groups that are not 1, 2, 4 or 8 heads: the kv head's query heads run in groups
-    # of up to 8 over the same keys, the last group partial; a per-head mask checks that every
-    # group reads its own heads' query and mask rows and writes its own output rows
+    # of up to 16 over the same keys (16: P.V on MFMA), the last group partial; a per-head mask
+    # checks that every group reads its own heads' query and mask rows and writes its own rows
     B, Hkv = 2, 2
     seed = G * 10 + D + S
     q = randn((B, Hkv * G, 1, D), seed, dtype)
