@@ -4,8 +4,8 @@ numpy front end of oracle/oracle_attn.c (a float64 C restatement of the referenc
 gt_flash_attention, csrc/gt_ops_nn.cpp:2423-2525, of FlashAttentionFn.backward,
 gguf_train/_functions.py:1933-1965, of the GGUF Q8_0 codec, csrc/gt_core.cpp:800-832, and of
 gt_rope / gt_rope_backward, csrc/gt_ops_nn.cpp:2298-2421).
-Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg import this package, as
-the checker; the product (gguf_train_amd) never does.
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg import this package, to
+check results or time the CPU baseline; the product (gguf_train_amd) never does.
 
 Arrays are passed as numpy arrays; bfloat16 data travels as its uint16 bit patterns wrapped
 in `BF16(bits)`.

@@ -1,7 +1,7 @@
 /*
  * oracle_attn.c - CPU ORACLE.  TEST INFRASTRUCTURE ONLY.
  *
- * A plain-C, float64 restatement of GGUF_train's attention path, used as the checker for the
+ * A plain-C, float64 restatement of GGUF_train's attention path, the parity reference for the
  * HIP library.  Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg load it,
  * and only to check or to time the CPU baseline; the library never calls it and has no CPU
  * compute path.

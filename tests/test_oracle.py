@@ -1,4 +1,4 @@
-"""Pins the CPU oracle (oracle/) before it is trusted as the checker.
+"""Pins the CPU oracle (oracle/) before the parity tests trust it.
 
 Each oracle function is checked against something other than its own formula: numpy/torch
 conversions over every bit pattern, the closed form softmax(QK^T*s + M).V evaluated by

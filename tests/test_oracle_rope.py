@@ -1,5 +1,5 @@
 """Pins the oracle's RoPE (oracle_rope, a restatement of gt_rope / gt_rope_backward,
-csrc/gt_ops_nn.cpp:2298-2421 -> ggml_rope_ext) before it is trusted as the checker.
+csrc/gt_ops_nn.cpp:2298-2421 -> ggml_rope_ext) before the parity tests trust it.
 
 Each check uses something other than the oracle's own formula:
   * the reference's own known-answer test (tests/test_losses_and_rope.py:254-291): the textbook
