@@ -373,7 +373,7 @@ def main():
         measure_mfma()
         return 0
     if args.gpus != 1:
-        print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
+        print(f"bench.py: the benchmark measures one GPU; --gpus {args.gpus} is not supported "
               "(the attention path has no multi-GPU exchange)", file=sys.stderr)
         return 2
     import torch
