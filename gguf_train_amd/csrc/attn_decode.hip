@@ -131,10 +131,10 @@ __global__ __launch_bounds__(256, 2) void decode_stream_kernel(DecodeArgs a) {
     constexpr int LPR = D / 8;     // lanes per V row (16 bytes each)
     constexpr int RPW = 64 / LPR;  // V rows per wave load
     constexpr int NV = 32 / RPW;   // V loads per lane and step
-    // G = 16 (query groups of more than 8 heads): P.V on MFMA with the heads as its columns,
-    // A = V^T gathered from the wave's V rows staged in LDS; otherwise P.V on VALU over the V
-    // rows in registers, the probabilities shared through LDS
-    constexpr bool PVM = G > 8;
+    // G = 8, 16: P.V on MFMA with the heads as its columns, A = V^T gathered from the wave's V
+    // rows staged in LDS; G <= 4: P.V on VALU over the V rows in registers, the probabilities
+    // shared through LDS
+    constexpr bool PVM = G >= 8;
     constexpr int VS = D + 8;  // row stride (halfs) of the staged V rows
     __shared__ __attribute__((aligned(16))) float s_p[4][PVM ? 1 : 32][G];  // per-wave probabilities
     __shared__ __attribute__((aligned(16))) uint16_t s_v[PVM ? 4 : 1][32][PVM ? VS : 8];
@@ -179,7 +179,7 @@ __global__ __launch_bounds__(256, 2) void decode_stream_kernel(DecodeArgs a) {
     // (16-head groups: plain loads, so that the other head groups of the kv head, which run at the
     // same time on the same XCD, find the lines in its L2)
     auto ld = [](const char *p) -> u32x4 {
-        if constexpr (PVM) return *(const u32x4 *)p;
+        if constexpr (G > 8) return *(const u32x4 *)p;
         else return __builtin_nontemporal_load((const u32x4 *)p);
     };
     auto load = [&](int step, Tile &tl) {
@@ -335,10 +335,12 @@ __global__ __launch_bounds__(256, 2) void decode_stream_kernel(DecodeArgs a) {
         s_l[w][lane] = lsum;
     }
     if constexpr (PVM) {
+        if (l16 < G) {
 #pragma unroll
-        for (int blk = 0; blk < D / 16; ++blk)
+            for (int blk = 0; blk < D / 16; ++blk)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) s_o[w][l16][16 * blk + 4 * q4 + i] = accm[blk][i];
+                for (int i = 0; i < 4; ++i) s_o[w][l16][16 * blk + 4 * q4 + i] = accm[blk][i];
+        }
     } else {
 #pragma unroll
         for (int h = 0; h < G; ++h)
