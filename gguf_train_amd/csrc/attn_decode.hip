@@ -261,9 +261,17 @@ __global__ __launch_bounds__(256, 2) void decode_stream_kernel(DecodeArgs a) {
 #pragma unroll
                 for (int blk = 0; blk < D / 16; ++blk) accm[blk] *= alpha;  // head l16's factor
             }
-            V8 bp;
+            // bf16 keeps 8 bits of a probability: P goes in as hi + lo bf16 operands (two MFMAs,
+            // ~16 bits, as lsum's fp32 P), fp16 as one operand (11 bits)
+            constexpr bool kSplitP = __is_same(T, __bf16);
+            V8 bp, bpl;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) bp[e] = (T)sc[e >> 2][e & 3];
+            for (int e = 0; e < 8; ++e) {
+                const float x = sc[e >> 2][e & 3];
+                const T xh = (T)x;
+                bp[e] = xh;
+                if constexpr (kSplitP) bpl[e] = (T)(x - (float)xh);
+            }
             __builtin_amdgcn_wave_barrier();  // s_v written by this wave before it is read
 #pragma unroll
             for (int blk = 0; blk < D / 16; ++blk) {
@@ -275,6 +283,7 @@ __global__ __launch_bounds__(256, 2) void decode_stream_kernel(DecodeArgs a) {
                     av[j] = (uint32_t)col[r * VS] | ((uint32_t)col[(r + 1) * VS] << 16);
                 }
                 accm[blk] = MM::mma(__builtin_bit_cast(V8, av), bp, accm[blk]);
+                if constexpr (kSplitP) accm[blk] = MM::mma(__builtin_bit_cast(V8, av), bpl, accm[blk]);
             }
             __builtin_amdgcn_wave_barrier();  // s_v read before the next step overwrites it
         } else {

@@ -96,3 +96,24 @@ def test_decode_lse(dev):
     want_o, want_l = oracle_forward(q, k, v, return_lse=True)
     assert_close(out, want_o, torch.bfloat16, "out")
     assert np.abs(lse.cpu().numpy() - want_l).max() < 1e-4
+
+
+@pytest.mark.parametrize("G", [8, 16, 20])
+@pytest.mark.parametrize("S", [64, 300, 4096])
+@pytest.mark.parametrize("masked", [False, True])
+def test_bf16_decode_with_peaked_logits(dev, G, S, masked):
+    # query heads in groups of 8 and 16 do P.V on MFMA; with bfloat16 the probabilities must keep
+    # more than bf16's 8 bits there (a few large weights dominate when the logits are peaked:
+    # q scaled by 4 gives logits of standard deviation 4)
+    B, Hkv, D = 2, 2, 128
+    seed = 7 * G + S + (1 if masked else 0)
+    q = randn((B, Hkv * G, 1, D), seed, torch.bfloat16, scale=4.0)
+    k, v = randn((B, Hkv, S, D), seed + 1, torch.bfloat16), randn((B, Hkv, S, D), seed + 2, torch.bfloat16)
+    mask = None
+    if masked:
+        allowed = torch.from_numpy(np.random.default_rng(seed).random((B, Hkv * G, 1, S)) < 0.5)
+        allowed[..., 0] = True
+        mask = allowed
+    got = g.flash_attention(q.to(dev), k.to(dev), v.to(dev), None if mask is None else mask.to(dev))
+    worst = assert_close(got, oracle_forward(q, k, v, mask=mask), torch.bfloat16, f"peaked G={G} S={S} masked={masked}")
+    print(f"[decode-peaked] G={G} S={S} masked={masked}: {worst:.3f}", flush=True)
