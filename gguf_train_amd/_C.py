@@ -128,6 +128,8 @@ def _configure(lib: ctypes.CDLL) -> ctypes.CDLL:
     lib.gt_flash_attention_backward.argtypes = [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                                                 c_void_p, c_float, c_int, p_vp, p_vp, p_vp]
     lib.gt_flash_attention_backward.restype = c_int
+    lib.gt_flash_attention_noalloc.argtypes = [c_void_p, c_void_p, c_void_p, c_void_p, c_float, c_int, c_void_p]
+    lib.gt_flash_attention_noalloc.restype = c_int
 
     lib.gt_attention_weights.argtypes = [c_void_p, c_void_p, c_void_p, c_void_p, c_float, c_int, c_int]
     lib.gt_attention_weights.restype = c_void_p

@@ -10,6 +10,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -531,6 +532,153 @@ extern "C" int gt_flash_attention_backward(const gt_tensor *grad_out, const gt_t
     *dk = gk;
     *dv = gv;
     return 0;
+}
+
+// ---------------------------------------------------------------------------------------------
+// Attention that allocates nothing (no counterpart in the reference)
+// ---------------------------------------------------------------------------------------------
+// For callers that cannot allocate device memory (code under HIP graph capture, tight serving
+// loops, harnesses that forbid hipMalloc): gt_flash_attention into an output the caller owns.
+// The only device memory beyond the inputs and the output is the split-K partials of the
+// decode kernels, and those live in `scratch`, a fixed array of device memory that each GPU
+// the library runs on holds until the process ends.  The decode launch then merges its splits
+// with a second kernel (the in-kernel merge of gt_flash_attention needs the uncached
+// workspace, which is allocated); every split writes all of its partial rows before the merge
+// reads them, so nothing in `scratch` needs clearing between calls.  All calls on one GPU share
+// its array: calls that overlap in time on one GPU (different streams, different threads)
+// race on it and must be serialised by the caller.
+
+namespace {
+
+constexpr size_t kNoAllocScratchBytes = (size_t)16 << 20;
+static __device__ __align__(256) char scratch[kNoAllocScratchBytes];
+
+// Device address of this GPU's `scratch` (the name is a host-side stand-in in host code), looked
+// up once per device with that device current; null with the error set on failure.
+char *noalloc_scratch(int dev) {
+    static std::mutex mu;
+    static std::vector<char *> ptrs;
+    std::lock_guard<std::mutex> lock(mu);
+    if ((size_t)dev >= ptrs.size()) ptrs.resize((size_t)dev + 1, nullptr);
+    if (!ptrs[(size_t)dev]) {
+        void *p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p) {
+            gt_set_error(std::string("flash_attention_noalloc: hipGetSymbolAddress of the scratch array failed: ") +
+                         hipGetErrorString(e));
+            (void)hipGetLastError();
+            return nullptr;
+        }
+        ptrs[(size_t)dev] = (char *)p;
+    }
+    return ptrs[(size_t)dev];
+}
+
+bool on_device(const gt_tensor *t, int dev) { return t->device_type == GT_DEV_CUDA && t->device_index == dev; }
+
+}  // namespace
+
+extern "C" int gt_flash_attention_noalloc(const gt_tensor *q, const gt_tensor *k, const gt_tensor *v,
+                                          const gt_tensor *mask, float scale, int is_causal, gt_tensor *out) {
+    const char *who = "flash_attention_noalloc";
+    if (!validate(who, q, k, v, mask)) return -1;
+    const int64_t B = q->shape[0], H = q->shape[1], L = q->shape[2], D = q->shape[3], Dv = v->shape[3];
+    const int dev = q->device_type == GT_DEV_CUDA ? q->device_index : 0;
+    for (const gt_tensor *t : {q, k, v, mask, (const gt_tensor *)out}) {
+        if (t && !on_device(t, dev)) {
+            gt_set_error(std::string(who) + ": q, k, v, mask and out must all be on HIP device " + std::to_string(dev) +
+                         " (nothing is staged: staging would allocate)");
+            return -1;
+        }
+    }
+    if (!out || out->ndim != 4 || out->shape[0] != B || out->shape[1] != H || out->shape[2] != L ||
+        out->shape[3] != Dv || out->dtype != q->dtype || !gt_is_dense(out)) {
+        gt_set_error(std::string(who) + ": out must be a dense (B, H, L, Dv) = [" + std::to_string(B) + ", " +
+                     std::to_string(H) + ", " + std::to_string(L) + ", " + std::to_string(Dv) + "] tensor of q's dtype");
+        return -1;
+    }
+    const bool q8 = k->dtype == GT_Q8_0 || v->dtype == GT_Q8_0;
+    if (q8 && !(k->dtype == GT_Q8_0 && v->dtype == GT_Q8_0 && q->dtype == GT_F16 && L == 1)) {
+        gt_set_error(std::string(who) + ": q8_0 k/v need float16 q with one query row (L = 1); other q8_0 "
+                     "calls dequantize, which allocates");
+        return -1;
+    }
+    const int cd = q8 ? GT_F16 : q->dtype;
+    if (!q8 && (k->dtype != cd || v->dtype != cd)) {
+        gt_set_error(std::string(who) + ": q, k and v must have one dtype (converting them would allocate), got " +
+                     gt_dtype_name(q->dtype) + ", " + gt_dtype_name(k->dtype) + ", " + gt_dtype_name(v->dtype));
+        return -1;
+    }
+    for (const gt_tensor *t : {q, k, v}) {
+        if (t->dtype != GT_Q8_0 && !inner_contiguous(t)) {
+            gt_set_error(std::string(who) + ": q, k and v need a contiguous innermost dimension (a copy would allocate)");
+            return -1;
+        }
+    }
+    const int mask_want = cd == GT_F64 ? GT_F64 : GT_F32;
+    if (mask && mask->dtype != GT_BOOL && mask->dtype != mask_want) {
+        gt_set_error(std::string(who) + ": the mask must be bool or " + gt_dtype_name(mask_want) + " (got " +
+                     gt_dtype_name(mask->dtype) + "; converting it would allocate)");
+        return -1;
+    }
+    if (!gt_device_ok(dev)) return -1;
+    if (scale <= 0.0f) scale = 1.0f / std::sqrt((float)D);  // csrc/gt_ops_nn.cpp:2433
+    if (out->numel == 0) return 0;
+
+    AttnFwdArgs a{};
+    fill_qkv(a, q, k, v);
+    a.o = gt_data(out);
+    a.scale = scale;
+    a.causal = is_causal ? 1 : 0;
+    a.out_dtype = q->dtype;
+    if (mask) {
+        // read in place through broadcast strides (a bool mask as bytes, not turned into a bias)
+        int64_t st[4] = {0, 0, 0, 0}, sh[4] = {1, 1, 1, 1};
+        for (int i = 0; i < mask->ndim; ++i) {
+            sh[4 - mask->ndim + i] = mask->shape[i];
+            st[4 - mask->ndim + i] = mask->strides[i];
+        }
+        a.mask = gt_data(mask);
+        a.mask_bool = mask->dtype == GT_BOOL;
+        a.m_sb = sh[0] == 1 ? 0 : st[0];
+        a.m_sh = sh[1] == 1 ? 0 : st[1];
+        a.m_sl = sh[2] == 1 ? 0 : st[2];
+        a.m_ss = sh[3] == 1 ? 0 : st[3];
+    }
+
+    const bool dec = q8 ? attn_decode_q8_supported(a, GT_F16) : attn_decode_supported(a, cd);
+    if (q8 && !dec) {
+        gt_set_error(std::string(who) + ": these q8_0 shapes need the dequantizing path, which allocates");
+        return -1;
+    }
+    if (dec) {
+        DecodeArgs da{};
+        da.f = a;
+        da.nsplit = q8 ? attn_decode_q8_splits(a) : attn_decode_splits(a, cd);
+        da.counters = nullptr;  // splits merged by a second launch
+        // partials: (B*H, nsplit, D) outputs then (B*H, nsplit, 2) (max, sum); the streaming
+        // kernels write the output themselves when there is one split
+        const bool partials = da.nsplit > 1 || (!q8 && D > 128);
+        if (partials) {
+            const size_t rows = (size_t)(B * H) * (size_t)da.nsplit;
+            const size_t need = rows * (size_t)(D + 2) * sizeof(float);
+            if (need > kNoAllocScratchBytes) {
+                gt_set_error(std::string(who) + ": the split partials of this call need " + std::to_string(need) +
+                             " bytes, more than the " + std::to_string(kNoAllocScratchBytes) +
+                             "-byte scratch array (B*H*splits*(D+2)*4 bytes); use gt_flash_attention");
+                return -1;
+            }
+            char *base = noalloc_scratch(dev);
+            if (!base) return -1;
+            da.part_o = (float *)base;
+            da.part_ml = da.part_o + rows * (size_t)D;
+        }
+        const hipError_t e = q8 ? launch_attn_decode_q8(da, gt_stream()) : launch_attn_decode(da, cd, gt_stream());
+        return gt_hip_check(e, "flash_attention_noalloc decode kernel") ? 0 : -1;
+    }
+    if (attn_prefill_supported(a, cd))
+        return gt_hip_check(launch_attn_prefill(a, cd, gt_stream()), "flash_attention_noalloc prefill kernel") ? 0 : -1;
+    return gt_hip_check(launch_attn_generic_fwd(a, cd, gt_stream()), "flash_attention_noalloc kernel") ? 0 : -1;
 }
 
 // ---------------------------------------------------------------------------------------------

@@ -179,6 +179,20 @@ GT_API int gt_flash_attention_backward(const gt_tensor *grad_out, const gt_tenso
 /* (out may be NULL together with lse: the forward is then recomputed.  A float32 out, from
  * gt_flash_attention_train, is used as is.) */
 
+/* No counterpart in the reference.  For callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc): gt_flash_attention
+ * written into `out`, a dense (B,H,L,Dv) device tensor of q's dtype that the caller owns, with no
+ * device allocation and no hipMalloc / hipFree.  q, k, v, mask and out must be on the same HIP
+ * device; q, k, v of one dtype with a contiguous innermost dimension (or q float16 with q8_0
+ * k/v and L = 1); mask NULL, bool, or float32 (float64 for float64 inputs), read in place.
+ * Inputs that would need staging or conversion are refused with an error.  The split-K
+ * partials of single-query calls go to a fixed 16 MiB device array per GPU (held until the
+ * process ends); a call whose partials (B*H*splits*(D+2)*4 bytes) exceed it is refused.  Calls
+ * that overlap in time on one GPU share that array and race: serialise them.  Asynchronous on
+ * the current stream (gt_set_stream).  Returns 0 on success, -1 with gt_last_error() set. */
+GT_API int gt_flash_attention_noalloc(const gt_tensor *q, const gt_tensor *k, const gt_tensor *v,
+                                      const gt_tensor *mask, float scale, int is_causal, gt_tensor *out);
+
 /* Replaces the explicit weights of MultiheadAttention(need_weights=True), which the reference
  * computes with ggml ops (gguf_train/nn/modules/transformer.py:153-166): softmax(q.k^T*scale +
  * mask) with the causal mask, recomputed from `lse`, the (B,H,L) log-sum-exp of the forward of
