@@ -32,7 +32,26 @@ def _load_native() -> ctypes.CDLL:
             f"{LIB_PATH} is not built; build it with `python gguf_train_amd/_build.py --lib` "
             "(hipcc, gfx950). There is no CPU fallback."
         )
-    return ctypes.CDLL(str(LIB_PATH))
+    lib = ctypes.CDLL(str(LIB_PATH))
+    _check_sources(lib)
+    return lib
+
+
+def _check_sources(lib: ctypes.CDLL) -> None:
+    """Refuses a library built from other sources than those beside it (a stale build)."""
+    from ._srchash import source_hash
+
+    want = source_hash()
+    if want is None:  # no sources here: nothing to compare with
+        return
+    lib.gt_source_hash.argtypes = []
+    lib.gt_source_hash.restype = c_char_p
+    got = (lib.gt_source_hash() or b"").decode()
+    if got != want:
+        raise ImportError(
+            f"{LIB_PATH} was built from other sources (library {got[:12]}, tree {want[:12]}); "
+            "rebuild it with `python gguf_train_amd/_build.py --lib`"
+        )
 
 
 def _configure(lib: ctypes.CDLL) -> ctypes.CDLL:
@@ -143,7 +162,7 @@ def _configure(lib: ctypes.CDLL) -> ctypes.CDLL:
                                             c_int, c_float, c_float]
     lib.gt_flash_attention_rope.restype = c_void_p
 
-    # Q8_0 (csrc/gguf_train.h:376-377)
+    # Q8_0 (csrc/gguf_train.h:381-382)
     lib.gt_quantize.argtypes = [c_void_p, c_int]
     lib.gt_quantize.restype = c_void_p
     lib.gt_dequantize.argtypes = [c_void_p, c_int]

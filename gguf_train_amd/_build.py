@@ -41,9 +41,19 @@ def _sources() -> list[Path]:
     return sorted(list(CSRC.glob("*.hip")) + list(CSRC.glob("*.cpp")))
 
 
-def _compile(src: Path) -> Path:
+def _source_hash() -> str:
+    # loaded by path: importing the package would load the library being built
+    import importlib.util
+
+    spec = importlib.util.spec_from_file_location("_gt_srchash", PKG_DIR / "_srchash.py")
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return mod.source_hash(PKG_DIR)
+
+
+def _compile(src: Path, digest: str) -> Path:
     obj = OBJ_DIR / (src.name + ".o")
-    cmd = [HIPCC, *HIP_FLAGS, "-x", "hip", "-c", str(src), "-o", str(obj)]
+    cmd = [HIPCC, *HIP_FLAGS, f'-DGT_SOURCE_HASH="{digest}"', "-x", "hip", "-c", str(src), "-o", str(obj)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src.name}:\n{' '.join(cmd)}\n{proc.stdout}\n{proc.stderr}")
@@ -59,8 +69,9 @@ def build_library(jobs: int | None = None) -> Path:
     OBJ_DIR.mkdir(exist_ok=True)
     srcs = _sources()
     jobs = jobs or min(len(srcs), max(1, min(8, os.cpu_count() or 1)))
+    digest = _source_hash()
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
-        objs = list(ex.map(_compile, srcs))
+        objs = list(ex.map(lambda s: _compile(s, digest), srcs))
     tmp = LIB_PATH.with_suffix(".so.tmp")
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
     proc = subprocess.run(cmd, capture_output=True, text=True)

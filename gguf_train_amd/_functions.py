@@ -61,3 +61,27 @@ class FlashAttentionFn(torch.autograd.Function):
         q, k, v, mask, out, lse = ctx.saved_tensors
         dq, dk, dv = _ops.flash_attention_backward(grad_out, q, k, v, mask, out, lse, ctx.scale, ctx.is_causal)
         return (dq, dk, dv, None, None, None)
+
+
+class FlashAttentionLseFn(torch.autograd.Function):
+    """FlashAttentionFn that also returns the per-row log-sum-exp (B, H, L) of the same forward
+    pass (not differentiable), for callers that need both - MultiheadAttention with
+    need_weights=True recomputes the explicit weights from it - without a second forward."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, mask, scale, is_causal):
+        ctx.scale = float(scale) if scale is not None else (1.0 / math.sqrt(q.shape[-1]))
+        ctx.is_causal = bool(is_causal)
+        out, lse, out32 = _ops.flash_attention_train(q, k, v, mask, ctx.scale, ctx.is_causal)
+        ctx.save_for_backward(q, k, v, mask, out if out32 is None else out32, lse)
+        ctx.mark_non_differentiable(lse)
+        return out, lse
+
+    @staticmethod
+    def backward(ctx, grad_out, grad_lse):
+        if grad_out is None:
+            return (None,) * 6
+        q, k, v, mask, out, lse = ctx.saved_tensors
+        dq, dk, dv = _ops.flash_attention_backward(grad_out, q, k, v, mask, out, lse, ctx.scale, ctx.is_causal)
+        return (dq, dk, dv, None, None, None)
+

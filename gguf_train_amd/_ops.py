@@ -110,7 +110,7 @@ def flash_attention_rope(q, k, v, pos, mask=None, scale: float = 0.0, is_causal:
 
 
 def quantize(t: torch.Tensor, qtype: str = "q8_0") -> QuantizedTensor:
-    """gt_quantize (csrc/gguf_train.h:376); rows of last-dim length, GGUF Q8_0 blocks."""
+    """gt_quantize (csrc/gguf_train.h:381); rows of last-dim length, GGUF Q8_0 blocks."""
     if qtype != "q8_0":
         raise ValueError(f"unsupported quantization type {qtype!r} (only 'q8_0')")
     bind_stream(t.device)
@@ -120,7 +120,7 @@ def quantize(t: torch.Tensor, qtype: str = "q8_0") -> QuantizedTensor:
 
 
 def dequantize(qt: QuantizedTensor, dtype: torch.dtype = torch.float32) -> torch.Tensor:
-    """gt_dequantize (csrc/gguf_train.h:377): y = float(qs) * float(d), then `dtype`."""
+    """gt_dequantize (csrc/gguf_train.h:382): y = float(qs) * float(d), then `dtype`."""
     if dtype not in _GT_DTYPE:
         raise ValueError(f"unsupported dequantize dtype {dtype}")
     bind_stream(qt.device)

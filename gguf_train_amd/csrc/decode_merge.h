@@ -33,6 +33,11 @@ __device__ inline float wsum(float v) {
 }
 
 // Merges the nsplit partials of output rows row0 .. row0 + nrows - 1 (one wavefront per row).
+// MEMORY INVARIANT: part_o / part_ml are written by other workgroups of this launch, possibly on
+// other XCDs, and read here with plain loads and no acquire fence.  That is correct only because
+// they live in uncached device memory (hipDeviceMallocUncached, gt_decode_workspace): no L2
+// holds a stale or dirty copy.  In ordinary (cached) memory these loads could miss stores still
+// sitting in another XCD's L2; such buffers must use the two-launch merge (counters == null).
 template <typename TO, int D>
 __device__ inline void merge_rows(const DecodeArgs &a, int64_t row0, int nrows) {
     typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -77,10 +82,15 @@ __device__ inline void merge_rows(const DecodeArgs &a, int64_t row0, int nrows) 
 
 // Called by every thread of a split workgroup after its partial stores (nsplit > 1, counters
 // set).  `bk` is the (sequence, kv head) index, rows row0 .. row0 + nrows - 1 its query rows.
+// MEMORY INVARIANT (see merge_rows): counters, part_o and part_ml are uncached device memory.
+// The order "partial stores complete, then the counter increment" is given by vmcnt(0) plus the
+// barrier, not by a release fence; with uncached memory a completed store is in memory and
+// visible to every XCD.  The relaxed agent-scope atomics are then enough for the count.
 template <typename TO, int D>
 __device__ inline void finish_split(const DecodeArgs &a, int64_t bk, int64_t row0, int nrows) {
     __shared__ int s_last;
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this thread's partial stores have completed
+    // this thread's partial stores have completed (reached the uncached memory)
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     if (threadIdx.x == 0)
         s_last = __hip_atomic_fetch_add(&a.counters[bk], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==

@@ -43,6 +43,13 @@ extern "C" void gt_set_last_error(const char *msg) { t_last_error = msg ? msg : 
 static std::once_flag g_init_once;
 static int g_device_count = 0;
 
+// Fingerprint of the sources this library was built from (the build passes it; the Python
+// loader compares it with the sources beside the library).
+#ifndef GT_SOURCE_HASH
+#define GT_SOURCE_HASH "unknown"
+#endif
+extern "C" const char *gt_source_hash(void) { return GT_SOURCE_HASH; }
+
 extern "C" void gt_init(void) {
     std::call_once(g_init_once, [] {
         int n = 0;
@@ -72,10 +79,16 @@ hipStream_t gt_stream() { return t_stream; }
 extern "C" void gt_set_stream(void *stream) { t_stream = (hipStream_t)stream; }
 extern "C" void *gt_get_stream(void) { return (void *)t_stream; }
 
-// One uncached buffer per (device, stream), grown on demand.  The kernels leave every counter at
-// zero, so a buffer is zeroed only when it is created; a buffer replaced by a larger one is kept
-// (launches in flight may use it, and uncached memory is not freed while the process runs).
+// One uncached buffer per (device, stream), grown on demand.  The decode kernels' in-kernel
+// split merge is correct only in this memory (hipDeviceMallocUncached: no XCD's L2 holds the
+// partials or the counters; see decode_merge.h).  The kernels leave every counter at zero, so a
+// buffer is zeroed only when it is created; a buffer replaced by a larger one is kept (launches
+// in flight may use it, and uncached memory is not freed while the process runs: memory
+// allocated after such a free has read wrong values on these GPUs).  Since nothing is freed, at
+// most kMaxWorkspaceStreams streams per device get one; calls on further streams return false
+// and their launches merge the splits with a second kernel over pooled scratch memory.
 bool gt_decode_workspace(int dev, hipStream_t s, int64_t n_counters, size_t part_bytes, gt_decode_ws &ws) {
+    constexpr size_t kMaxWorkspaceStreams = 16;
     static std::mutex mu;
     struct Buf {
         char *p = nullptr;
@@ -83,8 +96,15 @@ bool gt_decode_workspace(int dev, hipStream_t s, int64_t n_counters, size_t part
         size_t parts = 0;
     };
     static std::map<std::pair<int, hipStream_t>, Buf> bufs;
+    static std::map<int, size_t> streams_of;  // workspaces per device
     std::lock_guard<std::mutex> lock(mu);
-    Buf &e = bufs[{dev, s}];
+    auto found = bufs.find({dev, s});
+    if (found == bufs.end()) {
+        if (streams_of[dev] >= kMaxWorkspaceStreams) return false;
+        ++streams_of[dev];
+        found = bufs.emplace(std::make_pair(dev, s), Buf{}).first;
+    }
+    Buf &e = found->second;
     const size_t cbytes_of = 256;  // granule of the counter area
     auto cbytes = [&](int64_t n) { return ((size_t)n * sizeof(int) + cbytes_of - 1) / cbytes_of * cbytes_of; };
     if (!e.p || e.counters < n_counters || e.parts < part_bytes) {

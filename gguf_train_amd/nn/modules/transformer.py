@@ -26,7 +26,7 @@ import torch
 from torch import nn
 
 from ... import _ops
-from ..._functions import FlashAttentionFn
+from ..._functions import FlashAttentionLseFn
 from .. import functional as F
 
 
@@ -175,11 +175,15 @@ class MultiheadAttention(nn.Module):
         else:
             # native: the fused forward gives the output and the log-sum-exp, from which the
             # weights are recomputed (gt_attention_weights); gradients flow through the output
+            # one forward pass gives both (with its backward residuals when grads are needed)
             needs_grad = torch.is_grad_enabled() and any(t.requires_grad for t in (q, k, v))
+            if needs_grad:
+                attn_out, lse = FlashAttentionLseFn.apply(q, k, v, mask, scale, is_causal)
+            else:
+                attn_out, lse = _ops.flash_attention_lse(q, k, v, mask, scale, is_causal)
             with torch.no_grad():
-                out_nat, lse = _ops.flash_attention_lse(q, k, v, mask, scale, is_causal)
-                attn_weights = _ops.attention_weights(q, k, mask, lse, scale, is_causal, average_attn_weights)
-            attn_out = FlashAttentionFn.apply(q, k, v, mask, scale, is_causal) if needs_grad else out_nat
+                attn_weights = _ops.attention_weights(q.detach(), k.detach(), mask, lse, scale, is_causal,
+                                                      average_attn_weights)
 
         out = attn_out.transpose(1, 2).reshape(B, L, E)
         out = self.out_proj(out)

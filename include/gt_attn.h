@@ -93,6 +93,10 @@ GT_API void gt_set_last_error(const char *msg);
 GT_API void gt_set_stream(void *stream);
 GT_API void *gt_get_stream(void);
 
+/* No counterpart in the reference: the SHA-256 (hex) of the sources the library was built from
+ * (csrc/ and this header), so a loader can refuse a library that does not match its tree. */
+GT_API const char *gt_source_hash(void);
+
 /* ---- tensor lifecycle & metadata: csrc/gguf_train.h:188-227 ----------------------------- */
 
 GT_API gt_tensor *gt_tensor_empty(int ndim, const int64_t *shape, int dtype, int device_type, int device_index);
@@ -233,11 +237,11 @@ GT_API gt_tensor *gt_flash_attention_rope(const gt_tensor *q, const gt_tensor *k
 
 /* ---- GGUF Q8_0 ------------------------------------------------------------------------ */
 
-/* csrc/gguf_train.h:376 (gt_tensor_to_dtype, csrc/gt_core.cpp:784-847): quantizes rows of
+/* csrc/gguf_train.h:381 (gt_tensor_to_dtype, csrc/gt_core.cpp:784-847): quantizes rows of
  * last-dim length (one flat row when that is not a multiple of 32).  Only GT_Q8_0
  * (ggml_type_id 8) is supported. */
 GT_API gt_tensor *gt_quantize(const gt_tensor *t, int ggml_type_id);
-/* csrc/gguf_train.h:377: y = float(qs[j]) * float(d), then converted to out_dtype. */
+/* csrc/gguf_train.h:382: y = float(qs[j]) * float(d), then converted to out_dtype. */
 GT_API gt_tensor *gt_dequantize(const gt_tensor *t, int out_dtype);
 
 /* ---- GGUF files ----------------------------------------------------------------------- */

@@ -127,3 +127,20 @@ def test_compute_without_a_device_fails_loudly():
         g.flash_attention(q, q, q)
     with pytest.raises(RuntimeError, match="no HIP device"):
         g.quantize(torch.randn(64))
+
+
+def test_library_matches_the_sources_beside_it():
+    # the loaded library carries the fingerprint of the sources it was built from
+    from gguf_train_amd._srchash import source_hash
+
+    assert _C.lib.gt_source_hash().decode() == source_hash()
+
+    class Stale:
+        class gt_source_hash:  # a library built from other sources
+            argtypes = restype = None
+
+            def __new__(cls):
+                return b"0" * 64
+
+    with pytest.raises(ImportError, match="built from other sources"):
+        _C._check_sources(Stale)

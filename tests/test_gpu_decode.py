@@ -117,3 +117,28 @@ def test_bf16_decode_with_peaked_logits(dev, G, S, masked):
     got = g.flash_attention(q.to(dev), k.to(dev), v.to(dev), None if mask is None else mask.to(dev))
     worst = assert_close(got, oracle_forward(q, k, v, mask=mask), torch.bfloat16, f"peaked G={G} S={S} masked={masked}")
     print(f"[decode-peaked] G={G} S={S} masked={masked}: {worst:.3f}", flush=True)
+
+
+@pytest.mark.parametrize("q8", [False, True])
+def test_decode_on_many_streams_gives_the_same_bits(dev, q8):
+    # The in-kernel split merge needs a per-stream uncached workspace; at most 16 streams per
+    # device get one (uncached memory is never freed), calls on further streams merge their
+    # splits with a second launch over pooled memory.  Either way the output is the same bits.
+    B, H, Hkv, S, D = 4, 32, 8, 4096, 128
+    q = randn((B, H, 1, D), 61, torch.float16).to(dev)
+    k, v = randn((B, Hkv, S, D), 62, torch.float32).to(dev), randn((B, Hkv, S, D), 63, torch.float32).to(dev)
+    if q8:
+        k, v = g.quantize(k), g.quantize(v)
+    else:
+        k, v = k.half(), v.half()
+    want = g.flash_attention(q, k, v)
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream(device=dev) for _ in range(24)]
+    outs = []
+    for s in streams:
+        s.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.stream(s):
+            outs.append(g.flash_attention(q, k, v))
+    torch.cuda.synchronize()
+    for i, o in enumerate(outs):
+        assert torch.equal(o, want), f"stream {i}"
