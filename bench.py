@@ -17,9 +17,14 @@ reported under "configs".  Work is counted algorithmically: attention FLOPs = 4*
 unmasked (query, key) pair and head, backward = 2.5x forward; decode bytes = K + V (read once
 per kv head) + Q + O, Q8_0 = 34 bytes per 32 values.
 
-cpu_baseline: the float64 CPU restatement of the reference's gt_flash_attention (the oracle,
-OpenMP over (batch, head) like csrc/gt_ops_nn.cpp:2468) on a bounded sample of the headline
-workload, on this host's cores.
+Timing: each configuration runs its step untimed for --settle-ms (the GPU clocks leave their
+idle state), then --warmup steps, then exactly --steps steps between HIP events on the stream
+the library enqueues on (PyTorch's current stream).
+
+cpu_baseline: the CPU restatement of the reference path (the oracle: the float64
+gt_flash_attention loop with OpenMP over (batch, head) like csrc/gt_ops_nn.cpp:2468, closed-form
+Q8_0 dequantization, the backward composition in float32 GEMMs) on a bounded sample of every
+configuration, with all of this host's threads and with 8, 1 warm-up and the median of 3.
 """
 
 from __future__ import annotations
@@ -48,11 +53,12 @@ def parse_args():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=100)
-    # the GPU clocks take tens of milliseconds to settle: warm up for ~200 steps
     p.add_argument("--warmup", type=int, default=200)
     p.add_argument("--configs", default="prefill,decode,decode_q8_0,train,fp32")
+    p.add_argument("--settle-ms", type=float, default=30.0,
+                   help="before its warm-up steps, each configuration runs its own step untimed for this long "
+                        "(synchronising every 10 steps), so that the GPU clocks have left their idle state")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    p.add_argument("--cpu-heads", type=int, default=8, help="heads of the headline workload in the CPU sample")
     p.add_argument("--measure-traffic", action="store_true",
                    help="run rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes over the benchmark's kernels (child "
                         "processes), calibrate them against a plain copy and write the summary under profiles/")
@@ -83,11 +89,21 @@ class Runner:
     def handles(self, *ts):
         return [self.bridge.borrow(t) if t is not None else None for t in ts]
 
+    settle_ms = 0.0
+
     def time_steps(self, step, steps, warmup):
         """Mean over exactly `steps` steps bracketed by synchronisations (events on the current
         stream, which the native calls are bound to), then the median of a second pass timed
-        step by step."""
+        step by step.  Before the `warmup` steps the step runs untimed for `settle_ms` of wall
+        time: an idle MI355X drops its clocks within a fraction of a second and needs ~10 ms of
+        load to raise them again (measured: 197 us per prefill step after 5 warm-up steps,
+        161 us after 50, the same kernel)."""
         torch = self.torch
+        t0 = time.perf_counter()
+        while (time.perf_counter() - t0) * 1e3 < self.settle_ms:
+            for _ in range(10):
+                step(0)
+            torch.cuda.synchronize()
         for _ in range(warmup):
             step(0)
         torch.cuda.synchronize()
@@ -212,24 +228,102 @@ def bench_copy(r: Runner, steps, warmup):
             "frac_of_peak": nbytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS}
 
 
-def cpu_baseline(heads: int):
-    """The oracle (fp64 restatement of gt_flash_attention) on `heads` heads of the headline
-    workload (one sequence, L=S=2048, D=128, causal, fp16 inputs), OpenMP over heads."""
+def _cpu_threads():
+    """(threads the host gives this process, nproc as the OS reports it)."""
+    nproc = os.cpu_count() or 1
+    try:
+        avail = len(os.sched_getaffinity(0))
+    except AttributeError:
+        avail = nproc
+    env = os.environ.get("OMP_NUM_THREADS", "")
+    return (int(env) if env.isdigit() and int(env) > 0 else avail), nproc
+
+
+def _median_run(fn, reps=3):
+    """One warm-up call, then the median wall time of `reps` calls (seconds)."""
+    fn()
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return sorted(ts)[len(ts) // 2]
+
+
+def cpu_baseline():
+    """The CPU restatement of the reference path (the oracle: the float64 gt_flash_attention loop
+    of csrc/gt_ops_nn.cpp:2423-2525 with OpenMP over (batch, head), the closed-form Q8_0
+    dequantization, the backward composition of gguf_train/_functions.py:1933-1965 in float32
+    GEMMs) on a bounded sample of each workload, timed with T threads (OMP_NUM_THREADS, else
+    every CPU this process may use) and with 8 (the reference's default ggml thread cap,
+    csrc/gt_core.cpp:65-67): 1 warm-up and the median of 3 runs each.  Samples keep the
+    workload's shapes and per-element cost; each says what it covers."""
     import numpy as np
+    from threadpoolctl import threadpool_limits
 
     import oracle
 
-    threads = min(16, os.cpu_count() or 1)
+    T, nproc = _cpu_threads()
     rng = np.random.default_rng(7)
-    L, D = 2048, 128
-    q, k, v = ((rng.standard_normal((1, heads, L, D)) * 0.5).astype(np.float16) for _ in range(3))
-    t0 = time.perf_counter()
-    oracle.flash_attention(q, k, v, is_causal=True, nthreads=threads)
-    sec = time.perf_counter() - t0
-    flops = 4 * D * causal_pairs(L) * heads
-    return {"value": flops / sec / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
-            "sample": f"{heads} heads of one sequence of the prefill workload (L=S=2048, D=128, causal, fp16), "
-                      f"{sec:.1f} s"}
+    f16 = lambda shape, sc=1.0: (rng.standard_normal(shape) * sc).astype(np.float16)
+    bf16 = lambda shape: oracle.BF16(oracle.f32_to_bf16_bits(rng.standard_normal(shape).astype(np.float32)))
+    nh = max(T, 8)  # (batch, head) units of the samples: every thread has one at T threads
+    cases = {}
+
+    # fp32 forward, B1 H4 L=S=128 D64 causal: the whole configuration
+    q, k, v = (rng.standard_normal((1, 4, 128, 64)).astype(np.float32) for _ in range(3))
+    cases["fp32"] = dict(fn=lambda t: oracle.flash_attention(q, k, v, is_causal=True, nthreads=t),
+                         work=4 * 64 * causal_pairs(128) * 4, unit="TFLOP/s", sample="the whole configuration")
+    # causal fp16 prefill, L=S=2048 D128: nh of the 128 (sequence, head) units, whole
+    pq, pk, pv = (f16((1, nh, 2048, 128), 0.5) for _ in range(3))
+    cases["prefill"] = dict(fn=lambda t: oracle.flash_attention(pq, pk, pv, is_causal=True, nthreads=t),
+                            work=4 * 128 * causal_pairs(2048) * nh, unit="TFLOP/s",
+                            sample=f"{nh} of the 128 (sequence, head) units: L=S=2048, D=128, causal, fp16")
+    # GQA decode fp16: 4 of the 32 sequences, every head, KV length 4096
+    dq_, dk_, dv_ = f16((4, 32, 1, 128)), f16((4, 8, 4096, 128)), f16((4, 8, 4096, 128))
+    cases["decode"] = dict(fn=lambda t: oracle.flash_attention(dq_, dk_, dv_, nthreads=t),
+                           work=2 * 4 * 8 * 4096 * 128 * 2 + 2 * 4 * 32 * 128 * 2, unit="GB/s",
+                           sample="4 of the 32 sequences (Hq=32, Hkv=8, KV length 4096, D=128, fp16)")
+    # Q8_0 decode: 2 of the 16 sequences; closed-form dequantization, then the loop
+    qq = f16((2, 32, 1, 128))
+    kb = oracle.q8_0_quantize(rng.standard_normal((2, 8, 8192, 128)).astype(np.float32))
+    vb = oracle.q8_0_quantize(rng.standard_normal((2, 8, 8192, 128)).astype(np.float32))
+
+    def q8_step(t):
+        kd = oracle.q8_0_dequantize(kb).reshape(2, 8, 8192, 128)
+        vd = oracle.q8_0_dequantize(vb).reshape(2, 8, 8192, 128)
+        return oracle.flash_attention(qq, kd, vd, nthreads=t)
+
+    cases["decode_q8_0"] = dict(fn=q8_step, work=2 * (2 * 8 * 8192 * 128 // 32 * 34) + 2 * 2 * 32 * 128 * 2,
+                                unit="GB/s", sample="2 of the 16 sequences (Hq=32, Hkv=8, KV length 8192, D=128), "
+                                                    "dequantized in closed form then attended")
+    # training step bf16 D64: nh heads of one sequence, query rows and keys 0..511 (all valid at the
+    # workload's key lengths >= 512), forward loop + float32-GEMM backward composition
+    Lt = 512
+    tq, tk, tv, tg = (bf16((1, nh, Lt, 64)) for _ in range(4))
+
+    def train_step(t):
+        oracle.flash_attention(tq, tk, tv, is_causal=True, nthreads=t)
+        with threadpool_limits(limits=t):
+            oracle.backward_composition_f32(tg, tq, tk, tv, is_causal=True)
+
+    cases["train"] = dict(fn=train_step, work=int(3.5 * 4 * 64 * causal_pairs(Lt) * nh), unit="TFLOP/s",
+                          sample=f"{nh} heads of one sequence, query rows and keys 0..{Lt - 1} (L=S=1024, D=64, "
+                                 "causal, bf16); backward in float32 GEMMs (numpy BLAS), not ggml's")
+    out = {}
+    total = 0.0
+    for name, c in cases.items():
+        row = {"unit": c["unit"], "sample": c["sample"]}
+        for label, t in (("threads_all", T), ("threads_8", 8)):
+            sec = _median_run(lambda: c["fn"](t))
+            total += sec
+            scale = 1e12 if c["unit"] == "TFLOP/s" else 1e9
+            row[label] = {"threads": t, "seconds": sec, "value": c["work"] / sec / scale}
+        out[name] = row
+    head = out["prefill"]
+    return {"value": head["threads_all"]["value"], "unit": "TFLOP/s", "cores": T, "kind": "port",
+            "sample": head["sample"] + f"; {T} threads (nproc {nproc}), median of 3 after 1 warm-up",
+            "nproc": nproc, "configs": out, "timed_seconds": total}
 
 
 # Dominant kernel of each configuration (substring of its symbol) for the HBM byte counters.
@@ -246,7 +340,8 @@ def _pmc_pass(counters, config, steps=3, warmup=1):
     <config>`, from one rocprofv3 --pmc pass: {counter: {kernel: average}}."""
     with tempfile.TemporaryDirectory() as d:
         cmd = ["rocprofv3", "--pmc", *counters, "-d", d, "-o", "run", "--output-format", "csv", "--",
-               sys.executable, str(ROOT / "bench.py"), "--configs", config, "--no-cpu", "--steps", str(steps),
+               sys.executable, str(ROOT / "bench.py"), "--configs", config, "--no-cpu", "--settle-ms", "0",
+               "--steps", str(steps),
                "--warmup", str(warmup)]
         n = len(counters)
         print("[pmc] " + " ".join(cmd[:2 + n] + ["-d", "<tmp>"] + cmd[4 + n:]), file=sys.stderr, flush=True)
@@ -279,6 +374,7 @@ MFMA_FILE = ROOT / "profiles" / "mfma_counters_prefill_train.md"
 def measure_mfma():
     """MFMA utilisation and instruction mix of the prefill and training kernels."""
     lines = ["# MFMA utilisation and instruction mix of the prefill and training kernels", "",
+             f"Measured on library `{library_hash()[:16]}` (source fingerprint gt_source_hash).", "",
              "Command: `python bench.py --measure-mfma` (per config: `rocprofv3 --pmc " + " ".join(MFMA_COUNTERS) +
              " -d <tmp> -o run --output-format csv -- python bench.py --configs <config> --no-cpu --steps 3 "
              "--warmup 1`). Values are per dispatch, averaged over the run's dispatches of each kernel.", "",
@@ -331,6 +427,8 @@ def measure_traffic():
         r["bytes"] = (r["FETCH_SIZE"] * cal["FETCH_SIZE"]["factor"] + r["WRITE_SIZE"] * cal["WRITE_SIZE"]["factor"]) * 1024
         rows[config] = r
     lines = ["# HBM traffic per launch of the benchmark's dominant kernels", "",
+             f"Measured on library `{library_hash()[:16]}` (the source fingerprint gt_source_hash of the "
+             "libgt_attn.so that ran; bench.py uses these figures only while the loaded library matches).", "",
              "Command: `python bench.py --measure-traffic` (each pass: `rocprofv3 --pmc <COUNTER> -d <tmp> -o run "
              "--output-format csv -- python bench.py --configs <config> --no-cpu --steps 3 --warmup 1`).", "",
              "Calibration (plain 1 GiB device copy, `--configs copy`):", ""]
@@ -345,12 +443,28 @@ def measure_traffic():
     print("\n".join(lines))
 
 
-def committed_traffic(config):
-    """HBM bytes per launch of the config's dominant kernel as last measured by --measure-traffic."""
+def library_hash() -> str:
+    """Source fingerprint of libgt_attn.so (the package's loader refuses a library whose compiled-in
+    fingerprint differs from its sources, so the sources' fingerprint is the loaded library's)."""
+    import importlib.util
+
+    spec = importlib.util.spec_from_file_location("_gt_srchash", ROOT / "gguf_train_amd" / "_srchash.py")
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return mod.source_hash() or ""
+
+
+def committed_traffic(config, build):
+    """HBM bytes per launch of the config's dominant kernel as last measured by --measure-traffic,
+    or None when that measurement was made on a library built from other sources."""
     try:
-        m = re.search(r"traffic_bytes\[" + re.escape(config) + r"\] = (\d+)", TRAFFIC_FILE.read_text())
+        text = TRAFFIC_FILE.read_text()
     except OSError:
         return None
+    lib = re.search(r"library `([0-9a-f]+)`", text)
+    if not lib or not build.startswith(lib.group(1)):
+        return None
+    m = re.search(r"traffic_bytes\[" + re.escape(config) + r"\] = (\d+)", text)
     return int(m.group(1)) if m else None
 
 
@@ -380,7 +494,9 @@ def main():
 
     r = Runner()
     results = {}
-    for name in [c for c in args.configs.split(",") if c]:
+    r.settle_ms = args.settle_ms
+    names = [c for c in args.configs.split(",") if c]
+    for name in names:
         cfg = dict(CONFIGS[name])
         cfg["dtype"] = getattr(torch, cfg["dtype"])
         if name == "train":
@@ -392,12 +508,13 @@ def main():
         print(f"[bench] {name}: {json.dumps(results[name])}", file=sys.stderr, flush=True)
 
     head = results.get("prefill") or next(iter(results.values()))
+    build = library_hash()
     for name in TRAFFIC_KERNELS:
         if name in results:
-            results[name]["traffic_bytes"] = committed_traffic(name)
+            results[name]["traffic_bytes"] = committed_traffic(name, build)
     if head["unit"] == "TFLOP/s":
         roofline = {"bound": "mfma", "achieved": head["value"], "peak": PEAK_FP16_TFLOPS, "unit": "TFLOP/s",
-                    "frac": head["value"] / PEAK_FP16_TFLOPS, "traffic": committed_traffic("prefill")}
+                    "frac": head["value"] / PEAK_FP16_TFLOPS, "traffic": committed_traffic("prefill", build)}
     else:
         roofline = {"bound": "hbm", "achieved": head["value"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
                     "frac": head["value"] / PEAK_HBM_GBS, "traffic": None}
@@ -418,9 +535,11 @@ def main():
                    "batch": 4, "heads": 32, "seq_len": 2048, "head_dim": 128, "causal": True},
         "roofline": roofline,
         "configs": results,
+        "settle_ms": args.settle_ms,
+        "library": build[:16],
     }
     if not args.no_cpu:
-        line["cpu_baseline"] = cpu_baseline(args.cpu_heads)
+        line["cpu_baseline"] = cpu_baseline()
     print(json.dumps(line), flush=True)
     return 0
 

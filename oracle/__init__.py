@@ -222,3 +222,37 @@ def rope(x, pos, n_dims=None, mode: int = 0, freq_base: float = 10000.0, freq_sc
 
 def max_threads() -> int:
     return int(lib().oracle_max_threads())
+
+
+# ---- the reference's backward composition in float32 GEMMs (CPU baseline only) -------------
+
+def backward_composition_f32(dout, q, k, v, mask=None, scale: float = -1.0, is_causal: bool = False):
+    """FlashAttentionFn.backward as the reference composes it (gguf_train/_functions.py:1933-1965):
+    full (B, H, L, S) scores, causal -1e9, additive mask, softmax, then dV = P^T dO,
+    dP = dO V^T, dS = P (dP - rowsum(dP P)), dQ = dS K s, dK = dS^T Q s, GQA groups summed -
+    with float32 numpy GEMMs (BLAS) standing in for ggml's float32 mul_mat.  Used only as the CPU
+    baseline's timing of the training backward; the parity oracle is flash_attention_backward."""
+    g, q, k, v = (to_f64(a).astype(np.float32) for a in (dout, q, k, v))
+    B, H, L, D = q.shape
+    Hkv, S = k.shape[1], k.shape[2]
+    s = np.float32(1.0 / np.sqrt(D) if scale <= 0 else scale)
+    rep = H // Hkv
+    ku = np.repeat(k, rep, axis=1) if rep > 1 else k
+    vu = np.repeat(v, rep, axis=1) if rep > 1 else v
+    scores = np.matmul(q, ku.transpose(0, 1, 3, 2)) * s
+    if is_causal:
+        scores += np.triu(np.full((L, S), -1e9, np.float32), k=1)
+    if mask is not None:
+        scores += to_f64(mask).astype(np.float32)
+    scores -= scores.max(axis=-1, keepdims=True)
+    p = np.exp(scores)
+    p /= p.sum(axis=-1, keepdims=True)
+    dv = np.matmul(p.transpose(0, 1, 3, 2), g)
+    dp = np.matmul(g, vu.transpose(0, 1, 3, 2))
+    ds = p * (dp - (dp * p).sum(axis=-1, keepdims=True))
+    dq = np.matmul(ds, ku) * s
+    dk = np.matmul(ds.transpose(0, 1, 3, 2), q) * s
+    if rep > 1:
+        dk = dk.reshape(B, Hkv, rep, S, D).sum(axis=2)
+        dv = dv.reshape(B, Hkv, rep, S, v.shape[3]).sum(axis=2)
+    return dq, dk, dv
