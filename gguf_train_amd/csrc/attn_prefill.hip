@@ -413,8 +413,15 @@ __global__ __launch_bounds__(64 * nw_of<D>(), 8 / nw_of<D>()) void prefill_fwd_k
                     float p[8];
 #pragma unroll
                     for (int e = 0; e < 8; ++e) p[e] = fast_exp2(fmaf(s[kb][8 * hs + e], c, -msub));
-                    pack8<T>(p, pb[kb][hs], pl[kb][hs]);
-                    lsum = sum8<T>(p, pb[kb][hs], lsum);
+                    if constexpr (M::kSplit) {
+                        // bf16: sum the float32 p first; packing consumes them (the residuals are
+                        // formed in place)
+                        lsum = sum8<T>(p, pb[kb][hs], lsum);
+                        pack8<T>(p, pb[kb][hs], pl[kb][hs]);
+                    } else {
+                        pack8<T>(p, pb[kb][hs], pl[kb][hs]);
+                        lsum = sum8<T>(p, pb[kb][hs], lsum);
+                    }
                 }
             }
 

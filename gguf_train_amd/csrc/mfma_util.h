@@ -61,15 +61,30 @@ struct Mfma<__bf16> {
 };
 
 // Packs 8 floats as an MFMA operand; `lo` receives the rounding residuals when the type splits.
+// bf16: the residual x - hi of each element comes from the packed pair itself with one
+// v_dot2_f32_bf16 (hi pair . (-1, 0) + x, or . (0, -1)): the products are exact and x - hi is
+// exactly representable, so the result is the exact residual, in one instruction instead of
+// widening hi back to float and subtracting.
 template <typename T>
 __device__ inline void pack8(const float *x, typename Mfma<T>::V8 &hi, typename Mfma<T>::V8 &lo) {
     using M = Mfma<T>;
     u32x4 h = {M::pack(x[0], x[1]), M::pack(x[2], x[3]), M::pack(x[4], x[5]), M::pack(x[6], x[7])};
     hi = __builtin_bit_cast(typename M::V8, h);
     if constexpr (M::kSplit) {
+        typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+        // (-1, 0) and (0, -1), element 0 in the low half, kept opaque: the compiler folds the
+        // constant pair (-1, 0) into the inline constant -1.0, whose bits 0xbf800000 are (0, -1)
+        uint32_t nf_bits = 0x0000bf80u, ns_bits = 0xbf800000u;
+        asm("" : "+v"(nf_bits), "+v"(ns_bits));
+        const b2 neg_first = __builtin_bit_cast(b2, nf_bits), neg_second = __builtin_bit_cast(b2, ns_bits);
         float r[8];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) r[e] = x[e] - M::round(x[e]);
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t hj = h[j];  // through a scalar: bit-casting a vector element reads element 0
+            const b2 pair = __builtin_bit_cast(b2, hj);
+            r[2 * j] = __builtin_amdgcn_fdot2_f32_bf16(pair, neg_first, x[2 * j], false);
+            r[2 * j + 1] = __builtin_amdgcn_fdot2_f32_bf16(pair, neg_second, x[2 * j + 1], false);
+        }
         u32x4 l = {M::pack(r[0], r[1]), M::pack(r[2], r[3]), M::pack(r[4], r[5]), M::pack(r[6], r[7])};
         lo = __builtin_bit_cast(typename M::V8, l);
     }
