@@ -92,6 +92,11 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void bwd_dkdv_kernel(AttnBwdA
             kf[t] = __builtin_bit_cast(V8, *(const u32x4 *)(kr + 16 * t));
             vf[t] = __builtin_bit_cast(V8, *(const u32x4 *)(vr + 16 * t));
         }
+        // Wait for K and V here: otherwise the compiler's wait for these loads lands inside the
+        // loop, where (vector memory loads completing in order) it also waits for every Q / dO
+        // prefetch issued since, exposing the full global load latency on every step.
+#pragma unroll
+        for (int t = 0; t < DT; ++t) asm volatile("" ::"v"(kf[t]), "v"(vf[t]));
     }
     f32x16 dk[DB], dv[DB];
 #pragma unroll
@@ -119,9 +124,10 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void bwd_dkdv_kernel(AttnBwdA
             greg[i] = *(const u32x4 *)(gb + (int64_t)q * D + 8 * col);
         }
         if (tid < BQ) {
+            // raw values: the arithmetic waits for the loads, so it happens at store time
             const int64_t r = (b * f.H + h) * f.L + min(qs0 + tid, L - 1);
-            lreg = ((const float *)f.lse)[r] * kLog2e;
-            dreg = -((const float *)a.delta)[r];
+            lreg = ((const float *)f.lse)[r];
+            dreg = ((const float *)a.delta)[r];
         }
     };
     auto store_step = [&](int buf) {
@@ -132,8 +138,8 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void bwd_dkdv_kernel(AttnBwdA
             *(u32x4 *)&sG[buf][row * QP + 8 * col] = greg[i];
         }
         if (tid < BQ) {
-            sL[buf][tid] = lreg;
-            sD[buf][tid] = dreg;
+            sL[buf][tid] = lreg * kLog2e;  // lse * log2(e)
+            sD[buf][tid] = -dreg;          // -delta
         }
     };
 
@@ -344,7 +350,8 @@ __global__ __launch_bounds__(256, D <= 64 && (MASK == 0 || MASK == 4) ? 2 : 1) v
     float mreg = 0.0f;
     const float *mrow = MASK == 4 ? (const float *)f.mask + b * f.m_sb + h * f.m_sh : nullptr;
     auto load_tile = [&](int j) {
-        if (MASK == 4 && tid < BNK) mreg = mrow[(int64_t)min(j * BNK + tid, S - 1) * f.m_ss] * inv_scale;
+        // the raw mask value: scaled at store time, so that nothing waits for the load here
+        if (MASK == 4 && tid < BNK) mreg = mrow[(int64_t)min(j * BNK + tid, S - 1) * f.m_ss];
 #pragma unroll
         for (int i = 0; i < NLD; ++i) {
             const int cidx = tid + 256 * i, row = cidx / CH, col = cidx % CH;
@@ -354,7 +361,7 @@ __global__ __launch_bounds__(256, D <= 64 && (MASK == 0 || MASK == 4) ? 2 : 1) v
         }
     };
     auto store_tile = [&](int buf) {
-        if (MASK == 4 && tid < BNK) sMk[buf][tid] = mreg;
+        if (MASK == 4 && tid < BNK) sMk[buf][tid] = mreg * inv_scale;
 #pragma unroll
         for (int i = 0; i < NLD; ++i) {
             const int cidx = tid + 256 * i, row = cidx / CH, col = cidx % CH;
