@@ -38,33 +38,47 @@ __device__ inline float wsum(float v) {
 // they live in uncached device memory (hipDeviceMallocUncached, gt_decode_workspace): no L2
 // holds a stale or dirty copy.  In ordinary (cached) memory these loads could miss stores still
 // sitting in another XCD's L2; such buffers must use the two-launch merge (counters == null).
+// Every load of a row (the splits' (max, sum) pairs and their first SPW * U output pieces) is
+// issued before any is used: each uncached load is a round trip to the memory, and this runs at
+// the tail of the kernel.  The sums run in the order of the merge kernel (decode_merge_kernel),
+// so both merges give the same bits.
 template <typename TO, int D>
 __device__ inline void merge_rows(const DecodeArgs &a, int64_t row0, int nrows) {
     typedef float f32x4 __attribute__((ext_vector_type(4)));
     constexpr int LPS = D / 4;     // lanes per partial row
     constexpr int SPW = 64 / LPS;  // partial rows per wave load
+    constexpr int U = 8;           // partial rows per lane and batch
     const AttnFwdArgs &f = a.f;
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
-    const int ns = a.nsplit;
+    const int ns = a.nsplit;  // <= 64 (decode_split_count)
+    const int sub = lane % LPS, sp = lane / LPS;
     for (int r = w; r < nrows; r += nw) {
         const int64_t row = row0 + r;
         const float *ml = a.part_ml + row * ns * 2;
-        float M = -INFINITY;
-        for (int i = lane; i < ns; i += 64) M = fmaxf(M, ml[2 * i]);
-        M = wmax(M);
-        float L = 0.0f;
-        for (int i = lane; i < ns; i += 64) {
-            const float m = ml[2 * i];
-            L += m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m - M) * ml[2 * i + 1];
-        }
-        L = wsum(L);
-        const int sub = lane % LPS, sp = lane / LPS;
         const float *po = a.part_o + row * ns * D + 4 * sub;
+        // all loads first: split `lane`'s (max, sum) and the first batch of output pieces
+        const float mi = lane < ns ? ml[2 * lane] : -INFINITY;
+        const float li = lane < ns ? ml[2 * lane + 1] : 0.0f;
+        f32x4 x[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) x[u] = *(const f32x4 *)(po + (int64_t)min(SPW * u + sp, ns - 1) * D);
+        const float M = wmax(mi);
+        const float L = wsum(mi == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mi - M) * li);
         f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-        for (int i = sp; i < ns; i += SPW) {
-            const float m = ml[2 * i];
-            const float wgt = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m - M);
-            acc += wgt * *(const f32x4 *)(po + (int64_t)i * D);
+        for (int i0 = 0; i0 < ns; i0 += SPW * U) {
+            if (i0 > 0) {
+#pragma unroll
+                for (int u = 0; u < U; ++u) x[u] = *(const f32x4 *)(po + (int64_t)min(i0 + SPW * u + sp, ns - 1) * D);
+            }
+            float wgt[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int i = i0 + SPW * u + sp;
+                const float m = __shfl(mi, min(i, ns - 1), 64);  // split i's max sits in lane i
+                wgt[u] = (i >= ns || m == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m - M);
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u) acc += wgt[u] * x[u];
         }
 #pragma unroll
         for (int m = LPS; m < 64; m <<= 1) {
