@@ -41,14 +41,17 @@ namespace {
 // workgroups per CU: the two run their tiles independently (a workgroup's barrier does not hold
 // the other), which overlaps one's softmax with the other's MFMAs better than 8 wavefronts in
 // lockstep (measured: 3% for D = 128, 9% for the D = 64 training forward).  LDS per workgroup:
-// NST x 2 tiles of 64 x D, 64 KB either way.
+// NST = 2 stages x 2 tiles of BN x D, 64 KB for both head sizes.
 template <int D>
 constexpr int nw_of() { return 4; }
 template <int D>
-constexpr int nst_of() { return D == 128 ? 2 : 4; }
+constexpr int nst_of() { return 2; }
 template <int D>
 constexpr int bm_of() { return 32 * nw_of<D>(); }  // query rows per tile
-constexpr int BN = 64;          // keys per K/V tile
+// keys per K/V tile: 64, or 128 for head size 64 (a tile of 64 keys x 64 dims is too little work
+// per barrier)
+template <int D>
+constexpr int bn_of() { return D == 64 ? 128 : 64; }
 constexpr float kLazy = 8.0f;   // rescale threshold, log2 domain: probabilities stay <= 256
 using namespace gtmfma;
 
@@ -147,7 +150,7 @@ __device__ inline void rope_rows(typename Mfma<T>::V8 *q, const float2 *tab, int
 
 // Keys covered by query tile qt: the sequence's keys, or (causal) up to the tile's last row,
 // whose position is qpos + qt*BM + BM-1.
-template <bool CAUSAL, int BM>
+template <bool CAUSAL, int BM, int BN>
 __device__ inline int key_tiles(int qt, int nkv, int qpos) {
     const int kv_end = CAUSAL ? min(qt * BM + BM + qpos, nkv) : nkv;
     return kv_end > 0 ? (kv_end + BN - 1) / BN : 0;
@@ -157,7 +160,8 @@ __device__ inline int key_tiles(int qt, int nkv, int qpos) {
 // on the query row (key padding: the tile's mask row travels to LDS with the K/V tile).
 template <typename T, int D, bool CAUSAL, int MASK, bool ROPE = false>
 __global__ __launch_bounds__(64 * nw_of<D>(), 8 / nw_of<D>()) void prefill_fwd_kernel(AttnFwdArgs a, int nq, int npairs) {
-    constexpr int NW = nw_of<D>(), BM = bm_of<D>(), NST = nst_of<D>();
+    constexpr int NW = nw_of<D>(), BM = bm_of<D>(), NST = nst_of<D>(), BN = bn_of<D>();
+    constexpr int NKB = BN / 32;  // 32-key blocks per tile
     using M = Mfma<T>;
     using V8 = typename M::V8;
     constexpr int DT = D / 16;             // k-steps of S^T = K.Q^T
@@ -166,9 +170,9 @@ __global__ __launch_bounds__(64 * nw_of<D>(), 8 / nw_of<D>()) void prefill_fwd_k
     constexpr int TILE = BN * D;           // elements per tile
     constexpr int NPW = BN * CH / 64 / NW; // 1 KB wave loads per operand, wave and tile
     constexpr bool MROW = MASK == 4;
-    constexpr int PER = 2 * NPW + (MROW ? 1 : 0);  // loads per wave and tile (K, V, mask row)
+    constexpr int PER = 2 * NPW + (MROW ? BN / 64 : 0);  // loads per wave and tile (K, V, mask row)
     static_assert(NPW >= 1 && PER * (NST - 2) < 64, "tile split");
-    static_assert(BN == 64, "mask row: one key per lane");
+    static_assert(BN % 64 == 0, "mask row: one key per lane and load");
     __shared__ __attribute__((aligned(1024))) T sK[NST][TILE];
     __shared__ __attribute__((aligned(1024))) T sV[NST][TILE];
     __shared__ __attribute__((aligned(16))) float sMk[MROW ? NST : 1][BN];
@@ -197,12 +201,13 @@ __global__ __launch_bounds__(64 * nw_of<D>(), 8 / nw_of<D>()) void prefill_fwd_k
     const int nkv = attn_kv_len(a, b), qpos = attn_q_pos(a, b);
     const int qa = nq - 1 - pair, qb = pair;  // the heavier tile first
     const int nparts = qa == qb ? 1 : 2;
-    const int na = key_tiles<CAUSAL, BM>(qa, nkv, qpos);
-    const int total = na + (nparts == 2 ? key_tiles<CAUSAL, BM>(qb, nkv, qpos) : 0);
+    const int na = key_tiles<CAUSAL, BM, BN>(qa, nkv, qpos);
+    const int total = na + (nparts == 2 ? key_tiles<CAUSAL, BM, BN>(qb, nkv, qpos) : 0);
 
     const T *kbase = (const T *)a.k + b * a.k_sb + hk * a.k_sh;
     const T *vbase = (const T *)a.v + b * a.v_sb + hk * a.v_sh;
     const float c = a.scale * kLog2e;  // raw score -> log2 domain
+    const float inv_scale = 1.0f / a.scale;
 
     // Flat step s (key tile s of part 0, then key tile s - na of part 1) goes to stage s % NST;
     // wave w issues NPW 1 KB loads per operand: lane `lane` of load n fills 16-byte slot
@@ -231,7 +236,9 @@ __global__ __launch_bounds__(64 * nw_of<D>(), 8 / nw_of<D>()) void prefill_fwd_k
         if constexpr (MROW) {
             // the mask values of keys kt*BN .. +63 (keys past S repeat key S-1); every wave writes
             // the same row, which keeps the loads per wave and tile uniform and needs no exec mask
-            lds_dma4(lds_addr(&sMk[st][0]), mrow, (uint32_t)min(kt * BN + lane, S - 1) * (uint32_t)a.m_ss * 4u);
+#pragma unroll
+            for (int c = 0; c < BN / 64; ++c)
+                lds_dma4(lds_addr(&sMk[st][64 * c]), mrow, (uint32_t)min(kt * BN + 64 * c + lane, S - 1) * (uint32_t)a.m_ss * 4u);
         }
         const uint32_t dk = lds_addr(&sK[st][0]) + w * NPW * 1024;
         const uint32_t dv = lds_addr(&sV[st][0]) + w * NPW * 1024;
@@ -260,7 +267,9 @@ __global__ __launch_bounds__(64 * nw_of<D>(), 8 / nw_of<D>()) void prefill_fwd_k
     //   V^T, (kb, hs, db): rows (keys) 32kb + 16hs + 4(g16/2) + i16/4 and +8, column
     //   32db + 16(g16%2) + 4(i16%4); with D = 128 the swizzle only depends on row mod 16, so
     //   (kb, hs) is a constant 16(2kb + hs) rows further.
-    constexpr int NV = D == 128 ? DB : 4 * DB;
+    // the swizzle repeats every 16 rows (D = 128) or 32 rows (D = 64): offsets of the first
+    // period, later (kb, hs) groups a constant number of rows further
+    constexpr int NV = D == 128 ? DB : 2 * DB;
     int kofs[DT], vofs0[NV], vofs1[NV];
 #pragma unroll
     for (int t = 0; t < DT; ++t) kofs[t] = lrow * D + 8 * ((2 * t + half) ^ swz<D>(lrow));
@@ -325,53 +334,47 @@ __global__ __launch_bounds__(64 * nw_of<D>(), 8 / nw_of<D>()) void prefill_fwd_k
             // (causal) a wavefront whose rows all precede this tile still runs it: every score
             // is masked to -inf and p = 0; skipping it makes the compiler copy O on every tile
             // ---- S^T = K . Q^T ----
-            f32x16 s[2];
+            // MROW: the key-padding row enters as the accumulator's initial value (mask / scale,
+            // the raw-score units of the accumulator), so S^T = K.Q^T + mask costs no VALU add
+            f32x16 s[NKB];
 #pragma unroll
-            for (int kb = 0; kb < 2; ++kb) {
+            for (int kb = 0; kb < NKB; ++kb) {
                 V8 kf[DT];
 #pragma unroll
                 for (int t = 0; t < DT; ++t) kf[t] = *(const V8 *)&cK[kofs[t] + 32 * kb * D];
+                if constexpr (MROW) {
 #pragma unroll
-                for (int i = 0; i < 16; ++i) s[kb][i] = 0.0f;
+                    for (int g = 0; g < 4; ++g) {
+                        const f32x4 mv4 = *(const f32x4 *)&sMk[step % NST][32 * kb + 8 * g + 4 * half];
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) s[kb][4 * g + e] = mv4[e] * inv_scale;
+                    }
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) s[kb][i] = 0.0f;
+                }
 #pragma unroll
                 for (int t = 0; t < DT; ++t) s[kb] = M::mma(kf[t], qf[t], s[kb]);
             }
 
             // ---- masks: s[kb][i] is (key = k0 + 32kb + 8(i/4) + 4half + i%4, query = lq) ----
             const bool edge = k0 + BN > nkv || (CAUSAL && k0 + BN - 1 > wq0 + qpos);
-            if (MROW && !edge) {
-                // key padding away from the edges: the mask row is added, nothing is blocked
+            if ((MASK != 0 && !MROW) || edge) {
 #pragma unroll
-                for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-                    for (int g = 0; g < 4; ++g) {
-                        const f32x4 mv4 = *(const f32x4 *)&sMk[step % NST][32 * kb + 8 * g + 4 * half];
-#pragma unroll
-                        for (int e = 0; e < 4; ++e) s[kb][4 * g + e] = fmaf(mv4[e], 1.0f / a.scale, s[kb][4 * g + e]);
-                    }
-            } else if (MASK != 0 || edge) {
-                f32x4 mv[2][4];  // MROW: the mask values of this lane's keys, from LDS
-                if constexpr (MROW) {
-#pragma unroll
-                    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-                        for (int g = 0; g < 4; ++g) mv[kb][g] = *(const f32x4 *)&sMk[step % NST][32 * kb + 8 * g + 4 * half];
-                }
-#pragma unroll
-                for (int kb = 0; kb < 2; ++kb) {
+                for (int kb = 0; kb < NKB; ++kb) {
 #pragma unroll
                     for (int i = 0; i < 16; ++i) {
                         const int key = k0 + 32 * kb + 8 * (i / 4) + 4 * half + (i % 4);
                         float x = s[kb][i];
                         if constexpr (MROW) {
-                            x = fmaf(mv[kb][i / 4][i % 4], 1.0f / a.scale, x);
+                            // the mask row is already in s
                         } else if (MASK != 0) {
                             const int64_t mi = b * a.m_sb + h * a.m_sh + (int64_t)min(lq, L - 1) * a.m_sl +
                                                (int64_t)min(key, S - 1) * a.m_ss;
                             if (MASK == 1) {
                                 x = ((const uint8_t *)a.mask)[mi] ? x : -INFINITY;
                             } else {
-                                x = fmaf(((const float *)a.mask)[mi], 1.0f / a.scale, x);
+                                x = fmaf(((const float *)a.mask)[mi], inv_scale, x);
                             }
                         }
                         const bool blocked = key >= nkv || (CAUSAL && key > lq + qpos);
@@ -383,8 +386,8 @@ __global__ __launch_bounds__(64 * nw_of<D>(), 8 / nw_of<D>()) void prefill_fwd_k
             // ---- online softmax ----
             float tmax = max3(s[0][0], s[0][1], s[0][2]);
 #pragma unroll
-            for (int i = 3; i < 31; i += 2) tmax = max3(tmax, s[i / 16][i % 16], s[(i + 1) / 16][(i + 1) % 16]);
-            tmax = max3(tmax, s[1][15], s[1][15]);
+            for (int i = 3; i < 16 * NKB - 1; i += 2) tmax = max3(tmax, s[i / 16][i % 16], s[(i + 1) / 16][(i + 1) % 16]);
+            tmax = max3(tmax, s[NKB - 1][15], s[NKB - 1][15]);
             tmax = xhalf_max(tmax);
             // Lazy rescaling: the reference point m of a row only moves when the tile's max
             // exceeds it by more than kLazy, so p = 2^(s c - m) stays below 2^kLazy.  A row with
@@ -405,9 +408,9 @@ __global__ __launch_bounds__(64 * nw_of<D>(), 8 / nw_of<D>()) void prefill_fwd_k
             const float msub = m == -INFINITY ? 0.0f : m;
 
             // P^T as B operands: k-step (kb, hs) takes accumulator entries 8hs .. 8hs+7
-            V8 pb[2][2], pl[2][2];
+            V8 pb[NKB][2], pl[NKB][2];
 #pragma unroll
-            for (int kb = 0; kb < 2; ++kb) {
+            for (int kb = 0; kb < NKB; ++kb) {
 #pragma unroll
                 for (int hs = 0; hs < 2; ++hs) {
                     float p[8];
@@ -430,14 +433,15 @@ __global__ __launch_bounds__(64 * nw_of<D>(), 8 / nw_of<D>()) void prefill_fwd_k
             // waits for the previous one's result (a dependent 32x32x16 chain issues at ~44
             // cycles per MFMA instead of 32)
 #pragma unroll
-            for (int kb = 0; kb < 2; ++kb) {
+            for (int kb = 0; kb < NKB; ++kb) {
 #pragma unroll
                 for (int hs = 0; hs < 2; ++hs) {
 #pragma unroll
                     for (int db = 0; db < DB; ++db) {
                         const int g = 2 * kb + hs;
                         const V8 av = D == 128 ? read_tr8<T>(&cV[vofs0[db] + 16 * g * D], &cV[vofs1[db] + 16 * g * D])
-                                               : read_tr8<T>(&cV[vofs0[g * DB + db]], &cV[vofs1[g * DB + db]]);
+                                               : read_tr8<T>(&cV[vofs0[(g % 2) * DB + db] + 32 * kb * D],
+                                                             &cV[vofs1[(g % 2) * DB + db] + 32 * kb * D]);
                         o[db] = M::mma(av, pb[kb][hs], o[db]);
                         if constexpr (M::kSplit) o[db] = M::mma(av, pl[kb][hs], o[db]);
                     }
