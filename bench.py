@@ -65,6 +65,9 @@ def parse_args():
     p.add_argument("--measure-mfma", action="store_true",
                    help="run one rocprofv3 --pmc pass of MFMA / VALU / LDS counters over the prefill and training "
                         "configs (child processes) and write the summary under profiles/")
+    p.add_argument("--measure-trace", action="store_true",
+                   help="run rocprofv3 --kernel-trace --stats over the default benchmark (a child process) and write "
+                        "the per-kernel summary with the per-launch rates under profiles/")
     return p.parse_args()
 
 
@@ -454,6 +457,77 @@ def library_hash() -> str:
     return mod.source_hash() or ""
 
 
+TRACE_FILE = ROOT / "profiles" / "kernel_trace_bench_prefill_decode_q8_train_fp32.md"
+# kernel-name substrings of each configuration's kernels (the training step is three launches)
+TRACE_KERNELS = {
+    "prefill": ["prefill_fwd_kernelIDF16_Li128ELb1ELi0E"],
+    "decode": ["decode_stream_kernelIDF16_Li128ELi4ELi0E"],
+    "decode_q8_0": ["decode_q8_lds_kernel<128, 4, 0>"],
+    "train": ["prefill_fwd_kernelIDF16bLi64ELb1ELi4E", "bwd_dq_kernelIDF16bLi64ELb1ELi4E",
+              "bwd_dkdv_kernelIDF16bLi64ELb1ELi4E"],
+    "fp32": ["generic_fwd"],
+}
+
+
+def measure_trace():
+    """Kernel durations of the default benchmark from rocprofv3 --kernel-trace --stats, and each
+    configuration's work divided by its kernels' average duration per launch."""
+    with tempfile.TemporaryDirectory() as d:
+        cmd = ["rocprofv3", "--kernel-trace", "--stats", "-d", d, "-o", "run", "--output-format", "csv", "--",
+               sys.executable, str(ROOT / "bench.py"), "--no-cpu", "--steps", "200", "--warmup", "50"]
+        print("[trace] " + " ".join(cmd[:3] + ["-d", "<tmp>"] + cmd[5:]), file=sys.stderr, flush=True)
+        proc = subprocess.run(cmd, timeout=300, stdout=subprocess.PIPE, stderr=subprocess.DEVNULL, text=True)
+        files = list(Path(d).rglob("*kernel_stats.csv"))
+        if not files:
+            raise RuntimeError(f"rocprofv3 wrote no kernel statistics (exit {proc.returncode})")
+        rows = list(csv.DictReader(open(files[0])))
+        line = json.loads(proc.stdout.strip().splitlines()[-1])
+    total = sum(float(r["TotalDurationNs"]) for r in rows)
+    lines = ["# Kernel trace of the default benchmark", "",
+             "Workloads: prefill fp16 B4 H32 L2048 D128 causal; decode fp16 B32 H32/8 S4096 D128; decode Q8_0 B16 "
+             "H32/8 S8192 D128; train bf16 B8 H16 L1024 D64 causal + key padding; fp32 B1 H4 L128 D64 causal.", "",
+             f"Library `{library_hash()[:16]}` (source fingerprint gt_source_hash).", "",
+             "Command: `python bench.py --measure-trace`, which runs `rocprofv3 --kernel-trace --stats -d <tmp> -o run "
+             "--output-format csv -- python bench.py --no-cpu --steps 200 --warmup 50` and summarises "
+             "`run_kernel_stats.csv` (durations in microseconds; the PyTorch kernels are the benchmark's input "
+             "generation).", "",
+             "| kernel | calls | avg us | min us | max us | % of GPU time |", "|---|---|---|---|---|---|"]
+    rows.sort(key=lambda r: -float(r["TotalDurationNs"]))
+    avg = {}
+    for r in rows:
+        name = r["Name"]
+        a_us = float(r["AverageNs"]) / 1e3
+        avg[name] = a_us
+        short = name if len(name) <= 110 else name[:107] + "..."
+        lines.append(f"| `{short}` | {r['Calls']} | {a_us:.1f} | {float(r['MinNs']) / 1e3:.1f} | "
+                     f"{float(r['MaxNs']) / 1e3:.1f} | {100 * float(r['TotalDurationNs']) / total:.1f} |")
+    lines += ["", "Per launch (work as counted by the benchmark, divided by the summed average duration of the "
+              "configuration's kernels):", ""]
+    for cfg, pats in TRACE_KERNELS.items():
+        res = line["configs"].get(cfg)
+        if not res:
+            continue
+        us = sum(v for k, v in avg.items() for p in pats if p in k)
+        if us <= 0:
+            continue
+        if res["unit"] == "GB/s":
+            work = res["bytes_per_step"]
+            rate = work / (us * 1e-6) / 1e9
+            lines.append(f"- {cfg}: {work / 1e6:.1f} MB / {us:.1f} us = {rate:.0f} GB/s "
+                         f"({100 * rate / PEAK_HBM_GBS:.1f}% of 8 TB/s); bench.py's HIP-event time "
+                         f"{res['ms_per_step'] * 1e3:.1f} us per step")
+        else:
+            work = res["flop_per_step"]
+            rate = work / (us * 1e-6) / 1e12
+            peak = 157.3 if cfg == "fp32" else PEAK_FP16_TFLOPS
+            lines.append(f"- {cfg}: {work / 1e9:.2f} GFLOP / {us:.1f} us = {rate:.1f} TFLOP/s "
+                         f"({100 * rate / peak:.1f}% of {peak}); bench.py's HIP-event time "
+                         f"{res['ms_per_step'] * 1e3:.1f} us per step")
+    TRACE_FILE.parent.mkdir(exist_ok=True)
+    TRACE_FILE.write_text("\n".join(lines) + "\n")
+    print("\n".join(lines))
+
+
 def committed_traffic(config, build):
     """HBM bytes per launch of the config's dominant kernel as last measured by --measure-traffic,
     or None when that measurement was made on a library built from other sources."""
@@ -485,6 +559,9 @@ def main():
         return 0
     if args.measure_mfma:
         measure_mfma()
+        return 0
+    if args.measure_trace:
+        measure_trace()
         return 0
     if args.gpus != 1:
         print(f"bench.py: the benchmark measures one GPU; --gpus {args.gpus} is not supported "
