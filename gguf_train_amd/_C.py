@@ -12,7 +12,7 @@ builds, downloads or falls back to anything: a missing library is an ImportError
 from __future__ import annotations
 
 import ctypes
-from ctypes import POINTER, c_char_p, c_float, c_int, c_int64, c_size_t, c_uint64, c_void_p
+from ctypes import POINTER, c_char_p, c_double, c_float, c_int, c_int64, c_size_t, c_uint64, c_void_p
 from pathlib import Path
 
 _PKG_DIR = Path(__file__).resolve().parent
@@ -152,6 +152,21 @@ def _configure(lib: ctypes.CDLL) -> ctypes.CDLL:
 
     lib.gt_attention_weights.argtypes = [c_void_p, c_void_p, c_void_p, c_void_p, c_float, c_int, c_int]
     lib.gt_attention_weights.restype = c_void_p
+
+    # dropout of the attention probabilities (replaces gguf_train/nn/functional.py:750-767 and
+    # gguf_train/nn/modules/transformer.py:162-163; no counterpart in the reference ABI)
+    lib.gt_flash_attention_dropout.argtypes = [c_void_p, c_void_p, c_void_p, c_void_p, c_float, c_int, c_double,
+                                               c_uint64, c_uint64, p_vp, p_vp, p_vp]
+    lib.gt_flash_attention_dropout.restype = c_int
+    lib.gt_flash_attention_dropout_backward.argtypes = [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+                                                        c_void_p, c_float, c_int, c_double, c_uint64, c_uint64, p_vp,
+                                                        p_vp, p_vp]
+    lib.gt_flash_attention_dropout_backward.restype = c_int
+    lib.gt_attention_weights_dropout.argtypes = [c_void_p, c_void_p, c_void_p, c_void_p, c_float, c_int, c_int,
+                                                 c_double, c_uint64, c_uint64]
+    lib.gt_attention_weights_dropout.restype = c_void_p
+    lib.gt_attention_dropout_mask.argtypes = [c_int64, c_int64, c_int64, c_int64, c_double, c_uint64, c_uint64, c_int]
+    lib.gt_attention_dropout_mask.restype = c_void_p
 
     # RoPE (csrc/gguf_train.h:309-310; gguf_train/_C.py binds them with the same types)
     lib.gt_rope.argtypes = [c_void_p, c_void_p, c_int, c_int, c_int, c_float, c_float]

@@ -8,9 +8,10 @@ MultiheadAttention with the reference's signatures, and the GGUF Q8_0 codec.
 
 from . import _C
 from ._bridge import QuantizedTensor
-from ._functions import FlashAttentionFn, RoPEFn
-from ._ops import (dequantize, flash_attention, flash_attention_backward, flash_attention_lse, flash_attention_rope,
-                   flash_attention_train, quantize, rope)
+from ._functions import FlashAttentionDropoutFn, FlashAttentionFn, RoPEFn
+from ._ops import (attention_dropout_mask, attention_weights_dropout, dequantize, flash_attention,
+                   flash_attention_backward, flash_attention_dropout, flash_attention_dropout_backward,
+                   flash_attention_lse, flash_attention_rope, flash_attention_train, quantize, rope)
 from . import nn
 from .kv_cache import KVCache
 
@@ -18,6 +19,7 @@ __all__ = [
     "_C",
     "QuantizedTensor",
     "FlashAttentionFn",
+    "FlashAttentionDropoutFn",
     "RoPEFn",
     "rope",
     "flash_attention",
@@ -25,6 +27,10 @@ __all__ = [
     "flash_attention_train",
     "flash_attention_rope",
     "flash_attention_backward",
+    "flash_attention_dropout",
+    "flash_attention_dropout_backward",
+    "attention_weights_dropout",
+    "attention_dropout_mask",
     "quantize",
     "dequantize",
     "nn",

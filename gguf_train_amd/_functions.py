@@ -12,6 +12,14 @@ gradients summed into its kv head.  The reference's Python backward composition
 (matmul/softmax over full (B,H,L,S) intermediates) is replaced by the native recompute-based
 gt_flash_attention_backward, which works from the saved output and log-sum-exp.
 
+`FlashAttentionDropoutFn` replaces the reference's dropout composition in
+scaled_dot_product_attention (gguf_train/nn/functional.py:750-767), which builds the scores,
+softmax, a rand_like mask and two matmuls out of differentiable ops: one fused forward and one
+fused backward whose dropout decisions come from Philox4x32-10 keyed by a 64-bit seed drawn
+from torch's default CPU generator at the forward (so torch.manual_seed, fork_rng and
+checkpoint's RNG-state replay reproduce the same decisions); it returns the output and the
+non-differentiable log-sum-exp, from which MultiheadAttention recomputes the dropped weights.
+
 The Function subclasses torch.autograd.Function, whose engine - like the reference engine
 (gguf_train/_autograd_engine.py:325-326) - casts each gradient to its input's dtype.
 """
@@ -85,3 +93,30 @@ class FlashAttentionLseFn(torch.autograd.Function):
         dq, dk, dv = _ops.flash_attention_backward(grad_out, q, k, v, mask, out, lse, ctx.scale, ctx.is_causal)
         return (dq, dk, dv, None, None, None)
 
+
+def draw_dropout_seed() -> int:
+    """A 64-bit Philox key from torch's default CPU generator (advances its state)."""
+    return int(torch.randint(-(2 ** 63), 2 ** 63 - 1, (), dtype=torch.int64).item()) & 0xFFFFFFFFFFFFFFFF
+
+
+class FlashAttentionDropoutFn(torch.autograd.Function):
+    """Attention with dropout of the probabilities: (out, lse), lse not differentiable."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, mask, scale, is_causal, dropout_p, seed):
+        ctx.scale = float(scale) if scale is not None else (1.0 / math.sqrt(q.shape[-1]))
+        ctx.is_causal = bool(is_causal)
+        ctx.dropout = (float(dropout_p), int(seed))
+        out, lse, out32 = _ops.flash_attention_dropout(q, k, v, mask, ctx.scale, ctx.is_causal, *ctx.dropout)
+        ctx.save_for_backward(q, k, v, mask, out if out32 is None else out32, lse)
+        ctx.mark_non_differentiable(lse)
+        return out, lse
+
+    @staticmethod
+    def backward(ctx, grad_out, grad_lse):
+        if grad_out is None:
+            return (None,) * 8
+        q, k, v, mask, out, lse = ctx.saved_tensors
+        dq, dk, dv = _ops.flash_attention_dropout_backward(grad_out, q, k, v, mask, out, lse, ctx.scale,
+                                                           ctx.is_causal, *ctx.dropout)
+        return (dq, dk, dv, None, None, None, None, None)

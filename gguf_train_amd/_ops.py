@@ -73,6 +73,67 @@ def flash_attention_backward(dout, q, k, v, mask, out, lse, scale: float, is_cau
             adopt(pv.value, "flash_attention_backward"))
 
 
+def flash_attention_dropout(q, k, v, mask, scale: float, is_causal: bool, p: float, seed: int, offset: int = 0):
+    """Training forward with dropout of the probabilities: (out, lse, out32) as
+    flash_attention_train; decisions from Philox4x32-10 keyed by (seed, offset)."""
+    bind_stream(_device_of(q))
+    hq, hk, hv = borrow(q), borrow(k), borrow(v)
+    hm = borrow(mask) if mask is not None else None
+    po, pl, p32 = ctypes.c_void_p(), ctypes.c_void_p(), ctypes.c_void_p()
+    rc = _C.lib.gt_flash_attention_dropout(hq.ptr, hk.ptr, hv.ptr, hm.ptr if hm else None, ctypes.c_float(scale),
+                                           1 if is_causal else 0, float(p), _u64(seed), _u64(offset),
+                                           ctypes.byref(po), ctypes.byref(pl), ctypes.byref(p32))
+    _C.check_rc(rc, "flash_attention_dropout")
+    out32 = adopt(p32.value, "flash_attention_dropout") if p32.value else None
+    return adopt(po.value, "flash_attention_dropout"), adopt(pl.value, "flash_attention_dropout"), out32
+
+
+def flash_attention_dropout_backward(dout, q, k, v, mask, out, lse, scale: float, is_causal: bool, p: float,
+                                     seed: int, offset: int = 0):
+    """Backward of flash_attention_dropout with the same (p, seed, offset): (dq, dk, dv)."""
+    bind_stream(_device_of(q))
+    hg, hq, hk, hv = borrow(dout), borrow(q), borrow(k), borrow(v)
+    hm = borrow(mask) if mask is not None else None
+    ho = borrow(out) if out is not None else None
+    hl = borrow(lse) if lse is not None else None
+    pq, pk, pv = ctypes.c_void_p(), ctypes.c_void_p(), ctypes.c_void_p()
+    rc = _C.lib.gt_flash_attention_dropout_backward(hg.ptr, hq.ptr, hk.ptr, hv.ptr, hm.ptr if hm else None,
+                                                    ho.ptr if ho else None, hl.ptr if hl else None,
+                                                    ctypes.c_float(scale), 1 if is_causal else 0, float(p), _u64(seed),
+                                                    _u64(offset), ctypes.byref(pq), ctypes.byref(pk), ctypes.byref(pv))
+    _C.check_rc(rc, "flash_attention_dropout_backward")
+    who = "flash_attention_dropout_backward"
+    return adopt(pq.value, who), adopt(pk.value, who), adopt(pv.value, who)
+
+
+def attention_weights_dropout(q, k, mask, lse, scale: float, is_causal: bool, average_heads: bool, p: float,
+                              seed: int, offset: int = 0):
+    """The weights flash_attention_dropout multiplied V by (after dropout; averaged over the heads
+    when asked)."""
+    bind_stream(_device_of(q))
+    hq, hk, hl = borrow(q), borrow(k), borrow(lse)
+    hm = borrow(mask) if mask is not None else None
+    ptr = _C.lib.gt_attention_weights_dropout(hq.ptr, hk.ptr, hm.ptr if hm else None, hl.ptr, ctypes.c_float(scale),
+                                              1 if is_causal else 0, 1 if average_heads else 0, float(p), _u64(seed),
+                                              _u64(offset))
+    return adopt(ptr, "attention_weights_dropout")
+
+
+def attention_dropout_mask(shape, p: float, seed: int, offset: int = 0, device=None) -> torch.Tensor:
+    """The dropout decisions (B,H,L,S) bool (True = kept) of (p, seed, offset) on a HIP device."""
+    dev = torch.device("cuda") if device is None else torch.device(device)
+    index = dev.index if dev.index is not None else (torch.cuda.current_device() if torch.cuda.is_available() else 0)
+    if torch.cuda.is_available():
+        bind_stream(torch.device("cuda", index))
+    B, H, L, S = (int(x) for x in shape)
+    ptr = _C.lib.gt_attention_dropout_mask(B, H, L, S, float(p), _u64(seed), _u64(offset), index)
+    return adopt(ptr, "attention_dropout_mask")
+
+
+def _u64(x: int) -> int:
+    return int(x) & 0xFFFFFFFFFFFFFFFF
+
+
 def attention_weights(q, k, mask, lse, scale: float = 0.0, is_causal: bool = False, average_heads: bool = False):
     """gt_attention_weights: softmax(q.k^T*scale + mask) (causal-masked), recomputed from the
     forward's log-sum-exp `lse`; (B,H,L,S), or (B,L,S) averaged over the heads."""

@@ -18,6 +18,11 @@
 // bool / additive (read per element; an additive mask that does not depend on the query row is
 // read once per key: per head in dK/dV, staged with the K/V tile in dQ), keys >= S and
 // queries >= L contribute nothing.
+// Dropout (DROP): dV += (P*m)^T.dO and dP = m * dO.V^T in dS = P * (dP - delta), m the
+// element's multiplier (gt_philox.h).  dQ draws its lanes' Philox blocks directly (4 consecutive
+// keys of one query per block, as the forward); dK/dV, whose lanes hold 16 queries of one key,
+// has the workgroup draw the next step's 64 x 128 decisions into LDS as bits (one block per
+// thread and 4 keys, 8 per thread and step), read back as one 32-query word per lane.
 
 #include "attn_common.h"
 #include "gt_internal.h"
@@ -50,9 +55,9 @@ __device__ inline bool mask_at(const AttnFwdArgs &f, int64_t b, int64_t h, int q
 // ---- dK, dV ----------------------------------------------------------------------------------
 
 // D = 64 fits two wavefronts per SIMD without spills (with one, the compiler parks values in
-// AGPRs and moves them back and forth); D = 128 needs the whole register file.
-template <typename T, int D, bool CAUSAL, int MASK>
-__global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void bwd_dkdv_kernel(AttnBwdArgs a) {
+// AGPRs and moves them back and forth); D = 128, and dropout, need the whole register file.
+template <typename T, int D, bool CAUSAL, int MASK, bool DROP = false>
+__global__ __launch_bounds__(256, D <= 64 && !DROP ? 2 : 1) void bwd_dkdv_kernel(AttnBwdArgs a) {
     using M = Mfma<T>;
     using V8 = typename M::V8;
     constexpr int DT = D / 16, DB = D / 32, CH = D / 8;
@@ -63,6 +68,8 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void bwd_dkdv_kernel(AttnBwdA
     __shared__ __attribute__((aligned(16))) T sG[2][BQ * QP];  // dO
     __shared__ __attribute__((aligned(16))) float sL[2][BQ];    // lse * log2(e)
     __shared__ __attribute__((aligned(16))) float sD[2][BQ];    // -delta
+    // dropout: bit j of word [qb * BKV + key - k0] = decision of query qs0 + 32qb + j
+    __shared__ __attribute__((aligned(16))) uint32_t sDm[DROP ? 2 : 1][DROP ? 2 * BKV : 1];
 
     const AttnFwdArgs &f = a.f;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
@@ -80,6 +87,7 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void bwd_dkdv_kernel(AttnBwdA
     const int L = (int)f.L, S = (int)f.S;
     const int k0 = kt * BKV, wk0 = k0 + 32 * w, key = wk0 + lrow;  // this lane's key (n index)
     const float c = f.scale * kLog2e, inv_scale = 1.0f / f.scale;
+    const float dscale = DROP ? (float)f.drop.scale : 1.0f;
 
     // K and V rows of this lane's key as B operands (B[k = d][n = key])
     V8 kf[DT], vf[DT];
@@ -130,6 +138,24 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void bwd_dkdv_kernel(AttnBwdA
             dreg = ((const float *)a.delta)[r];
         }
     };
+    // dropout decisions of step st into sDm[buf]: thread t draws keys k0 + 4(t%32) .. +3 for
+    // the 8 queries qs0 + 8(t/32) .. +7 and writes one byte (8 query bits) per key
+    auto draw_step = [&](int st, int buf) {
+        const int hh = st / nqs, qs0 = qstart + (st % nqs) * BQ;
+        const int kg = tid & 31, qset = tid >> 5;
+        const uint64_t row0 = (uint64_t)((b * f.H + hk * G + hh) * f.L + qs0 + 8 * qset);
+        const uint64_t dblocks = (uint64_t)((f.S + 3) / 4), blk = (uint64_t)(k0 / 4 + kg);
+        uint32_t bits[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int r = 0; r < 8; ++r) {
+            const GtWord4 x = gt_philox4x32_10((row0 + r) * dblocks + blk, f.drop.offset, f.drop.seed);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) bits[j] |= (x.w[j] < f.drop.thresh ? 1u : 0u) << r;
+        }
+        uint8_t *dst = (uint8_t *)&sDm[buf][(qset >> 2) * BKV + 4 * kg];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) dst[4 * j + (qset & 3)] = (uint8_t)bits[j];
+    };
     auto store_step = [&](int buf) {
 #pragma unroll
         for (int i = 0; i < NLD; ++i) {
@@ -146,6 +172,7 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void bwd_dkdv_kernel(AttnBwdA
     if (nsteps > 0) {
         load_step(0);
         store_step(0);
+        if constexpr (DROP) draw_step(0, 0);
         if (nsteps > 1) load_step(1);
     }
     __syncthreads();
@@ -171,12 +198,13 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void bwd_dkdv_kernel(AttnBwdA
             const int q0 = qs0 + 32 * qb;
             if (CAUSAL && q0 + 31 < wk0) continue;  // every query of the block precedes our keys
             // s[i], dp[i]: query q0 + 8(i/4) + 4half + i%4, key `key`
+            // (dropout: dP starts at 0, -delta is added after the multiplier)
             f32x16 s, dp;
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
                 const f32x4 d4 = *(const f32x4 *)&sD[buf][32 * qb + 8 * g + 4 * half];
 #pragma unroll
-                for (int e = 0; e < 4; ++e) dp[4 * g + e] = d4[e];
+                for (int e = 0; e < 4; ++e) dp[4 * g + e] = DROP ? 0.0f : d4[e];
             }
 #pragma unroll
             for (int t = 0; t < DT; ++t) {
@@ -188,6 +216,17 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void bwd_dkdv_kernel(AttnBwdA
             float p[16], ds[16];
             // every (query, key) of the block visible and no per-element mask: no tests
             const bool interior = (MASK == 0 || MASK == 4) && wk0 + 31 < S && q0 + 31 < L && (!CAUSAL || q0 >= wk0 + 31);
+            // dropout: multiplier of entry i (query 8(i/4) + 4half + i%4 of the block)
+            const uint32_t dbits = DROP ? sDm[buf][qb * BKV + 32 * w + lrow] : 0u;
+            auto mult = [&](int i) { return (dbits >> (8 * (i / 4) + 4 * half + (i % 4))) & 1u ? dscale : 0.0f; };
+            if constexpr (DROP) {
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const f32x4 d4 = *(const f32x4 *)&sD[buf][32 * qb + 8 * g + 4 * half];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) dp[4 * g + e] = fmaf(dp[4 * g + e], mult(4 * g + e), d4[e]);  // m dO.V - delta
+                }
+            }
             if (interior) {
 #pragma unroll
                 for (int g = 0; g < 4; ++g) {
@@ -197,7 +236,7 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void bwd_dkdv_kernel(AttnBwdA
                     for (int e = 0; e < 4; ++e) {
                         const int i = 4 * g + e;
                         const float pv = fast_exp2(fmaf(s[i], c, -l4[e]));
-                        p[i] = pv;
+                        p[i] = DROP ? pv * mult(i) : pv;
                         ds[i] = pv * dp[i];
                     }
                 }
@@ -214,7 +253,7 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void bwd_dkdv_kernel(AttnBwdA
                         if (MASK == 1 || MASK == 2)
                             ok = ok && mask_at<MASK>(f, b, h, min(q, L - 1), min(key, S - 1), inv_scale, add);
                         const float pv = ok ? fast_exp2(fmaf(s[i] + add, c, -l4[e])) : 0.0f;
-                        p[i] = pv;
+                        p[i] = DROP ? pv * mult(i) : pv;
                         ds[i] = pv * dp[i];
                     }
                 }
@@ -244,6 +283,7 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void bwd_dkdv_kernel(AttnBwdA
         }
         if (st + 1 < nsteps) {
             store_step(buf ^ 1);
+            if constexpr (DROP) draw_step(st + 1, buf ^ 1);
             if (st + 2 < nsteps) load_step(st + 2);
         }
         __syncthreads();
@@ -268,7 +308,7 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void bwd_dkdv_kernel(AttnBwdA
 // ---- dQ --------------------------------------------------------------------------------------
 
 // (two per SIMD for D = 64 as in dK/dV, except with a per-element mask, which would spill)
-template <typename T, int D, bool CAUSAL, int MASK>
+template <typename T, int D, bool CAUSAL, int MASK, bool DROP = false>
 __global__ __launch_bounds__(256, D <= 64 && (MASK == 0 || MASK == 4) ? 2 : 1) void bwd_dq_kernel(AttnBwdArgs a, int nq) {
     using M = Mfma<T>;
     using V8 = typename M::V8;
@@ -292,6 +332,9 @@ __global__ __launch_bounds__(256, D <= 64 && (MASK == 0 || MASK == 4) ? 2 : 1) v
     const int q0 = qt * BMQ, wq0 = q0 + 32 * w, lq = wq0 + lrow;
     const int lqc = min(lq, L - 1);
     const float c = f.scale * kLog2e, inv_scale = 1.0f / f.scale;
+    const float dscale = DROP ? (float)f.drop.scale : 1.0f;
+    // dropout: Philox block of keys 0..3 of this lane's row
+    const uint64_t drow = DROP ? (uint64_t)(bh * f.L + lq) * (uint64_t)((f.S + 3) / 4) : 0;
 
     V8 qf[DT], gf[DT];
     {
@@ -308,6 +351,7 @@ __global__ __launch_bounds__(256, D <= 64 && (MASK == 0 || MASK == 4) ? 2 : 1) v
     // O is the training forward's float32 output when given, else the rounded one), written for
     // the dK/dV kernel that runs next; dP accumulates onto -delta (no per-element subtract)
     f32x16 dinit;
+    float dlt;
     {
         float part = 0.0f;
         if (a.o_f32) {
@@ -330,10 +374,11 @@ __global__ __launch_bounds__(256, D <= 64 && (MASK == 0 || MASK == 4) ? 2 : 1) v
                 for (int e = 0; e < 8; ++e) part = fmaf((float)gf[t][e], (float)ov[e], part);
             }
         }
-        const float dlt = xhalf_sum(part);
+        dlt = xhalf_sum(part);
         if (half == 0 && lq < L) ((float *)a.delta)[bh * f.L + lq] = dlt;
+        // (dropout: dP starts at 0, -delta is added after the multiplier)
 #pragma unroll
-        for (int i = 0; i < 16; ++i) dinit[i] = -dlt;
+        for (int i = 0; i < 16; ++i) dinit[i] = DROP ? 0.0f : -dlt;
     }
 
     f32x16 dq[DB];
@@ -408,6 +453,17 @@ __global__ __launch_bounds__(256, D <= 64 && (MASK == 0 || MASK == 4) ? 2 : 1) v
                 float ds[16];
                 // every (query, key) of the block visible and no per-element mask: no tests
                 const int kb0 = k0 + 32 * kb;
+                if constexpr (DROP) {
+                    // entries 4g .. 4g+3: keys kb0 + 8g + 4half + 0..3, one Philox block
+#pragma unroll
+                    for (int g = 0; g < 4; ++g) {
+                        const GtWord4 x = gt_philox4x32_10(drow + (uint64_t)((kb0 + 8 * g + 4 * half) >> 2),
+                                                           f.drop.offset, f.drop.seed);
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            dp[kb][4 * g + e] = fmaf(dp[kb][4 * g + e], x.w[e] < f.drop.thresh ? dscale : 0.0f, -dlt);
+                    }
+                }
                 const bool interior =
                     (MASK == 0 || MASK == 4) && kb0 + 31 < S && wq0 + 31 < L && (!CAUSAL || wq0 >= kb0 + 31);
                 if (interior) {
@@ -463,17 +519,22 @@ __global__ __launch_bounds__(256, D <= 64 && (MASK == 0 || MASK == 4) ? 2 : 1) v
     }
 }
 
-template <typename T, int D, bool CAUSAL, int MASK>
-hipError_t launch_bwd_typed(const AttnBwdArgs &a, hipStream_t s) {
+template <typename T, int D, bool CAUSAL, int MASK, bool DROP>
+hipError_t launch_bwd_drop(const AttnBwdArgs &a, hipStream_t s) {
     const AttnFwdArgs &f = a.f;
     // dQ first: it computes delta = rowsum(dO * O) per query row, which dK/dV reads
     const int nq = (int)((f.L + BMQ - 1) / BMQ);
-    hipLaunchKernelGGL((bwd_dq_kernel<T, D, CAUSAL, MASK>), dim3((unsigned)(nq * f.B * f.H)), dim3(256), 0, s, a, nq);
+    hipLaunchKernelGGL((bwd_dq_kernel<T, D, CAUSAL, MASK, DROP>), dim3((unsigned)(nq * f.B * f.H)), dim3(256), 0, s, a, nq);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const int nkt = (int)((f.S + BKV - 1) / BKV);
-    hipLaunchKernelGGL((bwd_dkdv_kernel<T, D, CAUSAL, MASK>), dim3((unsigned)(nkt * f.B * f.Hkv)), dim3(256), 0, s, a);
+    hipLaunchKernelGGL((bwd_dkdv_kernel<T, D, CAUSAL, MASK, DROP>), dim3((unsigned)(nkt * f.B * f.Hkv)), dim3(256), 0, s, a);
     return hipGetLastError();
+}
+
+template <typename T, int D, bool CAUSAL, int MASK>
+hipError_t launch_bwd_typed(const AttnBwdArgs &a, hipStream_t s) {
+    return a.f.dropout ? launch_bwd_drop<T, D, CAUSAL, MASK, true>(a, s) : launch_bwd_drop<T, D, CAUSAL, MASK, false>(a, s);
 }
 
 template <typename T, int D>

@@ -17,6 +17,8 @@
 
 #include <cstdint>
 
+#include "gt_philox.h"
+
 struct AttnFwdArgs {
     const void *q;
     const void *k;
@@ -43,6 +45,10 @@ struct AttnFwdArgs {
     // (cos, sin) of pair i of query row l at rope_q[l * D / 2 + i]; rope_neox: NeoX pairing.
     const void *rope_q;  // float2
     int rope_neox;
+    // Dropout of the probabilities (dropout != 0): P.V uses P * multiplier (gt_philox.h), the
+    // log-sum-exp stays that of the undropped scores.  Decode kernels never see it.
+    int dropout;
+    GtDropout drop;
 };
 
 __device__ inline int attn_kv_len(const AttnFwdArgs &a, int64_t b) { return a.kv_len ? a.kv_len[b] : (int)a.S; }
@@ -131,6 +137,8 @@ hipError_t launch_attn_decode_merge(const DecodeArgs &a, int out_dtype, hipStrea
 // Explicit attention weights from the forward's log-sum-exp: (B,H,L,S), or (B,L,S) averaged
 // over the heads, in f.out_dtype.
 hipError_t launch_attn_weights(const AttnFwdArgs &f, int cd, void *w, bool average, hipStream_t s);
+// Dropout decisions of `rows` attention rows of S keys as bytes (1 = kept; all 1 when keep_all).
+hipError_t launch_dropout_mask(const GtDropout &d, bool keep_all, int64_t rows, int64_t S, uint8_t *out, hipStream_t s);
 
 bool attn_bwd_mfma_supported(const AttnBwdArgs &a, int cd);
 hipError_t launch_attn_bwd_mfma(const AttnBwdArgs &a, int cd, hipStream_t s);

@@ -10,6 +10,9 @@
 // (generic_fwd_lds_kernel); otherwise each lane reads its key row from global memory.
 // Backward: a row kernel (dQ and delta = rowsum(P*dP)) and a column kernel (dK, dV) with one
 // wavefront per key; both recompute P from the saved log-sum-exp.
+// Dropout (a.dropout): the forward's P.V takes P * m (m = the element's multiplier, 0 or
+// 1/(1-p), gt_philox.h) while the normaliser sums P; the backward uses dV = (P*m)^T.dO and
+// dP = m * dO.V^T in dS = P * (dP - delta), delta = rowsum(P * dP) = rowsum(dO * O).
 
 #include "attn_common.h"
 #include "gt_internal.h"
@@ -61,6 +64,13 @@ __device__ inline A apply_mask(const AttnFwdArgs &a, A sc, int64_t b, int64_t h,
     const int64_t mi = b * a.m_sb + h * a.m_sh + l * a.m_sl + s * a.m_ss;
     if (a.mask_bool) return ((const uint8_t *)a.mask)[mi] ? sc : neg_inf<A>();
     return sc + ((const A *)a.mask)[mi];
+}
+
+// Dropout multiplier of element (row, s) (1 without dropout).
+template <typename A>
+__device__ inline A drop_mult(const AttnFwdArgs &a, int64_t row, int64_t s) {
+    if (!a.dropout) return (A)1;
+    return gt_dropout_mult<A>(a.drop, row, a.S, s, (A)a.drop.scale);
 }
 
 template <typename A>
@@ -118,9 +128,10 @@ __global__ __launch_bounds__(256) void generic_fwd_kernel(AttnFwdArgs a, int64_t
             m = mn;
             const A p = sc > ninf ? acc_exp(sc - m) : (A)0;
             lsum += wave_sum(p);
+            const A pd = sc > ninf ? p * drop_mult<A>(a, row, s) : (A)0;  // P.V weight
             const int nt = (int)((a.S - s0) < 64 ? (a.S - s0) : 64);
             for (int t = 0; t < nt; ++t) {
-                const A pt = __shfl(p, t, 64);
+                const A pt = __shfl(pd, t, 64);
                 if (pt == (A)0) continue;  // the reference skips p == 0 (gt_ops_nn.cpp:2515)
                 const T *vr = vb + (s0 + t) * a.v_ss;
 #pragma unroll
@@ -313,8 +324,9 @@ __global__ __launch_bounds__(256) void generic_fwd_lds_kernel(AttnFwdArgs a, int
 #pragma unroll
         for (int j = 0; j < NJ; ++j) acc[j] *= corr;
         m = mn;
-        const A p = sc > ninf ? acc_exp(sc - m) : (A)0;
+        A p = sc > ninf ? acc_exp(sc - m) : (A)0;
         lsum += wave_sum_reg(part == 0 ? p : (A)0);
+        if (a.dropout && p != (A)0 && part == 0) p *= drop_mult<A>(a, row, s);  // P.V weight
         // P.V over 8 keys at a time: their V words are read first; a key with p == 0 adds nothing
         // (its V word is replaced by 0, so an inf / NaN there is never touched, as the reference
         // skips such terms, gt_ops_nn.cpp:2515).  Keys past nk have p == 0 and zero rows.
@@ -378,7 +390,7 @@ __global__ __launch_bounds__(256) void generic_bwd_rows_kernel(AttnBwdArgs a, in
         A c = 0;
         if (s < f.S) {
             const A sc = score_of<T, A>(f, qr, kb, b, h, l, s);
-            if (sc > ninf) c = acc_exp(sc - lse) * dprob_of<T, A>(f, dor, vb, s);
+            if (sc > ninf) c = acc_exp(sc - lse) * dprob_of<T, A>(f, dor, vb, s) * drop_mult<A>(f, row, s);
         }
         delta += wave_sum(c);
     }
@@ -395,7 +407,7 @@ __global__ __launch_bounds__(256) void generic_bwd_rows_kernel(AttnBwdArgs a, in
                 const A sc = score_of<T, A>(f, qr, kb, b, h, l, s);
                 if (sc > ninf) {
                     const A p = acc_exp(sc - lse);
-                    ds = p * (dprob_of<T, A>(f, dor, vb, s) - delta);
+                    ds = p * (dprob_of<T, A>(f, dor, vb, s) * drop_mult<A>(f, row, s) - delta);
                 }
             }
             const int nt = (int)((f.S - s0) < 64 ? (f.S - s0) : 64);
@@ -454,7 +466,9 @@ __global__ __launch_bounds__(256) void generic_bwd_cols_kernel(AttnBwdArgs a, in
                         const int64_t row = bh * f.L + l;
                         p = acc_exp(sc - ((const A *)f.lse)[row]);
                         const T *dor = (const T *)a.dout + row * f.Dv;
-                        ds = p * (dprob_of<T, A>(f, dor, vb, s) - ((const A *)a.delta)[row]);
+                        const A mlt = drop_mult<A>(f, row, s);
+                        ds = p * (dprob_of<T, A>(f, dor, vb, s) * mlt - ((const A *)a.delta)[row]);
+                        p *= mlt;  // dV takes the dropped weight
                     }
                 }
                 const int nt = (int)((f.L - l0) < 64 ? (f.L - l0) : 64);
@@ -561,6 +575,7 @@ __global__ __launch_bounds__(256) void generic_bwd_rows_lds_kernel(AttnBwdArgs a
             const A sc = apply_mask<A>(f, dot * (A)f.scale, b, h, l, s);
             if (sc > ninf) p = acc_exp(sc - lse);
         }
+        if (f.dropout && p != (A)0 && part == 0) dpd *= drop_mult<A>(f, row, s);  // dP = m * dO.V
         const A pdp = p * dpd;
         delta += wave_sum_reg(part == 0 ? pdp : (A)0);
         for (int t0 = 0; t0 < nk; t0 += 8) {
@@ -671,7 +686,9 @@ __global__ __launch_bounds__(256) void generic_bwd_cols_lds_kernel(AttnBwdArgs a
                 const A sc = apply_mask<A>(f, dot * (A)f.scale, b, h, l, s);
                 if (sc > ninf) {
                     p = acc_exp(sc - Ls[r]);
-                    ds = p * (dpd - Ds[r]);
+                    const A mlt = drop_mult<A>(f, bh * f.L + l, s);
+                    ds = p * (dpd * mlt - Ds[r]);
+                    p *= mlt;  // dV takes the dropped weight
                 }
             }
             for (int t0 = 0; t0 < nq; t0 += 8) {

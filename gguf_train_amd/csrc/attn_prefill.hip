@@ -27,6 +27,9 @@
 //                                      through ds_read_b64_tr_b16.
 // bf16 P is split into hi + lo bf16 parts (two MFMAs) so the probabilities keep ~16 bits.
 // Causal tiles above the diagonal are never loaded.
+// Dropout (DROP): P.V takes P times the element's multiplier (gt_philox.h); the 8 scores a lane
+// packs for one k-step are two groups of 4 consecutive keys, one Philox block each.  The
+// running sum (and the log-sum-exp) keeps the undropped probabilities.
 
 #include "attn_common.h"
 #include "gt_internal.h"
@@ -158,8 +161,11 @@ __device__ inline int key_tiles(int qt, int nkv, int qpos) {
 
 // MASK: 0 = none, 1 = bool bytes, 2 = additive float, 4 = additive float that does not depend
 // on the query row (key padding: the tile's mask row travels to LDS with the K/V tile).
-template <typename T, int D, bool CAUSAL, int MASK, bool ROPE = false>
-__global__ __launch_bounds__(64 * nw_of<D>(), 8 / nw_of<D>()) void prefill_fwd_kernel(AttnFwdArgs a, int nq, int npairs) {
+// (dropout with a per-element mask: one workgroup per CU is the guaranteed minimum, so that the
+// Philox state does not spill)
+template <typename T, int D, bool CAUSAL, int MASK, bool ROPE = false, bool DROP = false>
+__global__ __launch_bounds__(64 * nw_of<D>(), DROP && (MASK == 1 || MASK == 2) ? 1 : 8 / nw_of<D>()) void prefill_fwd_kernel(
+    AttnFwdArgs a, int nq, int npairs) {
     constexpr int NW = nw_of<D>(), BM = bm_of<D>(), NST = nst_of<D>(), BN = bn_of<D>();
     constexpr int NKB = BN / 32;  // 32-key blocks per tile
     using M = Mfma<T>;
@@ -208,6 +214,8 @@ __global__ __launch_bounds__(64 * nw_of<D>(), 8 / nw_of<D>()) void prefill_fwd_k
     const T *vbase = (const T *)a.v + b * a.v_sb + hk * a.v_sh;
     const float c = a.scale * kLog2e;  // raw score -> log2 domain
     const float inv_scale = 1.0f / a.scale;
+    const float dscale = DROP ? (float)a.drop.scale : 1.0f;
+    const uint64_t dblocks = (uint64_t)((a.S + 3) / 4);  // Philox blocks per attention row
 
     // Flat step s (key tile s of part 0, then key tile s - na of part 1) goes to stage s % NST;
     // wave w issues NPW 1 KB loads per operand: lane `lane` of load n fills 16-byte slot
@@ -316,6 +324,8 @@ __global__ __launch_bounds__(64 * nw_of<D>(), 8 / nw_of<D>()) void prefill_fwd_k
             for (int i = 0; i < 16; ++i) o[db][i] = 0.0f;
         float m = -INFINITY;  // reference point of this lane's row, log2 domain
         float lsum = 0.0f;    // this lane's share of the running sum
+        // dropout: Philox block of keys 0..3 of this lane's row (rows past L draw unused words)
+        const uint64_t drow = DROP ? (uint64_t)(bh * a.L + lq) * dblocks : 0;
 
         for (int j = 0; j < ntiles; ++j, ++step) {
             const int k0 = j * BN;
@@ -416,7 +426,19 @@ __global__ __launch_bounds__(64 * nw_of<D>(), 8 / nw_of<D>()) void prefill_fwd_k
                     float p[8];
 #pragma unroll
                     for (int e = 0; e < 8; ++e) p[e] = fast_exp2(fmaf(s[kb][8 * hs + e], c, -msub));
-                    if constexpr (M::kSplit) {
+                    if constexpr (DROP) {
+                        // keys k0 + 32kb + 16hs + 4half + (0..3, 8..11): blocks g0 and g0 + 2
+                        const uint64_t g0 = drow + (uint64_t)((k0 + 32 * kb + 16 * hs + 4 * half) >> 2);
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) lsum += p[e];
+#pragma unroll
+                        for (int u = 0; u < 2; ++u) {
+                            const GtWord4 x = gt_philox4x32_10(g0 + 2 * u, a.drop.offset, a.drop.seed);
+#pragma unroll
+                            for (int e = 0; e < 4; ++e) p[4 * u + e] *= x.w[e] < a.drop.thresh ? dscale : 0.0f;
+                        }
+                        pack8<T>(p, pb[kb][hs], pl[kb][hs]);
+                    } else if constexpr (M::kSplit) {
                         // bf16: sum the float32 p first; packing consumes them (the residuals are
                         // formed in place)
                         lsum = sum8<T>(p, pb[kb][hs], lsum);
@@ -484,7 +506,22 @@ hipError_t launch_variant(const AttnFwdArgs &a, int nq, int npairs, int64_t grid
     hipLaunchKernelGGL((prefill_fwd_kernel<T, D, C, MK>), dim3((unsigned)grid), dim3(64 * nw_of<D>()), 0, s, a, nq, npairs)
 #define GT_PREFILL_LAUNCH_R(C, MK) \
     hipLaunchKernelGGL((prefill_fwd_kernel<T, D, C, MK, true>), dim3((unsigned)grid), dim3(64 * nw_of<D>()), 0, s, a, nq, npairs)
-    if (a.rope_q) {
+#define GT_PREFILL_LAUNCH_D(C, MK) \
+    hipLaunchKernelGGL((prefill_fwd_kernel<T, D, C, MK, false, true>), dim3((unsigned)grid), dim3(64 * nw_of<D>()), 0, s, a, nq, npairs)
+    if (a.dropout) {
+        if (a.rope_q) return hipErrorInvalidValue;  // dropout runs on unrotated queries only
+        if (a.causal) {
+            if (mode == 0) GT_PREFILL_LAUNCH_D(true, 0);
+            else if (mode == 1) GT_PREFILL_LAUNCH_D(true, 1);
+            else if (mode == 4) GT_PREFILL_LAUNCH_D(true, 4);
+            else GT_PREFILL_LAUNCH_D(true, 2);
+        } else {
+            if (mode == 0) GT_PREFILL_LAUNCH_D(false, 0);
+            else if (mode == 1) GT_PREFILL_LAUNCH_D(false, 1);
+            else if (mode == 4) GT_PREFILL_LAUNCH_D(false, 4);
+            else GT_PREFILL_LAUNCH_D(false, 2);
+        }
+    } else if (a.rope_q) {
         // fused query RoPE: no mask or a key-padding row (the host rotates q itself otherwise)
         if (mode != 0 && mode != 4) return hipErrorInvalidValue;
         if (a.causal) {
@@ -507,6 +544,7 @@ hipError_t launch_variant(const AttnFwdArgs &a, int nq, int npairs, int64_t grid
     }
 #undef GT_PREFILL_LAUNCH
 #undef GT_PREFILL_LAUNCH_R
+#undef GT_PREFILL_LAUNCH_D
     return hipGetLastError();
 }
 
@@ -515,6 +553,7 @@ hipError_t launch_variant(const AttnFwdArgs &a, int nq, int npairs, int64_t grid
 bool attn_prefill_supported(const AttnFwdArgs &f, int cd) {
     if (cd != GT_F16 && cd != GT_BF16) return false;
     if (f.rope_q && f.mask && (f.mask_bool || f.m_sl != 0)) return false;  // fused RoPE: no mask or key padding
+    if (f.rope_q && f.dropout) return false;
     if (f.out_dtype != cd || f.D != f.Dv || (f.D != 64 && f.D != 128)) return false;
     if (f.L < 1 || f.S < 1 || !(f.scale > 0.0f)) return false;
     if (f.L >= (1LL << 30) || f.S >= (1LL << 30)) return false;  // 32-bit row indices

@@ -14,6 +14,8 @@
 // consecutive keys of one query row.  HBM-bound: the weights written dominate the traffic.
 // Averaged weights: a workgroup walks all H heads of its rows and writes the mean once.
 // Other dtypes / head sizes: one thread per (query, key) in the compute precision.
+// Dropout (f.dropout): the weights are those the dropout forward multiplied V by, P * m with the
+// element's multiplier m (gt_philox.h); computed by the per-element kernel.
 
 #include "attn_common.h"
 #include "gt_internal.h"
@@ -143,9 +145,11 @@ __global__ __launch_bounds__(256) void attn_weights_generic_kernel(AttnFwdArgs f
                 x += sizeof(A) == 8 ? (A)((const double *)f.mask)[mi] : (A)((const float *)f.mask)[mi];
             }
         }
-        const A ls = sizeof(A) == 8 ? (A)((const double *)f.lse)[(b * f.H + h) * f.L + l]
-                                    : (A)((const float *)f.lse)[(b * f.H + h) * f.L + l];
-        sum += sizeof(A) == 8 ? (A)exp((double)(x - ls)) : (A)expf((float)(x - ls));
+        const int64_t row = (b * f.H + h) * f.L + l;
+        const A ls = sizeof(A) == 8 ? (A)((const double *)f.lse)[row] : (A)((const float *)f.lse)[row];
+        A p = sizeof(A) == 8 ? (A)exp((double)(x - ls)) : (A)expf((float)(x - ls));
+        if (f.dropout) p *= gt_dropout_mult<A>(f.drop, row, f.S, s, (A)f.drop.scale);
+        sum += p;
     }
     if (AVG) sum /= (A)nh;
     switch (f.out_dtype) {
@@ -155,6 +159,19 @@ __global__ __launch_bounds__(256) void attn_weights_generic_kernel(AttnFwdArgs f
         case GT_BF16: ((__bf16 *)wout)[i] = (__bf16)(float)sum; break;
         default: break;
     }
+}
+
+// One thread per Philox block (4 consecutive keys of one row).
+__global__ __launch_bounds__(256) void dropout_mask_kernel(GtDropout d, int keep_all, int64_t rows, int64_t S,
+                                                          uint8_t *out) {
+    const int64_t nb = (S + 3) / 4;
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= rows * nb) return;
+    const int64_t row = i / nb, s0 = 4 * (i % nb);
+    const GtWord4 x = gt_philox4x32_10(gt_dropout_block(row, S, s0 / 4), d.offset, d.seed);
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+        if (s0 + j < S) out[row * S + s0 + j] = keep_all || x.w[j] < d.thresh ? 1 : 0;
 }
 
 template <typename T, int D, bool AVG>
@@ -194,7 +211,7 @@ hipError_t launch_generic(const AttnFwdArgs &f, void *w, bool avg, hipStream_t s
 hipError_t launch_attn_weights(const AttnFwdArgs &f, int cd, void *w, bool average, hipStream_t st) {
     if (f.B * f.L * f.S == 0 || f.H == 0) return hipSuccess;
     bool mfma = (cd == GT_F16 || cd == GT_BF16) && (f.D == 64 || f.D == 128) && f.out_dtype == cd && !f.kv_len &&
-                !f.q_pos && (uintptr_t)f.q % 16 == 0 && (uintptr_t)f.k % 16 == 0;
+                !f.q_pos && !f.dropout && (uintptr_t)f.q % 16 == 0 && (uintptr_t)f.k % 16 == 0;
     for (int64_t st8 : {f.q_sb, f.q_sh, f.q_sl, f.k_sb, f.k_sh, f.k_ss}) mfma = mfma && st8 % 8 == 0;
     if (mfma) {
         if (cd == GT_F16) {
@@ -210,4 +227,13 @@ hipError_t launch_attn_weights(const AttnFwdArgs &f, int cd, void *w, bool avera
         case GT_BF16: return launch_generic<__bf16, float>(f, w, average, st);
         default: return launch_generic<float, float>(f, w, average, st);
     }
+}
+
+hipError_t launch_dropout_mask(const GtDropout &d, bool keep_all, int64_t rows, int64_t S, uint8_t *out, hipStream_t st) {
+    const int64_t n = rows * ((S + 3) / 4);
+    if (n == 0) return hipSuccess;
+    const int64_t blocks = (n + 255) / 256;
+    if (blocks > 0x7fffffffLL) return hipErrorInvalidConfiguration;
+    hipLaunchKernelGGL(dropout_mask_kernel, dim3((unsigned)blocks), dim3(256), 0, st, d, keep_all ? 1 : 0, rows, S, out);
+    return hipGetLastError();
 }

@@ -200,7 +200,7 @@ bool decode_partials(DecodeArgs &da, int64_t units, int dev, gt_scratch &scratch
 // Picks the kernel for a staged forward: split-K decode for single-query rows, the MFMA
 // prefill kernel for fp16/bf16 with head size 64/128, the generic kernel otherwise.
 bool dispatch_forward(const AttnFwdArgs &a, int cd, int dev) {
-    if (a.out_dtype == cd && !a.o32 && attn_decode_supported(a, cd)) {
+    if (a.out_dtype == cd && !a.o32 && !a.dropout && attn_decode_supported(a, cd)) {
         DecodeArgs da{};
         da.f = a;
         da.nsplit = attn_decode_splits(a, cd);
@@ -244,6 +244,37 @@ int run_q8_decode(const gt_tensor *q, const gt_tensor *k, const gt_tensor *v, co
     return gt_hip_check(launch_attn_decode_q8(da, gt_stream()), "flash_attention q8_0 decode kernel") ? 1 : -1;
 }
 
+// Dropout of the attention probabilities: the Philox key/counter and the keep threshold of
+// probability p (gt_philox.h).  p = 0 leaves `on` false (plain attention); p outside [0, 1] is an
+// error.  thresh = floor((1 - p) * 2^32) and scale = 1 / (1 - p) in double precision, 0 for p = 1.
+struct Dropout {
+    bool on = false;
+    GtDropout d{};
+};
+
+bool make_dropout(const char *who, double p, uint64_t seed, uint64_t offset, Dropout &out) {
+    if (!(p >= 0.0 && p <= 1.0)) {
+        gt_set_error(std::string(who) + ": dropout probability has to be between 0 and 1, but got " + std::to_string(p));
+        return false;
+    }
+    out = Dropout{};
+    if (p == 0.0) return true;
+    out.on = true;
+    out.d.seed = seed;
+    out.d.offset = offset;
+    const double t = std::floor((1.0 - p) * 4294967296.0);
+    out.d.thresh = t >= 4294967295.0 ? 4294967295u : (uint32_t)t;
+    out.d.scale = p < 1.0 ? 1.0 / (1.0 - p) : 0.0;
+    return true;
+}
+
+void apply_dropout(AttnFwdArgs &a, const Dropout *drop) {
+    if (drop && drop->on) {
+        a.dropout = 1;
+        a.drop = drop->d;
+    }
+}
+
 // RoPE of the queries fused into the prefill kernel: the (cos, sin) table of the L query rows.
 struct QRope {
     const void *table;  // float2 (L, D/2) on the device
@@ -252,7 +283,7 @@ struct QRope {
 
 int attention_forward(const char *who, const gt_tensor *q, const gt_tensor *k, const gt_tensor *v,
                       const gt_tensor *mask, float scale, int is_causal, gt_tensor **out_o, gt_tensor **out_lse,
-                      gt_tensor **out_o32 = nullptr, const QRope *qrope = nullptr) {
+                      gt_tensor **out_o32 = nullptr, const QRope *qrope = nullptr, const Dropout *drop = nullptr) {
     if (out_o) *out_o = nullptr;
     if (out_lse) *out_lse = nullptr;
     if (out_o32) *out_o32 = nullptr;
@@ -282,7 +313,7 @@ int attention_forward(const char *who, const gt_tensor *q, const gt_tensor *k, c
     bool ok = true;
     int q8 = 0;  // 1: the Q8_0 decode kernel ran
     if ((o->numel > 0 || (lse && lse->numel > 0)) && k->dtype == GT_Q8_0 && v->dtype == GT_Q8_0 &&
-        q->dtype == GT_F16 && L == 1 && !o32) {
+        q->dtype == GT_F16 && L == 1 && !o32 && !(drop && drop->on)) {
         q8 = run_q8_decode(q, k, v, mask, scale, is_causal, dev, o, lse, tmp);
         ok = q8 >= 0;
     }
@@ -306,6 +337,7 @@ int attention_forward(const char *who, const gt_tensor *q, const gt_tensor *k, c
             a.scale = scale;
             a.causal = is_causal ? 1 : 0;
             a.out_dtype = q->dtype;
+            apply_dropout(a, drop);
             if (qrope) {
                 a.rope_q = qrope->table;
                 a.rope_neox = qrope->neox;
@@ -423,30 +455,31 @@ extern "C" int gt_flash_attention_train(const gt_tensor *q, const gt_tensor *k, 
     return attention_forward("flash_attention_train", q, k, v, mask, scale, is_causal, out, lse, out32);
 }
 
-extern "C" int gt_flash_attention_backward(const gt_tensor *grad_out, const gt_tensor *q, const gt_tensor *k,
-                                           const gt_tensor *v, const gt_tensor *mask, const gt_tensor *out,
-                                           const gt_tensor *lse, float scale, int is_causal, gt_tensor **dq,
-                                           gt_tensor **dk, gt_tensor **dv) {
-    const char *who = "flash_attention_backward";
+namespace {
+
+int attention_backward(const char *who, const gt_tensor *grad_out, const gt_tensor *q, const gt_tensor *k,
+                       const gt_tensor *v, const gt_tensor *mask, const gt_tensor *out, const gt_tensor *lse,
+                       float scale, int is_causal, const Dropout *drop, gt_tensor **dq, gt_tensor **dk,
+                       gt_tensor **dv) {
     if (!dq || !dk || !dv) {
-        gt_set_error("flash_attention_backward: dq, dk and dv must not be NULL");
+        gt_set_error(std::string(who) + ": dq, dk and dv must not be NULL");
         return -1;
     }
     *dq = *dk = *dv = nullptr;
     if (!validate(who, q, k, v, mask)) return -1;
     if (k->dtype == GT_Q8_0 || v->dtype == GT_Q8_0) {
-        gt_set_error("flash_attention_backward: q8_0 k/v have no gradient");
+        gt_set_error(std::string(who) + ": q8_0 k/v have no gradient");
         return -1;
     }
     const int64_t B = q->shape[0], H = q->shape[1], L = q->shape[2], D = q->shape[3];
     const int64_t Hkv = k->shape[1], S = k->shape[2], Dv = v->shape[3];
     if (!grad_out || grad_out->ndim != 4 || grad_out->shape[0] != B || grad_out->shape[1] != H ||
         grad_out->shape[2] != L || grad_out->shape[3] != Dv) {
-        gt_set_error("flash_attention_backward: grad_out must have the output's shape (B, H, L, Dv)");
+        gt_set_error(std::string(who) + ": grad_out must have the output's shape (B, H, L, Dv)");
         return -1;
     }
     if (lse && (lse->ndim != 3 || lse->shape[0] != B || lse->shape[1] != H || lse->shape[2] != L)) {
-        gt_set_error("flash_attention_backward: lse must have shape (B, H, L)");
+        gt_set_error(std::string(who) + ": lse must have shape (B, H, L)");
         return -1;
     }
     const int dev = q->device_type == GT_DEV_CUDA ? q->device_index : 0;
@@ -466,7 +499,8 @@ extern "C" int gt_flash_attention_backward(const gt_tensor *grad_out, const gt_t
     const bool mfma_shape = (cd == GT_F16 || cd == GT_BF16) && D == Dv && (D == 64 || D == 128);
     if (!lse || !out || (mfma_shape && out->dtype != GT_F32)) {
         gt_tensor *o2 = nullptr, *l2 = nullptr, *o32 = nullptr;
-        if (attention_forward(who, q, k, v, mask, scale, is_causal, &o2, &l2, mfma_shape ? &o32 : nullptr) != 0)
+        if (attention_forward(who, q, k, v, mask, scale, is_causal, &o2, &l2, mfma_shape ? &o32 : nullptr, nullptr,
+                              drop) != 0)
             return -1;
         tmp.keep(o2);
         tmp.keep(l2);
@@ -511,6 +545,7 @@ extern "C" int gt_flash_attention_backward(const gt_tensor *grad_out, const gt_t
         a.delta = gt_data(delta);
         a.f.o = const_cast<void *>(gt_data(out_s));
         a.o_f32 = od == GT_F32 && cd != GT_F32;
+        apply_dropout(a.f, drop);
         if (attn_bwd_mfma_supported(a, cd))
             ok = gt_hip_check(launch_attn_bwd_mfma(a, cd, gt_stream()), "flash_attention_backward kernel");
         else
@@ -532,6 +567,77 @@ extern "C" int gt_flash_attention_backward(const gt_tensor *grad_out, const gt_t
     *dk = gk;
     *dv = gv;
     return 0;
+}
+
+}  // namespace
+
+extern "C" int gt_flash_attention_backward(const gt_tensor *grad_out, const gt_tensor *q, const gt_tensor *k,
+                                           const gt_tensor *v, const gt_tensor *mask, const gt_tensor *out,
+                                           const gt_tensor *lse, float scale, int is_causal, gt_tensor **dq,
+                                           gt_tensor **dk, gt_tensor **dv) {
+    return attention_backward("flash_attention_backward", grad_out, q, k, v, mask, out, lse, scale, is_causal, nullptr,
+                              dq, dk, dv);
+}
+
+// ---- dropout ------------------------------------------------------------------------------------
+// The reference's scaled_dot_product_attention with dropout_p > 0 composes explicit ops
+// (gguf_train/nn/functional.py:750-767: scores, softmax, dropout by rand_like(probs) < 1 - p,
+// scaled by 1 / (1 - p), then probs.matmul(v)); MultiheadAttention does the same on its explicit
+// weights (gguf_train/nn/modules/transformer.py:153-166).  Here the fused kernels take the dropout
+// decisions from a counter-based generator instead (gt_philox.h), so the forward, the backward
+// and the weights of one (seed, offset) agree element for element without storing a mask.
+
+extern "C" int gt_flash_attention_dropout(const gt_tensor *q, const gt_tensor *k, const gt_tensor *v,
+                                          const gt_tensor *mask, float scale, int is_causal, double dropout_p,
+                                          uint64_t seed, uint64_t offset, gt_tensor **out, gt_tensor **lse,
+                                          gt_tensor **out32) {
+    const char *who = "flash_attention_dropout";
+    if (!out || !lse || !out32) {
+        gt_set_error("flash_attention_dropout: out, lse and out32 must not be NULL");
+        return -1;
+    }
+    *out = *lse = *out32 = nullptr;
+    Dropout drop;
+    if (!make_dropout(who, dropout_p, seed, offset, drop)) return -1;
+    return attention_forward(who, q, k, v, mask, scale, is_causal, out, lse, out32, nullptr, &drop);
+}
+
+extern "C" int gt_flash_attention_dropout_backward(const gt_tensor *grad_out, const gt_tensor *q, const gt_tensor *k,
+                                                   const gt_tensor *v, const gt_tensor *mask, const gt_tensor *out,
+                                                   const gt_tensor *lse, float scale, int is_causal, double dropout_p,
+                                                   uint64_t seed, uint64_t offset, gt_tensor **dq, gt_tensor **dk,
+                                                   gt_tensor **dv) {
+    const char *who = "flash_attention_dropout_backward";
+    if (dq) *dq = nullptr;
+    if (dk) *dk = nullptr;
+    if (dv) *dv = nullptr;
+    Dropout drop;
+    if (!make_dropout(who, dropout_p, seed, offset, drop)) return -1;
+    return attention_backward(who, grad_out, q, k, v, mask, out, lse, scale, is_causal, &drop, dq, dk, dv);
+}
+
+// The dropout decisions themselves, (B,H,L,S) bool on device `device_index` (1 = kept): the
+// elements the dropout kernels of the same (p, seed, offset) keep.
+extern "C" gt_tensor *gt_attention_dropout_mask(int64_t B, int64_t H, int64_t L, int64_t S, double dropout_p,
+                                                uint64_t seed, uint64_t offset, int device_index) {
+    const char *who = "attention_dropout_mask";
+    if (B < 0 || H < 0 || L < 0 || S < 0) {
+        gt_set_error("attention_dropout_mask: negative dimension");
+        return nullptr;
+    }
+    Dropout drop;
+    if (!make_dropout(who, dropout_p, seed, offset, drop)) return nullptr;
+    if (!gt_device_ok(device_index)) return nullptr;
+    const int64_t sh[4] = {B, H, L, S};
+    gt_tensor *m = gt_new_tensor(4, sh, GT_BOOL, GT_DEV_CUDA, device_index);
+    if (!m) return nullptr;
+    // p = 0: every element kept
+    if (!gt_hip_check(launch_dropout_mask(drop.d, !drop.on, B * H * L, S, (uint8_t *)gt_data(m), gt_stream()),
+                      "dropout mask kernel")) {
+        gt_tensor_free(m);
+        return nullptr;
+    }
+    return m;
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -752,8 +858,10 @@ extern "C" gt_tensor *gt_dequantize(const gt_tensor *t, int out_dtype) {
 // masks) with ggml ops (gguf_train/nn/modules/transformer.py:153-166).  Here the fused forward
 // gives the output and the log-sum-exp; this entry point recomputes the weights from them.
 
-extern "C" gt_tensor *gt_attention_weights(const gt_tensor *q, const gt_tensor *k, const gt_tensor *mask,
-                                           const gt_tensor *lse, float scale, int is_causal, int average_heads) {
+namespace {
+
+gt_tensor *attention_weights(const gt_tensor *q, const gt_tensor *k, const gt_tensor *mask, const gt_tensor *lse,
+                             float scale, int is_causal, int average_heads, const Dropout *drop) {
     if (!validate("attention_weights", q, k, k, mask)) return nullptr;
     if (!lse || lse->ndim != 3 || lse->shape[0] != q->shape[0] || lse->shape[1] != q->shape[1] ||
         lse->shape[2] != q->shape[2]) {
@@ -784,6 +892,7 @@ extern "C" gt_tensor *gt_attention_weights(const gt_tensor *q, const gt_tensor *
     a.scale = scale;
     a.causal = is_causal ? 1 : 0;
     a.out_dtype = q->dtype;
+    apply_dropout(a, drop);
     const int64_t wsh4[4] = {B, H, L, S}, wsh3[3] = {B, L, S};
     gt_tensor *w = average_heads ? gt_new_tensor(3, wsh3, q->dtype, GT_DEV_CUDA, dev)
                                  : gt_new_tensor(4, wsh4, q->dtype, GT_DEV_CUDA, dev);
@@ -794,6 +903,21 @@ extern "C" gt_tensor *gt_attention_weights(const gt_tensor *q, const gt_tensor *
         return nullptr;
     }
     return deliver(w, q->device_type != GT_DEV_CUDA);
+}
+
+}  // namespace
+
+extern "C" gt_tensor *gt_attention_weights(const gt_tensor *q, const gt_tensor *k, const gt_tensor *mask,
+                                           const gt_tensor *lse, float scale, int is_causal, int average_heads) {
+    return attention_weights(q, k, mask, lse, scale, is_causal, average_heads, nullptr);
+}
+
+extern "C" gt_tensor *gt_attention_weights_dropout(const gt_tensor *q, const gt_tensor *k, const gt_tensor *mask,
+                                                   const gt_tensor *lse, float scale, int is_causal, int average_heads,
+                                                   double dropout_p, uint64_t seed, uint64_t offset) {
+    Dropout drop;
+    if (!make_dropout("attention_weights_dropout", dropout_p, seed, offset, drop)) return nullptr;
+    return attention_weights(q, k, mask, lse, scale, is_causal, average_heads, &drop);
 }
 
 // ---- KV cache --------------------------------------------------------------------------------

@@ -6,7 +6,10 @@
   attention weights (B, H, L, S) from the right and reshaped to 4-D;
 - is_causal masks s > l (top-left aligned);
 - dropout_p == 0 runs the fused native kernel through FlashAttentionFn; dropout_p > 0 runs the
-  reference's explicit composition (matmul, softmax, dropout, matmul);
+  fused native dropout kernels through FlashAttentionDropoutFn (the reference composes matmul,
+  softmax, dropout, matmul; here the dropout decisions come from a counter-based generator
+  seeded from torch's default generator, and a row with nothing to attend to yields 0 as on the
+  dropout_p == 0 path, where the reference's -1e9 fill would average V);
 - inside autocast, q/k/v (and a float mask) are cast to the autocast dtype
   (gguf_train/_tensor.py:261-283, gguf_train/amp.py:8-10);
 - k/v may be QuantizedTensor (GGUF Q8_0); they are read as their dequantized values and carry
@@ -20,7 +23,7 @@ import math
 import torch
 
 from .._bridge import QuantizedTensor
-from .._functions import FlashAttentionFn, RoPEFn
+from .._functions import FlashAttentionDropoutFn, FlashAttentionFn, RoPEFn, draw_dropout_seed
 from .. import _ops
 
 
@@ -68,24 +71,11 @@ def scaled_dot_product_attention(
             return _ops.flash_attention(query, key, value, attn_mask, sc, is_causal)
         if dropout_p == 0.0:
             return FlashAttentionFn.apply(query, key, value, attn_mask, sc, is_causal)
-        # dropout: the reference's explicit composition (gguf_train/nn/functional.py:750-767)
-        B, H, L, D = query.shape
-        H_kv = key.shape[1]
-        k_u = key if H == H_kv else key.repeat_interleave(H // H_kv, dim=1)
-        v_u = value if H == H_kv else value.repeat_interleave(H // H_kv, dim=1)
-        scores = query.matmul(k_u.transpose(-2, -1).contiguous()) * sc
-        if is_causal:
-            S = key.shape[-2]
-            cm = torch.ones((L, S), dtype=query.dtype, device=query.device).triu(diagonal=1) * (-1e9)
-            scores = scores + cm
-        if attn_mask is not None:
-            if attn_mask.dtype == torch.bool:
-                scores = scores.masked_fill(~attn_mask, -1e9)
-            else:
-                scores = scores + attn_mask
-        probs = torch.softmax(scores, dim=-1)
-        probs = torch.nn.functional.dropout(probs, p=dropout_p, training=True)
-        return probs.matmul(v_u)
+        # dropout (the reference composes it, gguf_train/nn/functional.py:750-767): fused forward
+        # and backward drawing the decisions from a seed of torch's generator
+        out, _ = FlashAttentionDropoutFn.apply(query, key, value, attn_mask, sc, is_causal, float(dropout_p),
+                                               draw_dropout_seed())
+        return out
 
 
 def rope(input, positions, n_dims: int | None = None, mode: int = 0, n_ctx_orig: int = 0, freq_base: float = 10000.0,

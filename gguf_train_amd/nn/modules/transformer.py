@@ -12,7 +12,8 @@
   weights from them (the reference composes them with ggml ops, transformer.py:153-166).  The
   causal mask excludes future keys rather than adding -1e9 (the same weights unless every
   visible key of a row is masked out); gradients flow through the output, not the returned
-  weights; with dropout in training the reference's composition runs.
+  weights; with dropout in training the fused dropout kernels run and the returned weights are
+  the dropped ones the output was formed with (gt_attention_weights_dropout, same decisions).
 
 The projections are plain GEMMs (torch.nn.functional.linear); the attention itself is the
 native kernel.
@@ -26,7 +27,7 @@ import torch
 from torch import nn
 
 from ... import _ops
-from ..._functions import FlashAttentionLseFn
+from ..._functions import FlashAttentionDropoutFn, FlashAttentionLseFn, draw_dropout_seed
 from .. import functional as F
 
 
@@ -161,17 +162,14 @@ class MultiheadAttention(nn.Module):
             )
             attn_weights = None
         elif self.dropout > 0.0 and self.training:
-            # dropout on the explicit weights: the reference's composition (transformer.py:153-166)
-            scores = q.matmul(k.transpose(-2, -1).contiguous()) * scale
-            if is_causal:
-                cm = torch.ones((L, S), dtype=q.dtype, device=q.device).triu(diagonal=1) * (-1e9)
-                scores = scores + cm
-            if mask is not None:
-                scores = scores + mask
-            attn_weights = torch.nn.functional.dropout(torch.softmax(scores, dim=-1), p=self.dropout, training=True)
-            attn_out = attn_weights.matmul(v)
-            if average_attn_weights:
-                attn_weights = attn_weights.mean(dim=1)
+            # dropout on the explicit weights (the reference composes it, transformer.py:153-166):
+            # the fused dropout forward, and the weights it multiplied V by, recomputed from its
+            # log-sum-exp with the same dropout decisions
+            seed = draw_dropout_seed()
+            attn_out, lse = FlashAttentionDropoutFn.apply(q, k, v, mask, scale, is_causal, float(self.dropout), seed)
+            with torch.no_grad():
+                attn_weights = _ops.attention_weights_dropout(q.detach(), k.detach(), mask, lse, scale, is_causal,
+                                                              average_attn_weights, float(self.dropout), seed)
         else:
             # native: the fused forward gives the output and the log-sum-exp, from which the
             # weights are recomputed (gt_attention_weights); gradients flow through the output

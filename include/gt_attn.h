@@ -206,6 +206,46 @@ GT_API int gt_flash_attention_noalloc(const gt_tensor *q, const gt_tensor *k, co
 GT_API gt_tensor *gt_attention_weights(const gt_tensor *q, const gt_tensor *k, const gt_tensor *mask,
                                        const gt_tensor *lse, float scale, int is_causal, int average_heads);
 
+/* ---- dropout ---------------------------------------------------------------------------- */
+
+/* Replaces the reference's dropout composition in scaled_dot_product_attention
+ * (gguf_train/nn/functional.py:750-767: softmax(q.k^T*scale + masks), then probs * (rand < 1-p)
+ * / (1-p), then .matmul(v)) with the fused training forward: as gt_flash_attention_train, with
+ * the probabilities multiplied by 1/(1-p) where kept and by 0 where dropped before P.V; lse is
+ * that of the undropped scores.  The decisions come from Philox4x32-10 keyed by `seed`, counter
+ * (element block, `offset`) (gt_philox.h: element (b,h,l,s) uses word s%4 of block
+ * ((b*H + h)*L + l)*ceil(S/4) + s/4 and is kept when the word < floor((1-p)*2^32)), not from the
+ * reference's sequential mt19937_64 draws.  0 <= dropout_p <= 1 (0: no dropout, 1: all dropped).
+ * The causal mask and bool masks block with -inf where the reference adds -1e9: identical
+ * except for a row with nothing to attend to, which yields 0 here.  Returns 0 on success. */
+GT_API int gt_flash_attention_dropout(const gt_tensor *q, const gt_tensor *k, const gt_tensor *v,
+                                      const gt_tensor *mask, float scale, int is_causal, double dropout_p,
+                                      uint64_t seed, uint64_t offset, gt_tensor **out, gt_tensor **lse,
+                                      gt_tensor **out32);
+
+/* The backward of gt_flash_attention_dropout with the same (dropout_p, seed, offset): the
+ * gradients of the reference's composition under the same dropout decisions, as
+ * gt_flash_attention_backward otherwise (out / lse may be NULL: recomputed). */
+GT_API int gt_flash_attention_dropout_backward(const gt_tensor *grad_out, const gt_tensor *q, const gt_tensor *k,
+                                               const gt_tensor *v, const gt_tensor *mask, const gt_tensor *out,
+                                               const gt_tensor *lse, float scale, int is_causal, double dropout_p,
+                                               uint64_t seed, uint64_t offset, gt_tensor **dq, gt_tensor **dk,
+                                               gt_tensor **dv);
+
+/* Replaces MultiheadAttention's dropout on its explicit weights
+ * (gguf_train/nn/modules/transformer.py:162-163): gt_attention_weights multiplied by the dropout
+ * multipliers of the same (dropout_p, seed, offset) as gt_flash_attention_dropout, i.e. the
+ * weights that forward multiplied V by (averaged over the heads after the dropout). */
+GT_API gt_tensor *gt_attention_weights_dropout(const gt_tensor *q, const gt_tensor *k, const gt_tensor *mask,
+                                               const gt_tensor *lse, float scale, int is_causal, int average_heads,
+                                               double dropout_p, uint64_t seed, uint64_t offset);
+
+/* No counterpart in the reference: the dropout decisions of (dropout_p, seed, offset) for a
+ * (B,H,L,S) attention, as a bool tensor on HIP device `device_index` (1 = kept, scaled by
+ * 1/(1-p)).  What the dropout kernels use, element for element. */
+GT_API gt_tensor *gt_attention_dropout_mask(int64_t B, int64_t H, int64_t L, int64_t S, double dropout_p,
+                                            uint64_t seed, uint64_t offset, int device_index);
+
 /* ---- RoPE ------------------------------------------------------------------------------ */
 
 /* csrc/gguf_train.h:309-310 (implementation csrc/gt_ops_nn.cpp:2298-2421, ggml_rope_ext /

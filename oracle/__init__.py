@@ -2,8 +2,10 @@
 
 numpy front end of oracle/oracle_attn.c (a float64 C restatement of the reference's
 gt_flash_attention, csrc/gt_ops_nn.cpp:2423-2525, of FlashAttentionFn.backward,
-gguf_train/_functions.py:1933-1965, of the GGUF Q8_0 codec, csrc/gt_core.cpp:800-832, and of
-gt_rope / gt_rope_backward, csrc/gt_ops_nn.cpp:2298-2421).
+gguf_train/_functions.py:1933-1965, of the GGUF Q8_0 codec, csrc/gt_core.cpp:800-832, of
+gt_rope / gt_rope_backward, csrc/gt_ops_nn.cpp:2298-2421, and of the dropout path of
+scaled_dot_product_attention, gguf_train/nn/functional.py:750-767), plus the dropout
+decisions' generator, Philox4x32-10 (Salmon et al., SC 2011), in numpy.
 Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg import this package, to
 check results or time the CPU baseline; the product (gguf_train_amd) never does.
 
@@ -52,6 +54,10 @@ def lib() -> ctypes.CDLL:
         L.oracle_rope.argtypes = [vp, c_int, i64, i64, i64, i64, vp, c_int, c_int, ctypes.c_float, ctypes.c_float,
                                   c_int, vp]
         L.oracle_rope.restype = c_int
+        L.oracle_attention_dropout.argtypes = [vp, c_int, vp, c_int, vp, c_int, vp, c_int, c_int, vp, vp,
+                                               ctypes.c_double, vp, c_int, i64, i64, i64, i64, i64, i64, i64,
+                                               ctypes.c_float, c_int, vp, c_int, vp, vp, vp, c_int]
+        L.oracle_attention_dropout.restype = c_int
         _lib = L
     return _lib
 
@@ -174,6 +180,92 @@ def flash_attention_backward(dout, q, k, v, mask=None, scale: float = -1.0, is_c
     if rc != 0:
         raise ValueError("oracle_flash_attention_backward: inconsistent shapes")
     return dq, dk, dv
+
+
+# ---- dropout ---------------------------------------------------------------------------------
+
+_PHILOX_M = (np.uint64(0xD2511F53), np.uint64(0xCD9E8D57))
+_PHILOX_W = (0x9E3779B9, 0xBB67AE85)
+_LO32 = np.uint64(0xFFFFFFFF)
+
+
+def philox4x32_10(counter, key) -> np.ndarray:
+    """Philox4x32-10 (Salmon, Moraes, Dror, Shaw, "Parallel random numbers: as easy as 1, 2, 3",
+    SC 2011): counter (N, 4) and key (N, 2) or (2,) of uint32 -> (N, 4) uint32 words.  Each round
+    takes the two 32x32 -> 64-bit products M0 * c0 and M1 * c2 and maps
+    (c0, c1, c2, c3) -> (hi(M1 c2) ^ c1 ^ k0, lo(M1 c2), hi(M0 c0) ^ c3 ^ k1, lo(M0 c0)); the key is
+    bumped by the Weyl constants (W0, W1) between rounds."""
+    c = np.array(counter, dtype=np.uint64).reshape(-1, 4)
+    k = np.broadcast_to(np.array(key, dtype=np.uint64).reshape(-1, 2), (c.shape[0], 2)).copy()
+    c0, c1, c2, c3 = (c[:, i].copy() for i in range(4))
+    k0, k1 = k[:, 0], k[:, 1]
+    for _ in range(10):
+        p0 = _PHILOX_M[0] * c0
+        p1 = _PHILOX_M[1] * c2
+        c0, c1, c2, c3 = (p1 >> np.uint64(32)) ^ c1 ^ k0, p1 & _LO32, (p0 >> np.uint64(32)) ^ c3 ^ k1, p0 & _LO32
+        k0 = (k0 + np.uint64(_PHILOX_W[0])) & _LO32
+        k1 = (k1 + np.uint64(_PHILOX_W[1])) & _LO32
+    return np.stack([c0, c1, c2, c3], axis=1).astype(np.uint32)
+
+
+def dropout_threshold(p: float) -> int:
+    """Keep when the element's word < floor((1 - p) * 2^32) (at most 2^32 - 1); 0 for p = 1."""
+    return int(min(np.floor((1.0 - float(p)) * 4294967296.0), 4294967295.0))
+
+
+def dropout_keep(B: int, H: int, L: int, S: int, p: float, seed: int, offset: int = 0) -> np.ndarray:
+    """The dropout decisions (B, H, L, S) bool of the library's attention dropout: element
+    (b, h, l, s) takes word s % 4 of Philox4x32-10 with counter (n mod 2^32, n / 2^32,
+    offset mod 2^32, offset / 2^32), n = ((b*H + h)*L + l) * ceil(S/4) + s/4, and key (seed mod
+    2^32, seed / 2^32); kept when the word is below dropout_threshold(p).  p = 0 keeps all."""
+    if p == 0.0:
+        return np.ones((B, H, L, S), dtype=bool)
+    nb = (S + 3) // 4
+    n = np.arange(B * H * L * nb, dtype=np.uint64)
+    seed, offset = int(seed) & 0xFFFFFFFFFFFFFFFF, int(offset) & 0xFFFFFFFFFFFFFFFF
+    ctr = np.stack([n & _LO32, n >> np.uint64(32), np.full_like(n, offset & 0xFFFFFFFF),
+                    np.full_like(n, offset >> 32)], axis=1)
+    words = philox4x32_10(ctr, (seed & 0xFFFFFFFF, seed >> 32)).reshape(B * H * L, nb * 4)[:, :S]
+    return (words < np.uint32(dropout_threshold(p)) if p < 1.0 else np.zeros_like(words, dtype=bool)).reshape(
+        B, H, L, S)
+
+
+def attention_dropout(q, k, v, keep, p: float, mask=None, scale: float = -1.0, is_causal: bool = False,
+                      dout=None, out_dtype=None, nthreads: int = 0):
+    """scaled_dot_product_attention with dropout (gguf_train/nn/functional.py:750-767) in float64
+    for the keep mask `keep` (B,H,L,S bool).  Returns the output in q's dtype (or `out_dtype`;
+    float16/bfloat16 as uint16 bits) and, when `dout` is given, (dq, dk, dv) float64."""
+    qa, qc = _code(q)
+    ka, kc = _code(k)
+    va, vc = _code(v)
+    B, H, L, D = qa.shape
+    _, Hkv, S, Dv = va.shape
+    kp = np.ascontiguousarray(keep, dtype=np.uint8)
+    if kp.shape != (B, H, L, S):
+        raise ValueError("oracle_attention_dropout: keep must be (B, H, L, S)")
+    oc = qc if out_dtype is None else out_dtype
+    out = np.empty((B, H, L, Dv), dtype={F32: np.float32, F64: np.float64, F16: np.uint16, BF16_CODE: np.uint16}[oc])
+    if mask is not None:
+        ma, mc = _code(mask)
+        mshape = (ctypes.c_int64 * 4)(*ma.shape, *([0] * (4 - ma.ndim)))
+        mptr, mnd = _ptr(ma), ma.ndim
+    else:
+        ma, mc, mshape, mptr, mnd = None, 0, None, None, 0
+    if dout is not None:
+        ga, gc = _code(dout)
+        dq = np.empty((B, H, L, D), dtype=np.float64)
+        dk = np.empty((B, Hkv, S, D), dtype=np.float64)
+        dv = np.empty((B, Hkv, S, Dv), dtype=np.float64)
+    else:
+        ga, gc, dq, dk, dv = None, 0, None, None, None
+    rc = lib().oracle_attention_dropout(_ptr(qa), qc, _ptr(ka), kc, _ptr(va), vc, mptr, mc, mnd,
+                                        ctypes.cast(mshape, ctypes.c_void_p) if mshape is not None else None,
+                                        _ptr(kp), float(p), _ptr(ga) if ga is not None else None, gc,
+                                        B, H, Hkv, L, S, D, Dv, float(scale), int(bool(is_causal)), _ptr(out), oc,
+                                        *(_ptr(x) if x is not None else None for x in (dq, dk, dv)), int(nthreads))
+    if rc != 0:
+        raise ValueError("oracle_attention_dropout: inconsistent shapes")
+    return out if dout is None else (out, (dq, dk, dv))
 
 
 # ---- Q8_0 ----------------------------------------------------------------------------------

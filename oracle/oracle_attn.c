@@ -19,6 +19,10 @@
  *                                        not vendored: restated from its published algorithm)
  *   oracle_rope                          csrc/gt_ops_nn.cpp:2298-2421 -> ggml_rope_ext(_back)
  *                                        (same ggml, restated from its published algorithm)
+ *   oracle_attention_dropout(_backward)  gguf_train/nn/functional.py:750-767 (the dropout path of
+ *                                        scaled_dot_product_attention: scores, -1e9 fills,
+ *                                        softmax, probs * keep / (1 - p), .matmul(v)) and its
+ *                                        autograd gradients, in float64, for a given keep mask
  *
  * How each is pinned (tests/test_oracle.py): the converters against numpy float16 and torch
  * bfloat16 over every 16-bit pattern and edge values; the forward against the closed form
@@ -31,6 +35,9 @@
  * closed form in float64), the closed form at large positions within the float32 angle
  * chain's error bound, position 0 = identity, backward = inverse and adjoint, norm kept, NeoX =
  * NORMAL under the pair permutation, pass-through beyond n_dims (tests/test_oracle_rope.py).
+ * The dropout composition against torch.autograd in float64 with the same keep mask, and the
+ * keep mask's generator (Philox4x32-10, oracle/__init__.py) against the Random123 known answers
+ * and rocRAND's engine (tests/golden/philox4x32_10.json).
  * Parity unpinned: the byte output of ggml_quantize_chunk itself (ggml cannot be built here),
  * bfloat16 results whose magnitude is below 2^-126 (ggml versions differ on flushing them).
  */
@@ -348,6 +355,131 @@ int oracle_flash_attention_backward(const void *dout, int dout_dtype, const void
             }
             free(P);
             free(dP);
+        }
+    }
+    return 0;
+}
+
+/*
+ * scaled_dot_product_attention with dropout_p > 0 (gguf_train/nn/functional.py:750-767) in
+ * float64, dense inputs, for a given keep mask (B,H,L,S bytes, 1 = kept):
+ *   scores = q.k^T * scale; causal adds -1e9 above the diagonal; a bool mask fills blocked
+ *   positions with -1e9, a float mask is added; P = softmax(scores); Pd = P * keep / (1 - p)
+ *   (0 for p = 1, where the reference's dropout returns zeros); out = Pd.v.
+ * Backward (grad_out given, dq/dk/dv float64): dV = Pd^T.dO; dPd = dO.V^T; dP = dPd * keep /
+ * (1 - p); dS = P * (dP - rowsum(dP * P)); dQ = dS.K * scale; dK = dS^T.Q * scale; a GQA
+ * group's dK/dV are summed into its kv head (repeat_interleave's gradient).
+ * out (forward) in out_dtype; either of out / dq may be NULL to skip that half.
+ */
+static void dropout_probs(const void *q, int q_dtype, const void *k, int k_dtype, const void *mask, int mask_dtype,
+                          int mask_ndim, const int64_t *mask_shape, int64_t b, int64_t h, int64_t hk, int64_t H,
+                          int64_t Hkv, int64_t L, int64_t S, int64_t D, float scale, int is_causal, double *P) {
+    for (int64_t l = 0; l < L; ++l) {
+        double mx = -INFINITY;
+        for (int64_t s = 0; s < S; ++s) {
+            double dot = 0.0;
+            const int64_t qo = ((b * H + h) * L + l) * D, ko = ((b * Hkv + hk) * S + s) * D;
+            for (int64_t d = 0; d < D; ++d) dot += oracle_read_f64(q, q_dtype, qo + d) * oracle_read_f64(k, k_dtype, ko + d);
+            double sc = dot * (double)scale;
+            if (is_causal && s > l) sc += -1e9;
+            if (mask) {
+                const int64_t mi = mask_index(mask_ndim, mask_shape, b, h, l, s);
+                if (mask_dtype == O_BOOL) {
+                    if (((const uint8_t *)mask)[mi] == 0) sc = -1e9;
+                } else {
+                    sc += oracle_read_f64(mask, mask_dtype, mi);
+                }
+            }
+            P[l * S + s] = sc;
+            if (sc > mx) mx = sc;
+        }
+        double se = 0.0;
+        for (int64_t s = 0; s < S; ++s) {
+            P[l * S + s] = exp(P[l * S + s] - mx);
+            se += P[l * S + s];
+        }
+        for (int64_t s = 0; s < S; ++s) P[l * S + s] /= se;
+    }
+}
+
+int oracle_attention_dropout(const void *q, int q_dtype, const void *k, int k_dtype, const void *v, int v_dtype,
+                             const void *mask, int mask_dtype, int mask_ndim, const int64_t *mask_shape,
+                             const uint8_t *keep, double p, const void *dout, int dout_dtype, int64_t B, int64_t H,
+                             int64_t Hkv, int64_t L, int64_t S, int64_t D, int64_t Dv, float scale, int is_causal,
+                             void *out, int out_dtype, double *dq, double *dk, double *dv, int nthreads) {
+    if (Hkv <= 0 || H % Hkv != 0) return -1;
+    if (mask && mask_ndim != 2 && mask_ndim != 4) return -1;
+    if (dq && !dout) return -1;
+    const int64_t group = H / Hkv;
+    if (scale <= 0.0f) scale = 1.0f / sqrtf((float)D);
+    const double r = p < 1.0 ? 1.0 / (1.0 - p) : 0.0;
+#ifdef _OPENMP
+    if (nthreads > 0) omp_set_num_threads(nthreads);
+#else
+    (void)nthreads;
+#endif
+    if (dk) memset(dk, 0, sizeof(double) * (size_t)(B * Hkv * S * D));
+    if (dv) memset(dv, 0, sizeof(double) * (size_t)(B * Hkv * S * Dv));
+#pragma omp parallel for collapse(2) schedule(static)
+    for (int64_t b = 0; b < B; ++b) {
+        for (int64_t hk = 0; hk < Hkv; ++hk) {
+            const size_t n = (size_t)(L * S > 0 ? L * S : 1);
+            double *P = (double *)malloc(sizeof(double) * n);
+            double *Pd = (double *)malloc(sizeof(double) * n);
+            double *dS = (double *)malloc(sizeof(double) * n);
+            for (int64_t h = hk * group; h < (hk + 1) * group; ++h) {
+                dropout_probs(q, q_dtype, k, k_dtype, mask, mask_dtype, mask_ndim, mask_shape, b, h, hk, H, Hkv, L, S, D,
+                              scale, is_causal, P);
+                const uint8_t *kp = keep + (b * H + h) * L * S;
+                for (int64_t i = 0; i < L * S; ++i) Pd[i] = kp[i] ? P[i] * r : 0.0;
+                if (out) {
+                    for (int64_t l = 0; l < L; ++l)
+                        for (int64_t d = 0; d < Dv; ++d) {
+                            double acc = 0.0;
+                            for (int64_t s = 0; s < S; ++s)
+                                acc += Pd[l * S + s] * oracle_read_f64(v, v_dtype, ((b * Hkv + hk) * S + s) * Dv + d);
+                            oracle_write_f64(out, out_dtype, ((b * H + h) * L + l) * Dv + d, acc);
+                        }
+                }
+                if (!dq) continue;
+                for (int64_t l = 0; l < L; ++l) {
+                    double rs = 0.0;
+                    const int64_t go = ((b * H + h) * L + l) * Dv;
+                    for (int64_t s = 0; s < S; ++s) {
+                        double acc = 0.0;
+                        const int64_t vo = ((b * Hkv + hk) * S + s) * Dv;
+                        for (int64_t d = 0; d < Dv; ++d)
+                            acc += oracle_read_f64(dout, dout_dtype, go + d) * oracle_read_f64(v, v_dtype, vo + d);
+                        dS[l * S + s] = kp[l * S + s] ? acc * r : 0.0; /* dP */
+                        rs += dS[l * S + s] * P[l * S + s];
+                    }
+                    for (int64_t s = 0; s < S; ++s) dS[l * S + s] = P[l * S + s] * (dS[l * S + s] - rs);
+                }
+                for (int64_t l = 0; l < L; ++l)
+                    for (int64_t d = 0; d < D; ++d) {
+                        double acc = 0.0;
+                        for (int64_t s = 0; s < S; ++s)
+                            acc += dS[l * S + s] * oracle_read_f64(k, k_dtype, ((b * Hkv + hk) * S + s) * D + d);
+                        dq[((b * H + h) * L + l) * D + d] = acc * (double)scale;
+                    }
+                for (int64_t s = 0; s < S; ++s) {
+                    for (int64_t d = 0; d < D; ++d) {
+                        double acc = 0.0;
+                        for (int64_t l = 0; l < L; ++l)
+                            acc += dS[l * S + s] * oracle_read_f64(q, q_dtype, ((b * H + h) * L + l) * D + d);
+                        dk[((b * Hkv + hk) * S + s) * D + d] += acc * (double)scale;
+                    }
+                    for (int64_t d = 0; d < Dv; ++d) {
+                        double acc = 0.0;
+                        for (int64_t l = 0; l < L; ++l)
+                            acc += Pd[l * S + s] * oracle_read_f64(dout, dout_dtype, ((b * H + h) * L + l) * Dv + d);
+                        dv[((b * Hkv + hk) * S + s) * Dv + d] += acc;
+                    }
+                }
+            }
+            free(P);
+            free(Pd);
+            free(dS);
         }
     }
     return 0;

@@ -120,6 +120,15 @@ def test_shape_errors_match_the_reference_text():
         g.flash_attention(torch.randn(1, 2, 4, 8), torch.randn(1, 2, 4, 7), torch.randn(1, 2, 4, 8))
 
 
+def test_dropout_probability_is_checked_first():
+    q = torch.randn(1, 1, 2, 4)
+    for p in (-0.1, 1.5, float("nan")):
+        with pytest.raises(RuntimeError, match="dropout probability has to be between 0 and 1"):
+            g.flash_attention_dropout(q, q, q, None, 0.0, False, p, 1)
+        with pytest.raises(RuntimeError, match="dropout probability has to be between 0 and 1"):
+            g.attention_dropout_mask((1, 1, 2, 2), p, 1, device="cuda:0")
+
+
 @pytest.mark.skipif(_C.device_count() > 0, reason="checks the behaviour without a HIP device")
 def test_compute_without_a_device_fails_loudly():
     q = torch.randn(1, 1, 2, 4)
@@ -127,6 +136,8 @@ def test_compute_without_a_device_fails_loudly():
         g.flash_attention(q, q, q)
     with pytest.raises(RuntimeError, match="no HIP device"):
         g.quantize(torch.randn(64))
+    with pytest.raises(RuntimeError, match="no HIP device"):
+        g.flash_attention_dropout(q, q, q, None, 0.0, False, 0.5, 1)
 
 
 def test_library_matches_the_sources_beside_it():
