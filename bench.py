@@ -8,6 +8,8 @@ handles made once over device-resident inputs) over one batch of synthetic data:
   decode       GQA decode fp16, B=32 Hq=32 Hkv=8, one query row, KV length 4096, D=128
   decode_q8_0  GQA decode over a GGUF Q8_0 K/V cache, B=16 Hq=32 Hkv=8, KV length 8192, D=128
   train        bf16 forward + backward, B=8 H=16 L=S=1024 D=64, causal + key padding (-inf)
+  train_dropout  the same with dropout p = 0.1 on the probabilities (a fresh seed per step; not in
+               the default list)
   fp32         fp32 causal forward, B=1 H=4 L=S=128 D=64 (the parity configuration)
   copy         (not in the default list) a plain 1 GiB device copy, the calibration workload
                for the HBM byte counters (FETCH_SIZE / WRITE_SIZE) of the traffic figures
@@ -190,16 +192,26 @@ def bench_train(r: Runner, cfg, steps, warmup):
     for b, n in enumerate(lens):
         mask[b, ..., int(n):] = float("-inf")
     hq, hk, hv, hm, hg = r.handles(q, k, v, mask, dout)
+    p_drop = float(cfg.get("dropout", 0.0))
 
     def step(i):
         po, pl, p32 = ctypes.c_void_p(), ctypes.c_void_p(), ctypes.c_void_p()
-        rc = lib.gt_flash_attention_train(hq.ptr, hk.ptr, hv.ptr, hm.ptr, ctypes.c_float(0.0), 1, ctypes.byref(po),
-                                          ctypes.byref(pl), ctypes.byref(p32))
+        if p_drop:
+            rc = lib.gt_flash_attention_dropout(hq.ptr, hk.ptr, hv.ptr, hm.ptr, ctypes.c_float(0.0), 1, p_drop, i + 1, 0,
+                                                ctypes.byref(po), ctypes.byref(pl), ctypes.byref(p32))
+        else:
+            rc = lib.gt_flash_attention_train(hq.ptr, hk.ptr, hv.ptr, hm.ptr, ctypes.c_float(0.0), 1,
+                                              ctypes.byref(po), ctypes.byref(pl), ctypes.byref(p32))
         if rc:
             raise RuntimeError(r.C.last_error())
         dq, dk, dv = ctypes.c_void_p(), ctypes.c_void_p(), ctypes.c_void_p()
-        rc = lib.gt_flash_attention_backward(hg.ptr, hq.ptr, hk.ptr, hv.ptr, hm.ptr, p32, pl, ctypes.c_float(0.0), 1,
-                                             ctypes.byref(dq), ctypes.byref(dk), ctypes.byref(dv))
+        if p_drop:
+            rc = lib.gt_flash_attention_dropout_backward(hg.ptr, hq.ptr, hk.ptr, hv.ptr, hm.ptr, p32, pl,
+                                                         ctypes.c_float(0.0), 1, p_drop, i + 1, 0, ctypes.byref(dq),
+                                                         ctypes.byref(dk), ctypes.byref(dv))
+        else:
+            rc = lib.gt_flash_attention_backward(hg.ptr, hq.ptr, hk.ptr, hv.ptr, hm.ptr, p32, pl, ctypes.c_float(0.0),
+                                                 1, ctypes.byref(dq), ctypes.byref(dk), ctypes.byref(dv))
         if rc:
             raise RuntimeError(r.C.last_error())
         for p in (po, pl, p32, dq, dk, dv):
@@ -547,6 +559,7 @@ CONFIGS = {
     "decode": dict(B=32, H=32, Hkv=8, L=1, S=4096, D=128, dtype="float16", rotate=3),
     "decode_q8_0": dict(B=16, H=32, Hkv=8, L=1, S=8192, D=128, dtype="float16", q8_0=True, rotate=3),
     "train": dict(B=8, H=16, L=1024, D=64, dtype="bfloat16"),
+    "train_dropout": dict(B=8, H=16, L=1024, D=64, dtype="bfloat16", dropout=0.1),
     "fp32": dict(B=1, H=4, Hkv=4, L=128, S=128, D=64, dtype="float32", causal=True),
     "copy": dict(dtype="float16"),
 }
@@ -576,7 +589,7 @@ def main():
     for name in names:
         cfg = dict(CONFIGS[name])
         cfg["dtype"] = getattr(torch, cfg["dtype"])
-        if name == "train":
+        if name in ("train", "train_dropout"):
             results[name] = bench_train(r, cfg, args.steps, args.warmup)
         elif name == "copy":
             results[name] = bench_copy(r, args.steps, args.warmup)

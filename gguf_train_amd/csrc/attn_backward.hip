@@ -20,9 +20,9 @@
 // queries >= L contribute nothing.
 // Dropout (DROP): dV += (P*m)^T.dO and dP = m * dO.V^T in dS = P * (dP - delta), m the
 // element's multiplier (gt_philox.h).  dQ draws its lanes' Philox blocks directly (4 consecutive
-// keys of one query per block, as the forward); dK/dV, whose lanes hold 16 queries of one key,
-// has the workgroup draw the next step's 64 x 128 decisions into LDS as bits (one block per
-// thread and 4 keys, 8 per thread and step), read back as one 32-query word per lane.
+// keys of one query per block, as the forward) and writes the decisions as bits, one word per
+// (query row, 32 keys); dK/dV, whose lanes hold 16 queries of one key, streams those words in
+// with each query step (64 rows x 4 words through LDS) instead of drawing again.
 
 #include "attn_common.h"
 #include "gt_internal.h"
@@ -55,9 +55,11 @@ __device__ inline bool mask_at(const AttnFwdArgs &f, int64_t b, int64_t h, int q
 // ---- dK, dV ----------------------------------------------------------------------------------
 
 // D = 64 fits two wavefronts per SIMD without spills (with one, the compiler parks values in
-// AGPRs and moves them back and forth); D = 128, and dropout, need the whole register file.
+// AGPRs and moves them back and forth); D = 128 needs the whole register file.  (Dropout with the
+// key-padding row spills ~60 bytes per lane at two per SIMD and is still faster there: 255 against
+// 285 us for the training step with dropout.)
 template <typename T, int D, bool CAUSAL, int MASK, bool DROP = false>
-__global__ __launch_bounds__(256, D <= 64 && !DROP ? 2 : 1) void bwd_dkdv_kernel(AttnBwdArgs a) {
+__global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void bwd_dkdv_kernel(AttnBwdArgs a) {
     using M = Mfma<T>;
     using V8 = typename M::V8;
     constexpr int DT = D / 16, DB = D / 32, CH = D / 8;
@@ -68,8 +70,8 @@ __global__ __launch_bounds__(256, D <= 64 && !DROP ? 2 : 1) void bwd_dkdv_kernel
     __shared__ __attribute__((aligned(16))) T sG[2][BQ * QP];  // dO
     __shared__ __attribute__((aligned(16))) float sL[2][BQ];    // lse * log2(e)
     __shared__ __attribute__((aligned(16))) float sD[2][BQ];    // -delta
-    // dropout: bit j of word [qb * BKV + key - k0] = decision of query qs0 + 32qb + j
-    __shared__ __attribute__((aligned(16))) uint32_t sDm[DROP ? 2 : 1][DROP ? 2 * BKV : 1];
+    // dropout: word [w][r] = decisions of keys k0 + 32w .. +31 for query qs0 + r (bit j: key 32w + j)
+    __shared__ __attribute__((aligned(16))) uint32_t sDm[DROP ? 2 : 1][DROP ? 4 * BQ : 1];
 
     const AttnFwdArgs &f = a.f;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
@@ -88,6 +90,7 @@ __global__ __launch_bounds__(256, D <= 64 && !DROP ? 2 : 1) void bwd_dkdv_kernel
     const int k0 = kt * BKV, wk0 = k0 + 32 * w, key = wk0 + lrow;  // this lane's key (n index)
     const float c = f.scale * kLog2e, inv_scale = 1.0f / f.scale;
     const float dscale = DROP ? (float)f.drop.scale : 1.0f;
+    const int64_t dwords = (f.S + 31) / 32;  // decision words per query row
 
     // K and V rows of this lane's key as B operands (B[k = d][n = key])
     V8 kf[DT], vf[DT];
@@ -119,11 +122,18 @@ __global__ __launch_bounds__(256, D <= 64 && !DROP ? 2 : 1) void bwd_dkdv_kernel
 
     u32x4 qreg[NLD], greg[NLD];
     float lreg = 0.0f, dreg = 0.0f;
+    uint32_t mreg = 0u;  // dropout: this thread's decision word of the step
     auto load_step = [&](int st) {
         const int hh = st / nqs, qs0 = qstart + (st % nqs) * BQ;
         const int64_t h = hk * G + hh;
         const T *qb = (const T *)f.q + b * f.q_sb + h * f.q_sh;
         const T *gb = (const T *)a.dout + ((b * f.H + h) * f.L) * D;
+        if constexpr (DROP) {
+            // thread t: row t % 64 of the step, key word t / 64 of the tile (words past the
+            // sequence's keys repeat the last one: their keys have P = 0)
+            const int r = tid % BQ, wd = min((int)(k0 / 32 + tid / BQ), (int)dwords - 1);
+            mreg = a.dbits[((b * f.H + h) * f.L + min(qs0 + r, L - 1)) * dwords + wd];
+        }
 #pragma unroll
         for (int i = 0; i < NLD; ++i) {
             const int cidx = tid + 256 * i, row = cidx / CH, col = cidx % CH;
@@ -138,24 +148,6 @@ __global__ __launch_bounds__(256, D <= 64 && !DROP ? 2 : 1) void bwd_dkdv_kernel
             dreg = ((const float *)a.delta)[r];
         }
     };
-    // dropout decisions of step st into sDm[buf]: thread t draws keys k0 + 4(t%32) .. +3 for
-    // the 8 queries qs0 + 8(t/32) .. +7 and writes one byte (8 query bits) per key
-    auto draw_step = [&](int st, int buf) {
-        const int hh = st / nqs, qs0 = qstart + (st % nqs) * BQ;
-        const int kg = tid & 31, qset = tid >> 5;
-        const uint64_t row0 = (uint64_t)((b * f.H + hk * G + hh) * f.L + qs0 + 8 * qset);
-        const uint64_t dblocks = (uint64_t)((f.S + 3) / 4), blk = (uint64_t)(k0 / 4 + kg);
-        uint32_t bits[4] = {0u, 0u, 0u, 0u};
-#pragma unroll
-        for (int r = 0; r < 8; ++r) {
-            const GtWord4 x = gt_philox4x32_10((row0 + r) * dblocks + blk, f.drop.offset, f.drop.seed);
-#pragma unroll
-            for (int j = 0; j < 4; ++j) bits[j] |= (x.w[j] < f.drop.thresh ? 1u : 0u) << r;
-        }
-        uint8_t *dst = (uint8_t *)&sDm[buf][(qset >> 2) * BKV + 4 * kg];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) dst[4 * j + (qset & 3)] = (uint8_t)bits[j];
-    };
     auto store_step = [&](int buf) {
 #pragma unroll
         for (int i = 0; i < NLD; ++i) {
@@ -167,12 +159,12 @@ __global__ __launch_bounds__(256, D <= 64 && !DROP ? 2 : 1) void bwd_dkdv_kernel
             sL[buf][tid] = lreg * kLog2e;  // lse * log2(e)
             sD[buf][tid] = -dreg;          // -delta
         }
+        if constexpr (DROP) sDm[buf][tid] = mreg;  // [tid / 64][tid % 64]
     };
 
     if (nsteps > 0) {
         load_step(0);
         store_step(0);
-        if constexpr (DROP) draw_step(0, 0);
         if (nsteps > 1) load_step(1);
     }
     __syncthreads();
@@ -216,9 +208,18 @@ __global__ __launch_bounds__(256, D <= 64 && !DROP ? 2 : 1) void bwd_dkdv_kernel
             float p[16], ds[16];
             // every (query, key) of the block visible and no per-element mask: no tests
             const bool interior = (MASK == 0 || MASK == 4) && wk0 + 31 < S && q0 + 31 < L && (!CAUSAL || q0 >= wk0 + 31);
-            // dropout: multiplier of entry i (query 8(i/4) + 4half + i%4 of the block)
-            const uint32_t dbits = DROP ? sDm[buf][qb * BKV + 32 * w + lrow] : 0u;
-            auto mult = [&](int i) { return (dbits >> (8 * (i / 4) + 4 * half + (i % 4))) & 1u ? dscale : 0.0f; };
+            // dropout: multiplier of entry i (query 32qb + 8(i/4) + 4half + i%4 of the step, this
+            // lane's key 32w + lrow of the tile): bit lrow of word [w][query]
+            uint32_t dbits = 0u;  // bit i: entry i kept
+            if constexpr (DROP) {
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const u32x4 dw = *(const u32x4 *)&sDm[buf][w * BQ + 32 * qb + 8 * g + 4 * half];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) dbits |= ((dw[e] >> lrow) & 1u) << (4 * g + e);
+                }
+            }
+            auto mult = [&](int i) { return (dbits >> i) & 1u ? dscale : 0.0f; };
             if constexpr (DROP) {
 #pragma unroll
                 for (int g = 0; g < 4; ++g) {
@@ -283,7 +284,6 @@ __global__ __launch_bounds__(256, D <= 64 && !DROP ? 2 : 1) void bwd_dkdv_kernel
         }
         if (st + 1 < nsteps) {
             store_step(buf ^ 1);
-            if constexpr (DROP) draw_step(st + 1, buf ^ 1);
             if (st + 2 < nsteps) load_step(st + 2);
         }
         __syncthreads();
@@ -454,15 +454,23 @@ __global__ __launch_bounds__(256, D <= 64 && (MASK == 0 || MASK == 4) ? 2 : 1) v
                 // every (query, key) of the block visible and no per-element mask: no tests
                 const int kb0 = k0 + 32 * kb;
                 if constexpr (DROP) {
-                    // entries 4g .. 4g+3: keys kb0 + 8g + 4half + 0..3, one Philox block
+                    // entries 4g .. 4g+3: keys kb0 + 8g + 4half + 0..3, one Philox block; the
+                    // decisions also go out as bit 8g + 4half + e of the (row, 32 keys) word
+                    uint32_t bits = 0u;
 #pragma unroll
                     for (int g = 0; g < 4; ++g) {
                         const GtWord4 x = gt_philox4x32_10(drow + (uint64_t)((kb0 + 8 * g + 4 * half) >> 2),
                                                            f.drop.offset, f.drop.seed);
 #pragma unroll
-                        for (int e = 0; e < 4; ++e)
-                            dp[kb][4 * g + e] = fmaf(dp[kb][4 * g + e], x.w[e] < f.drop.thresh ? dscale : 0.0f, -dlt);
+                        for (int e = 0; e < 4; ++e) {
+                            const bool keep = x.w[e] < f.drop.thresh;
+                            bits |= (keep ? 1u : 0u) << (8 * g + 4 * half + e);
+                            dp[kb][4 * g + e] = fmaf(dp[kb][4 * g + e], keep ? dscale : 0.0f, -dlt);
+                        }
                     }
+                    const auto r = __builtin_amdgcn_permlane32_swap(bits, bits, false, false);
+                    if (half == 0 && lq < L && kb0 < S)
+                        a.dbits[(bh * f.L + lq) * ((f.S + 31) / 32) + kb0 / 32] = r[0] | r[1];
                 }
                 const bool interior =
                     (MASK == 0 || MASK == 4) && kb0 + 31 < S && wq0 + 31 < L && (!CAUSAL || wq0 >= kb0 + 31);

@@ -67,6 +67,9 @@ struct AttnBwdArgs {
     void *dk;              // (B,Hkv,S,D) dense
     void *dv;              // (B,Hkv,S,Dv) dense
     void *delta;           // (B,H,L) scratch: rowsum(P * dP)
+    // dropout, MFMA kernels: (B,H,L, ceil(S/32)) words, bit j of word [row][w] = decision of key
+    // 32w + j; written by the dQ kernel (which draws them), read by the dK/dV kernel
+    uint32_t *dbits;
 };
 
 // Query heads per decode workgroup: a kv head's gtot query heads (GQA / MQA) run in groups of

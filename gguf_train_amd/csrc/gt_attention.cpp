@@ -546,9 +546,14 @@ int attention_backward(const char *who, const gt_tensor *grad_out, const gt_tens
         a.f.o = const_cast<void *>(gt_data(out_s));
         a.o_f32 = od == GT_F32 && cd != GT_F32;
         apply_dropout(a.f, drop);
-        if (attn_bwd_mfma_supported(a, cd))
-            ok = gt_hip_check(launch_attn_bwd_mfma(a, cd, gt_stream()), "flash_attention_backward kernel");
-        else
+        gt_scratch bits;  // dropout on the MFMA kernels: the dQ kernel's decisions for dK/dV, 1 bit each
+        if (attn_bwd_mfma_supported(a, cd)) {
+            if (a.f.dropout) {
+                ok = gt_scratch_alloc(bits, (size_t)(B * H * L) * (size_t)((S + 31) / 32) * sizeof(uint32_t), dev);
+                a.dbits = (uint32_t *)bits.ptr();
+            }
+            ok = ok && gt_hip_check(launch_attn_bwd_mfma(a, cd, gt_stream()), "flash_attention_backward kernel");
+        } else
             ok = gt_hip_check(launch_attn_generic_bwd(a, cd, gt_stream()), "flash_attention_backward kernel");
     }
     if (ok) {
