@@ -68,6 +68,9 @@ CASES = [
     (torch.float64, 1, 3, 1, 33, 47, 40, False, "add", (), 0.6),
     (torch.float16, 1, 2, 2, 40, 41, 40, True, "bool", (), 0.4),
     (torch.bfloat16, 1, 2, 2, 64, 64, 64, True, None, (), 1.0),
+    (torch.float32, 1, 2, 1, 20, 30, 300, True, None, (), 0.3),        # generic kernels without LDS staging
+    (torch.float16, 1, 2, 2, 50, 61, 256, False, "bool", (), 0.5),     # generic, LDS-staged, 4 blocks of 64 dims
+    (torch.bfloat16, 2, 4, 4, 96, 130, 128, True, "pad", (130, 67), 0.05),
 ]
 
 
