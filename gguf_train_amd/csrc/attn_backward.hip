@@ -242,6 +242,14 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void bwd_dkdv_kernel(AttnBwdA
                     }
                 }
             } else {
+                // query q0 + 4half + c (c = 8(i/4) + i%4) sees this lane's key when lo <= c <= lo + span
+                // (key < S, q < L, causal q >= key), as one unsigned compare per score
+                int lo = (CAUSAL ? key : 0) - (q0 + 4 * half);
+                int span = (L - 1 - (q0 + 4 * half)) - lo;
+                if (key >= S || span < 0) {
+                    lo = 32;  // no c in 0..27 passes
+                    span = 0;
+                }
 #pragma unroll
                 for (int g = 0; g < 4; ++g) {
                     const int qi = 32 * qb + 8 * g + 4 * half;  // 4 consecutive queries
@@ -250,7 +258,7 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void bwd_dkdv_kernel(AttnBwdA
                     for (int e = 0; e < 4; ++e) {
                         const int i = 4 * g + e, q = qs0 + qi + e;
                         float add = 0.0f;  // MASK 4: already in s
-                        bool ok = key < S && q < L && (!CAUSAL || key <= q);
+                        bool ok = (uint32_t)(8 * g + e - lo) <= (uint32_t)span;
                         if (MASK == 1 || MASK == 2)
                             ok = ok && mask_at<MASK>(f, b, h, min(q, L - 1), min(key, S - 1), inv_scale, add);
                         const float pv = ok ? fast_exp2(fmaf(s[i] + add, c, -l4[e])) : 0.0f;
@@ -478,11 +486,13 @@ __global__ __launch_bounds__(256, D <= 64 && (MASK == 0 || MASK == 4) ? 2 : 1) v
 #pragma unroll
                     for (int i = 0; i < 16; ++i) ds[i] = fast_exp2(fmaf(s[kb][i], c, -lse2)) * dp[kb][i];
                 } else {
+                    // key kb0 + 4half + c (c = 8(i/4) + i%4) is visible to this lane's row when c <= vis
+                    const int vis = (lq < L ? (CAUSAL ? min(lq, S - 1) : S - 1) : -1) - (kb0 + 4 * half);
 #pragma unroll
                     for (int i = 0; i < 16; ++i) {
                         const int kk = kb0 + 8 * (i / 4) + 4 * half + (i % 4);
                         float add = 0.0f;  // MASK 4: already in s
-                        bool ok = kk < S && lq < L && (!CAUSAL || kk <= lq);
+                        bool ok = 8 * (i / 4) + (i % 4) <= vis;
                         if (MASK == 1 || MASK == 2)
                             ok = ok && mask_at<MASK>(f, b, h, lqc, min(kk, S - 1), inv_scale, add);
                         const float pv = ok ? fast_exp2(fmaf(s[kb][i] + add, c, -lse2)) : 0.0f;

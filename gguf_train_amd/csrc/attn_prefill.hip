@@ -370,6 +370,9 @@ __global__ __launch_bounds__(64 * nw_of<D>(), DROP && (MASK == 1 || MASK == 2) ?
             // ---- masks: s[kb][i] is (key = k0 + 32kb + 8(i/4) + 4half + i%4, query = lq) ----
             const bool edge = k0 + BN > nkv || (CAUSAL && k0 + BN - 1 > wq0 + qpos);
             if ((MASK != 0 && !MROW) || edge) {
+                // key k0 + 4half + c (c = 32kb + 8(i/4) + i%4, a constant per entry) is visible
+                // to this lane's row when c <= vis: one compare per score
+                const int vis = min(nkv - 1, CAUSAL ? lq + qpos : nkv - 1) - (k0 + 4 * half);
 #pragma unroll
                 for (int kb = 0; kb < NKB; ++kb) {
 #pragma unroll
@@ -387,7 +390,7 @@ __global__ __launch_bounds__(64 * nw_of<D>(), DROP && (MASK == 1 || MASK == 2) ?
                                 x = fmaf(((const float *)a.mask)[mi], inv_scale, x);
                             }
                         }
-                        const bool blocked = key >= nkv || (CAUSAL && key > lq + qpos);
+                        const bool blocked = 32 * kb + 8 * (i / 4) + (i % 4) > vis;
                         s[kb][i] = blocked ? -INFINITY : x;
                     }
                 }
