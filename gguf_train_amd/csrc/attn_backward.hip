@@ -22,7 +22,9 @@
 // element's multiplier (gt_philox.h).  dQ draws its lanes' Philox blocks directly (4 consecutive
 // keys of one query per block, as the forward) and writes the decisions as bits, one word per
 // (query row, 32 keys); dK/dV, whose lanes hold 16 queries of one key, streams those words in
-// with each query step (64 rows x 4 words through LDS) instead of drawing again.
+// with each query step (64 rows x 4 words through LDS) instead of drawing again.  Without that
+// buffer (a.dbits null: the caller bounds its size) each dK/dV thread draws its word itself, 8
+// Philox blocks per step.
 
 #include "attn_common.h"
 #include "gt_internal.h"
@@ -132,7 +134,20 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void bwd_dkdv_kernel(AttnBwdA
             // thread t: row t % 64 of the step, key word t / 64 of the tile (words past the
             // sequence's keys repeat the last one: their keys have P = 0)
             const int r = tid % BQ, wd = min((int)(k0 / 32 + tid / BQ), (int)dwords - 1);
-            mreg = a.dbits[((b * f.H + h) * f.L + min(qs0 + r, L - 1)) * dwords + wd];
+            const int64_t row = (b * f.H + h) * f.L + min(qs0 + r, L - 1);
+            if (a.dbits) {
+                mreg = a.dbits[row * dwords + wd];
+            } else {
+                const uint64_t n0 = (uint64_t)row * (uint64_t)((f.S + 3) / 4) + (uint64_t)(8 * wd);
+                uint32_t word = 0u;
+#pragma unroll 2
+                for (int u = 0; u < 8; ++u) {
+                    const GtWord4 x = gt_philox4x32_10(n0 + u, f.drop.offset, f.drop.seed);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) word |= (x.w[e] < f.drop.thresh ? 1u : 0u) << (4 * u + e);
+                }
+                mreg = word;
+            }
         }
 #pragma unroll
         for (int i = 0; i < NLD; ++i) {
@@ -477,7 +492,7 @@ __global__ __launch_bounds__(256, D <= 64 && (MASK == 0 || MASK == 4) ? 2 : 1) v
                         }
                     }
                     const auto r = __builtin_amdgcn_permlane32_swap(bits, bits, false, false);
-                    if (half == 0 && lq < L && kb0 < S)
+                    if (a.dbits && half == 0 && lq < L && kb0 < S)
                         a.dbits[(bh * f.L + lq) * ((f.S + 31) / 32) + kb0 / 32] = r[0] | r[1];
                 }
                 const bool interior =

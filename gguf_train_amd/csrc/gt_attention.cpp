@@ -10,6 +10,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
 #include <mutex>
 #include <string>
 #include <vector>
@@ -266,6 +267,14 @@ bool make_dropout(const char *who, double p, uint64_t seed, uint64_t offset, Dro
     out.d.thresh = t >= 4294967295.0 ? 4294967295u : (uint32_t)t;
     out.d.scale = p < 1.0 ? 1.0 / (1.0 - p) : 0.0;
     return true;
+}
+
+// Largest buffer of dropout decision bits the backward allocates (B*H*L*ceil(S/32)*4 bytes):
+// 512 MiB, or GT_ATTN_DROPOUT_BITS_MAX bytes when set; beyond it the dK/dV kernel draws the
+// decisions itself (bounded memory, more Philox work).
+size_t dropout_bits_max() {
+    const char *v = std::getenv("GT_ATTN_DROPOUT_BITS_MAX");
+    return v && *v ? (size_t)std::strtoull(v, nullptr, 10) : ((size_t)512 << 20);
 }
 
 void apply_dropout(AttnFwdArgs &a, const Dropout *drop) {
@@ -548,8 +557,9 @@ int attention_backward(const char *who, const gt_tensor *grad_out, const gt_tens
         apply_dropout(a.f, drop);
         gt_scratch bits;  // dropout on the MFMA kernels: the dQ kernel's decisions for dK/dV, 1 bit each
         if (attn_bwd_mfma_supported(a, cd)) {
-            if (a.f.dropout) {
-                ok = gt_scratch_alloc(bits, (size_t)(B * H * L) * (size_t)((S + 31) / 32) * sizeof(uint32_t), dev);
+            const size_t nbits = (size_t)(B * H * L) * (size_t)((S + 31) / 32) * sizeof(uint32_t);
+            if (a.f.dropout && nbits <= dropout_bits_max()) {
+                ok = gt_scratch_alloc(bits, nbits, dev);
                 a.dbits = (uint32_t *)bits.ptr();
             }
             ok = ok && gt_hip_check(launch_attn_bwd_mfma(a, cd, gt_stream()), "flash_attention_backward kernel");

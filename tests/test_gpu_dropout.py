@@ -109,6 +109,21 @@ def test_forward_and_backward_match_the_oracle(dev, dtype, B, H, Hkv, L, S, D, c
         assert not out.any() and not dq.any() and not dk.any() and not dv.any()
 
 
+@pytest.mark.parametrize("dtype,D,S", [(torch.bfloat16, 64, 300), (torch.float16, 128, 257)])
+def test_backward_without_the_decision_buffer_gives_the_same_bits(dev, monkeypatch, dtype, D, S):
+    # past GT_ATTN_DROPOUT_BITS_MAX bytes the dK/dV kernel draws the decisions itself
+    B, H, L, p, seed = 2, 4, 200, 0.2, 31
+    q, k, v, dout = (randn(shape, i, dtype).to(dev) for i, shape in
+                     enumerate([(B, H, L, D), (B, 2, S, D), (B, 2, S, D), (B, H, L, D)]))
+    mask = _mask("pad", B, H, L, S, (S, S - 77), 1).to(dev)
+    out, lse, out32 = g.flash_attention_dropout(q, k, v, mask, 0.0, True, p, seed)
+    with_buffer = g.flash_attention_dropout_backward(dout, q, k, v, mask, out32, lse, 0.0, True, p, seed)
+    monkeypatch.setenv("GT_ATTN_DROPOUT_BITS_MAX", "0")
+    drawn = g.flash_attention_dropout_backward(dout, q, k, v, mask, out32, lse, 0.0, True, p, seed)
+    for a, b in zip(with_buffer, drawn):
+        assert torch.equal(a, b)
+
+
 def test_same_seed_same_bits_other_offset_other_mask(dev):
     q, k, v = (randn((2, 4, 128, 64), i, torch.bfloat16).to(dev) for i in range(3))
     a = g.flash_attention_dropout(q, k, v, None, 0.0, True, 0.2, 77, 0)[0]
