@@ -160,11 +160,13 @@ __device__ inline int key_tiles(int qt, int nkv, int qpos) {
 }
 
 // MASK: 0 = none, 1 = bool bytes, 2 = additive float, 4 = additive float that does not depend
-// on the query row (key padding: the tile's mask row travels to LDS with the K/V tile).
+// on the query row (key padding: the tile's mask row travels to LDS with the K/V tile),
+// 5 / 6 = bool / float with contiguous keys and 4-key aligned rows: a lane's 4 consecutive keys
+// in one 4- / 16-byte load, issued with the tile's DMA so that they land during S = K.Q^T.
 // (dropout with a per-element mask: one workgroup per CU is the guaranteed minimum, so that the
 // Philox state does not spill)
 template <typename T, int D, bool CAUSAL, int MASK, bool ROPE = false, bool DROP = false>
-__global__ __launch_bounds__(64 * nw_of<D>(), DROP && (MASK == 1 || MASK == 2) ? 1 : 8 / nw_of<D>()) void prefill_fwd_kernel(
+__global__ __launch_bounds__(64 * nw_of<D>(), DROP && (MASK == 1 || MASK == 2 || MASK >= 5) ? 1 : 8 / nw_of<D>()) void prefill_fwd_kernel(
     AttnFwdArgs a, int nq, int npairs) {
     constexpr int NW = nw_of<D>(), BM = bm_of<D>(), NST = nst_of<D>(), BN = bn_of<D>();
     constexpr int NKB = BN / 32;  // 32-key blocks per tile
@@ -176,6 +178,8 @@ __global__ __launch_bounds__(64 * nw_of<D>(), DROP && (MASK == 1 || MASK == 2) ?
     constexpr int TILE = BN * D;           // elements per tile
     constexpr int NPW = BN * CH / 64 / NW; // 1 KB wave loads per operand, wave and tile
     constexpr bool MROW = MASK == 4;
+    constexpr bool MVEC = MASK >= 5;                     // per-element mask, 4 keys per load
+    constexpr bool MBOOL = MASK == 1 || MASK == 5;
     constexpr int PER = 2 * NPW + (MROW ? BN / 64 : 0);  // loads per wave and tile (K, V, mask row)
     static_assert(NPW >= 1 && PER * (NST - 2) < 64, "tile split");
     static_assert(BN % 64 == 0, "mask row: one key per lane and load");
@@ -326,6 +330,8 @@ __global__ __launch_bounds__(64 * nw_of<D>(), DROP && (MASK == 1 || MASK == 2) ?
         float lsum = 0.0f;    // this lane's share of the running sum
         // dropout: Philox block of keys 0..3 of this lane's row (rows past L draw unused words)
         const uint64_t drow = DROP ? (uint64_t)(bh * a.L + lq) * dblocks : 0;
+        // MVEC: element offset of this lane's mask row
+        const int64_t mrb = MVEC ? b * a.m_sb + h * a.m_sh + (int64_t)min(lq, L - 1) * a.m_sl : 0;
 
         for (int j = 0; j < ntiles; ++j, ++step) {
             const int k0 = j * BN;
@@ -340,6 +346,20 @@ __global__ __launch_bounds__(64 * nw_of<D>(), DROP && (MASK == 1 || MASK == 2) ?
             if (step + NST - 1 < total) issue(step + NST - 1);
             const T *cK = sK[step % NST];
             const T *cV = sV[step % NST];
+            // MVEC: keys k0 + 32kb + 8g + 4half + 0..3 of this lane's row (starts past the last
+            // 4 keys read those: their scores are blocked below)
+            f32x4 mvf[MVEC && !MBOOL ? NKB : 1][4];
+            uint32_t mvb[MVEC && MBOOL ? NKB : 1][4];
+            if constexpr (MVEC) {
+#pragma unroll
+                for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+                    for (int g = 0; g < 4; ++g) {
+                        const int64_t at = mrb + min(k0 + 32 * kb + 8 * g + 4 * half, S - 4);
+                        if constexpr (MBOOL) mvb[kb][g] = *(const uint32_t *)((const uint8_t *)a.mask + at);
+                        else mvf[kb][g] = *(const f32x4 *)((const float *)a.mask + at);
+                    }
+            }
 
             // (causal) a wavefront whose rows all precede this tile still runs it: every score
             // is masked to -inf and p = 0; skipping it makes the compiler copy O on every tile
@@ -381,6 +401,9 @@ __global__ __launch_bounds__(64 * nw_of<D>(), DROP && (MASK == 1 || MASK == 2) ?
                         float x = s[kb][i];
                         if constexpr (MROW) {
                             // the mask row is already in s
+                        } else if constexpr (MVEC) {
+                            if constexpr (MBOOL) x = (mvb[kb][i / 4] >> (8 * (i % 4))) & 0xffu ? x : -INFINITY;
+                            else x = fmaf(mvf[kb][i / 4][i % 4], inv_scale, x);
                         } else if (MASK != 0) {
                             const int64_t mi = b * a.m_sb + h * a.m_sh + (int64_t)min(lq, L - 1) * a.m_sl +
                                                (int64_t)min(key, S - 1) * a.m_ss;
@@ -502,9 +525,20 @@ __global__ __launch_bounds__(64 * nw_of<D>(), DROP && (MASK == 1 || MASK == 2) ?
     }
 }
 
+// Mask mode of a forward (MASK above): per-element masks whose keys are contiguous, with rows and
+// broadcast strides of whole 4-key groups and an aligned base, take the 4-key loads.
+inline int mask_mode(const AttnFwdArgs &a) {
+    if (!a.mask) return 0;
+    if (!a.mask_bool && a.m_sl == 0) return 4;
+    const bool vec = a.m_ss == 1 && a.S >= 4 && a.S % 4 == 0 && a.m_sb % 4 == 0 && a.m_sh % 4 == 0 &&
+                     a.m_sl % 4 == 0 && (uintptr_t)a.mask % (a.mask_bool ? 4 : 16) == 0;
+    if (a.mask_bool) return vec ? 5 : 1;
+    return vec ? 6 : 2;
+}
+
 template <typename T, int D>
 hipError_t launch_variant(const AttnFwdArgs &a, int nq, int npairs, int64_t grid, hipStream_t s) {
-    const int mode = !a.mask ? 0 : (a.mask_bool ? 1 : (a.m_sl == 0 ? 4 : 2));
+    const int mode = mask_mode(a);
 #define GT_PREFILL_LAUNCH(C, MK) \
     hipLaunchKernelGGL((prefill_fwd_kernel<T, D, C, MK>), dim3((unsigned)grid), dim3(64 * nw_of<D>()), 0, s, a, nq, npairs)
 #define GT_PREFILL_LAUNCH_R(C, MK) \
@@ -517,11 +551,15 @@ hipError_t launch_variant(const AttnFwdArgs &a, int nq, int npairs, int64_t grid
             if (mode == 0) GT_PREFILL_LAUNCH_D(true, 0);
             else if (mode == 1) GT_PREFILL_LAUNCH_D(true, 1);
             else if (mode == 4) GT_PREFILL_LAUNCH_D(true, 4);
+            else if (mode == 5) GT_PREFILL_LAUNCH_D(true, 5);
+            else if (mode == 6) GT_PREFILL_LAUNCH_D(true, 6);
             else GT_PREFILL_LAUNCH_D(true, 2);
         } else {
             if (mode == 0) GT_PREFILL_LAUNCH_D(false, 0);
             else if (mode == 1) GT_PREFILL_LAUNCH_D(false, 1);
             else if (mode == 4) GT_PREFILL_LAUNCH_D(false, 4);
+            else if (mode == 5) GT_PREFILL_LAUNCH_D(false, 5);
+            else if (mode == 6) GT_PREFILL_LAUNCH_D(false, 6);
             else GT_PREFILL_LAUNCH_D(false, 2);
         }
     } else if (a.rope_q) {
@@ -538,11 +576,15 @@ hipError_t launch_variant(const AttnFwdArgs &a, int nq, int npairs, int64_t grid
         if (mode == 0) GT_PREFILL_LAUNCH(true, 0);
         else if (mode == 1) GT_PREFILL_LAUNCH(true, 1);
         else if (mode == 4) GT_PREFILL_LAUNCH(true, 4);
+        else if (mode == 5) GT_PREFILL_LAUNCH(true, 5);
+        else if (mode == 6) GT_PREFILL_LAUNCH(true, 6);
         else GT_PREFILL_LAUNCH(true, 2);
     } else {
         if (mode == 0) GT_PREFILL_LAUNCH(false, 0);
         else if (mode == 1) GT_PREFILL_LAUNCH(false, 1);
         else if (mode == 4) GT_PREFILL_LAUNCH(false, 4);
+        else if (mode == 5) GT_PREFILL_LAUNCH(false, 5);
+        else if (mode == 6) GT_PREFILL_LAUNCH(false, 6);
         else GT_PREFILL_LAUNCH(false, 2);
     }
 #undef GT_PREFILL_LAUNCH

@@ -29,9 +29,11 @@ def test_prefill_ragged(dev, dtype, D, L, S, causal):
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
-@pytest.mark.parametrize("mshape", [(2, 4, 150, 150), (2, 1, 1, 150), (150, 150), (1, 4, 150, 1), (2, 1, 150, 150)])
+@pytest.mark.parametrize("mshape", [(2, 4, 150, 150), (2, 1, 1, 150), (150, 150), (1, 4, 150, 1), (2, 1, 150, 150),
+                                    (2, 4, 160, 160), (160, 160), (2, 1, 1, 160), (1, 4, 160, 160)])
 def test_prefill_masks(dev, dtype, mshape):
-    B, H, L, D = 2, 4, 150, 64
+    # 150 keys: per-element mask loads; 160 (whole 4-key groups, contiguous): 4-key loads
+    B, H, L, D = 2, 4, mshape[-2] if mshape[-2] > 1 else mshape[-1], 64
     q, k, v = randn((B, H, L, D), 1, dtype), randn((B, H, L, D), 2, dtype), randn((B, H, L, D), 3, dtype)
     rng = np.random.default_rng(4)
     allowed = torch.from_numpy(rng.random(mshape) < 0.7)
@@ -44,6 +46,29 @@ def test_prefill_masks(dev, dtype, mshape):
     bias = randn(mshape, 5)
     assert_close(g.flash_attention(q.to(dev), k.to(dev), v.to(dev), bias.to(dev), 0.0, True),
                  oracle_forward(q, k, v, mask=bias, is_causal=True), dtype, f"bias {mshape}")
+
+
+@pytest.mark.parametrize("dtype,D", [(torch.float16, 128), (torch.bfloat16, 64)])
+@pytest.mark.parametrize("kind", ["bool", "float"])
+def test_mask_loads_of_every_layout_give_the_same_bits(dev, dtype, D, kind):
+    # a contiguous (L, S) mask takes 4-key loads; the same values as a view with a key stride of
+    # 2, or at a base that is not 16-byte aligned, take per-element loads: identical outputs
+    B, H, L, S = 2, 4, 192, 256
+    q, k, v = randn((B, H, L, D), 7, dtype), randn((B, H, S, D), 8, dtype), randn((B, H, S, D), 9, dtype)
+    rng = np.random.default_rng(11)
+    vals = rng.random((L, S)) < 0.8 if kind == "bool" else rng.standard_normal((L, S)).astype(np.float32)
+    m = torch.from_numpy(vals).to(dev)
+    wide = torch.zeros((L, 2 * S), dtype=m.dtype, device=dev)
+    wide[:, ::2] = m
+    shifted = torch.zeros(L * S + 1, dtype=m.dtype, device=dev)
+    shifted[1:] = m.reshape(-1)
+    qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
+    for causal in (False, True):
+        ref = g.flash_attention(qd, kd, vd, m, 0.0, causal)
+        for other in (wide[:, ::2], shifted[1:].view(L, S)):
+            assert torch.equal(g.flash_attention(qd, kd, vd, other, 0.0, causal), ref)
+        want = oracle_forward(q, k, v, mask=m.cpu().reshape(1, 1, L, S), is_causal=causal)
+        assert_close(ref, want, dtype, f"{kind} causal={causal}")
 
 
 def test_prefill_key_padding_training_shape(dev):
