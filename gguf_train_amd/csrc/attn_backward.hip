@@ -41,19 +41,6 @@ constexpr int BQ = 64;    // query rows per dK/dV step
 constexpr int BMQ = 128;  // query rows per dQ workgroup (32 per wavefront)
 constexpr int BNK = 64;   // key rows per dQ step
 
-// Mask value for (b, h, query, key) under the compile-time mask mode: returns false when the
-// position is blocked; `add` receives an additive term in raw-score units.
-template <int MASK>
-__device__ inline bool mask_at(const AttnFwdArgs &f, int64_t b, int64_t h, int q, int key, float inv_scale,
-                               float &add) {
-    add = 0.0f;
-    if (MASK == 0) return true;
-    const int64_t mi = b * f.m_sb + h * f.m_sh + (int64_t)q * f.m_sl + (int64_t)key * f.m_ss;
-    if (MASK == 1) return ((const uint8_t *)f.mask)[mi] != 0;
-    add = ((const float *)f.mask)[mi] * inv_scale;
-    return true;
-}
-
 // ---- dK, dV ----------------------------------------------------------------------------------
 
 // D = 64 fits two wavefronts per SIMD without spills (with one, the compiler parks values in
@@ -258,7 +245,12 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void bwd_dkdv_kernel(AttnBwdA
                 }
             } else {
                 // query q0 + 4half + c (c = 8(i/4) + i%4) sees this lane's key when lo <= c <= lo + span
-                // (key < S, q < L, causal q >= key), as one unsigned compare per score
+                // (key < S, q < L, causal q >= key), as one unsigned compare per score; a
+                // per-element mask is read only there, at this lane's offset plus c rows
+                const int64_t mlane = (MASK == 1 || MASK == 2)
+                                          ? b * f.m_sb + h * f.m_sh + (int64_t)min(key, S - 1) * f.m_ss +
+                                                (int64_t)(q0 + 4 * half) * f.m_sl
+                                          : 0;
                 int lo = (CAUSAL ? key : 0) - (q0 + 4 * half);
                 int span = (L - 1 - (q0 + 4 * half)) - lo;
                 if (key >= S || span < 0) {
@@ -271,11 +263,16 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void bwd_dkdv_kernel(AttnBwdA
                     const f32x4 l4 = *(const f32x4 *)&sL[buf][qi];
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
-                        const int i = 4 * g + e, q = qs0 + qi + e;
+                        const int i = 4 * g + e;
                         float add = 0.0f;  // MASK 4: already in s
                         bool ok = (uint32_t)(8 * g + e - lo) <= (uint32_t)span;
-                        if (MASK == 1 || MASK == 2)
-                            ok = ok && mask_at<MASK>(f, b, h, min(q, L - 1), min(key, S - 1), inv_scale, add);
+                        if (MASK == 1 || MASK == 2) {
+                            if (ok) {
+                                const int64_t mi = mlane + (int64_t)(8 * g + e) * f.m_sl;
+                                if (MASK == 1) ok = ((const uint8_t *)f.mask)[mi] != 0;
+                                else add = ((const float *)f.mask)[mi] * inv_scale;
+                            }
+                        }
                         const float pv = ok ? fast_exp2(fmaf(s[i] + add, c, -l4[e])) : 0.0f;
                         p[i] = DROP ? pv * mult(i) : pv;
                         ds[i] = pv * dp[i];
@@ -331,6 +328,8 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void bwd_dkdv_kernel(AttnBwdA
 // ---- dQ --------------------------------------------------------------------------------------
 
 // (two per SIMD for D = 64 as in dK/dV, except with a per-element mask, which would spill)
+// MASK 5 / 6: bool / float per-element mask with contiguous keys and 4-key aligned rows, read
+// as a lane's 4 consecutive keys per load at the start of the tile (as the forward).
 template <typename T, int D, bool CAUSAL, int MASK, bool DROP = false>
 __global__ __launch_bounds__(256, D <= 64 && (MASK == 0 || MASK == 4) ? 2 : 1) void bwd_dq_kernel(AttnBwdArgs a, int nq) {
     using M = Mfma<T>;
@@ -449,6 +448,22 @@ __global__ __launch_bounds__(256, D <= 64 && (MASK == 0 || MASK == 4) ? 2 : 1) v
         const T *cK = sK[buf];
         const T *cV = sV[buf];
         if (!CAUSAL || k0 <= wq0 + 31) {
+            // MASK 5 / 6: keys k0 + 32kb + 8g + 4half + 0..3 of this lane's row (starts past
+            // the last 4 keys read those: their scores are blocked)
+            constexpr bool MVEC = MASK >= 5;
+            f32x4 mvf[MASK == 6 ? 2 : 1][4];
+            uint32_t mvb[MASK == 5 ? 2 : 1][4];
+            if constexpr (MVEC) {
+                const int64_t mrb = b * f.m_sb + h * f.m_sh + (int64_t)lqc * f.m_sl;
+#pragma unroll
+                for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                    for (int g = 0; g < 4; ++g) {
+                        const int64_t at = mrb + min(k0 + 32 * kb + 8 * g + 4 * half, S - 4);
+                        if constexpr (MASK == 5) mvb[kb][g] = *(const uint32_t *)((const uint8_t *)f.mask + at);
+                        else mvf[kb][g] = *(const f32x4 *)((const float *)f.mask + at);
+                    }
+            }
             // s[kb][i]: key k0 + 32kb + 8(i/4) + 4half + i%4, query lq.  S accumulates onto the
             // tile's mask row (MASK 4: the keys' additive terms), dP onto -delta.
             f32x16 s[2], dp[2];
@@ -503,13 +518,25 @@ __global__ __launch_bounds__(256, D <= 64 && (MASK == 0 || MASK == 4) ? 2 : 1) v
                 } else {
                     // key kb0 + 4half + c (c = 8(i/4) + i%4) is visible to this lane's row when c <= vis
                     const int vis = (lq < L ? (CAUSAL ? min(lq, S - 1) : S - 1) : -1) - (kb0 + 4 * half);
+                    const int64_t mlane = (MASK == 1 || MASK == 2)
+                                              ? b * f.m_sb + h * f.m_sh + (int64_t)lqc * f.m_sl +
+                                                    (int64_t)(kb0 + 4 * half) * f.m_ss
+                                              : 0;
 #pragma unroll
                     for (int i = 0; i < 16; ++i) {
-                        const int kk = kb0 + 8 * (i / 4) + 4 * half + (i % 4);
                         float add = 0.0f;  // MASK 4: already in s
                         bool ok = 8 * (i / 4) + (i % 4) <= vis;
-                        if (MASK == 1 || MASK == 2)
-                            ok = ok && mask_at<MASK>(f, b, h, lqc, min(kk, S - 1), inv_scale, add);
+                        if (MASK == 1 || MASK == 2) {
+                            // read only where visible: this lane's offset plus c keys
+                            if (ok) {
+                                const int64_t mi = mlane + (int64_t)(8 * (i / 4) + (i % 4)) * f.m_ss;
+                                if (MASK == 1) ok = ((const uint8_t *)f.mask)[mi] != 0;
+                                else add = ((const float *)f.mask)[mi] * inv_scale;
+                            }
+                        } else if constexpr (MVEC) {
+                            if constexpr (MASK == 5) ok = ok && ((mvb[kb][i / 4] >> (8 * (i % 4))) & 0xffu) != 0;
+                            else add = mvf[kb][i / 4][i % 4] * inv_scale;
+                        }
                         const float pv = ok ? fast_exp2(fmaf(s[kb][i] + add, c, -lse2)) : 0.0f;
                         ds[i] = pv * dp[kb][i];
                     }
@@ -560,8 +587,11 @@ hipError_t launch_bwd_drop(const AttnBwdArgs &a, hipStream_t s) {
     hipLaunchKernelGGL((bwd_dq_kernel<T, D, CAUSAL, MASK, DROP>), dim3((unsigned)(nq * f.B * f.H)), dim3(256), 0, s, a, nq);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
+    // dK/dV reads a per-element mask one element per lane (its lanes hold one key each): modes
+    // 5 / 6 are 1 / 2 there
+    constexpr int MKV = MASK >= 5 ? MASK - 4 : MASK;
     const int nkt = (int)((f.S + BKV - 1) / BKV);
-    hipLaunchKernelGGL((bwd_dkdv_kernel<T, D, CAUSAL, MASK, DROP>), dim3((unsigned)(nkt * f.B * f.Hkv)), dim3(256), 0, s, a);
+    hipLaunchKernelGGL((bwd_dkdv_kernel<T, D, CAUSAL, MKV, DROP>), dim3((unsigned)(nkt * f.B * f.Hkv)), dim3(256), 0, s, a);
     return hipGetLastError();
 }
 
@@ -572,17 +602,22 @@ hipError_t launch_bwd_typed(const AttnBwdArgs &a, hipStream_t s) {
 
 template <typename T, int D>
 hipError_t launch_bwd_d(const AttnBwdArgs &a, hipStream_t s) {
-    // mode 4: a float mask that does not depend on the query row (key padding)
-    const int mode = !a.f.mask ? 0 : (a.f.mask_bool ? 1 : (a.f.m_sl == 0 ? 4 : 2));
+    // mode 4: a float mask that does not depend on the query row (key padding); 5 / 6: bool /
+    // float per-element masks with contiguous, 4-key aligned keys (attn_mask_mode)
+    const int mode = attn_mask_mode(a.f);
     if (a.f.causal) {
         if (mode == 0) return launch_bwd_typed<T, D, true, 0>(a, s);
         if (mode == 1) return launch_bwd_typed<T, D, true, 1>(a, s);
         if (mode == 4) return launch_bwd_typed<T, D, true, 4>(a, s);
+        if (mode == 5) return launch_bwd_typed<T, D, true, 5>(a, s);
+        if (mode == 6) return launch_bwd_typed<T, D, true, 6>(a, s);
         return launch_bwd_typed<T, D, true, 2>(a, s);
     }
     if (mode == 0) return launch_bwd_typed<T, D, false, 0>(a, s);
     if (mode == 1) return launch_bwd_typed<T, D, false, 1>(a, s);
     if (mode == 4) return launch_bwd_typed<T, D, false, 4>(a, s);
+    if (mode == 5) return launch_bwd_typed<T, D, false, 5>(a, s);
+    if (mode == 6) return launch_bwd_typed<T, D, false, 6>(a, s);
     return launch_bwd_typed<T, D, false, 2>(a, s);
 }
 

@@ -51,6 +51,19 @@ struct AttnFwdArgs {
     GtDropout drop;
 };
 
+// Mask mode of the MFMA kernels: 0 none; 1 bool bytes, 2 additive float (per element, any
+// strides); 4 additive float that does not depend on the query row (key padding); 5 / 6 bool /
+// float per element with contiguous keys, rows and broadcast strides of whole 4-key groups and
+// an aligned base (4-key loads).
+inline int attn_mask_mode(const AttnFwdArgs &a) {
+    if (!a.mask) return 0;
+    if (!a.mask_bool && a.m_sl == 0) return 4;
+    const bool vec = a.m_ss == 1 && a.S >= 4 && a.S % 4 == 0 && a.m_sb % 4 == 0 && a.m_sh % 4 == 0 &&
+                     a.m_sl % 4 == 0 && (uintptr_t)a.mask % (a.mask_bool ? 4 : 16) == 0;
+    if (a.mask_bool) return vec ? 5 : 1;
+    return vec ? 6 : 2;
+}
+
 __device__ inline int attn_kv_len(const AttnFwdArgs &a, int64_t b) { return a.kv_len ? a.kv_len[b] : (int)a.S; }
 __device__ inline int attn_q_pos(const AttnFwdArgs &a, int64_t b) { return a.q_pos ? a.q_pos[b] : 0; }
 // Keys [0, end) are visible to a single query row (L == 1) of batch b.

@@ -525,20 +525,9 @@ __global__ __launch_bounds__(64 * nw_of<D>(), DROP && (MASK == 1 || MASK == 2 ||
     }
 }
 
-// Mask mode of a forward (MASK above): per-element masks whose keys are contiguous, with rows and
-// broadcast strides of whole 4-key groups and an aligned base, take the 4-key loads.
-inline int mask_mode(const AttnFwdArgs &a) {
-    if (!a.mask) return 0;
-    if (!a.mask_bool && a.m_sl == 0) return 4;
-    const bool vec = a.m_ss == 1 && a.S >= 4 && a.S % 4 == 0 && a.m_sb % 4 == 0 && a.m_sh % 4 == 0 &&
-                     a.m_sl % 4 == 0 && (uintptr_t)a.mask % (a.mask_bool ? 4 : 16) == 0;
-    if (a.mask_bool) return vec ? 5 : 1;
-    return vec ? 6 : 2;
-}
-
 template <typename T, int D>
 hipError_t launch_variant(const AttnFwdArgs &a, int nq, int npairs, int64_t grid, hipStream_t s) {
-    const int mode = mask_mode(a);
+    const int mode = attn_mask_mode(a);
 #define GT_PREFILL_LAUNCH(C, MK) \
     hipLaunchKernelGGL((prefill_fwd_kernel<T, D, C, MK>), dim3((unsigned)grid), dim3(64 * nw_of<D>()), 0, s, a, nq, npairs)
 #define GT_PREFILL_LAUNCH_R(C, MK) \

@@ -47,6 +47,59 @@ def test_native_backward_matches_oracle(dev, dtype, B, H, Hkv, L, S, D, causal):
     assert_close(dv, wv, tol_dtype, "dv", out_dtype=torch.float32)
 
 
+def _full_mask(kind, shape, seed):
+    rng = np.random.default_rng(seed)
+    if kind == "bool":
+        m = torch.from_numpy(rng.random(shape) < 0.8)
+        m[..., 0] = True  # every row sees a key
+        return m
+    return torch.from_numpy((rng.standard_normal(shape) * 0.7).astype(np.float32))
+
+
+@pytest.mark.parametrize("dtype,D", [(torch.bfloat16, 64), (torch.float16, 128)])
+@pytest.mark.parametrize("kind", ["bool", "float"])
+@pytest.mark.parametrize("mshape", ["LS", "BHLS"])
+@pytest.mark.parametrize("L,S", [(160, 256), (150, 150)])
+@pytest.mark.parametrize("causal", [False, True])
+def test_mfma_backward_with_per_element_masks(dev, dtype, D, kind, mshape, L, S, causal):
+    # S % 4 == 0 with contiguous keys: the dQ kernel's 4-key mask loads; 150 keys: per element
+    B, H, Hkv = 2, 4, 2
+    seed = L + S + D
+    q, k, v = randn((B, H, L, D), seed, dtype), randn((B, Hkv, S, D), seed + 1, dtype), randn((B, Hkv, S, D), seed + 2, dtype)
+    dout = randn((B, H, L, D), seed + 3, dtype)
+    mask = _full_mask(kind, (L, S) if mshape == "LS" else (B, H, L, S), seed)
+    md = mask.to(dev)
+    out, lse, out32 = g.flash_attention_train(q.to(dev), k.to(dev), v.to(dev), md, 0.0, causal)
+    dq, dk, dv = g.flash_attention_backward(dout.to(dev), q.to(dev), k.to(dev), v.to(dev), md, out32, lse, 0.0, causal)
+    m4 = mask.reshape((1, 1) + tuple(mask.shape)) if mask.ndim == 2 else mask
+    wq, wk, wv = oracle_grads(dout, q, k, v, mask=m4, is_causal=causal)
+    for name, got, want in (("dq", dq, wq), ("dk", dk, wk), ("dv", dv, wv)):
+        assert_close(got, want, torch.bfloat16, f"{name} {kind} {mshape}", out_dtype=torch.float32)
+
+
+@pytest.mark.parametrize("kind", ["bool", "float"])
+def test_backward_mask_loads_of_every_layout_give_the_same_bits(dev, kind):
+    # the contiguous mask (4-key loads in dQ) and the same values strided by 2 or at an unaligned
+    # base (per-element loads) give identical gradients
+    B, H, L, S, D, dtype = 2, 4, 128, 192, 64, torch.bfloat16
+    q, k, v, dout = (randn(sh, i, dtype).to(dev) for i, sh in enumerate([(B, H, L, D), (B, H, S, D), (B, H, S, D),
+                                                                         (B, H, L, D)]))
+    m = _full_mask(kind, (L, S), 3).to(dev)
+    wide = torch.zeros((L, 2 * S), dtype=m.dtype, device=dev)
+    wide[:, ::2] = m
+    flat = torch.zeros(L * S + 1, dtype=m.dtype, device=dev)
+    flat[1:] = m.reshape(-1)
+
+    def grads(mask):
+        out, lse, out32 = g.flash_attention_train(q, k, v, mask, 0.0, True)
+        return g.flash_attention_backward(dout, q, k, v, mask, out32, lse, 0.0, True)
+
+    ref = grads(m)
+    for other in (wide[:, ::2], flat[1:].view(L, S)):
+        for a, b in zip(grads(other), ref):
+            assert torch.equal(a, b)
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
 @pytest.mark.parametrize("D,Dv", [(64, 96), (256, 256), (200, 160), (16, 8), (300, 40), (1, 1)])
 @pytest.mark.parametrize("causal", [False, True])
