@@ -191,6 +191,31 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void bwd_dkdv_kernel(AttnBwdA
         for (int qb = 0; qb < 2; ++qb) {
             const int q0 = qs0 + 32 * qb;
             if (CAUSAL && q0 + 31 < wk0) continue;  // every query of the block precedes our keys
+            // MASK 1 / 2: this lane's 16 mask values of the block (query q0 + 4half + c, c = 8(i/4) +
+            // i%4), loaded before the S and dP products so that they land during them; the loads
+            // are unconditional (no branch, no wait per element), an invisible element reading
+            // the lane's key in the last query row instead
+            constexpr bool MFULL = MASK == 1 || MASK == 2;
+            float madd[MASK == 2 ? 16 : 1];
+            uint32_t mbyte[MASK == 1 ? 16 : 1];
+            if constexpr (MFULL) {
+                const int64_t mkey = b * f.m_sb + h * f.m_sh + (int64_t)min(key, S - 1) * f.m_ss;
+                const int64_t mlane = mkey + (int64_t)(q0 + 4 * half) * f.m_sl;
+                const int64_t msafe = mkey + (int64_t)(L - 1) * f.m_sl;
+                int lo = (CAUSAL ? key : 0) - (q0 + 4 * half);
+                int span = (L - 1 - (q0 + 4 * half)) - lo;
+                if (key >= S || span < 0) {
+                    lo = 32;
+                    span = 0;
+                }
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    const int cq = 8 * (i / 4) + (i % 4);
+                    const int64_t mi = (uint32_t)(cq - lo) <= (uint32_t)span ? mlane + (int64_t)cq * f.m_sl : msafe;
+                    if constexpr (MASK == 2) madd[i] = ((const float *)f.mask)[mi];
+                    else mbyte[i] = ((const uint8_t *)f.mask)[mi];
+                }
+            }
             // s[i], dp[i]: query q0 + 8(i/4) + 4half + i%4, key `key`
             // (dropout: dP starts at 0, -delta is added after the multiplier)
             f32x16 s, dp;
@@ -247,10 +272,6 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void bwd_dkdv_kernel(AttnBwdA
                 // query q0 + 4half + c (c = 8(i/4) + i%4) sees this lane's key when lo <= c <= lo + span
                 // (key < S, q < L, causal q >= key), as one unsigned compare per score; a
                 // per-element mask is read only there, at this lane's offset plus c rows
-                const int64_t mlane = (MASK == 1 || MASK == 2)
-                                          ? b * f.m_sb + h * f.m_sh + (int64_t)min(key, S - 1) * f.m_ss +
-                                                (int64_t)(q0 + 4 * half) * f.m_sl
-                                          : 0;
                 int lo = (CAUSAL ? key : 0) - (q0 + 4 * half);
                 int span = (L - 1 - (q0 + 4 * half)) - lo;
                 if (key >= S || span < 0) {
@@ -266,13 +287,8 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void bwd_dkdv_kernel(AttnBwdA
                         const int i = 4 * g + e;
                         float add = 0.0f;  // MASK 4: already in s
                         bool ok = (uint32_t)(8 * g + e - lo) <= (uint32_t)span;
-                        if (MASK == 1 || MASK == 2) {
-                            if (ok) {
-                                const int64_t mi = mlane + (int64_t)(8 * g + e) * f.m_sl;
-                                if (MASK == 1) ok = ((const uint8_t *)f.mask)[mi] != 0;
-                                else add = ((const float *)f.mask)[mi] * inv_scale;
-                            }
-                        }
+                        if constexpr (MASK == 1) ok = ok && mbyte[i] != 0u;
+                        else if constexpr (MASK == 2) add = madd[i] * inv_scale;
                         const float pv = ok ? fast_exp2(fmaf(s[i] + add, c, -l4[e])) : 0.0f;
                         p[i] = DROP ? pv * mult(i) : pv;
                         ds[i] = pv * dp[i];
@@ -518,21 +534,20 @@ __global__ __launch_bounds__(256, D <= 64 && (MASK == 0 || MASK == 4) ? 2 : 1) v
                 } else {
                     // key kb0 + 4half + c (c = 8(i/4) + i%4) is visible to this lane's row when c <= vis
                     const int vis = (lq < L ? (CAUSAL ? min(lq, S - 1) : S - 1) : -1) - (kb0 + 4 * half);
-                    const int64_t mlane = (MASK == 1 || MASK == 2)
-                                              ? b * f.m_sb + h * f.m_sh + (int64_t)lqc * f.m_sl +
-                                                    (int64_t)(kb0 + 4 * half) * f.m_ss
-                                              : 0;
+                    // per-element mask: this lane's offset plus c keys where visible, else the
+                    // lane's row at the last key (unconditional loads: no branch per element)
+                    const int64_t mrow0 = b * f.m_sb + h * f.m_sh + (int64_t)lqc * f.m_sl;
+                    const int64_t mlane = mrow0 + (int64_t)(kb0 + 4 * half) * f.m_ss;
+                    const int64_t msafe = mrow0 + (int64_t)(S - 1) * f.m_ss;
 #pragma unroll
                     for (int i = 0; i < 16; ++i) {
                         float add = 0.0f;  // MASK 4: already in s
-                        bool ok = 8 * (i / 4) + (i % 4) <= vis;
-                        if (MASK == 1 || MASK == 2) {
-                            // read only where visible: this lane's offset plus c keys
-                            if (ok) {
-                                const int64_t mi = mlane + (int64_t)(8 * (i / 4) + (i % 4)) * f.m_ss;
-                                if (MASK == 1) ok = ((const uint8_t *)f.mask)[mi] != 0;
-                                else add = ((const float *)f.mask)[mi] * inv_scale;
-                            }
+                        const int ck = 8 * (i / 4) + (i % 4);
+                        bool ok = ck <= vis;
+                        if constexpr (MASK == 1 || MASK == 2) {
+                            const int64_t mi = ok ? mlane + (int64_t)ck * f.m_ss : msafe;
+                            if constexpr (MASK == 1) ok = ok && ((const uint8_t *)f.mask)[mi] != 0;
+                            else add = ((const float *)f.mask)[mi] * inv_scale;
                         } else if constexpr (MVEC) {
                             if constexpr (MASK == 5) ok = ok && ((mvb[kb][i / 4] >> (8 * (i % 4))) & 0xffu) != 0;
                             else add = mvf[kb][i / 4][i % 4] * inv_scale;
