@@ -284,6 +284,42 @@ void apply_dropout(AttnFwdArgs &a, const Dropout *drop) {
     }
 }
 
+// ---- head padding ----------------------------------------------------------------------------
+// The MFMA kernels take head sizes 64 and 128.  Float16/bfloat16 attention with another head size
+// up to 128 and more than one query row runs on them with q, k, v (and in the backward dO and the
+// output) zero-padded to 64 or 128 dims: the zero dims add nothing to Q.K^T (the scale stays that
+// of the real head size), padded V columns give output columns that are dropped, and the padded
+// columns of dQ, dK, dV are zero and dropped.  Single-query rows keep their kernels (padding would
+// copy the whole K/V).
+int64_t mfma_head(int64_t d) { return d <= 0 ? 0 : d <= 64 ? 64 : d <= 128 ? 128 : 0; }
+
+int64_t padded_head(int cd, int64_t L, int64_t D, int64_t Dv) {
+    if ((cd != GT_F16 && cd != GT_BF16) || L <= 1) return 0;
+    if (D == Dv && (D == 64 || D == 128)) return 0;
+    if (!mfma_head(D) || !mfma_head(Dv)) return 0;
+    return std::max(mfma_head(D), mfma_head(Dv));
+}
+
+// A dense (d0, d1, d2, Dp) copy of the 4-D device tensor t (innermost contiguous, 2- or 4-byte
+// elements) whose dims past t's last are zero; kept in tmp.
+const gt_tensor *pad_heads(const gt_tensor *t, int64_t Dp, int dev, Temps &tmp) {
+    const int64_t sh[4] = {t->shape[0], t->shape[1], t->shape[2], Dp};
+    gt_tensor *p = tmp.keep(gt_new_tensor(4, sh, t->dtype, GT_DEV_CUDA, dev));
+    if (!p || !gt_hip_check(gt_launch_pad_rows(gt_data(t), (int)gt_elem_bytes(t->dtype), t->strides, sh[0], sh[1],
+                                               sh[2], t->shape[3], gt_data(p), Dp, gt_stream()),
+                            "head padding kernel"))
+        return nullptr;
+    return p;
+}
+
+// The first t->shape[3] dims of every row of the dense padded buffer `src` into the dense t.
+bool unpad_heads(const gt_tensor *src, gt_tensor *t) {
+    const int64_t rows = t->shape[0] * t->shape[1] * t->shape[2];
+    return gt_hip_check(gt_launch_unpad_rows(gt_data(src), (int)gt_elem_bytes(t->dtype), rows, src->shape[3],
+                                             gt_data(t), t->shape[3], gt_stream()),
+                        "head padding kernel");
+}
+
 // RoPE of the queries fused into the prefill kernel: the (cos, sin) table of the L query rows.
 struct QRope {
     const void *table;  // float2 (L, D/2) on the device
@@ -347,6 +383,22 @@ int attention_forward(const char *who, const gt_tensor *q, const gt_tensor *k, c
             a.causal = is_causal ? 1 : 0;
             a.out_dtype = q->dtype;
             apply_dropout(a, drop);
+            // heads padded to the MFMA kernels' sizes (output and float32 output unpadded after)
+            const gt_tensor *po = nullptr, *po32 = nullptr;
+            const int64_t Dp = qrope || a.out_dtype != cd ? 0 : padded_head(cd, L, D, Dv);
+            if (Dp) {
+                const gt_tensor *qp = pad_heads(qs, Dp, dev, tmp), *kp = pad_heads(ks, Dp, dev, tmp);
+                const gt_tensor *vp = pad_heads(vs, Dp, dev, tmp);
+                const int64_t psh[4] = {B, H, L, Dp};
+                po = tmp.keep(gt_new_tensor(4, psh, q->dtype, GT_DEV_CUDA, dev));
+                po32 = o32 ? tmp.keep(gt_new_tensor(4, psh, GT_F32, GT_DEV_CUDA, dev)) : nullptr;
+                ok = qp && kp && vp && po && (!o32 || po32);
+                if (ok) {
+                    fill_qkv(a, qp, kp, vp);
+                    a.o = const_cast<void *>(gt_data(po));
+                    a.o32 = po32 ? const_cast<void *>(gt_data(po32)) : nullptr;
+                }
+            }
             if (qrope) {
                 a.rope_q = qrope->table;
                 a.rope_neox = qrope->neox;
@@ -359,6 +411,7 @@ int attention_forward(const char *who, const gt_tensor *q, const gt_tensor *k, c
                 }
             }
             ok = ok && dispatch_forward(a, cd, dev);
+            if (ok && po) ok = unpad_heads(po, o) && (!po32 || unpad_heads(po32, o32));
         }
     }
     if (!ok) {
@@ -505,7 +558,8 @@ int attention_backward(const char *who, const gt_tensor *grad_out, const gt_tens
     // into every dS, so that case recomputes the float32 output (the forward is deterministic:
     // it is the training forward's copy bit for bit).
     const gt_tensor *lse_s = nullptr, *out_s = nullptr;
-    const bool mfma_shape = (cd == GT_F16 || cd == GT_BF16) && D == Dv && (D == 64 || D == 128);
+    const int64_t Dp = padded_head(cd, L, D, Dv);  // heads padded for the MFMA kernels (0: none)
+    const bool mfma_shape = ((cd == GT_F16 || cd == GT_BF16) && D == Dv && (D == 64 || D == 128)) || Dp != 0;
     if (!lse || !out || (mfma_shape && out->dtype != GT_F32)) {
         gt_tensor *o2 = nullptr, *l2 = nullptr, *o32 = nullptr;
         if (attention_forward(who, q, k, v, mask, scale, is_causal, &o2, &l2, mfma_shape ? &o32 : nullptr, nullptr,
@@ -555,16 +609,38 @@ int attention_backward(const char *who, const gt_tensor *grad_out, const gt_tens
         a.f.o = const_cast<void *>(gt_data(out_s));
         a.o_f32 = od == GT_F32 && cd != GT_F32;
         apply_dropout(a.f, drop);
+        // heads padded to the MFMA kernels' sizes: padded inputs, padded gradients unpadded after
+        const gt_tensor *pq = nullptr, *pk = nullptr, *pv = nullptr;
+        if (Dp) {
+            const gt_tensor *qp = pad_heads(qs, Dp, dev, tmp), *kp = pad_heads(ks, Dp, dev, tmp);
+            const gt_tensor *vp = pad_heads(vs, Dp, dev, tmp), *gp = pad_heads(gos, Dp, dev, tmp);
+            const gt_tensor *op = pad_heads(out_s, Dp, dev, tmp);
+            const int64_t qsh2[4] = {B, H, L, Dp}, ksh2[4] = {B, Hkv, S, Dp};
+            pq = tmp.keep(gt_new_tensor(4, qsh2, gd, GT_DEV_CUDA, dev));
+            pk = tmp.keep(gt_new_tensor(4, ksh2, gd, GT_DEV_CUDA, dev));
+            pv = tmp.keep(gt_new_tensor(4, ksh2, gd, GT_DEV_CUDA, dev));
+            ok = qp && kp && vp && gp && op && pq && pk && pv;
+            if (ok) {
+                fill_qkv(a.f, qp, kp, vp);
+                a.dout = gt_data(gp);
+                a.f.o = const_cast<void *>(gt_data(op));
+                a.dq = const_cast<void *>(gt_data(pq));
+                a.dk = const_cast<void *>(gt_data(pk));
+                a.dv = const_cast<void *>(gt_data(pv));
+            }
+        }
         gt_scratch bits;  // dropout on the MFMA kernels: the dQ kernel's decisions for dK/dV, 1 bit each
-        if (attn_bwd_mfma_supported(a, cd)) {
+        if (ok && attn_bwd_mfma_supported(a, cd)) {
             const size_t nbits = (size_t)(B * H * L) * (size_t)((S + 31) / 32) * sizeof(uint32_t);
             if (a.f.dropout && nbits <= dropout_bits_max()) {
                 ok = gt_scratch_alloc(bits, nbits, dev);
                 a.dbits = (uint32_t *)bits.ptr();
             }
             ok = ok && gt_hip_check(launch_attn_bwd_mfma(a, cd, gt_stream()), "flash_attention_backward kernel");
-        } else
+        } else if (ok) {
             ok = gt_hip_check(launch_attn_generic_bwd(a, cd, gt_stream()), "flash_attention_backward kernel");
+        }
+        if (ok && Dp) ok = unpad_heads(pq, gq) && unpad_heads(pk, gk) && unpad_heads(pv, gv);
     }
     if (ok) {
         gq = deliver(gq, host_io);

@@ -269,6 +269,26 @@ __global__ void bool_to_bias_kernel(const uint8_t *__restrict__ src, float *__re
         dst[i] = src[i] ? 0.0f : -INFINITY;
 }
 
+// Rows of a 4-D tensor (rows (b, h, l) at b*sb + h*sh + l*sl, D contiguous elements of ES bytes)
+// into a dense (B*H*L, Dp) buffer, dims D .. Dp-1 set to zero; or back (unpad: the first D of
+// every Dp).  One thread per destination element.
+template <typename E>
+__global__ void pad_rows_kernel(const E *__restrict__ src, int64_t sb, int64_t sh, int64_t sl, int64_t H, int64_t L,
+                                int64_t D, E *__restrict__ dst, int64_t Dp, int64_t n) {
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+        const int64_t r = i / Dp, d = i % Dp;
+        const int64_t l = r % L, bh = r / L, h = bh % H, b = bh / H;
+        dst[i] = d < D ? src[b * sb + h * sh + l * sl + d] : E(0);
+    }
+}
+template <typename E>
+__global__ void unpad_rows_kernel(const E *__restrict__ src, int64_t Dp, E *__restrict__ dst, int64_t D, int64_t n) {
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
+        dst[i] = src[(i / D) * Dp + i % D];
+}
+
 inline unsigned grid_for(int64_t n, int block) {
     const int64_t g = (n + block - 1) / block;
     return (unsigned)(g < 65536 * 16 ? (g > 0 ? g : 1) : 65536 * 16);
@@ -330,5 +350,35 @@ hipError_t gt_launch_kv_append_blocks(const void *src, void *dst, const int32_t 
     if (D % 32 != 0 || blocks > 0x7fffffffLL) return hipErrorInvalidConfiguration;
     hipLaunchKernelGGL(kv_append_blocks_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, (const uint16_t *)src,
                        (uint16_t *)dst, pos, Hkv, T, hpr, cap, n);
+    return hipGetLastError();
+}
+
+hipError_t gt_launch_pad_rows(const void *src, int elem_bytes, const int64_t *strides, int64_t B, int64_t H, int64_t L,
+                              int64_t D, void *dst, int64_t Dp, hipStream_t stream) {
+    const int64_t n = B * H * L * Dp;
+    if (n <= 0) return hipSuccess;
+    if (elem_bytes == 2)
+        hipLaunchKernelGGL(pad_rows_kernel<uint16_t>, dim3(grid_for(n, 256)), dim3(256), 0, stream, (const uint16_t *)src,
+                           strides[0], strides[1], strides[2], H, L, D, (uint16_t *)dst, Dp, n);
+    else if (elem_bytes == 4)
+        hipLaunchKernelGGL(pad_rows_kernel<uint32_t>, dim3(grid_for(n, 256)), dim3(256), 0, stream, (const uint32_t *)src,
+                           strides[0], strides[1], strides[2], H, L, D, (uint32_t *)dst, Dp, n);
+    else
+        return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
+hipError_t gt_launch_unpad_rows(const void *src, int elem_bytes, int64_t rows, int64_t Dp, void *dst, int64_t D,
+                                hipStream_t stream) {
+    const int64_t n = rows * D;
+    if (n <= 0) return hipSuccess;
+    if (elem_bytes == 2)
+        hipLaunchKernelGGL(unpad_rows_kernel<uint16_t>, dim3(grid_for(n, 256)), dim3(256), 0, stream,
+                           (const uint16_t *)src, Dp, (uint16_t *)dst, D, n);
+    else if (elem_bytes == 4)
+        hipLaunchKernelGGL(unpad_rows_kernel<uint32_t>, dim3(grid_for(n, 256)), dim3(256), 0, stream,
+                           (const uint32_t *)src, Dp, (uint32_t *)dst, D, n);
+    else
+        return hipErrorInvalidValue;
     return hipGetLastError();
 }

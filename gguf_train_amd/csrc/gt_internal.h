@@ -148,6 +148,13 @@ bool gt_rope_check_args(const char *who, int64_t head_dim, int n_dims, int mode,
 float gt_rope_theta_scale(float freq_base, int n_dims);
 // Dense bool bytes -> dense float additive mask (0 where true, -inf where false).
 hipError_t gt_launch_bool_to_bias(const void *src, float *dst, int64_t n, hipStream_t stream);
+// Head padding for the MFMA kernels: rows of a 4-D (B,H,L,D) tensor (element strides
+// strides[0..2], innermost contiguous, 2- or 4-byte elements) into a dense (B,H,L,Dp) buffer with
+// zero dims D .. Dp-1; and the first D of each dense Dp-row back into a dense (rows, D) buffer.
+hipError_t gt_launch_pad_rows(const void *src, int elem_bytes, const int64_t *strides, int64_t B, int64_t H, int64_t L,
+                              int64_t D, void *dst, int64_t Dp, hipStream_t stream);
+hipError_t gt_launch_unpad_rows(const void *src, int elem_bytes, int64_t rows, int64_t Dp, void *dst, int64_t D,
+                                hipStream_t stream);
 // Q8_0 (ggml block_q8_0) quantize `nrows` rows of `row_len` floats (row_len % 32 == 0).
 hipError_t gt_launch_q8_0_quantize(const float *src, void *dst, int64_t nblocks, hipStream_t stream);
 // Q8_0 dequantize into `dst_dtype` (f32/f16/bf16/f64).
