@@ -9,7 +9,9 @@
 // nq-1-p of one head one after the other: under the causal mask their key ranges add up to
 // the same length for every p, so all workgroups carry equal work.  K/V tiles of BN = 64 rows
 // stream through NST LDS stages: global_load_lds_dwordx4 writes tile s+NST-1 straight into LDS
-// (no staging registers) while tile s is computed, with one barrier per tile.  Tiles are
+// (no staging registers) while tile s is computed, with one barrier per tile; the loads are
+// issued after tile s's S MFMAs, so that their LDS writes land during the softmax and P.V
+// rather than among the K fragment reads (the prefill workload 2-3% faster).  Tiles are
 // unpadded; 16-byte chunk c of row r sits at chunk c ^ f(r), which keeps both the row reads of
 // K (16 rows per LDS cycle) and the transposed reads of V (4 rows x 4 chunks per cycle) free of
 // bank conflicts on the 64-bank LDS: f(r) = (r ^ 4r) mod 16 for 16-chunk rows (D = 128),
@@ -343,7 +345,6 @@ __global__ __launch_bounds__(64 * nw_of<D>(), DROP && (MASK == 1 || MASK == 2 ||
             else if (later == 1) wait_vm<PER>();
             else wait_vm<0>();
             __syncthreads();
-            if (step + NST - 1 < total) issue(step + NST - 1);
             const T *cK = sK[step % NST];
             const T *cV = sV[step % NST];
             // MVEC: keys k0 + 32kb + 8g + 4half + 0..3 of this lane's row (starts past the last
@@ -386,6 +387,9 @@ __global__ __launch_bounds__(64 * nw_of<D>(), DROP && (MASK == 1 || MASK == 2 ||
 #pragma unroll
                 for (int t = 0; t < DT; ++t) s[kb] = M::mma(kf[t], qf[t], s[kb]);
             }
+
+            // the next tile's loads into the stage every wavefront finished with before the barrier
+            if (step + NST - 1 < total) issue(step + NST - 1);
 
             // ---- masks: s[kb][i] is (key = k0 + 32kb + 8(i/4) + 4half + i%4, query = lq) ----
             const bool edge = k0 + BN > nkv || (CAUSAL && k0 + BN - 1 > wq0 + qpos);
