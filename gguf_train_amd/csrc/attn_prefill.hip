@@ -10,8 +10,8 @@
 // the same length for every p, so all workgroups carry equal work.  K/V tiles of BN = 64 rows
 // stream through NST LDS stages: global_load_lds_dwordx4 writes tile s+NST-1 straight into LDS
 // (no staging registers) while tile s is computed, with one barrier per tile; the loads are
-// issued after tile s's S MFMAs, so that their LDS writes land during the softmax and P.V
-// rather than among the K fragment reads (the prefill workload 2-3% faster).  Tiles are
+// issued after tile s's S MFMAs (2-3% faster on the prefill workload than right after the
+// barrier).  Tiles are
 // unpadded; 16-byte chunk c of row r sits at chunk c ^ f(r), which keeps both the row reads of
 // K (16 rows per LDS cycle) and the transposed reads of V (4 rows x 4 chunks per cycle) free of
 // bank conflicts on the 64-bank LDS: f(r) = (r ^ 4r) mod 16 for 16-chunk rows (D = 128),
