@@ -95,3 +95,19 @@ def test_padded_heads_with_dropout(dev):
     assert_close(out32, ref, torch.bfloat16, "out32", out_dtype=torch.float32)
     for name, got, want in (("dq", dq, rq), ("dk", dk, rk), ("dv", dv, rv)):
         assert_close(got, want, torch.bfloat16, name, out_dtype=torch.float32)
+
+
+def test_padded_heads_read_strided_views(dev):
+    # (B, L, H, D) storage viewed as (B, H, L, D): the padding copy reads the strides
+    B, H, L, D = 2, 4, 90, 80
+    base = [randn((B, L, H, D), 30 + i, torch.float16).to(dev) for i in range(4)]
+    views = [t.transpose(1, 2) for t in base]
+    dense = [t.contiguous() for t in views]
+    assert not views[0].is_contiguous()
+    out, lse, out32 = g.flash_attention_train(views[0], views[1], views[2], None, 0.0, True)
+    ref, ref_lse, ref32 = g.flash_attention_train(dense[0], dense[1], dense[2], None, 0.0, True)
+    assert torch.equal(out, ref) and torch.equal(out32, ref32) and torch.equal(lse, ref_lse)
+    grads = g.flash_attention_backward(views[3], views[0], views[1], views[2], None, out32, lse, 0.0, True)
+    ref_grads = g.flash_attention_backward(dense[3], dense[0], dense[1], dense[2], None, ref32, ref_lse, 0.0, True)
+    for a, b in zip(grads, ref_grads):
+        assert torch.equal(a, b)
