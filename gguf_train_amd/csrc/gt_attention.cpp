@@ -1330,16 +1330,32 @@ extern "C" gt_tensor *gt_kv_cache_attention(gt_kv_cache *c, const gt_tensor *q, 
         const gt_tensor *ks = ok ? stage(kv, dev, cd, tmp) : nullptr;
         const gt_tensor *vs = ok ? stage(vv, dev, cd, tmp) : nullptr;
         ok = qs && ks && vs;
+        // heads padded to the MFMA kernels' sizes (the cache's first maxlen rows are copied)
+        const gt_tensor *po = nullptr;
+        const int64_t Dp = ok && q->dtype == cd ? padded_head(cd, L, D, D) : 0;
+        if (Dp) {
+            const gt_tensor *qp = pad_heads(qs, Dp, dev, tmp), *kp = pad_heads(ks, Dp, dev, tmp);
+            const gt_tensor *vp = pad_heads(vs, Dp, dev, tmp);
+            const int64_t psh[4] = {B, H, L, Dp};
+            po = tmp.keep(gt_new_tensor(4, psh, q->dtype, GT_DEV_CUDA, dev));
+            ok = qp && kp && vp && po;
+            if (ok) {
+                qs = qp;
+                ks = kp;
+                vs = vp;
+            }
+        }
         if (ok) {
             AttnFwdArgs a{};
             fill_qkv(a, qs, ks, vs);
-            a.o = gt_data(o);
+            a.o = const_cast<void *>(gt_data(po ? po : o));
             a.scale = scale;
             a.causal = is_causal ? 1 : 0;
             a.out_dtype = q->dtype;
             a.kv_len = kv_len;
             a.q_pos = q_pos;
             ok = dispatch_forward(a, cd, dev);
+            if (ok && po) ok = unpad_heads(po, o);
         }
     }
     if (!ok) {

@@ -39,7 +39,7 @@ def dense_kv(cache, dtype):
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
-@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("D", [64, 128, 96])  # 96: heads padded for the MFMA kernels (fp16 / bf16)
 def test_two_pieces_equal_the_whole_sequence(dev, dtype, D):
     B, H, Hkv, T = 2, 8, 2, 300
     q, k, v = randn((B, H, T, D), 1, dtype), randn((B, Hkv, T, D), 2, dtype), randn((B, Hkv, T, D), 3, dtype)
@@ -67,8 +67,9 @@ def test_decode_steps_equal_prefill_rows(dev, dtype):
     assert_close(torch.cat(rows, dim=2), want, dtype, "decode steps")
 
 
-def test_per_sequence_lengths_and_clear(dev):
-    dtype, B, H, Hkv, D = torch.float16, 3, 4, 4, 64
+@pytest.mark.parametrize("D", [64, 80])  # 80: heads padded for the MFMA kernels
+def test_per_sequence_lengths_and_clear(dev, D):
+    dtype, B, H, Hkv = torch.float16, 3, 4, 4
     cache = g.KVCache(B, Hkv, 256, D, dtype, dev)
     k1, v1 = randn((B, Hkv, 100, D), 7, dtype), randn((B, Hkv, 100, D), 8, dtype)
     cache.append(k1.to(dev), v1.to(dev))
