@@ -198,7 +198,10 @@ class MultiheadAttention(nn.Module):
         """torch.nn convention: True in a boolean mask blocks the position (-1e9); a float mask
         is added as it is."""
         if mask.dtype == torch.bool:
-            return torch.zeros(mask.shape, dtype=dtype, device=mask.device).masked_fill(mask, -1e9)
+            # -1e9 does not fit float16: reduced-precision calls get a float32 mask (the kernels add
+            # masks to the scores in float32)
+            mdt = torch.float32 if dtype in (torch.float16, torch.bfloat16) else dtype
+            return torch.zeros(mask.shape, dtype=mdt, device=mask.device).masked_fill(mask, -1e9)
         if not mask.is_floating_point():
             raise RuntimeError(f"MultiheadAttention: {name} must be a boolean or floating point tensor, got {mask.dtype}")
         return mask if mask.dtype == dtype else mask.to(dtype)

@@ -100,3 +100,23 @@ def test_gradients_reach_every_parameter(dev):
         out.sum().backward()
         for name, p in m.named_parameters():
             assert p.grad is not None and torch.isfinite(p.grad).all(), name
+
+
+def test_half_precision_with_a_head_size_the_kernels_pad(dev):
+    # head size 96: the fused kernels run with heads zero-padded to 128 (forward and backward)
+    torch.manual_seed(5)
+    E, H, B, L = 384, 4, 2, 40
+    m = MultiheadAttention(E, H, batch_first=True).to(dev).half()
+    x = (torch.randn(B, L, E, device=dev) * 0.5).half().requires_grad_()
+    causal = torch.triu(torch.ones(L, L, device=dev), diagonal=1).bool()
+    out, _ = m(x, x, x, attn_mask=causal, need_weights=False)
+    m32 = MultiheadAttention(E, H, batch_first=True).to(dev)
+    m32.load_state_dict({k: t.float() for k, t in m.state_dict().items()})
+    with torch.no_grad():
+        want, _ = mha_reference(m32, x.float(), x.float(), x.float(), None, causal)
+    err = ((out.float() - want).abs() / want.abs().clamp_min(1.0)).max().item()
+    assert err < 5e-3, err
+    out.float().sum().backward()
+    assert x.grad is not None and torch.isfinite(x.grad).all()
+    for name, p in m.named_parameters():
+        assert p.grad is not None and torch.isfinite(p.grad).all(), name
