@@ -120,3 +120,47 @@ def test_half_precision_with_a_head_size_the_kernels_pad(dev):
     assert x.grad is not None and torch.isfinite(x.grad).all()
     for name, p in m.named_parameters():
         assert p.grad is not None and torch.isfinite(p.grad).all(), name
+
+
+@pytest.mark.parametrize("dtype,tol", [(torch.float16, 5e-3), (torch.bfloat16, 3e-2)])
+def test_reduced_precision_masks_and_weights(dev, dtype, tol):
+    # every mask kind with float16 / bfloat16 parameters and inputs, with and without the
+    # returned weights, against the float32 composition on the same rounded values
+    torch.manual_seed(6)
+    E, H, B, L, S = 256, 4, 2, 24, 30
+    m = MultiheadAttention(E, H, batch_first=True).to(dev).to(dtype)
+    m32 = MultiheadAttention(E, H, batch_first=True).to(dev)
+    m32.load_state_dict({k: t.float() for k, t in m.state_dict().items()})
+    q = (torch.randn(B, L, E, device=dev) * 0.5).to(dtype)
+    kv = (torch.randn(B, S, E, device=dev) * 0.5).to(dtype)
+    for name, (kpm, am) in masks(B, L, S, H, dev).items():
+        for need_weights in (False, True):
+            with torch.no_grad():
+                want, weights = mha_reference(m32, q.float(), kv.float(), kv.float(), kpm, am)
+                out, got_w = m(q, kv, kv, key_padding_mask=kpm, attn_mask=am, need_weights=need_weights)
+            err = ((out.float() - want).abs() / want.abs().clamp_min(1.0)).max().item()
+            assert err < tol, (name, need_weights, err)
+            if need_weights:
+                assert (got_w.float() - weights.mean(dim=1)).abs().max().item() < tol, (name, "weights")
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_reduced_precision_training_with_dropout(dev, dtype):
+    torch.manual_seed(7)
+    E, H, B, L = 256, 4, 2, 24
+    m = MultiheadAttention(E, H, dropout=0.1, batch_first=True).to(dev).to(dtype)
+    m.train()
+    x = (torch.randn(B, L, E, device=dev) * 0.5).to(dtype).requires_grad_()
+    kpm = torch.zeros(B, L, dtype=torch.bool, device=dev)
+    kpm[:, -3:] = True
+    for need_weights in (False, True):
+        m.zero_grad()
+        x.grad = None
+        out, w = m(x, x, x, key_padding_mask=kpm, need_weights=need_weights)
+        assert out.shape == (B, L, E) and torch.isfinite(out.float()).all()
+        if need_weights:
+            assert w.shape == (B, L, L) and torch.isfinite(w.float()).all()
+        out.float().sum().backward()
+        assert torch.isfinite(x.grad.float()).all()
+        for name, p in m.named_parameters():
+            assert p.grad is not None and torch.isfinite(p.grad.float()).all(), name
