@@ -130,25 +130,57 @@ class Runner:
         return e0.elapsed_time(e1) / steps, wall * 1e3 / steps, per[len(per) // 2]
 
 
-def bench_forward(r: Runner, name, cfg, steps, warmup):
-    torch = r.torch
-    lib = r.C.lib
+def forward_inputs(cfg, dev, nbuf=1, keep_draws=False):
+    """The synthetic (q, k, v) sets of a forward configuration on device `dev`: N(0,1) (times
+    cfg["amp"]) from torch's generator seeded 1234, in the order q, k, v of set 0, then set 1 ...;
+    Q8_0 K/V are the library's quantization of the float32 draws (with keep_draws, each set also
+    carries those float32 K and V: (q, k, v, k32, v32)).  cfg["dtype"] is a torch dtype."""
+    import torch
+
     B, H, Hkv, L, S, D = cfg["B"], cfg["H"], cfg["Hkv"], cfg["L"], cfg["S"], cfg["D"]
     dt = cfg["dtype"]
-    g = torch.Generator(device=r.dev).manual_seed(1234)
-    nbuf = cfg.get("rotate", 1)
+    g = torch.Generator(device=dev).manual_seed(1234)
     sets = []
     for _ in range(nbuf):
-        q = (torch.randn(B, H, L, D, device=r.dev, generator=g) * cfg.get("amp", 1.0)).to(dt)
-        k = (torch.randn(B, Hkv, S, D, device=r.dev, generator=g) * cfg.get("amp", 1.0))
-        v = (torch.randn(B, Hkv, S, D, device=r.dev, generator=g) * cfg.get("amp", 1.0))
+        q = (torch.randn(B, H, L, D, device=dev, generator=g) * cfg.get("amp", 1.0)).to(dt)
+        k = (torch.randn(B, Hkv, S, D, device=dev, generator=g) * cfg.get("amp", 1.0))
+        v = (torch.randn(B, Hkv, S, D, device=dev, generator=g) * cfg.get("amp", 1.0))
+        k32, v32 = k, v
         if cfg.get("q8_0"):
             from gguf_train_amd import quantize
 
             k, v = quantize(k), quantize(v)
         else:
             k, v = k.to(dt), v.to(dt)
-        sets.append((q, k, v))
+        sets.append((q, k, v, k32, v32) if keep_draws else (q, k, v))
+    return sets
+
+
+def train_inputs(cfg, dev):
+    """(q, k, v, dout, mask, valid_lengths) of the training configuration on device `dev`: q, k,
+    v, dout ~ N(0,1) from torch's generator seeded 99 (in that order), rounded to cfg["dtype"];
+    key lengths uniform in [512, 1024] from numpy's default_rng(5); mask (B, 1, 1, L) float32,
+    0 for valid keys and -inf past each sequence's length."""
+    import numpy as np
+    import torch
+
+    B, H, L, D = cfg["B"], cfg["H"], cfg["L"], cfg["D"]
+    g = torch.Generator(device=dev).manual_seed(99)
+    q, k, v, dout = (torch.randn(B, H, L, D, device=dev, generator=g).to(cfg["dtype"]) for _ in range(4))
+    lens = np.random.default_rng(5).integers(512, 1025, size=B)
+    mask = torch.zeros(B, 1, 1, L, device=dev)
+    for b, n in enumerate(lens):
+        mask[b, ..., int(n):] = float("-inf")
+    return q, k, v, dout, mask, [int(x) for x in lens]
+
+
+def bench_forward(r: Runner, name, cfg, steps, warmup):
+    torch = r.torch
+    lib = r.C.lib
+    B, H, Hkv, L, S, D = cfg["B"], cfg["H"], cfg["Hkv"], cfg["L"], cfg["S"], cfg["D"]
+    dt = cfg["dtype"]
+    nbuf = cfg.get("rotate", 1)
+    sets = forward_inputs(cfg, r.dev, nbuf)
     hs = [r.handles(*s) for s in sets]
     causal = 1 if cfg.get("causal") else 0
 
@@ -160,7 +192,7 @@ def bench_forward(r: Runner, name, cfg, steps, warmup):
         lib.gt_tensor_free(p)
 
     ms, wall_ms, med_ms = r.time_steps(step, steps, warmup)
-    out = {"ms_per_step": ms, "wall_ms_per_step": wall_ms, "median_ms": med_ms}
+    out = {"ms_per_step": ms, "wall_ms_per_step": wall_ms, "median_ms": med_ms, "launch": r.C.last_launch()}
     es = 2 if dt != torch.float32 else 4
     if "decode" in name:
         if cfg.get("q8_0"):
@@ -179,18 +211,9 @@ def bench_forward(r: Runner, name, cfg, steps, warmup):
 
 
 def bench_train(r: Runner, cfg, steps, warmup):
-    import numpy as np
-
-    torch = r.torch
     lib = r.C.lib
     B, H, L, D = cfg["B"], cfg["H"], cfg["L"], cfg["D"]
-    dt = cfg["dtype"]
-    g = torch.Generator(device=r.dev).manual_seed(99)
-    q, k, v, dout = (torch.randn(B, H, L, D, device=r.dev, generator=g).to(dt) for _ in range(4))
-    lens = np.random.default_rng(5).integers(512, 1025, size=B)
-    mask = torch.zeros(B, 1, 1, L, device=r.dev)
-    for b, n in enumerate(lens):
-        mask[b, ..., int(n):] = float("-inf")
+    q, k, v, dout, mask, lens = train_inputs(cfg, r.dev)
     hq, hk, hv, hm, hg = r.handles(q, k, v, mask, dout)
     p_drop = float(cfg.get("dropout", 0.0))
 
@@ -221,9 +244,9 @@ def bench_train(r: Runner, cfg, steps, warmup):
     fwd = sum(4 * D * causal_pairs(L, int(n)) * H for n in lens)
     flops = int(fwd * 3.5)
     return {"ms_per_step": ms, "wall_ms_per_step": wall_ms, "median_ms": med_ms, "flop_per_step": flops,
-            "forward_flop": fwd,
+            "forward_flop": fwd, "launch": r.C.last_launch(),
             "value": flops / (ms * 1e-3) / 1e12, "unit": "TFLOP/s",
-            "frac_of_peak": flops / (ms * 1e-3) / 1e12 / PEAK_FP16_TFLOPS, "valid_lengths": [int(x) for x in lens]}
+            "frac_of_peak": flops / (ms * 1e-3) / 1e12 / PEAK_FP16_TFLOPS, "valid_lengths": lens}
 
 
 def bench_copy(r: Runner, steps, warmup):

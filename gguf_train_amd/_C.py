@@ -29,7 +29,7 @@ GT_DEV_CPU, GT_DEV_CUDA = 0, 1
 def _load_native() -> ctypes.CDLL:
     if not LIB_PATH.exists():
         raise ImportError(
-            f"{LIB_PATH} is not built; build it with `python gguf_train_amd/_build.py --lib` "
+            f"{LIB_PATH} is not built; build it with `python gguf_train_amd/_build.py` "
             "(hipcc, gfx950). There is no CPU fallback."
         )
     lib = ctypes.CDLL(str(LIB_PATH))
@@ -50,7 +50,7 @@ def _check_sources(lib: ctypes.CDLL) -> None:
     if got != want:
         raise ImportError(
             f"{LIB_PATH} was built from other sources (library {got[:12]}, tree {want[:12]}); "
-            "rebuild it with `python gguf_train_amd/_build.py --lib`"
+            "rebuild it with `python gguf_train_amd/_build.py`"
         )
 
 
@@ -78,6 +78,8 @@ def _configure(lib: ctypes.CDLL) -> ctypes.CDLL:
     lib.gt_set_stream.restype = None
     lib.gt_get_stream.argtypes = []
     lib.gt_get_stream.restype = c_void_p
+    lib.gt_last_launch.argtypes = []
+    lib.gt_last_launch.restype = c_char_p
 
     lib.gt_tensor_empty.argtypes = [c_int, p_i64, c_int, c_int, c_int]
     lib.gt_tensor_empty.restype = c_void_p
@@ -241,6 +243,12 @@ def _configure(lib: ctypes.CDLL) -> ctypes.CDLL:
 
 
 lib = _configure(_load_native())
+
+
+def last_launch() -> str:
+    """The kernels this thread's last attention call launched (gt_last_launch)."""
+    msg = lib.gt_last_launch()
+    return msg.decode("utf-8", errors="replace") if msg else ""
 
 
 def last_error() -> str:

@@ -1,10 +1,10 @@
-"""In-tree build of libgt_attn.so (hipcc, gfx950) and of the CPU oracle (gcc).
+"""In-tree build of libgt_attn.so (hipcc, gfx950).
 
-    python gguf_train_amd/_build.py            # both (a script: the package needs the library)
-    python gguf_train_amd/_build.py --lib      # only the HIP library
+    python gguf_train_amd/_build.py            (a script: the package needs the library)
 
 Objects go to gguf_train_amd/_build/ (ignored by git); the shared library is written next to
-this file so that it travels with the source tree.
+this file so that it travels with the source tree.  (The test-only CPU oracle has its own
+build, oracle/build.py.)
 """
 
 from __future__ import annotations
@@ -17,7 +17,6 @@ import sys
 from pathlib import Path
 
 PKG_DIR = Path(__file__).resolve().parent
-ROOT = PKG_DIR.parent
 CSRC = PKG_DIR / "csrc"
 OBJ_DIR = PKG_DIR / "_build"
 LIB_PATH = PKG_DIR / "libgt_attn.so"
@@ -81,20 +80,8 @@ def build_library(jobs: int | None = None) -> Path:
     return LIB_PATH
 
 
-def build_oracle() -> Path:
-    sys.path.insert(0, str(ROOT))
-    try:
-        from oracle import build as oracle_build
-    finally:
-        sys.path.pop(0)
-    return oracle_build.build()
-
-
 def main(argv: list[str]) -> int:
-    if "--oracle" not in argv or "--lib" in argv:
-        print(f"[gt_attn build] {build_library()}")
-    if "--lib" not in argv or "--oracle" in argv:
-        print(f"[gt_attn build] {build_oracle()}")
+    print(f"[gt_attn build] {build_library()}")
     return 0
 
 

@@ -58,6 +58,19 @@ constexpr int bm_of() { return 32 * nw_of<D>(); }  // query rows per tile
 template <int D>
 constexpr int bn_of() { return D == 64 ? 128 : 64; }
 constexpr float kLazy = 8.0f;   // rescale threshold, log2 domain: probabilities stay <= 256
+
+// p = 2^(fma(s, c, -m)) rounds the product s c only once, after subtracting m, while m itself
+// comes from the rounded product of the row max; the two differ by up to half an ulp of m.
+// That is below 2^-4 while |m| < 2^20 and is ignored there.  Beyond it (an additive mask of
+// -1e9 on every key of a row puts m near -1.4e9, where an ulp is 128) the reference point
+// moves above the max by |m| 2^-21 (more than that rounding error), and a tile only keeps the
+// reference point when its max lies |m| 2^-22 below the usual threshold, so that no
+// probability exceeds 2^kLazy: such rows give finite results (0 where every probability
+// underflows, the rule for a row with nothing visible).
+__device__ inline float huge_margin(float x) {
+    const float ax = fabsf(x);
+    return ax >= 0x1p20f ? ax * 0x1p-21f : 0.0f;
+}
 using namespace gtmfma;
 
 template <typename T>
@@ -328,7 +341,8 @@ __global__ __launch_bounds__(64 * nw_of<D>(), DROP && (MASK == 1 || MASK == 2 ||
         for (int db = 0; db < DB; ++db)
 #pragma unroll
             for (int i = 0; i < 16; ++i) o[db][i] = 0.0f;
-        float m = -INFINITY;  // reference point of this lane's row, log2 domain
+        float m = -INFINITY;     // reference point of this lane's row, log2 domain
+        float mthr = -INFINITY;  // a tile whose row max exceeds this moves m
         float lsum = 0.0f;    // this lane's share of the running sum
         // dropout: Philox block of keys 0..3 of this lane's row (rows past L draw unused words)
         const uint64_t drow = DROP ? (uint64_t)(bh * a.L + lq) * dblocks : 0;
@@ -434,9 +448,9 @@ __global__ __launch_bounds__(64 * nw_of<D>(), DROP && (MASK == 1 || MASK == 2 ||
             // nothing visible yet keeps m = -inf and p = 0 (no branch: the MFMAs below combine
             // the two lanes of each row and run for the whole wave).
             const float tm = tmax * c;
-            const bool move = tm > m + kLazy;
+            const bool move = tm > mthr;
             if (!__all(!move)) {
-                const float mnew = move ? tm : m;
+                const float mnew = move ? tm + huge_margin(tm) : m;
                 const float alpha = move ? fast_exp2(m - mnew) : 1.0f;  // m = -inf: 0 (O and l are 0)
                 lsum *= alpha;
 #pragma unroll
@@ -444,6 +458,7 @@ __global__ __launch_bounds__(64 * nw_of<D>(), DROP && (MASK == 1 || MASK == 2 ||
 #pragma unroll
                     for (int i = 0; i < 16; ++i) o[db][i] *= alpha;
                 m = mnew;
+                mthr = m + kLazy - 0.5f * huge_margin(m);
             }
             const float msub = m == -INFINITY ? 0.0f : m;
 

@@ -17,6 +17,25 @@
 
 namespace {
 
+// What the current (outermost) attention call on this thread launched, for gt_last_launch: one
+// entry per kernel family, "; "-separated.  A call that starts while none is running clears it.
+thread_local std::string t_launches;
+thread_local int t_call_depth = 0;
+
+struct LaunchScope {
+    LaunchScope() {
+        if (t_call_depth++ == 0) t_launches.clear();
+    }
+    ~LaunchScope() { --t_call_depth; }
+};
+
+void note_launch(const std::string &s) {
+    if (!t_launches.empty()) t_launches += "; ";
+    t_launches += s;
+}
+
+const char *dtype_tag(int cd) { return cd == GT_F16 ? "f16" : cd == GT_BF16 ? "bf16" : cd == GT_F32 ? "f32" : "f64"; }
+
 // Owns the temporaries of one call.
 struct Temps {
     std::vector<gt_tensor *> list;
@@ -200,6 +219,21 @@ bool decode_partials(DecodeArgs &da, int64_t units, int dev, gt_scratch &scratch
 
 // Picks the kernel for a staged forward: split-K decode for single-query rows, the MFMA
 // prefill kernel for fp16/bf16 with head size 64/128, the generic kernel otherwise.
+// Launch-log entry of a split-K decode launch.
+std::string decode_note(const char *kind, const DecodeArgs &da, int max_tile) {
+    const AttnFwdArgs &a = da.f;
+    const bool merged_in_kernel = da.counters && da.nsplit > 1 && a.D <= 128;
+    return std::string(kind) + " D=" + std::to_string(a.D) +
+           " heads_per_group=" + std::to_string(decode_head_tile(a.H / a.Hkv, max_tile)) +
+           " splits=" + std::to_string(da.nsplit) + " units=" + std::to_string(decode_units(a.B, a.H, a.Hkv, max_tile)) +
+           " merge=" + (da.nsplit == 1 && a.D <= 128 ? "none" : merged_in_kernel ? "in-kernel" : "second-launch");
+}
+
+std::string prefill_note(const AttnFwdArgs &a, int cd) {
+    return std::string("prefill ") + dtype_tag(cd) + " D=" + std::to_string(a.D) + " B=" + std::to_string(a.B) +
+           " H=" + std::to_string(a.H) + " L=" + std::to_string(a.L) + " S=" + std::to_string(a.S);
+}
+
 bool dispatch_forward(const AttnFwdArgs &a, int cd, int dev) {
     if (a.out_dtype == cd && !a.o32 && !a.dropout && attn_decode_supported(a, cd)) {
         DecodeArgs da{};
@@ -207,10 +241,14 @@ bool dispatch_forward(const AttnFwdArgs &a, int cd, int dev) {
         da.nsplit = attn_decode_splits(a, cd);
         gt_scratch ws;
         if (!decode_partials(da, decode_units(a.B, a.H, a.Hkv, kDecodeMaxTile), dev, ws)) return false;
+        note_launch(decode_note((std::string("decode ") + dtype_tag(cd)).c_str(), da, kDecodeMaxTile));
         return gt_hip_check(launch_attn_decode(da, cd, gt_stream()), "flash_attention decode kernel");
     }
-    if (attn_prefill_supported(a, cd))
+    if (attn_prefill_supported(a, cd)) {
+        note_launch(prefill_note(a, cd));
         return gt_hip_check(launch_attn_prefill(a, cd, gt_stream()), "flash_attention prefill kernel");
+    }
+    note_launch(std::string("generic ") + dtype_tag(cd));
     return gt_hip_check(launch_attn_generic_fwd(a, cd, gt_stream()), "flash_attention kernel");
 }
 
@@ -242,6 +280,7 @@ int run_q8_decode(const gt_tensor *q, const gt_tensor *k, const gt_tensor *v, co
     da.nsplit = attn_decode_q8_splits(a);
     gt_scratch ws;
     if (!decode_partials(da, decode_units(a.B, a.H, a.Hkv, kDecodeQ8MaxTile), dev, ws)) return -1;
+    note_launch(decode_note("decode q8_0", da, kDecodeQ8MaxTile));
     return gt_hip_check(launch_attn_decode_q8(da, gt_stream()), "flash_attention q8_0 decode kernel") ? 1 : -1;
 }
 
@@ -329,6 +368,7 @@ struct QRope {
 int attention_forward(const char *who, const gt_tensor *q, const gt_tensor *k, const gt_tensor *v,
                       const gt_tensor *mask, float scale, int is_causal, gt_tensor **out_o, gt_tensor **out_lse,
                       gt_tensor **out_o32 = nullptr, const QRope *qrope = nullptr, const Dropout *drop = nullptr) {
+    LaunchScope scope;
     if (out_o) *out_o = nullptr;
     if (out_lse) *out_lse = nullptr;
     if (out_o32) *out_o32 = nullptr;
@@ -365,6 +405,7 @@ int attention_forward(const char *who, const gt_tensor *q, const gt_tensor *k, c
     if (q8 == 0 && (o->numel > 0 || (lse && lse->numel > 0))) {
         // Q8_0 K/V are dequantized to float32 for the generic kernel (exact values).
         const gt_tensor *qs = stage(q, dev, cd, tmp);
+        if (k->dtype == GT_Q8_0 || v->dtype == GT_Q8_0) note_launch("dequantize q8_0 k/v");
         const gt_tensor *ks = k->dtype == GT_Q8_0 ? tmp.keep(gt_dequantize(k, cd)) : stage(k, dev, cd, tmp);
         const gt_tensor *vs = v->dtype == GT_Q8_0 ? tmp.keep(gt_dequantize(v, cd)) : stage(v, dev, cd, tmp);
         if (ks && ks->device_type != GT_DEV_CUDA) ks = stage(ks, dev, cd, tmp);
@@ -437,6 +478,8 @@ int attention_forward(const char *who, const gt_tensor *q, const gt_tensor *k, c
 
 }  // namespace
 
+extern "C" const char *gt_last_launch(void) { return t_launches.c_str(); }
+
 extern "C" gt_tensor *gt_flash_attention(const gt_tensor *q, const gt_tensor *k, const gt_tensor *v,
                                          const gt_tensor *mask, float scale, int is_causal) {
     gt_tensor *o = nullptr;
@@ -453,6 +496,7 @@ extern "C" gt_tensor *gt_flash_attention_rope(const gt_tensor *q, const gt_tenso
                                               const gt_tensor *mask, float scale, int is_causal, const gt_tensor *pos,
                                               int n_dims, int mode, float freq_base, float freq_scale) {
     const char *who = "flash_attention_rope";
+    LaunchScope scope;
     if (!validate(who, q, k, v, mask)) return nullptr;
     const int64_t L = q->shape[2], S = k->shape[2], D = q->shape[3];
     if (!gt_rope_check_args(who, D, n_dims, mode, freq_base, freq_scale)) return nullptr;
@@ -523,6 +567,7 @@ int attention_backward(const char *who, const gt_tensor *grad_out, const gt_tens
                        const gt_tensor *v, const gt_tensor *mask, const gt_tensor *out, const gt_tensor *lse,
                        float scale, int is_causal, const Dropout *drop, gt_tensor **dq, gt_tensor **dk,
                        gt_tensor **dv) {
+    LaunchScope scope;
     if (!dq || !dk || !dv) {
         gt_set_error(std::string(who) + ": dq, dk and dv must not be NULL");
         return -1;
@@ -636,8 +681,10 @@ int attention_backward(const char *who, const gt_tensor *grad_out, const gt_tens
                 ok = gt_scratch_alloc(bits, nbits, dev);
                 a.dbits = (uint32_t *)bits.ptr();
             }
+            if (ok) note_launch(std::string("backward mfma ") + dtype_tag(cd) + " D=" + std::to_string(a.f.D));
             ok = ok && gt_hip_check(launch_attn_bwd_mfma(a, cd, gt_stream()), "flash_attention_backward kernel");
         } else if (ok) {
+            note_launch(std::string("backward generic ") + dtype_tag(cd));
             ok = gt_hip_check(launch_attn_generic_bwd(a, cd, gt_stream()), "flash_attention_backward kernel");
         }
         if (ok && Dp) ok = unpad_heads(pq, gq) && unpad_heads(pk, gk) && unpad_heads(pv, gv);
@@ -743,7 +790,9 @@ extern "C" gt_tensor *gt_attention_dropout_mask(int64_t B, int64_t H, int64_t L,
 // workspace, which is allocated); every split writes all of its partial rows before the merge
 // reads them, so nothing in `scratch` needs clearing between calls.  All calls on one GPU share
 // its array: calls that overlap in time on one GPU (different streams, different threads)
-// race on it and must be serialised by the caller.
+// race on it and must be serialised by the caller.  A call that would write it while the last
+// call that did, on another stream, has not finished is refused (scratch_claim below); calls on
+// one stream are ordered by the stream, and streams under graph capture are not checked.
 
 namespace {
 
@@ -773,11 +822,76 @@ char *noalloc_scratch(int dev) {
 
 bool on_device(const gt_tensor *t, int dev) { return t->device_type == GT_DEV_CUDA && t->device_index == dev; }
 
+// Overlap detection for the calls that use `scratch`: the last such call's stream and an event
+// recorded after its launches, per device.  A call on another stream while that event is still
+// pending would race on the array, so it is refused.  (Calls on one stream are ordered by the
+// stream; a stream under graph capture is not checked: its launches run when the graph does.)
+struct ScratchUse {
+    hipStream_t stream = nullptr;
+    hipEvent_t done = nullptr;
+    bool used = false;
+};
+
+std::mutex g_scratch_mu;
+std::vector<ScratchUse> g_scratch_use;
+
+bool capturing(hipStream_t s) {
+    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(s, &st) != hipSuccess) {
+        (void)hipGetLastError();
+        return false;
+    }
+    return st != hipStreamCaptureStatusNone;
+}
+
+// Before a launch into `scratch` on the current stream: false (error set) when the previous
+// such launch, on another stream, may still be running.
+bool scratch_claim(const char *who, int dev) {
+    const hipStream_t s = gt_stream();
+    if (capturing(s)) return true;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if ((size_t)dev >= g_scratch_use.size()) g_scratch_use.resize((size_t)dev + 1);
+    ScratchUse &u = g_scratch_use[(size_t)dev];
+    if (u.used && u.stream != s) {
+        const hipError_t e = hipEventQuery(u.done);
+        if (e == hipErrorNotReady) {
+            (void)hipGetLastError();
+            gt_set_error(std::string(who) + ": a call on another stream that uses this GPU's scratch array may still "
+                         "be running; calls that overlap in time on one GPU race on it (serialise them)");
+            return false;
+        }
+        if (e != hipSuccess) (void)hipGetLastError();
+    }
+    return true;
+}
+
+// After the launches: records where the scratch array was last written.
+void scratch_release(int dev) {
+    const hipStream_t s = gt_stream();
+    if (capturing(s)) return;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    ScratchUse &u = g_scratch_use[(size_t)dev];
+    if (!u.done && hipEventCreateWithFlags(&u.done, hipEventDisableTiming) != hipSuccess) {
+        (void)hipGetLastError();
+        u.done = nullptr;
+        u.used = false;
+        return;
+    }
+    if (hipEventRecord(u.done, s) != hipSuccess) {
+        (void)hipGetLastError();
+        u.used = false;
+        return;
+    }
+    u.stream = s;
+    u.used = true;
+}
+
 }  // namespace
 
 extern "C" int gt_flash_attention_noalloc(const gt_tensor *q, const gt_tensor *k, const gt_tensor *v,
                                           const gt_tensor *mask, float scale, int is_causal, gt_tensor *out) {
     const char *who = "flash_attention_noalloc";
+    LaunchScope scope;
     if (!validate(who, q, k, v, mask)) return -1;
     const int64_t B = q->shape[0], H = q->shape[1], L = q->shape[2], D = q->shape[3], Dv = v->shape[3];
     const int dev = q->device_type == GT_DEV_CUDA ? q->device_index : 0;
@@ -866,15 +980,21 @@ extern "C" int gt_flash_attention_noalloc(const gt_tensor *q, const gt_tensor *k
                 return -1;
             }
             char *base = noalloc_scratch(dev);
-            if (!base) return -1;
+            if (!base || !scratch_claim(who, dev)) return -1;
             da.part_o = (float *)base;
             da.part_ml = da.part_o + rows * (size_t)D;
         }
+        note_launch(q8 ? decode_note("decode q8_0", da, kDecodeQ8MaxTile)
+                       : decode_note((std::string("decode ") + dtype_tag(cd)).c_str(), da, kDecodeMaxTile));
         const hipError_t e = q8 ? launch_attn_decode_q8(da, gt_stream()) : launch_attn_decode(da, cd, gt_stream());
+        if (partials) scratch_release(dev);
         return gt_hip_check(e, "flash_attention_noalloc decode kernel") ? 0 : -1;
     }
-    if (attn_prefill_supported(a, cd))
+    if (attn_prefill_supported(a, cd)) {
+        note_launch(prefill_note(a, cd));
         return gt_hip_check(launch_attn_prefill(a, cd, gt_stream()), "flash_attention_noalloc prefill kernel") ? 0 : -1;
+    }
+    note_launch(std::string("generic ") + dtype_tag(cd));
     return gt_hip_check(launch_attn_generic_fwd(a, cd, gt_stream()), "flash_attention_noalloc kernel") ? 0 : -1;
 }
 
@@ -953,6 +1073,7 @@ namespace {
 
 gt_tensor *attention_weights(const gt_tensor *q, const gt_tensor *k, const gt_tensor *mask, const gt_tensor *lse,
                              float scale, int is_causal, int average_heads, const Dropout *drop) {
+    LaunchScope scope;
     if (!validate("attention_weights", q, k, k, mask)) return nullptr;
     if (!lse || lse->ndim != 3 || lse->shape[0] != q->shape[0] || lse->shape[1] != q->shape[1] ||
         lse->shape[2] != q->shape[2]) {
@@ -1263,6 +1384,7 @@ extern "C" int gt_kv_cache_append_rope(gt_kv_cache *c, const gt_tensor *k, const
 }
 
 extern "C" gt_tensor *gt_kv_cache_attention(gt_kv_cache *c, const gt_tensor *q, float scale, int is_causal) {
+    LaunchScope scope;
     if (!c) {
         gt_set_error("kv_cache_attention: NULL cache");
         return nullptr;

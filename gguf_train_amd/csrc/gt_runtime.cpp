@@ -82,13 +82,19 @@ extern "C" void *gt_get_stream(void) { return (void *)t_stream; }
 // One uncached buffer per (device, stream), grown on demand.  The decode kernels' in-kernel
 // split merge is correct only in this memory (hipDeviceMallocUncached: no XCD's L2 holds the
 // partials or the counters; see decode_merge.h).  The kernels leave every counter at zero, so a
-// buffer is zeroed only when it is created; a buffer replaced by a larger one is kept (launches
-// in flight may use it, and uncached memory is not freed while the process runs: memory
-// allocated after such a free has read wrong values on these GPUs).  Since nothing is freed, at
-// most kMaxWorkspaceStreams streams per device get one; calls on further streams return false
-// and their launches merge the splits with a second kernel over pooled scratch memory.
+// buffer is zeroed only when it is created.  Uncached memory is never freed while the process
+// runs (memory allocated after such a free has read wrong values on these GPUs, and launches in
+// flight may still use a replaced buffer), so the footprint is bounded instead:
+//   - a buffer grows at least twofold, to at most kMaxWorkspaceBytes; a request beyond that
+//     returns false (the launch then merges its splits with a second kernel over pooled memory);
+//   - a replaced buffer stays listed in `retired` (held, not lost), so one stream holds less
+//     than 2 x kMaxWorkspaceBytes in all (the sizes form a doubling series);
+//   - at most kMaxWorkspaceStreams streams per device get a workspace; calls on further streams
+//     return false.
+// Per device that is at most 16 x 2 x 64 MiB; the benchmark's decode shapes need 1 MiB each.
 bool gt_decode_workspace(int dev, hipStream_t s, int64_t n_counters, size_t part_bytes, gt_decode_ws &ws) {
     constexpr size_t kMaxWorkspaceStreams = 16;
+    constexpr size_t kMaxWorkspaceBytes = (size_t)64 << 20;
     static std::mutex mu;
     struct Buf {
         char *p = nullptr;
@@ -97,6 +103,10 @@ bool gt_decode_workspace(int dev, hipStream_t s, int64_t n_counters, size_t part
     };
     static std::map<std::pair<int, hipStream_t>, Buf> bufs;
     static std::map<int, size_t> streams_of;  // workspaces per device
+    static std::vector<char *> retired;       // replaced buffers, held until the process ends
+    const size_t cbytes_of = 256;  // granule of the counter area
+    auto cbytes = [&](int64_t n) { return ((size_t)n * sizeof(int) + cbytes_of - 1) / cbytes_of * cbytes_of; };
+    if (n_counters < 0 || cbytes(n_counters) + part_bytes > kMaxWorkspaceBytes) return false;
     std::lock_guard<std::mutex> lock(mu);
     auto found = bufs.find({dev, s});
     if (found == bufs.end()) {
@@ -105,12 +115,15 @@ bool gt_decode_workspace(int dev, hipStream_t s, int64_t n_counters, size_t part
         found = bufs.emplace(std::make_pair(dev, s), Buf{}).first;
     }
     Buf &e = found->second;
-    const size_t cbytes_of = 256;  // granule of the counter area
-    auto cbytes = [&](int64_t n) { return ((size_t)n * sizeof(int) + cbytes_of - 1) / cbytes_of * cbytes_of; };
     if (!e.p || e.counters < n_counters || e.parts < part_bytes) {
         Buf nb;
-        nb.counters = std::max<int64_t>({n_counters, e.counters, 4096});
-        nb.parts = std::max<size_t>({part_bytes, e.parts, (size_t)1 << 20});
+        nb.counters = std::max<int64_t>({n_counters, 2 * e.counters, 4096});
+        nb.parts = std::max<size_t>({part_bytes, 2 * e.parts, (size_t)1 << 20});
+        // the doubling stops at the cap (the request itself fits, checked above)
+        while (cbytes(nb.counters) + nb.parts > kMaxWorkspaceBytes) {
+            if (nb.parts > part_bytes) nb.parts = std::max(part_bytes, nb.parts / 2);
+            else nb.counters = std::max(n_counters, nb.counters / 2);
+        }
         if (hipExtMallocWithFlags((void **)&nb.p, cbytes(nb.counters) + nb.parts, hipDeviceMallocUncached) !=
                 hipSuccess ||
             !nb.p) {
@@ -119,8 +132,10 @@ bool gt_decode_workspace(int dev, hipStream_t s, int64_t n_counters, size_t part
         }
         if (hipMemsetAsync(nb.p, 0, cbytes(nb.counters), s) != hipSuccess) {
             (void)hipGetLastError();
-            return false;  // the buffer is kept (never freed), unused
+            retired.push_back(nb.p);  // held (never freed), unused
+            return false;
         }
+        if (e.p) retired.push_back(e.p);
         e = nb;
     }
     ws.counters = (int *)e.p;

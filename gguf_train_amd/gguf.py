@@ -188,6 +188,12 @@ class GGUFFile(Mapping):
     def close(self) -> None:
         """Nothing to release: the file was closed once it had been read."""
 
+    # Identity equality and hashing, as the reference's GGUFFile (a plain class,
+    # gguf_train/gguf/__init__.py:69): Mapping would compare the tensor dicts (ambiguous for
+    # multi-element tensors) and make instances unhashable.
+    __eq__ = object.__eq__
+    __hash__ = object.__hash__
+
 
 def load_gguf(path: str | Path, dequantize: bool = False, return_metadata: bool = False, device=None):
     """The tensors of a .gguf file: the GGUFFile, or (tensors, metadata) with return_metadata."""

@@ -5,7 +5,9 @@
   q/k/v projection weights otherwise; xavier-uniform init, zero biases;
 - query/key/value: batched 3-D ((L, B, E), or (B, L, E) with batch_first) or unbatched 2-D;
 - boolean attn_mask / key_padding_mask: True marks a position that must NOT be attended to and
-  becomes -1e9; float masks are added; a 2-D attn_mask is (L, S), a 3-D one (B*H, L, S);
+  becomes -1e9 in the scores' dtype (-inf in float16, where a row whose every key is blocked
+  then gives 0; autocast lowers the mask with q/k/v, so it behaves the same); float masks are
+  added; a 2-D attn_mask is (L, S), a 3-D one (B*H, L, S);
 - need_weights=False runs the fused attention kernel (scaled_dot_product_attention);
   need_weights=True returns the softmax weights too (averaged over heads by default): the fused
   kernel gives the output and its log-sum-exp, the native gt_attention_weights recomputes the
@@ -198,10 +200,12 @@ class MultiheadAttention(nn.Module):
         """torch.nn convention: True in a boolean mask blocks the position (-1e9); a float mask
         is added as it is."""
         if mask.dtype == torch.bool:
-            # -1e9 does not fit float16: reduced-precision calls get a float32 mask (the kernels add
-            # masks to the scores in float32)
-            mdt = torch.float32 if dtype in (torch.float16, torch.bfloat16) else dtype
-            return torch.zeros(mask.shape, dtype=mdt, device=mask.device).masked_fill(mask, -1e9)
+            # in the scores' dtype, as the reference (transformer.py:187-188): -1e9 is -inf in
+            # float16, so a float16 row whose every key is blocked gives 0 (the rule for a row
+            # with nothing visible), with or without autocast (which lowers the mask as well)
+            # (-1e9 rounded to `dtype` as a cast rounds it: -inf for float16)
+            fill = torch.tensor(-1e9, dtype=torch.float64).to(dtype).item()
+            return torch.zeros(mask.shape, dtype=dtype, device=mask.device).masked_fill(mask, fill)
         if not mask.is_floating_point():
             raise RuntimeError(f"MultiheadAttention: {name} must be a boolean or floating point tensor, got {mask.dtype}")
         return mask if mask.dtype == dtype else mask.to(dtype)

@@ -97,6 +97,12 @@ GT_API void *gt_get_stream(void);
  * (csrc/ and this header), so a loader can refuse a library that does not match its tree. */
 GT_API const char *gt_source_hash(void);
 
+/* No counterpart in the reference (a diagnostic): the kernels the last attention call made on
+ * this thread launched, "; "-separated, e.g. "decode q8_0 D=128 heads_per_group=4 splits=4
+ * units=128 merge=in-kernel" or "prefill f16 D=128 B=4 H=32 L=2048 S=2048".  Valid until this
+ * thread's next attention call; "" before the first. */
+GT_API const char *gt_last_launch(void);
+
 /* ---- tensor lifecycle & metadata: csrc/gguf_train.h:188-227 ----------------------------- */
 
 GT_API gt_tensor *gt_tensor_empty(int ndim, const int64_t *shape, int dtype, int device_type, int device_index);
@@ -192,8 +198,10 @@ GT_API int gt_flash_attention_backward(const gt_tensor *grad_out, const gt_tenso
  * Inputs that would need staging or conversion are refused with an error.  The split-K
  * partials of single-query calls go to a fixed 16 MiB device array per GPU (held until the
  * process ends); a call whose partials (B*H*splits*(D+2)*4 bytes) exceed it is refused.  Calls
- * that overlap in time on one GPU share that array and race: serialise them.  Asynchronous on
- * the current stream (gt_set_stream).  Returns 0 on success, -1 with gt_last_error() set. */
+ * that overlap in time on one GPU share that array and race: serialise them.  A call that would
+ * write the array while the previous such call, made on another stream, has not finished is
+ * refused with an error (not checked for streams under graph capture).  Asynchronous on the
+ * current stream (gt_set_stream).  Returns 0 on success, -1 with gt_last_error() set. */
 GT_API int gt_flash_attention_noalloc(const gt_tensor *q, const gt_tensor *k, const gt_tensor *v,
                                       const gt_tensor *mask, float scale, int is_causal, gt_tensor *out);
 

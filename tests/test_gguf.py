@@ -38,6 +38,15 @@ def test_files_from_other_writers(tmp_path):
     assert list(loaded.keys()) == ["m", "b"] and len(loaded) == 2 and "m" in loaded
 
 
+def test_gguf_files_compare_and_hash_by_identity(tmp_path):
+    # the reference's GGUFFile is a plain class (gguf_train/gguf/__init__.py:69): identity
+    # equality, hashable - two readings of one file are two objects
+    p = GGUFBuilder().tensor("m", [4], gf.T_F32, f32s(1, 2, 3, 4)).write(tmp_path / "eq.gguf")
+    a, b = load_gguf(p), load_gguf(p)
+    assert a == a and a != b
+    assert len({a, b, a}) == 2 and {a: 1}[a] == 1
+
+
 def test_every_plain_type_and_natural_shapes(tmp_path):
     rng = np.random.default_rng(1)
     cases = {

@@ -71,6 +71,12 @@ CASES = [
     (torch.float32, 1, 2, 1, 20, 30, 300, True, None, (), 0.3),        # generic kernels without LDS staging
     (torch.float16, 1, 2, 2, 50, 61, 256, False, "bool", (), 0.5),     # generic, LDS-staged, 4 blocks of 64 dims
     (torch.bfloat16, 2, 4, 4, 96, 130, 128, True, "pad", (130, 67), 0.05),
+    # per-element masks whose keys come in whole 4-key groups (S % 4 == 0): the 4-key mask loads
+    # of the forward and dQ kernels (bool: mode 5, float: mode 6) together with dropout
+    (torch.float16, 1, 2, 2, 256, 256, 64, True, "bool", (), 0.3),
+    (torch.float16, 1, 2, 2, 256, 256, 64, False, "bool", (), 0.2),
+    (torch.bfloat16, 1, 2, 1, 192, 320, 128, True, "bool", (), 0.1),
+    (torch.bfloat16, 1, 2, 2, 128, 192, 128, True, "add", (), 0.15),
 ]
 
 

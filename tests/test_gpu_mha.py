@@ -164,3 +164,33 @@ def test_reduced_precision_training_with_dropout(dev, dtype):
         assert torch.isfinite(x.grad.float()).all()
         for name, p in m.named_parameters():
             assert p.grad is not None and torch.isfinite(p.grad.float()).all(), name
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_fully_padded_sequence_is_the_same_under_autocast(dev, dtype):
+    # a sequence whose every key is padded: the boolean key_padding_mask becomes -1e9 in the
+    # scores' dtype as in the reference (transformer.py:187-188), i.e. -inf in float16 and a
+    # finite -1e9 in bfloat16; either way the sequence's rows have nothing visible and give 0,
+    # so its outputs are the out_proj bias; the module run under autocast (which lowers the
+    # mask with q/k/v) equals the module cast to `dtype`, for need_weights on and off
+    torch.manual_seed(5)
+    m = MultiheadAttention(64, 4, batch_first=True).to(dev)
+    x = torch.randn(2, 8, 64, device=dev)
+    kpm = torch.zeros(2, 8, dtype=torch.bool, device=dev)
+    kpm[0] = True
+    kpm[1, 5:] = True
+    half = MultiheadAttention(64, 4, batch_first=True).to(dev)
+    half.load_state_dict(m.state_dict())
+    half = half.to(dtype)
+    for need_weights in (False, True):
+        with torch.no_grad():
+            with torch.autocast("cuda", dtype=dtype):
+                got, w_got = m(x, x, x, key_padding_mask=kpm, need_weights=need_weights)
+            want, w_want = half(x.to(dtype), x.to(dtype), x.to(dtype), key_padding_mask=kpm, need_weights=need_weights)
+        assert got.dtype == want.dtype == dtype
+        assert torch.isfinite(got).all() and torch.isfinite(want).all()
+        tol = 2e-2 if dtype == torch.bfloat16 else 2e-3
+        assert torch.allclose(got.float(), want.float(), atol=tol, rtol=tol), (need_weights, (got - want).abs().max())
+        assert torch.equal(want[0], half.out_proj.bias.expand(8, 64)), need_weights
+        if need_weights:
+            assert not w_got[0].any() and not w_want[0].any()

@@ -111,3 +111,29 @@ def test_prefill_lse_matches_oracle(dev):
     want_o, want_l = oracle_forward(q, k, v, is_causal=True, return_lse=True)
     assert_close(out, want_o, torch.bfloat16, "out")
     assert np.abs(lse.cpu().numpy() - want_l).max() < 1e-4
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("mshape", [(2, 1, 1, 96), (96, 96)])
+def test_huge_finite_mask_values(dev, dtype, mshape):
+    # float32 masks of -1e9 (a finite value far below the scores): rows where it covers only
+    # some keys match the oracle; rows where it covers every key put the softmax reference
+    # point near -1.4e9 (an ulp of 128 in float32) and must stay finite: every probability
+    # underflows there, which gives 0 (the rule for a row with nothing visible)
+    B, H, L, S, D = 2, 4, 96, 96, 64
+    q, k, v = randn((B, H, L, D), 21, dtype), randn((B, H, S, D), 22, dtype), randn((B, H, S, D), 23, dtype)
+    blocked = torch.zeros(mshape, dtype=torch.bool)
+    blocked[..., 40:] = True
+    if len(mshape) == 2:
+        blocked[10] = True  # query row 10: every key blocked
+    else:
+        blocked[1] = True   # sequence 1: every key blocked
+    mask = torch.zeros(mshape).masked_fill(blocked, -1e9)
+    got = g.flash_attention(q.to(dev), k.to(dev), v.to(dev), mask.to(dev)).cpu()
+    assert torch.isfinite(got).all()
+    full = blocked.all(-1).reshape((1,) * (4 - blocked.ndim) + tuple(blocked.shape[:-1])).expand(B, H, L)
+    assert not got[full].any()
+    m4 = mask.reshape((1,) * (4 - mask.ndim) + tuple(mask.shape))
+    want = oracle_forward(q, k, v, mask=m4)
+    keep = ~full
+    assert_close(got[keep], want[keep.numpy()], dtype, f"-1e9 mask {mshape}")

@@ -4,10 +4,15 @@ scratch array), for each kernel the entry point can reach - the split-K decode k
 bf16 groups of 16 heads, head size 256, Q8_0 K/V), the MFMA prefill and the generic kernel -
 at the attention bar (fp32: 1e-4 max-abs; fp16/bf16: 2e-3 * max(1, |ref|) plus half an ulp of
 the output), and bit for bit where both entry points run the same kernels with the same splits.
+Every noalloc call runs with the library's allocation failure switch on (GT_ATTN_FAIL_ALLOC=1:
+every device storage allocation fails), so a call that allocated would fail.
 Also: the refusals (host tensors, mixed dtypes, q8_0 prefill, a wrong output, partials larger
-than the scratch array) leave an error and touch nothing."""
+than the scratch array, a call that would overlap one still running on another stream) leave an
+error and touch nothing."""
 
+import contextlib
 import ctypes
+import os
 
 import pytest
 import torch
@@ -20,14 +25,40 @@ from _util import assert_close, oracle_forward, randn
 pytestmark = pytest.mark.gpu
 
 
+@contextlib.contextmanager
+def allocation_fails():
+    """While active, every device storage allocation of the library fails (GT_ATTN_FAIL_ALLOC)."""
+    old = os.environ.get("GT_ATTN_FAIL_ALLOC")
+    os.environ["GT_ATTN_FAIL_ALLOC"] = "1"
+    try:
+        yield
+    finally:
+        if old is None:
+            del os.environ["GT_ATTN_FAIL_ALLOC"]
+        else:
+            os.environ["GT_ATTN_FAIL_ALLOC"] = old
+
+
 def noalloc(q, k, v, mask=None, scale=0.0, causal=False, out=None):
+    """gt_flash_attention_noalloc on borrowed handles made beforehand, with allocation failing."""
     _bridge.bind_stream(q.device)
     hs = [_bridge.borrow(t) for t in (q, k, v)]
     hm = _bridge.borrow(mask) if mask is not None else None
     ho = _bridge.borrow(out)
-    rc = _C.lib.gt_flash_attention_noalloc(hs[0].ptr, hs[1].ptr, hs[2].ptr, hm.ptr if hm else None,
-                                           ctypes.c_float(scale), 1 if causal else 0, ho.ptr)
+    with allocation_fails():
+        rc = _C.lib.gt_flash_attention_noalloc(hs[0].ptr, hs[1].ptr, hs[2].ptr, hm.ptr if hm else None,
+                                               ctypes.c_float(scale), 1 if causal else 0, ho.ptr)
     return rc
+
+
+def test_the_allocation_switch_makes_allocating_calls_fail(dev):
+    # the switch the noalloc calls run under: gt_flash_attention, which allocates its output,
+    # fails while it is on and works again once it is off
+    q, k, v = (randn((1, 2, 1, 128), i, torch.float16).to(dev) for i in range(3))
+    with allocation_fails():
+        with pytest.raises(Exception):
+            g.flash_attention(q, k, v)
+    assert g.flash_attention(q, k, v).shape == (1, 2, 1, 128)
 
 
 def _inputs(dev, dtype, B, H, Hkv, L, S, D, seed, q8=False):
@@ -123,3 +154,32 @@ def test_noalloc_refuses_partials_larger_than_the_scratch_array(dev):
     del k, v
     # the entry point still works after the refusal
     _check(dev, torch.float16, (2, 8, 2, 1, 1000, 128))
+
+
+def test_noalloc_refuses_an_overlapping_call_on_another_stream(dev):
+    # stream s1 is busy (matrix products queued ahead of a split decode that writes the scratch
+    # array); the same decode on stream s2 would race on the array: it is refused while s1's
+    # call is pending and runs once s1 has finished
+    shape = (8, 32, 8, 1, 4096, 128)  # 2 splits: partials in the scratch array
+    B, H, Hkv, L, S, D = shape
+    q, k, v = _inputs(dev, torch.float16, B, H, Hkv, L, S, D, seed=77)
+    out1 = torch.zeros(B, H, L, D, dtype=torch.float16, device=dev)
+    out2 = torch.zeros_like(out1)
+    a = torch.randn(8192, 8192, device=dev)
+    c = torch.empty_like(a)
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    torch.cuda.synchronize()
+    with torch.cuda.stream(s1):
+        for _ in range(20):
+            torch.mm(a, a, out=c)
+        assert noalloc(q, k, v, out=out1) == 0, _C.last_error()
+    with torch.cuda.stream(s2):
+        assert noalloc(q, k, v, out=out2) != 0
+        assert "may still be running" in _C.last_error(), _C.last_error()
+    torch.cuda.synchronize()
+    assert not out2.any()
+    with torch.cuda.stream(s2):
+        assert noalloc(q, k, v, out=out2) == 0, _C.last_error()
+    torch.cuda.synchronize()
+    assert torch.equal(out1, out2)
+    assert torch.equal(out1, g.flash_attention(q, k, v))
