@@ -50,9 +50,18 @@ def _source_hash() -> str:
     return mod.source_hash(PKG_DIR)
 
 
+def _generate() -> None:
+    """Generated sources (into the object directory, which the compiles search): the pipelined
+    prefill kernel's assembly body."""
+    gen = CSRC / "prefill_asm_gen.py"
+    proc = subprocess.run([sys.executable, str(gen), str(OBJ_DIR / "prefill_asm_body.inc")], capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"{gen.name} failed:\n{proc.stdout}\n{proc.stderr}")
+
+
 def _compile(src: Path, digest: str) -> Path:
     obj = OBJ_DIR / (src.name + ".o")
-    cmd = [HIPCC, *HIP_FLAGS, f'-DGT_SOURCE_HASH="{digest}"', "-x", "hip", "-c", str(src), "-o", str(obj)]
+    cmd = [HIPCC, *HIP_FLAGS, f'-DGT_SOURCE_HASH="{digest}"', f"-I{OBJ_DIR}", "-x", "hip", "-c", str(src), "-o", str(obj)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src.name}:\n{' '.join(cmd)}\n{proc.stdout}\n{proc.stderr}")
@@ -66,6 +75,7 @@ def _compile(src: Path, digest: str) -> Path:
 
 def build_library(jobs: int | None = None) -> Path:
     OBJ_DIR.mkdir(exist_ok=True)
+    _generate()
     srcs = _sources()
     jobs = jobs or min(len(srcs), max(1, min(8, os.cpu_count() or 1)))
     digest = _source_hash()

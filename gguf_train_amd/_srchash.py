@@ -2,8 +2,8 @@
 
 The build compiles the fingerprint into the library (gt_source_hash) and the loader compares it
 with the sources next to it, so a library built from other sources than the tree it sits in is
-refused instead of silently run.  Inputs: every csrc/*.hip, *.cpp and *.h file and
-include/gt_attn.h, by name and content, in sorted order.
+refused instead of silently run.  Inputs: every csrc/*.hip, *.cpp, *.h and *.py (source
+generators) file and include/gt_attn.h, by name and content, in sorted order.
 """
 
 from __future__ import annotations
@@ -16,7 +16,7 @@ PKG_DIR = Path(__file__).resolve().parent
 
 def source_files(pkg_dir: Path = PKG_DIR) -> list[Path]:
     csrc = pkg_dir / "csrc"
-    files = [p for pat in ("*.hip", "*.cpp", "*.h") for p in csrc.glob(pat)]
+    files = [p for pat in ("*.hip", "*.cpp", "*.h", "*.py") for p in csrc.glob(pat)]
     files.append(pkg_dir.parent / "include" / "gt_attn.h")
     return sorted(files, key=lambda p: p.name)
 

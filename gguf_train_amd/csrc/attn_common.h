@@ -143,7 +143,11 @@ int attn_decode_splits(const AttnFwdArgs &f, int cd);
 hipError_t launch_attn_decode(const DecodeArgs &a, int cd, hipStream_t s);
 
 bool attn_prefill_supported(const AttnFwdArgs &f, int cd);
+// (launch_attn_prefill runs the software-pipelined fp16 head-size-128 kernel where
+// attn_prefill_asm_supported holds, the HIP prefill kernel otherwise)
 hipError_t launch_attn_prefill(const AttnFwdArgs &a, int cd, hipStream_t s);
+bool attn_prefill_asm_supported(const AttnFwdArgs &f, int cd);
+hipError_t launch_attn_prefill_asm(const AttnFwdArgs &a, hipStream_t s);
 
 bool attn_decode_q8_supported(const AttnFwdArgs &f, int q_dtype);
 int attn_decode_q8_splits(const AttnFwdArgs &f);

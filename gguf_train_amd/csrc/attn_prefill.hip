@@ -622,6 +622,7 @@ bool attn_prefill_supported(const AttnFwdArgs &f, int cd) {
 }
 
 hipError_t launch_attn_prefill(const AttnFwdArgs &a, int cd, hipStream_t s) {
+    if (attn_prefill_asm_supported(a, cd)) return launch_attn_prefill_asm(a, s);
     const int BM = a.D == 64 ? bm_of<64>() : bm_of<128>();
     const int nq = (int)((a.L + BM - 1) / BM);
     const int npairs = (nq + 1) / 2;  // query tiles p and nq-1-p share a workgroup
