@@ -112,9 +112,13 @@ bool validate(const char *who, const gt_tensor *q, const gt_tensor *k, const gt_
 }
 
 // Compute dtype of q/k/v: float64 if any operand is float64; the common dtype when all agree
-// on float32/float16/bfloat16; float32 otherwise (every such widening is exact).
+// on float32/float16/bfloat16; float32 otherwise (every such widening is exact).  A Q8_0 k/v
+// counts as float16 when q is float16 (its dequantized values, rounded once to float16, 2^-12
+// relative, feed the MFMA kernels), as float32 otherwise (exact values: rounded to bfloat16
+// the keys would move the scores by ~2^-9 relative, more than the bfloat16 bar allows).
 int compute_dtype(const gt_tensor *q, const gt_tensor *k, const gt_tensor *v) {
-    const int dq = q->dtype, dk = k->dtype == GT_Q8_0 ? GT_F32 : k->dtype, dv = v->dtype == GT_Q8_0 ? GT_F32 : v->dtype;
+    const int q8_as = q->dtype == GT_F16 ? GT_F16 : GT_F32;
+    const int dq = q->dtype, dk = k->dtype == GT_Q8_0 ? q8_as : k->dtype, dv = v->dtype == GT_Q8_0 ? q8_as : v->dtype;
     if (dq == GT_F64 || dk == GT_F64 || dv == GT_F64) return GT_F64;
     if (dq == dk && dk == dv) return dq;
     return GT_F32;
@@ -403,11 +407,28 @@ int attention_forward(const char *who, const gt_tensor *q, const gt_tensor *k, c
         ok = q8 >= 0;
     }
     if (q8 == 0 && (o->numel > 0 || (lse && lse->numel > 0))) {
-        // Q8_0 K/V are dequantized to float32 for the generic kernel (exact values).
+        // Q8_0 K/V are dequantized to the compute dtype: float16 for float16 queries (values
+        // rounded once; the MFMA kernels run), float32 otherwise (exact values)
         const gt_tensor *qs = stage(q, dev, cd, tmp);
         if (k->dtype == GT_Q8_0 || v->dtype == GT_Q8_0) note_launch("dequantize q8_0 k/v");
-        const gt_tensor *ks = k->dtype == GT_Q8_0 ? tmp.keep(gt_dequantize(k, cd)) : stage(k, dev, cd, tmp);
-        const gt_tensor *vs = v->dtype == GT_Q8_0 ? tmp.keep(gt_dequantize(v, cd)) : stage(v, dev, cd, tmp);
+        // Causal without a mask or dropout: keys >= L are visible to no query row (top-left
+        // alignment), so only the first L rows of Q8_0 K/V are dequantized and attended.
+        const int64_t S = k->shape[2];
+        const int64_t Sq = is_causal && !mask && !(drop && drop->on) && L < S && k->dtype == GT_Q8_0 &&
+                                   v->dtype == GT_Q8_0 ? L : S;
+        auto dequant = [&](const gt_tensor *t) -> const gt_tensor * {
+            if (Sq == S) return tmp.keep(gt_dequantize(t, cd));
+            const gt_tensor *src = t->device_type == GT_DEV_CUDA ? t : tmp.keep(gt_to_device_dense(t, dev, GT_Q8_0));
+            const int64_t sh[4] = {t->shape[0], t->shape[1], Sq, t->shape[3]}, rb = t->shape[3] / 32;
+            gt_tensor *d = src ? tmp.keep(gt_new_tensor(4, sh, cd, GT_DEV_CUDA, dev)) : nullptr;
+            if (!d || !gt_hip_check(gt_launch_q8_0_dequantize_rows(gt_data(src), gt_data(d), cd, sh[0] * sh[1] * Sq * rb,
+                                                                   Sq * rb, S * rb, gt_stream()),
+                                    "q8_0 dequantize kernel"))
+                return nullptr;
+            return d;
+        };
+        const gt_tensor *ks = k->dtype == GT_Q8_0 ? dequant(k) : stage(k, dev, cd, tmp);
+        const gt_tensor *vs = v->dtype == GT_Q8_0 ? dequant(v) : stage(v, dev, cd, tmp);
         if (ks && ks->device_type != GT_DEV_CUDA) ks = stage(ks, dev, cd, tmp);
         if (vs && vs->device_type != GT_DEV_CUDA) vs = stage(vs, dev, cd, tmp);
         ok = qs && ks && vs;
@@ -1429,19 +1450,26 @@ extern "C" gt_tensor *gt_kv_cache_attention(gt_kv_cache *c, const gt_tensor *q, 
         ok = q8 >= 0;
     }
     if (ok && q8 == 0 && o->numel > 0) {
-        // the float cache is read in place through a view of its first maxlen rows; a Q8_0
-        // cache is dequantized to float32 (exact values) first
-        const gt_tensor *kc = c->k, *vc = c->v;
-        if (c->dtype == GT_Q8_0) {
-            const int kd = q->dtype == GT_F64 ? GT_F64 : GT_F32;  // exact, as gt_flash_attention does
-            kc = tmp.keep(gt_dequantize(c->k, kd));
-            vc = kc ? tmp.keep(gt_dequantize(c->v, kd)) : nullptr;
-        }
+        // the float cache is read in place through a view of its first maxlen rows; of a Q8_0
+        // cache only those rows are dequantized, to float16 for float16 queries (the MFMA
+        // kernels run) or to float32 / float64 (exact values), as gt_flash_attention does
         const gt_tensor *kv_views[2] = {nullptr, nullptr};
-        if (kc && vc) {
-            const int64_t vsh[4] = {B, c->Hkv, maxlen, D};
+        const int64_t vsh[4] = {B, c->Hkv, maxlen, D};
+        if (c->dtype == GT_Q8_0) {
+            const int kd = q->dtype == GT_F16 ? GT_F16 : q->dtype == GT_F64 ? GT_F64 : GT_F32;
+            note_launch("dequantize q8_0 cache rows");
+            for (int i = 0; i < 2 && ok; ++i) {
+                gt_tensor *d = tmp.keep(gt_new_tensor(4, vsh, kd, GT_DEV_CUDA, dev));
+                const int64_t rb = D / 32;  // blocks per row
+                ok = d && gt_hip_check(gt_launch_q8_0_dequantize_rows(gt_data(i == 0 ? c->k : c->v), gt_data(d), kd,
+                                                                      B * c->Hkv * maxlen * rb, maxlen * rb,
+                                                                      c->cap * rb, gt_stream()),
+                                       "q8_0 dequantize kernel");
+                kv_views[i] = ok ? d : nullptr;
+            }
+        } else {
             for (int i = 0; i < 2; ++i) {
-                const gt_tensor *base = i == 0 ? kc : vc;
+                const gt_tensor *base = i == 0 ? c->k : c->v;
                 kv_views[i] = tmp.keep(gt_tensor_view(base, 4, vsh, base->strides, base->offset));
             }
         }

@@ -242,14 +242,18 @@ __global__ void kv_append_blocks_kernel(const uint16_t *__restrict__ src, uint16
     dst[(bh * cap + pos[b] + t) * hpr + j] = src[i];
 }
 
+// Block blk of the output reads source block blk, or, with group_blocks > 0, the blocks of each
+// group of group_blocks consecutive output blocks read from a source group src_group_blocks
+// blocks long (the first rows of every (sequence, kv head) of a KV cache).
 __global__ void q8_0_dequantize_kernel(const uint8_t *__restrict__ in, void *__restrict__ out, int dst_dtype,
-                                       int64_t nblocks) {
+                                       int64_t nblocks, int64_t group_blocks, int64_t src_group_blocks) {
     const int lane = threadIdx.x & 63;
     const int64_t wave = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
     const int64_t blk = wave * 2 + (lane >> 5);
     const int j = lane & 31;
     if (blk >= nblocks) return;
-    const uint8_t *b = in + blk * 34;
+    const int64_t sblk = group_blocks > 0 ? blk / group_blocks * src_group_blocks + blk % group_blocks : blk;
+    const uint8_t *b = in + sblk * 34;
     const float d = d_f16_to_f32((uint16_t)(b[0] | (b[1] << 8)));
     const float y = (float)(int8_t)b[2 + j] * d;
     const int64_t i = blk * 32 + j;
@@ -259,6 +263,43 @@ __global__ void q8_0_dequantize_kernel(const uint8_t *__restrict__ in, void *__r
         case GT_F16: ((uint16_t *)out)[i] = d_f32_to_f16(y); break;
         case GT_BF16: ((uint16_t *)out)[i] = d_f32_to_bf16(y); break;
         default: write_elem(out, dst_dtype, i, (double)y); break;
+    }
+}
+
+// The same for float32 / float16 / bfloat16 outputs: thread t dequantizes values 8 (t % 4) .. +7
+// of block t / 4 (the scale and four 16-bit quant loads: a block starts at an even byte) and
+// writes them with 16-byte stores.  Same values as q8_0_dequantize_kernel.
+template <int DT>
+__global__ void q8_0_dequantize_vec_kernel(const uint8_t *__restrict__ in, void *__restrict__ out, int64_t nblocks,
+                                           int64_t group_blocks, int64_t src_group_blocks) {
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t blk = t >> 2;
+    const int part = (int)(t & 3);
+    if (blk >= nblocks) return;
+    const int64_t sblk = group_blocks > 0 ? blk / group_blocks * src_group_blocks + blk % group_blocks : blk;
+    const uint16_t *b = (const uint16_t *)(in + sblk * 34);
+    const float d = d_f16_to_f32(b[0]);
+    float y[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint16_t two = b[1 + 4 * part + i];
+        y[2 * i] = (float)(int8_t)(two & 0xffu) * d;
+        y[2 * i + 1] = (float)(int8_t)(two >> 8) * d;
+    }
+    const int64_t i0 = blk * 32 + 8 * part;
+    if constexpr (DT == GT_F32) {
+        float4 *o = (float4 *)((float *)out + i0);
+        o[0] = make_float4(y[0], y[1], y[2], y[3]);
+        o[1] = make_float4(y[4], y[5], y[6], y[7]);
+    } else {
+        uint32_t w[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t lo = DT == GT_F16 ? d_f32_to_f16(y[2 * i]) : d_f32_to_bf16(y[2 * i]);
+            const uint32_t hi = DT == GT_F16 ? d_f32_to_f16(y[2 * i + 1]) : d_f32_to_bf16(y[2 * i + 1]);
+            w[i] = lo | (hi << 16);
+        }
+        *(uint4 *)((uint16_t *)out + i0) = make_uint4(w[0], w[1], w[2], w[3]);
     }
 }
 
@@ -314,10 +355,31 @@ hipError_t gt_launch_q8_0_quantize(const float *src, void *dst, int64_t nblocks,
 }
 
 hipError_t gt_launch_q8_0_dequantize(const void *src, void *dst, int dst_dtype, int64_t nblocks, hipStream_t stream) {
+    return gt_launch_q8_0_dequantize_rows(src, dst, dst_dtype, nblocks, 0, 0, stream);
+}
+
+hipError_t gt_launch_q8_0_dequantize_rows(const void *src, void *dst, int dst_dtype, int64_t nblocks,
+                                          int64_t group_blocks, int64_t src_group_blocks, hipStream_t stream) {
     if (nblocks <= 0) return hipSuccess;
+    if (dst_dtype == GT_F32 || dst_dtype == GT_F16 || dst_dtype == GT_BF16) {
+        // four threads per block, eight values each, one or two 16-byte stores
+        const int64_t wgs = (nblocks * 4 + 255) / 256;
+        if (wgs > 0x7fffffffLL) return hipErrorInvalidConfiguration;
+        if (dst_dtype == GT_F32)
+            hipLaunchKernelGGL(q8_0_dequantize_vec_kernel<GT_F32>, dim3((unsigned)wgs), dim3(256), 0, stream,
+                               (const uint8_t *)src, dst, nblocks, group_blocks, src_group_blocks);
+        else if (dst_dtype == GT_F16)
+            hipLaunchKernelGGL(q8_0_dequantize_vec_kernel<GT_F16>, dim3((unsigned)wgs), dim3(256), 0, stream,
+                               (const uint8_t *)src, dst, nblocks, group_blocks, src_group_blocks);
+        else
+            hipLaunchKernelGGL(q8_0_dequantize_vec_kernel<GT_BF16>, dim3((unsigned)wgs), dim3(256), 0, stream,
+                               (const uint8_t *)src, dst, nblocks, group_blocks, src_group_blocks);
+        return hipGetLastError();
+    }
     const int64_t waves = (nblocks + 1) / 2;
+    if ((waves + 3) / 4 > 0x7fffffffLL) return hipErrorInvalidConfiguration;
     hipLaunchKernelGGL(q8_0_dequantize_kernel, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, stream,
-                       (const uint8_t *)src, dst, dst_dtype, nblocks);
+                       (const uint8_t *)src, dst, dst_dtype, nblocks, group_blocks, src_group_blocks);
     return hipGetLastError();
 }
 

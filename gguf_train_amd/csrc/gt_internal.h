@@ -159,3 +159,7 @@ hipError_t gt_launch_unpad_rows(const void *src, int elem_bytes, int64_t rows, i
 hipError_t gt_launch_q8_0_quantize(const float *src, void *dst, int64_t nblocks, hipStream_t stream);
 // Q8_0 dequantize into `dst_dtype` (f32/f16/bf16/f64).
 hipError_t gt_launch_q8_0_dequantize(const void *src, void *dst, int dst_dtype, int64_t nblocks, hipStream_t stream);
+// Dequantizes nblocks blocks: output block i reads source block i / group_blocks *
+// src_group_blocks + i % group_blocks (group_blocks 0: block i).
+hipError_t gt_launch_q8_0_dequantize_rows(const void *src, void *dst, int dst_dtype, int64_t nblocks,
+                                          int64_t group_blocks, int64_t src_group_blocks, hipStream_t stream);

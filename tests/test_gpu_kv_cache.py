@@ -137,3 +137,26 @@ def test_errors(dev):
         cache.append(k[:, :1], k[:, :1])
     with pytest.raises(RuntimeError, match="multiple of 32"):
         g.KVCache(1, 1, 8, 48, "q8_0", dev)
+
+
+@pytest.mark.parametrize("qdtype", [torch.float16, torch.bfloat16])
+def test_q8_0_cache_prefill_chunk_on_mfma(dev, qdtype):
+    # a prefill chunk over a Q8_0 cache much larger than what it holds: only the rows the
+    # sequences hold are dequantized (float16 for float16 queries, attended by the MFMA prefill
+    # kernel with the cache's lengths and query positions; float32 for bfloat16 queries)
+    from gguf_train_amd import _C
+
+    B, H, Hkv, D, cap = 2, 8, 2, 128, 4096
+    k, v = randn((B, Hkv, 430, D), 31), randn((B, Hkv, 430, D), 32)
+    cache = g.KVCache(B, Hkv, cap, D, "q8_0", dev)
+    cache.append(k[:, :, :300].to(dev), v[:, :, :300].to(dev))
+    cache.append(k[:, :, 300:].to(dev), v[:, :, 300:].to(dev))
+    T, L = 430, 130
+    q = randn((B, H, L, D), 33, qdtype, 0.5)
+    got = cache.attention(q.to(dev))
+    launch = _C.last_launch()
+    want_kernel = "prefill f16 D=128" if qdtype == torch.float16 else "generic f32"
+    assert launch.startswith("dequantize q8_0 cache rows") and want_kernel in launch, launch
+    K, V = dense_kv(cache, torch.float32)
+    want = oracle_forward(q, K[:, :, :T].cpu(), V[:, :, :T].cpu(), mask=cache_mask(cache.lengths, L, T, True))
+    assert_close(got, want, qdtype, "q8_0 cache prefill chunk")

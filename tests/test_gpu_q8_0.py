@@ -141,3 +141,29 @@ def test_q8_0_decode_lse_exposes_the_scores(dev):
     want_o, want_l = oracle_forward(q, kd, vd, return_lse=True)
     assert np.abs(lse.cpu().numpy() - want_l).max() < 1e-3, (lse.cpu().numpy().ravel(), want_l.ravel())
     assert_close(out, want_o, torch.float16, "q8_0 out")
+
+
+@pytest.mark.parametrize("qdtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("L", [2, 130, 512])
+@pytest.mark.parametrize("causal", [False, True])
+def test_prefill_chunks_over_q8_0_kv_run_on_mfma(dev, qdtype, L, causal):
+    # L > 1 over Q8_0 K/V: for float16 queries the blocks are dequantized once to float16 and
+    # the MFMA prefill kernel attends; bfloat16 queries take the exact float32 values (generic
+    # kernel).  The reference's meaning: csrc/gt_core.cpp:800-808, then
+    # csrc/gt_ops_nn.cpp:2423-2525; checked against the oracle on the exact dequantized values
+    from gguf_train_amd import _C
+
+    B, H, Hkv, S, D = 2, 8, 2, 640, 128
+    seed = L * 7 + (3 if causal else 0)
+    q = randn((B, H, L, D), seed, qdtype, 0.5)
+    k, v = randn((B, Hkv, S, D), seed + 1), randn((B, Hkv, S, D), seed + 2)
+    kb, vb = oracle.q8_0_quantize(k.numpy()), oracle.q8_0_quantize(v.numpy())
+    kq = g.QuantizedTensor(torch.from_numpy(kb).to(dev), tuple(k.shape))
+    vq = g.QuantizedTensor(torch.from_numpy(vb).to(dev), tuple(v.shape))
+    got = g.flash_attention(q.to(dev), kq, vq, None, 0.0, causal)
+    launch = _C.last_launch()
+    want_kernel = "prefill f16 D=128" if qdtype == torch.float16 else "generic f32"
+    assert launch.startswith("dequantize q8_0 k/v") and want_kernel in launch, launch
+    kd = torch.from_numpy(oracle.q8_0_dequantize(kb).reshape(k.shape))
+    vd = torch.from_numpy(oracle.q8_0_dequantize(vb).reshape(v.shape))
+    assert_close(got, oracle_forward(q, kd, vd, is_causal=causal), qdtype, f"q8_0 prefill L={L} causal={causal}")
