@@ -178,6 +178,7 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void bwd_dkdv_kernel(AttnBwdA
     for (int st = 0; st < nsteps; ++st) {
         const int buf = st & 1;
         const int hh = st / nqs, qs0 = qstart + (st % nqs) * BQ;
+        if constexpr (D <= 64) progress_priority(st);  // two workgroups per CU
         const int64_t h = hk * G + hh;
         const T *cQ = sQ[buf];
         const T *cG = sG[buf];
@@ -461,6 +462,7 @@ __global__ __launch_bounds__(256, D <= 64 && (MASK == 0 || MASK == 4) ? 2 : 1) v
     __syncthreads();
     for (int j = 0; j < ntiles; ++j) {
         const int buf = j & 1, k0 = j * BNK;
+        if constexpr (D <= 64) progress_priority(j);  // two workgroups per CU (MASK 0 / 4)
         const T *cK = sK[buf];
         const T *cV = sV[buf];
         if (!CAUSAL || k0 <= wq0 + 31) {

@@ -324,20 +324,17 @@ __global__ __launch_bounds__(256, 2) void decode_stream_kernel(DecodeArgs a) {
 
     // two tiles in flight, unrolled by two so they swap roles without copies.  (Measured: issuing
     // the prefetch under these branches, which makes the compiler wait for it as well, is faster
-    // on this kernel than keeping it in flight across the compute.)  Wave priority 3, 2, 1, 0 over
-    // each four steps: among equal priorities the SIMD issues the older wave first, which lets
-    // the first-dispatched workgroup on a CU run ahead of the other; a wave behind now outranks it.
+    // on this kernel than keeping it in flight across the compute.)  Wave priority follows the
+    // step (progress_priority: the two workgroups on a CU stay level).
     Tile ta, tb;
     if (nsteps > 0) load(0, ta);
     for (int st = 0; st < nsteps; st += 2) {
-        if (st & 2) __builtin_amdgcn_s_setprio(1);
-        else __builtin_amdgcn_s_setprio(3);
+        progress_priority(st);
         if (st + 1 < nsteps) load(st + 1, tb);
         __builtin_amdgcn_sched_barrier(0);
         compute(st, ta);
         if (st + 1 < nsteps) {
-            if (st & 2) __builtin_amdgcn_s_setprio(0);
-            else __builtin_amdgcn_s_setprio(2);
+            progress_priority(st + 1);
             if (st + 2 < nsteps) load(st + 2, ta);
             __builtin_amdgcn_sched_barrier(0);
             compute(st + 1, tb);

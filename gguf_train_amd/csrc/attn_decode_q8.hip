@@ -591,21 +591,12 @@ __global__ __launch_bounds__(256, 2) void decode_q8_lds_kernel(DecodeArgs a) {
     // flight.  Inside the loop the loads are unconditional (clamped) so the compiler's load
     // counters stay exact; the last step is peeled off so that no workgroup fetches the rows
     // past its split (the next split's first step, which another XCD's L2 fetches again).
-    //
-    // Wave priority falls by one each step and wraps every four (3, 2, 1, 0, 3, ...): the two
-    // workgroups on a CU share its SIMDs, which issue the older wave first among equal
-    // priorities, so without this the first-dispatched workgroup streams ~15% faster and the
-    // other one finishes alone; a wave one or two steps behind now outranks the one ahead.  Only
-    // the issue order changes, never the results.
+    // Wave priority follows the step (progress_priority: the two workgroups on a CU stay level).
     if (nsteps > 0) {
         load(0);
         __builtin_amdgcn_s_setprio(3);
         for (int st = 0; st + 1 < nsteps; ++st) {
-            const int qn = (st + 1) & 3;
-            if (qn == 0) __builtin_amdgcn_s_setprio(3);
-            else if (qn == 1) __builtin_amdgcn_s_setprio(2);
-            else if (qn == 2) __builtin_amdgcn_s_setprio(1);
-            else __builtin_amdgcn_s_setprio(0);
+            progress_priority(st + 1);
             __builtin_amdgcn_wave_barrier();  // the previous step's LDS reads come before the overwrite
             stage();
             __builtin_amdgcn_sched_barrier(0);

@@ -359,6 +359,9 @@ __global__ __launch_bounds__(64 * nw_of<D>(), DROP && (MASK == 1 || MASK == 2 ||
             else if (later == 1) wait_vm<PER>();
             else wait_vm<0>();
             __syncthreads();
+            // head size 64: priority by progress (training forward 2.5 us faster per step); at 128
+            // it measured neutral (the two workgroups even out, but each runs slower)
+            if constexpr (D <= 64) progress_priority(step);
             const T *cK = sK[step % NST];
             const T *cV = sV[step % NST];
             // MVEC: keys k0 + 32kb + 8g + 4half + 0..3 of this lane's row (starts past the last
