@@ -409,11 +409,14 @@ __global__ __launch_bounds__(256, 2) void decode_q8_lds_kernel(DecodeArgs a) {
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int l16 = lane & 15, q4 = lane >> 4;
-    const int split = blockIdx.x;
-    // blockIdx.y = (sequence, kv head, head group): the kv head's gtot query heads run in
-    // groups of G (the last group may hold fewer, gv; its padding columns are blocked)
+    // blockIdx.x = (sequence, kv head, head group), blockIdx.y = split: workgroups are dealt to
+    // the XCDs round robin by linear index, so an XCD gets whole (sequence, kv head) slices rather
+    // than one split position of every other slice (measured 50.2 against 50.6 us); the kv
+    // head's gtot query heads run in groups of G (the last group may hold fewer, gv; its padding
+    // columns are blocked)
+    const int split = blockIdx.y;
     const int gtot = (int)(f.H / f.Hkv), ngrp = (gtot + G - 1) / G;
-    const int64_t bkg = blockIdx.y, bk = bkg / ngrp, b = bk / f.Hkv, hk = bk % f.Hkv;
+    const int64_t bkg = blockIdx.x, bk = bkg / ngrp, b = bk / f.Hkv, hk = bk % f.Hkv;
     const int hg = (int)(bkg % ngrp);
     const int h0 = (int)hk * gtot + hg * G, gv = min(G, gtot - hg * G);
     const int S = (int)f.S;
@@ -720,7 +723,7 @@ bool attn_decode_q8_supported(const AttnFwdArgs &f, int q_dtype) {
     if (f.L != 1 || f.S <= 0 || f.D != f.Dv || (f.D != 64 && f.D != 128)) return false;
     if (f.S >= (1LL << 30) || f.S * (f.D / 32 * 34) > 0xffffffffLL) return false;  // 32-bit offsets
     // any number of query heads per kv head, in groups of up to 8
-    if (decode_units(f.B, f.H, f.Hkv, kDecodeQ8MaxTile) > 65535) return false;  // grid.y
+    if (decode_units(f.B, f.H, f.Hkv, kDecodeQ8MaxTile) > 65535) return false;  // grid.y (register kernel)
     if (f.q_sh % 8 != 0 || f.q_sb % 8 != 0 || (uintptr_t)f.q % 16 != 0) return false;
     // K/V are whole dense Q8_0 tensors; rows are 4-byte aligned when the base is
     for (const void *p : {f.k, f.v}) if ((uintptr_t)p % 8 != 0) return false;
@@ -730,7 +733,9 @@ bool attn_decode_q8_supported(const AttnFwdArgs &f, int q_dtype) {
 hipError_t launch_attn_decode_q8(const DecodeArgs &a, hipStream_t s) {
     const void *kernel = q8_kernel(a.f);
     if (!kernel) return hipErrorInvalidValue;
-    dim3 grid((unsigned)a.nsplit, (unsigned)decode_units(a.f.B, a.f.H, a.f.Hkv, kDecodeQ8MaxTile));
+    const unsigned units = (unsigned)decode_units(a.f.B, a.f.H, a.f.Hkv, kDecodeQ8MaxTile);
+    // streaming kernel: (units, splits); register kernel: (splits, units)
+    const dim3 grid = q8_stream_ok(a.f) ? dim3(units, (unsigned)a.nsplit) : dim3((unsigned)a.nsplit, units);
     void *args[] = {(void *)&a};
     hipError_t e = hipLaunchKernel(kernel, grid, dim3(256), args, 0, s);
     // one split, or the last split merged in the kernel: the kernel wrote the output
