@@ -462,7 +462,7 @@ __global__ __launch_bounds__(256, D <= 64 && (MASK == 0 || MASK == 4) ? 2 : 1) v
     __syncthreads();
     for (int j = 0; j < ntiles; ++j) {
         const int buf = j & 1, k0 = j * BNK;
-        if constexpr (D <= 64) progress_priority(j);  // two workgroups per CU (MASK 0 / 4)
+        if constexpr (D <= 64) progress_priority(j);  // two workgroups per CU with MASK 0 / 4 (one otherwise: no effect)
         const T *cK = sK[buf];
         const T *cV = sV[buf];
         if (!CAUSAL || k0 <= wq0 + 31) {
