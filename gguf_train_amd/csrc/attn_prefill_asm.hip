@@ -15,7 +15,6 @@
 #include "gt_internal.h"
 #include "prefill_asm_body.inc"
 
-#include <cstdlib>
 #include <cstring>
 
 namespace {
@@ -67,14 +66,12 @@ __global__ __launch_bounds__(128, 1) void prefill_asm_kernel(AttnFwdArgs a, int 
     }
 }
 
-// Off unless GT_ATTN_PREFILL_ASM=1: the first GPU run of this kernel (causal, L = S = 128) did not
-// finish, while every path of the same instruction stream runs to completion with correct
-// results in a functional model of the documented instruction semantics; until the cause is
-// known the HIP prefill kernel serves these calls.
-bool asm_enabled() {
-    const char *e = std::getenv("GT_ATTN_PREFILL_ASM");
-    return e && std::strcmp(e, "1") == 0;
-}
+// Switched off, with no way to enable it: the first GPU run of this kernel (causal, L = S = 128)
+// did not finish, while every path of the same instruction stream runs to completion with
+// correct results in a functional model of the documented instruction semantics (alignment, LDS
+// bounds, waits and barriers included).  Until the cause is known the HIP prefill kernel serves
+// every call; the kernel stays compiled so that the generator's output is built and checked.
+bool asm_enabled() { return false; }
 
 }  // namespace
 
