@@ -39,6 +39,7 @@
 #include "gt_rope_math.h"
 
 #include <cmath>
+#include <type_traits>
 
 namespace {
 
@@ -180,7 +181,10 @@ __device__ inline int key_tiles(int qt, int nkv, int qpos) {
 // in one 4- / 16-byte load, issued with the tile's DMA so that they land during S = K.Q^T.
 // (dropout with a per-element mask: one workgroup per CU is the guaranteed minimum, so that the
 // Philox state does not spill)
-template <typename T, int D, bool CAUSAL, int MASK, bool ROPE = false, bool DROP = false>
+// HILO (fp16 training forward): P enters P.V as hi + lo fp16 operands and the row sums add the
+// float32 probabilities, as the bf16 kernels do, so that the float32 output and the log-sum-exp
+// the backward recomputes P from are exact to ~22 bits instead of fp16's 11.
+template <typename T, int D, bool CAUSAL, int MASK, bool ROPE = false, bool DROP = false, bool HILO = false>
 __global__ __launch_bounds__(64 * nw_of<D>(), DROP && (MASK == 1 || MASK == 2 || MASK >= 5) ? 1 : 8 / nw_of<D>()) void prefill_fwd_kernel(
     AttnFwdArgs a, int nq, int npairs) {
     constexpr int NW = nw_of<D>(), BM = bm_of<D>(), NST = nst_of<D>(), BN = bn_of<D>();
@@ -491,6 +495,10 @@ __global__ __launch_bounds__(64 * nw_of<D>(), DROP && (MASK == 1 || MASK == 2 ||
                         // formed in place)
                         lsum = sum8<T>(p, pb[kb][hs], lsum);
                         pack8<T>(p, pb[kb][hs], pl[kb][hs]);
+                    } else if constexpr (HILO) {
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) lsum += p[e];
+                        pack8_hilo<T>(p, pb[kb][hs], pl[kb][hs]);
                     } else {
                         pack8<T>(p, pb[kb][hs], pl[kb][hs]);
                         lsum = sum8<T>(p, pb[kb][hs], lsum);
@@ -513,7 +521,7 @@ __global__ __launch_bounds__(64 * nw_of<D>(), DROP && (MASK == 1 || MASK == 2 ||
                                                : read_tr8<T>(&cV[vofs0[(g % 2) * DB + db] + 32 * kb * D],
                                                              &cV[vofs1[(g % 2) * DB + db] + 32 * kb * D]);
                         o[db] = M::mma(av, pb[kb][hs], o[db]);
-                        if constexpr (M::kSplit) o[db] = M::mma(av, pl[kb][hs], o[db]);
+                        if constexpr (M::kSplit || HILO) o[db] = M::mma(av, pl[kb][hs], o[db]);
                     }
                 }
             }
@@ -556,6 +564,8 @@ hipError_t launch_variant(const AttnFwdArgs &a, int nq, int npairs, int64_t grid
     hipLaunchKernelGGL((prefill_fwd_kernel<T, D, C, MK, true>), dim3((unsigned)grid), dim3(64 * nw_of<D>()), 0, s, a, nq, npairs)
 #define GT_PREFILL_LAUNCH_D(C, MK) \
     hipLaunchKernelGGL((prefill_fwd_kernel<T, D, C, MK, false, true>), dim3((unsigned)grid), dim3(64 * nw_of<D>()), 0, s, a, nq, npairs)
+#define GT_PREFILL_LAUNCH_X(C, MK) \
+    hipLaunchKernelGGL((prefill_fwd_kernel<T, D, C, MK, false, false, true>), dim3((unsigned)grid), dim3(64 * nw_of<D>()), 0, s, a, nq, npairs)
     if (a.dropout) {
         if (a.rope_q) return hipErrorInvalidValue;  // dropout runs on unrotated queries only
         if (a.causal) {
@@ -583,6 +593,27 @@ hipError_t launch_variant(const AttnFwdArgs &a, int nq, int npairs, int64_t grid
             if (mode == 0) GT_PREFILL_LAUNCH_R(false, 0);
             else GT_PREFILL_LAUNCH_R(false, 4);
         }
+    } else if (std::is_same<T, _Float16>::value && a.o32) {
+        // fp16 training forward (HILO): its float32 output and log-sum-exp feed the backward.  With
+        // single fp16 probabilities the row sum is off by up to ~2^-12 where few keys are visible,
+        // and dV, dK sum that per-row error over every query row (measured 1.01x the 2e-3 bar).
+        if constexpr (std::is_same<T, _Float16>::value) {
+            if (a.causal) {
+                if (mode == 0) GT_PREFILL_LAUNCH_X(true, 0);
+                else if (mode == 1) GT_PREFILL_LAUNCH_X(true, 1);
+                else if (mode == 4) GT_PREFILL_LAUNCH_X(true, 4);
+                else if (mode == 5) GT_PREFILL_LAUNCH_X(true, 5);
+                else if (mode == 6) GT_PREFILL_LAUNCH_X(true, 6);
+                else GT_PREFILL_LAUNCH_X(true, 2);
+            } else {
+                if (mode == 0) GT_PREFILL_LAUNCH_X(false, 0);
+                else if (mode == 1) GT_PREFILL_LAUNCH_X(false, 1);
+                else if (mode == 4) GT_PREFILL_LAUNCH_X(false, 4);
+                else if (mode == 5) GT_PREFILL_LAUNCH_X(false, 5);
+                else if (mode == 6) GT_PREFILL_LAUNCH_X(false, 6);
+                else GT_PREFILL_LAUNCH_X(false, 2);
+            }
+        }
     } else if (a.causal) {
         if (mode == 0) GT_PREFILL_LAUNCH(true, 0);
         else if (mode == 1) GT_PREFILL_LAUNCH(true, 1);
@@ -601,6 +632,7 @@ hipError_t launch_variant(const AttnFwdArgs &a, int nq, int npairs, int64_t grid
 #undef GT_PREFILL_LAUNCH
 #undef GT_PREFILL_LAUNCH_R
 #undef GT_PREFILL_LAUNCH_D
+#undef GT_PREFILL_LAUNCH_X
     return hipGetLastError();
 }
 

@@ -38,7 +38,7 @@ struct Mfma;
 template <>
 struct Mfma<_Float16> {
     typedef half8 V8;
-    static constexpr bool kSplit = false;  // fp16 operands keep 11 bits: no hi/lo split
+    static constexpr bool kSplit = false;  // fp16 keeps 11 bits: one operand where sums run along normalised rows (pack8_hilo elsewhere)
     static __device__ inline f32x16 mma(V8 a, V8 b, f32x16 c) { return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0); }
     static __device__ inline uint32_t pack(float x, float y) {
         typedef _Float16 h2 __attribute__((ext_vector_type(2)));
@@ -84,6 +84,37 @@ __device__ inline void pack8(const float *x, typename Mfma<T>::V8 &hi, typename 
             const b2 pair = __builtin_bit_cast(b2, hj);
             r[2 * j] = __builtin_amdgcn_fdot2_f32_bf16(pair, neg_first, x[2 * j], false);
             r[2 * j + 1] = __builtin_amdgcn_fdot2_f32_bf16(pair, neg_second, x[2 * j + 1], false);
+        }
+        u32x4 l = {M::pack(r[0], r[1]), M::pack(r[2], r[3]), M::pack(r[4], r[5]), M::pack(r[6], r[7])};
+        lo = __builtin_bit_cast(typename M::V8, l);
+    }
+}
+
+// pack8 with a residual operand for either type: `lo` = x - hi rounded to T, so that hi + lo
+// carries about twice T's significand.  For sums whose terms are not normalised per row (dV =
+// P^T.dO and dK = dS^T.Q add a key's contributions over every query row), where a single fp16
+// operand's 2^-12 relative rounding accumulates with the column sums of P.  fp16: the residual of
+// each element is exact, from the packed pair with one v_dot2_f32_f16 ((hi0, hi1) . (-1, 0) + x0).
+template <typename T>
+__device__ inline void pack8_hilo(const float *x, typename Mfma<T>::V8 &hi, typename Mfma<T>::V8 &lo) {
+    using M = Mfma<T>;
+    if constexpr (M::kSplit) {
+        pack8<T>(x, hi, lo);
+    } else {
+        typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+        u32x4 h = {M::pack(x[0], x[1]), M::pack(x[2], x[3]), M::pack(x[4], x[5]), M::pack(x[6], x[7])};
+        hi = __builtin_bit_cast(typename M::V8, h);
+        // (-1, 0) and (0, -1), element 0 in the low half, kept opaque (see pack8)
+        uint32_t nf_bits = 0x0000bc00u, ns_bits = 0xbc000000u;
+        asm("" : "+v"(nf_bits), "+v"(ns_bits));
+        const h2 neg_first = __builtin_bit_cast(h2, nf_bits), neg_second = __builtin_bit_cast(h2, ns_bits);
+        float r[8];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t hj = h[j];  // through a scalar: bit-casting a vector element reads element 0
+            const h2 pair = __builtin_bit_cast(h2, hj);
+            r[2 * j] = __builtin_amdgcn_fdot2(pair, neg_first, x[2 * j], false);
+            r[2 * j + 1] = __builtin_amdgcn_fdot2(pair, neg_second, x[2 * j + 1], false);
         }
         u32x4 l = {M::pack(r[0], r[1]), M::pack(r[2], r[3]), M::pack(r[4], r[5]), M::pack(r[6], r[7])};
         lo = __builtin_bit_cast(typename M::V8, l);
