@@ -181,9 +181,10 @@ __device__ inline int key_tiles(int qt, int nkv, int qpos) {
 // in one 4- / 16-byte load, issued with the tile's DMA so that they land during S = K.Q^T.
 // (dropout with a per-element mask: one workgroup per CU is the guaranteed minimum, so that the
 // Philox state does not spill)
-// HILO (fp16 training forward): P enters P.V as hi + lo fp16 operands and the row sums add the
-// float32 probabilities, as the bf16 kernels do, so that the float32 output and the log-sum-exp
-// the backward recomputes P from are exact to ~22 bits instead of fp16's 11.
+// HILO (fp16 training forwards, with and without dropout): P enters P.V as hi + lo fp16 operands
+// and the row sums add the float32 probabilities, as the bf16 kernels do, so that the float32
+// output (whose rowsum(dO.O) forms dS) and the log-sum-exp the backward recomputes P from are
+// exact to ~22 bits instead of fp16's 11.
 template <typename T, int D, bool CAUSAL, int MASK, bool ROPE = false, bool DROP = false, bool HILO = false>
 __global__ __launch_bounds__(64 * nw_of<D>(), DROP && (MASK == 1 || MASK == 2 || MASK >= 5) ? 1 : 8 / nw_of<D>()) void prefill_fwd_kernel(
     AttnFwdArgs a, int nq, int npairs) {
@@ -489,7 +490,8 @@ __global__ __launch_bounds__(64 * nw_of<D>(), DROP && (MASK == 1 || MASK == 2 ||
 #pragma unroll
                             for (int e = 0; e < 4; ++e) p[4 * u + e] *= x.w[e] < a.drop.thresh ? dscale : 0.0f;
                         }
-                        pack8<T>(p, pb[kb][hs], pl[kb][hs]);
+                        if constexpr (HILO) pack8_hilo<T>(p, pb[kb][hs], pl[kb][hs]);
+                        else pack8<T>(p, pb[kb][hs], pl[kb][hs]);
                     } else if constexpr (M::kSplit) {
                         // bf16: sum the float32 p first; packing consumes them (the residuals are
                         // formed in place)
@@ -563,7 +565,7 @@ hipError_t launch_variant(const AttnFwdArgs &a, int nq, int npairs, int64_t grid
 #define GT_PREFILL_LAUNCH_R(C, MK) \
     hipLaunchKernelGGL((prefill_fwd_kernel<T, D, C, MK, true>), dim3((unsigned)grid), dim3(64 * nw_of<D>()), 0, s, a, nq, npairs)
 #define GT_PREFILL_LAUNCH_D(C, MK) \
-    hipLaunchKernelGGL((prefill_fwd_kernel<T, D, C, MK, false, true>), dim3((unsigned)grid), dim3(64 * nw_of<D>()), 0, s, a, nq, npairs)
+    hipLaunchKernelGGL((prefill_fwd_kernel<T, D, C, MK, false, true, std::is_same<T, _Float16>::value>), dim3((unsigned)grid), dim3(64 * nw_of<D>()), 0, s, a, nq, npairs)
 #define GT_PREFILL_LAUNCH_X(C, MK) \
     hipLaunchKernelGGL((prefill_fwd_kernel<T, D, C, MK, false, false, true>), dim3((unsigned)grid), dim3(64 * nw_of<D>()), 0, s, a, nq, npairs)
     if (a.dropout) {

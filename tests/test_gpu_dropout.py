@@ -77,6 +77,9 @@ CASES = [
     (torch.float16, 1, 2, 2, 256, 256, 64, False, "bool", (), 0.2),
     (torch.bfloat16, 1, 2, 1, 192, 320, 128, True, "bool", (), 0.1),
     (torch.bfloat16, 1, 2, 2, 128, 192, 128, True, "add", (), 0.15),
+    # few keys per row with fp16: a random-shape sweep found dK at 1.23x the bar while the fp16
+    # dropout forward fed P.V single fp16 probabilities (its float32 output forms rowsum(dO.O))
+    (torch.float16, 1, 4, 2, 141, 3, 128, False, "bool", (), 0.5),
 ]
 
 
