@@ -53,8 +53,9 @@ def test_attention_runs_in_the_autocast_dtype(dev, device_type, dtype):
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 def test_autocast_casts_operands_and_mask_and_returns_float32_grads(dev, dtype):
-    # the result equals the kernel run on the operands cast to `dtype` (a float mask too), and
-    # the float32 leaves receive float32 gradients of those cast operands
+    # the result equals the training forward (the one the autograd function runs) on the operands
+    # cast to `dtype` (a float mask too), and the float32 leaves receive float32 gradients of those
+    # cast operands
     B, H, L, D = 2, 4, 70, 64
     q, k, v = (randn((B, H, L, D), s).to(dev).requires_grad_() for s in (1, 2, 3))
     mask = torch.from_numpy(np.random.default_rng(4).standard_normal((L, L)).astype(np.float32) * 0.3).to(dev)
@@ -62,7 +63,7 @@ def test_autocast_casts_operands_and_mask_and_returns_float32_grads(dev, dtype):
         out = F.scaled_dot_product_attention(q, k, v, attn_mask=mask, is_causal=True)
     assert out.dtype == dtype
     qc, kc, vc, mc = (t.detach().to(dtype) for t in (q, k, v, mask))
-    want = g.flash_attention(qc, kc, vc, mc.reshape(1, 1, L, L), 1 / math.sqrt(D), True)
+    want = g.flash_attention_train(qc, kc, vc, mc.reshape(1, 1, L, L), 1 / math.sqrt(D), True)[0]
     assert torch.equal(out.detach(), want)
     dout = randn((B, H, L, D), 5, dtype).to(dev)
     out.backward(dout)
