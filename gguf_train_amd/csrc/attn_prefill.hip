@@ -90,12 +90,15 @@ __device__ inline int swz(int r) {
 // lds + 16 l.  Issued from assembly so that the compiler does not see an LDS write it would
 // have to wait for (vmcnt(0)) before every later LDS read, which would serialise the prefetch
 // of later tiles with the compute of the current one; the kernel waits for it explicitly
-// (vmcnt + barrier) before reading the destination.  m0 is saved and restored.
+// (vmcnt + barrier) before reading the destination.  m0 is saved and restored.  An LDS DMA
+// that reads m0 right after a scalar write of it needs one wait state (the compiler inserts
+// that s_nop itself around its own LDS DMA; inside assembly it cannot).
 __device__ inline void lds_dma16(uint32_t lds, const void *gbase, uint32_t voff) {
     uint32_t save;
     asm volatile(
         "s_mov_b32 %0, m0\n\t"
         "s_mov_b32 m0, %1\n\t"
+        "s_nop 0\n\t"
         "global_load_lds_dwordx4 %2, %3\n\t"
         "s_mov_b32 m0, %0"
         : "=&s"(save)
@@ -110,6 +113,7 @@ __device__ inline void lds_dma4(uint32_t lds, const void *gbase, uint32_t voff) 
     asm volatile(
         "s_mov_b32 %0, m0\n\t"
         "s_mov_b32 m0, %1\n\t"
+        "s_nop 0\n\t"
         "global_load_lds_dword %2, %3\n\t"
         "s_mov_b32 m0, %0"
         : "=&s"(save)
@@ -129,12 +133,12 @@ __device__ inline void wait_vm() {
     __builtin_amdgcn_s_waitcnt(0x0f70 | (N & 15) | ((N >> 4) << 14));
 }
 
-// max of three floats in one v_max3_f32 (fmaxf would first quiet each MFMA result with a
-// v_max_f32 x, x, x; the scores are never signalling NaNs)
+// max of three floats in one v_maximum3_f32 (fmaxf would first quiet each MFMA result with a
+// v_max_f32 x, x, x).  Compiler-visible rather than assembly: a VALU read of an MFMA result
+// needs wait states that the compiler only places around instructions it can see.  A NaN score
+// makes the tile's max NaN (v_max3_f32 would skip it); that row's output is NaN either way.
 __device__ inline float max3(float a, float b, float c) {
-    float r;
-    asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
-    return r;
+    return __builtin_elementwise_maximum(__builtin_elementwise_maximum(a, b), c);
 }
 
 // RoPE of the lane's query row as it is loaded (all D dims rotated): q[t] holds dims
