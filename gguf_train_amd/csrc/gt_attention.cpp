@@ -866,11 +866,13 @@ bool capturing(hipStream_t s) {
 }
 
 // Before a launch into `scratch` on the current stream: false (error set) when the previous
-// such launch, on another stream, may still be running.
-bool scratch_claim(const char *who, int dev) {
+// such launch, on another stream, may still be running.  On success `held` keeps the lock until
+// scratch_release has recorded this call's launches, so that two threads cannot both pass the
+// check before either has launched.
+bool scratch_claim(const char *who, int dev, std::unique_lock<std::mutex> &held) {
     const hipStream_t s = gt_stream();
     if (capturing(s)) return true;
-    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    held = std::unique_lock<std::mutex>(g_scratch_mu);
     if ((size_t)dev >= g_scratch_use.size()) g_scratch_use.resize((size_t)dev + 1);
     ScratchUse &u = g_scratch_use[(size_t)dev];
     if (u.used && u.stream != s) {
@@ -886,11 +888,12 @@ bool scratch_claim(const char *who, int dev) {
     return true;
 }
 
-// After the launches: records where the scratch array was last written.
-void scratch_release(int dev) {
+// After the launches: records where the scratch array was last written, then lets the next
+// claim in (the lock taken by scratch_claim; none under graph capture).
+void scratch_release(int dev, std::unique_lock<std::mutex> &held) {
+    if (!held.owns_lock()) return;
     const hipStream_t s = gt_stream();
-    if (capturing(s)) return;
-    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    std::unique_lock<std::mutex> lock(std::move(held));
     ScratchUse &u = g_scratch_use[(size_t)dev];
     if (!u.done && hipEventCreateWithFlags(&u.done, hipEventDisableTiming) != hipSuccess) {
         (void)hipGetLastError();
@@ -991,6 +994,7 @@ extern "C" int gt_flash_attention_noalloc(const gt_tensor *q, const gt_tensor *k
         // partials: (B*H, nsplit, D) outputs then (B*H, nsplit, 2) (max, sum); the streaming
         // kernels write the output themselves when there is one split
         const bool partials = da.nsplit > 1 || (!q8 && D > 128);
+        std::unique_lock<std::mutex> held;  // the scratch check's lock, until the launch is recorded
         if (partials) {
             const size_t rows = (size_t)(B * H) * (size_t)da.nsplit;
             const size_t need = rows * (size_t)(D + 2) * sizeof(float);
@@ -1001,14 +1005,14 @@ extern "C" int gt_flash_attention_noalloc(const gt_tensor *q, const gt_tensor *k
                 return -1;
             }
             char *base = noalloc_scratch(dev);
-            if (!base || !scratch_claim(who, dev)) return -1;
+            if (!base || !scratch_claim(who, dev, held)) return -1;
             da.part_o = (float *)base;
             da.part_ml = da.part_o + rows * (size_t)D;
         }
         note_launch(q8 ? decode_note("decode q8_0", da, kDecodeQ8MaxTile)
                        : decode_note((std::string("decode ") + dtype_tag(cd)).c_str(), da, kDecodeMaxTile));
         const hipError_t e = q8 ? launch_attn_decode_q8(da, gt_stream()) : launch_attn_decode(da, cd, gt_stream());
-        if (partials) scratch_release(dev);
+        if (partials) scratch_release(dev, held);
         return gt_hip_check(e, "flash_attention_noalloc decode kernel") ? 0 : -1;
     }
     if (attn_prefill_supported(a, cd)) {
