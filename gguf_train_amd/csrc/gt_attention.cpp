@@ -1187,7 +1187,7 @@ bool kv_upload(gt_tensor *dst, const std::vector<int32_t> &src) {
 }
 
 bool kv_zero(gt_tensor *t) {
-    return gt_hip_check(hipMemsetAsync(gt_data(t), 0, gt_dtype_nbytes(t->dtype, t->numel), gt_stream()),
+    return gt_hip_check(gt_launch_fill_zero(gt_data(t), (int64_t)gt_dtype_nbytes(t->dtype, t->numel), gt_stream()),
                         "kv cache: zero fill");
 }
 

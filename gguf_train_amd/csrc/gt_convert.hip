@@ -310,6 +310,18 @@ __global__ void bool_to_bias_kernel(const uint8_t *__restrict__ src, float *__re
         dst[i] = src[i] ? 0.0f : -INFINITY;
 }
 
+// Zero fill of `bytes` bytes at p, as a kernel so that a stream under graph capture records a
+// kernel node, not a memset node: 16-byte stores over the first n16 chunks, byte stores for the
+// remaining bytes (all of them when p is not 16-byte aligned: n16 = 0).
+__global__ void fill_zero_kernel(uint8_t *__restrict__ p, int64_t n16, int64_t bytes) {
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    const int64_t n = n16 + (bytes - 16 * n16);
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+        if (i < n16) *(uint4 *)(p + 16 * i) = make_uint4(0u, 0u, 0u, 0u);
+        else p[16 * n16 + (i - n16)] = 0;
+    }
+}
+
 // Rows of a 4-D tensor (rows (b, h, l) at b*sb + h*sh + l*sl, D contiguous elements of ES bytes)
 // into a dense (B*H*L, Dp) buffer, dims D .. Dp-1 set to zero; or back (unpad: the first D of
 // every Dp).  One thread per destination element.
@@ -386,6 +398,14 @@ hipError_t gt_launch_q8_0_dequantize_rows(const void *src, void *dst, int dst_dt
 hipError_t gt_launch_bool_to_bias(const void *src, float *dst, int64_t n, hipStream_t stream) {
     if (n <= 0) return hipSuccess;
     hipLaunchKernelGGL(bool_to_bias_kernel, dim3(grid_for(n, 256)), dim3(256), 0, stream, (const uint8_t *)src, dst, n);
+    return hipGetLastError();
+}
+
+hipError_t gt_launch_fill_zero(void *p, int64_t bytes, hipStream_t stream) {
+    if (bytes <= 0) return hipSuccess;
+    const int64_t n16 = (uintptr_t)p % 16 == 0 ? bytes / 16 : 0;
+    hipLaunchKernelGGL(fill_zero_kernel, dim3(grid_for(n16 + (bytes - 16 * n16), 256)), dim3(256), 0, stream,
+                       (uint8_t *)p, n16, bytes);
     return hipGetLastError();
 }
 

@@ -146,6 +146,9 @@ hipError_t gt_launch_rope(const void *x, int dtype, const int64_t *strides, void
 bool gt_rope_check_args(const char *who, int64_t head_dim, int n_dims, int mode, float freq_base, float freq_scale);
 // powf(freq_base, -2 / n_dims), as ggml computes it.
 float gt_rope_theta_scale(float freq_base, int n_dims);
+// Zero fill of `bytes` bytes at p on `stream` (a kernel, not hipMemsetAsync, so that a captured
+// stream records no memset node).
+hipError_t gt_launch_fill_zero(void *p, int64_t bytes, hipStream_t stream);
 // Dense bool bytes -> dense float additive mask (0 where true, -inf where false).
 hipError_t gt_launch_bool_to_bias(const void *src, float *dst, int64_t n, hipStream_t stream);
 // Head padding for the MFMA kernels: rows of a 4-D (B,H,L,D) tensor (element strides

@@ -130,7 +130,7 @@ bool gt_decode_workspace(int dev, hipStream_t s, int64_t n_counters, size_t part
             (void)hipGetLastError();
             return false;
         }
-        if (hipMemsetAsync(nb.p, 0, cbytes(nb.counters), s) != hipSuccess) {
+        if (gt_launch_fill_zero(nb.p, (int64_t)cbytes(nb.counters), s) != hipSuccess) {
             (void)hipGetLastError();
             retired.push_back(nb.p);  // held (never freed), unused
             return false;

@@ -111,6 +111,24 @@ def test_q8_0_cache_rows_and_attention(dev, D):
         assert_close(got, want, torch.float16, f"q8_0 L={L}")
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, "q8_0"])
+def test_a_new_cache_starts_zero_filled(dev, dtype):
+    """A cache's storage is zero-filled when it is created (by a fill kernel, byte by byte past
+    the last whole 16-byte chunk: 2 x 7 rows of 68-byte Q8_0 blocks are 952 bytes), also where
+    it takes over memory that a freed cache had written."""
+    B, Hkv, cap, D = 2, 1, 7, 64
+    first = g.KVCache(B, Hkv, cap, D, dtype, dev)
+    first.append(randn((B, Hkv, cap, D), 30).to(dev), randn((B, Hkv, cap, D), 31).to(dev))
+    torch.cuda.synchronize()
+    del first
+    cache = g.KVCache(B, Hkv, cap, D, dtype, dev)
+    for name, st in (("keys", cache.keys()), ("values", cache.values())):
+        data = st.data if dtype == "q8_0" else st
+        nbytes = data.numel() * data.element_size()
+        assert nbytes == (B * Hkv * cap * (D // 32 * 34) if dtype == "q8_0" else B * Hkv * cap * D * 2)
+        assert not data.contiguous().view(torch.uint8).any(), name
+
+
 def test_host_inputs_and_explicit_scale(dev):
     dtype, B, H, Hkv, D = torch.float16, 1, 2, 1, 128
     cache = g.KVCache(B, Hkv, 16, D, dtype, dev)
