@@ -23,7 +23,7 @@ __device__ inline uint32_t f2u(float f) { return __float_as_uint(f); }
 __device__ inline float u2f(uint32_t u) { return __uint_as_float(u); }
 
 // IEEE binary16 <-> binary32, round to nearest even (bit-exact with the host converter).
-__device__ inline uint16_t d_f32_to_f16(float f) {
+__device__ inline uint16_t d_f32_to_f16_bits(float f) {
     const uint32_t x = f2u(f);
     const uint32_t sign = (x >> 16) & 0x8000u;
     const uint32_t ax = x & 0x7fffffffu;
@@ -42,6 +42,15 @@ __device__ inline uint16_t d_f32_to_f16(float f) {
     const uint32_t rem = ax & 0x1fffu;
     if (rem > 0x1000u || (rem == 0x1000u && (r & 1u))) ++r;
     return (uint16_t)(sign | r);
+}
+
+// The same rounding by the hardware (v_cvt_f16_f32 in the default round-to-nearest-even mode,
+// half subnormals kept), a few times cheaper than the bit-level routine; a NaN keeps the
+// routine's payload rule.  The two agree on every non-NaN input (a GPU test checks every Q8_0
+// value q * d: all 2^16 scale bit patterns times all 256 quants).
+__device__ inline uint16_t d_f32_to_f16(float f) {
+    if (f != f) return d_f32_to_f16_bits(f);
+    return __builtin_bit_cast(uint16_t, (_Float16)f);
 }
 
 __device__ inline float d_f16_to_f32(uint16_t h) {

@@ -31,6 +31,29 @@ def test_quantize_and_dequantize_are_bit_exact(dev):
         assert np.array_equal(y.float().cpu().numpy(), torch.from_numpy(ref).to(dt).float().numpy())
 
 
+def test_dequantize_to_float16_every_scale_and_quant(dev):
+    """Every Q8_0 value q * d (all 2^16 scale bit patterns, including subnormal, infinite and NaN
+    scales, times all 256 int8 quants) dequantized to float16 on the device equals the
+    round-to-nearest-even float16 of the exact float32 product, computed here by numpy; NaN
+    products stay NaN (their payload bits are not compared: inf * 0 has no portable payload)."""
+    nd = 65536
+    d_bits = np.arange(nd, dtype=np.uint32).astype(np.uint16)
+    quants = (np.arange(256) - 128).astype(np.int8).reshape(8, 32)  # 8 blocks per scale
+    nb = nd * 8
+    blocks = np.zeros((nb, 34), np.uint8)
+    blocks[:, 0:2] = np.repeat(d_bits, 8).view(np.uint8).reshape(nb, 2)
+    blocks[:, 2:] = np.tile(quants, (nd, 1)).view(np.uint8)
+    qt = g.QuantizedTensor(torch.from_numpy(blocks.reshape(-1)).to(dev), (nb, 32))
+    got = g.dequantize(qt, torch.float16).cpu().numpy().view(np.uint16).reshape(nb, 32)
+    with np.errstate(over="ignore", invalid="ignore"):
+        y = np.tile(quants, (nd, 1)).astype(np.float32) * np.repeat(d_bits.view(np.float16).astype(np.float32), 8)[:, None]
+        want = y.astype(np.float16).view(np.uint16)
+    nan = np.isnan(y)
+    assert nan.any() and np.isinf(y).any() and (np.abs(y[y != 0]) < 2 ** -14).any()
+    assert np.array_equal(got[~nan], want[~nan])
+    assert np.isnan(got.view(np.float16)[nan]).all()
+
+
 def test_quantize_host_and_half_inputs(dev):
     x = randn((4, 96), 3, torch.float16)
     q = g.quantize(x)  # host input: quantized on the device, returned on the host
