@@ -190,15 +190,55 @@ __device__ inline void q8_0_quantize_lane(float v, bool live, uint8_t *b, int j)
     }
 }
 
-// 64 lanes = two blocks of 32 values; lane j of a half handles value j of its block.
-__global__ void q8_0_quantize_kernel(const float *__restrict__ x, uint8_t *__restrict__ out, int64_t nblocks) {
-    const int lane = threadIdx.x & 63;
-    const int64_t wave = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
-    const int64_t blk = wave * 2 + (lane >> 5);
-    const int j = lane & 31;
+// 64 blocks per workgroup of 256 threads, four threads per block: thread t quantizes values
+// 8 (t % 4) .. +7 of block t / 4 (two 16-byte loads; the block's |x| max over its four threads
+// by two lane exchanges), with the same operations as q8_0_quantize_lane.  A full tile whose
+// output starts 16-byte aligned (34 * 64 = 2176 bytes) is assembled in LDS and written with
+// 16-byte stores; otherwise every thread stores its bytes directly.
+__global__ __launch_bounds__(256) void q8_0_quantize_kernel(const float *__restrict__ x, uint8_t *__restrict__ out,
+                                                            int64_t nblocks) {
+    __shared__ __attribute__((aligned(16))) uint8_t tile[64 * 34];
+    const int tid = threadIdx.x, part = tid & 3;
+    const int64_t blk0 = (int64_t)blockIdx.x * 64, blk = blk0 + (tid >> 2);
     const bool live = blk < nblocks;
-    const float v = live ? x[blk * 32 + j] : 0.0f;
-    q8_0_quantize_lane(v, live, out + (live ? blk : 0) * 34, j);
+    float v[8];
+    const float *src = x + (live ? blk : 0) * 32 + 8 * part;
+    if ((uintptr_t)x % 16 == 0) {
+        const float4 a = ((const float4 *)src)[0], b = ((const float4 *)src)[1];
+        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+    } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = src[e];
+    }
+    float amax = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(v[e]));
+    // the four threads of a block are lanes 4k .. 4k+3 of one wavefront
+    amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+    amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
+    const float d = __fdiv_rn(amax, 127.0f);
+    const float id = d != 0.0f ? __fdiv_rn(1.0f, d) : 0.0f;
+    uint32_t w[2] = {0u, 0u};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) w[e >> 2] |= (uint32_t)(uint8_t)(int8_t)roundf(v[e] * id) << (8 * (e & 3));
+    const uint16_t h = d_f32_to_f16(d);
+    // uniform over the workgroup: every thread takes the same branch (the barrier is inside one)
+    if (blk0 + 64 <= nblocks && (uintptr_t)out % 16 == 0) {
+        uint16_t *tb = (uint16_t *)&tile[34 * (tid >> 2)];  // 2-byte aligned: 34 is even
+        if (part == 0) tb[0] = h;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) tb[1 + 4 * part + i] = (uint16_t)(w[i >> 1] >> (16 * (i & 1)));
+        __syncthreads();
+        if (tid < 136) *(uint4 *)(out + blk0 * 34 + 16 * tid) = *(const uint4 *)&tile[16 * tid];
+    } else if (live) {
+        uint8_t *b = out + blk * 34;
+        if (part == 0) {
+            b[0] = (uint8_t)(h & 0xff);
+            b[1] = (uint8_t)(h >> 8);
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) b[2 + 8 * part + e] = (uint8_t)(w[e >> 2] >> (8 * (e & 3)));
+    }
 }
 
 // KV-cache append: row (b, h, t) of src (B, Hkv, T, D), any strides, goes to row pos[b] + t of
@@ -369,9 +409,9 @@ hipError_t gt_launch_convert(const void *src, int src_dtype, const gt_layout &sr
 
 hipError_t gt_launch_q8_0_quantize(const float *src, void *dst, int64_t nblocks, hipStream_t stream) {
     if (nblocks <= 0) return hipSuccess;
-    const int64_t waves = (nblocks + 1) / 2;
-    hipLaunchKernelGGL(q8_0_quantize_kernel, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, stream, src,
-                       (uint8_t *)dst, nblocks);
+    const int64_t wgs = (nblocks + 63) / 64;
+    if (wgs > 0x7fffffffLL) return hipErrorInvalidConfiguration;
+    hipLaunchKernelGGL(q8_0_quantize_kernel, dim3((unsigned)wgs), dim3(256), 0, stream, src, (uint8_t *)dst, nblocks);
     return hipGetLastError();
 }
 

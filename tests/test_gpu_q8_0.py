@@ -31,6 +31,20 @@ def test_quantize_and_dequantize_are_bit_exact(dev):
         assert np.array_equal(y.float().cpu().numpy(), torch.from_numpy(ref).to(dt).float().numpy())
 
 
+@pytest.mark.parametrize("nblocks,offset", [(64 * 37 + 13, 0), (64 * 5, 1), (7, 3)])
+def test_quantize_tiles_tails_and_misaligned_inputs(dev, nblocks, offset):
+    """Whole 64-block tiles (assembled in LDS, 16-byte stores), a ragged last tile and an input
+    view that starts off 16-byte alignment (element loads) all give the oracle's bytes."""
+    rng = np.random.default_rng(nblocks + offset)
+    x = (rng.standard_normal(nblocks * 32 + offset) * rng.choice([1e-3, 1.0, 300.0], nblocks * 32 + offset))
+    x = x.astype(np.float32)
+    x[offset:offset + 32] = 0.0
+    xd = torch.from_numpy(x).to(dev)[offset:].reshape(nblocks, 32)
+    assert xd.data_ptr() % 16 == (4 * offset) % 16
+    q = g.quantize(xd)
+    assert np.array_equal(q.data.cpu().numpy(), oracle.q8_0_quantize(x[offset:]))
+
+
 def test_dequantize_to_float16_every_scale_and_quant(dev):
     """Every Q8_0 value q * d (all 2^16 scale bit patterns, including subnormal, infinite and NaN
     scales, times all 256 int8 quants) dequantized to float16 on the device equals the
