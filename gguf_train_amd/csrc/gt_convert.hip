@@ -278,6 +278,124 @@ __global__ void kv_append_kernel(const void *__restrict__ src, int sdt, int64_t 
     }
 }
 
+// float16 bits -> float32: the hardware conversion (exact) except for NaNs, which keep
+// d_f16_to_f32's payload rule
+__device__ inline float d_f16_to_f32_fast(uint16_t h) {
+    if ((h & 0x7c00u) == 0x7c00u && (h & 0x3ffu)) return d_f16_to_f32(h);
+    return (float)__builtin_bit_cast(_Float16, h);
+}
+
+// 8 consecutive elements of a float32 / float16 / bfloat16 source as float32 (exact), from a
+// 16-byte aligned address.
+template <int SDT>
+__device__ inline void load8(const void *base, int64_t e0, float *v) {
+    if constexpr (SDT == GT_F32) {
+        const float4 a = ((const float4 *)((const float *)base + e0))[0];
+        const float4 c = ((const float4 *)((const float *)base + e0))[1];
+        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = c.x; v[5] = c.y; v[6] = c.z; v[7] = c.w;
+    } else {
+        const uint4 q = *(const uint4 *)((const uint16_t *)base + e0);
+        const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            if constexpr (SDT == GT_F16) {
+                v[2 * i] = d_f16_to_f32_fast((uint16_t)(w[i] & 0xffffu));
+                v[2 * i + 1] = d_f16_to_f32_fast((uint16_t)(w[i] >> 16));
+            } else {
+                v[2 * i] = u2f(w[i] << 16);
+                v[2 * i + 1] = u2f(w[i] & 0xffff0000u);
+            }
+        }
+    }
+}
+
+// KV-cache append, fast path: source rows of D contiguous float32 / float16 / bfloat16 elements
+// starting 16-byte aligned (and, with RoPE, n_dims a multiple of 16, so that no 8-element chunk
+// straddles n_dims or a NeoX half).  One thread per 8 consecutive elements of a row: 16- or
+// 32-byte loads and stores, 32-bit index arithmetic below the row.  Same values and bytes as
+// kv_append_kernel: the rotation in float32 rounded to the source dtype, then the cache dtype;
+// a Q8_0 cache quantizes with four threads per block (the block's |x| max by two lane
+// exchanges) and the operations of q8_0_quantize_lane.
+template <int SDT, int DDT>
+__global__ __launch_bounds__(256) void kv_append_vec_kernel(const void *__restrict__ src, int64_t s_sb, int64_t s_sh,
+                                                            int64_t s_st, void *__restrict__ dst,
+                                                            const int32_t *__restrict__ pos, int Hkv, int T, int D,
+                                                            int64_t cap, int64_t n8, const float2 *__restrict__ rope_table,
+                                                            int n_dims, int neox) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const bool live = i < n8;
+    const int64_t ic = live ? i : 0;
+    const int per = D / 8;
+    const int j = (int)(ic % per);
+    const int64_t r = ic / per;  // source row (b, h, t)
+    const int t = (int)(r % T);
+    const int64_t bh = r / T;
+    const int h = (int)(bh % Hkv);
+    const int64_t b = bh / Hkv;
+    const int d0 = 8 * j;
+    const int64_t srow = b * s_sb + h * s_sh + (int64_t)t * s_st;
+    float v[8];
+    load8<SDT>(src, srow + d0, v);
+    if (rope_table && d0 < n_dims) {
+        const int half = n_dims / 2;
+        const bool lo_chunk = d0 < half;  // NeoX: the whole chunk is on one side of half
+        float w[8];
+        if (neox) load8<SDT>(src, srow + (lo_chunk ? d0 + half : d0 - half), w);
+        float rr[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const int d = d0 + e;
+            const bool lo = neox ? lo_chunk : (e & 1) == 0;
+            const float other = neox ? w[e] : v[e ^ 1];
+            const int pair = neox ? (lo ? d : d - half) : (d >> 1);
+            const float2 cs = rope_table[((int64_t)b * T + t) * half + pair];
+            float x = lo ? rope_rot_lo(v[e], other, cs) : rope_rot_hi(other, v[e], cs);
+            if constexpr (SDT == GT_F16) x = d_f16_to_f32(d_f32_to_f16(x));
+            else if constexpr (SDT == GT_BF16) x = u2f((uint32_t)d_f32_to_bf16(x) << 16);
+            rr[e] = x;
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = rr[e];
+    }
+    const int64_t row = ((int64_t)b * Hkv + h) * cap + pos[b] + t;
+    if constexpr (DDT == GT_Q8_0) {
+        // the four threads of a block are lanes 4k .. 4k+3 (D / 8 is a multiple of 4), all live or
+        // none (n8 is too)
+        float amax = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(v[e]));
+        amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+        amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
+        const float d = __fdiv_rn(amax, 127.0f);
+        const float id = d != 0.0f ? __fdiv_rn(1.0f, d) : 0.0f;
+        if (!live) return;
+        uint16_t *blk = (uint16_t *)((uint8_t *)dst + (row * (D / 32) + d0 / 32) * 34);  // 34 is even
+        const int part = j & 3;
+        if (part == 0) blk[0] = d_f32_to_f16(d);
+#pragma unroll
+        for (int e = 0; e < 8; e += 2) {
+            const uint32_t q0 = (uint8_t)(int8_t)roundf(v[e] * id), q1 = (uint8_t)(int8_t)roundf(v[e + 1] * id);
+            blk[1 + 4 * part + e / 2] = (uint16_t)(q0 | (q1 << 8));
+        }
+    } else {
+        if (!live) return;
+        const int64_t o = row * D + d0;
+        if constexpr (DDT == GT_F32) {
+            ((float4 *)((float *)dst + o))[0] = make_float4(v[0], v[1], v[2], v[3]);
+            ((float4 *)((float *)dst + o))[1] = make_float4(v[4], v[5], v[6], v[7]);
+        } else {
+            uint32_t w[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const uint32_t a = DDT == GT_F16 ? d_f32_to_f16(v[2 * k]) : d_f32_to_bf16(v[2 * k]);
+                const uint32_t c = DDT == GT_F16 ? d_f32_to_f16(v[2 * k + 1]) : d_f32_to_bf16(v[2 * k + 1]);
+                w[k] = a | (c << 16);
+            }
+            *(uint4 *)((uint16_t *)dst + o) = make_uint4(w[0], w[1], w[2], w[3]);
+        }
+    }
+}
+
 // KV-cache append of rows that are already Q8_0: row (b, h, t) of the dense Q8_0 src
 // (B, Hkv, T, D) is copied, block bytes unchanged, to row pos[b] + t of the Q8_0 cache.  A row is
 // D / 32 blocks of 34 bytes; one thread moves one 16-bit half-word of it.
@@ -458,6 +576,24 @@ hipError_t gt_launch_fill_zero(void *p, int64_t bytes, hipStream_t stream) {
     return hipGetLastError();
 }
 
+template <int SDT>
+hipError_t launch_kv_append_vec(const void *src, const int64_t *st, void *dst, int ddt, const int32_t *pos, int64_t Hkv,
+                                int64_t T, int64_t D, int64_t cap, int64_t n8, const gt_rope_apply *rope,
+                                hipStream_t stream) {
+    const dim3 grid((unsigned)((n8 + 255) / 256));
+    const float2 *tab = rope ? (const float2 *)rope->table : nullptr;
+    const int nd = rope ? rope->n_dims : 0, nx = rope ? rope->neox : 0;
+#define GT_KV_APPEND_VEC(DDT)                                                                                          \
+    hipLaunchKernelGGL((kv_append_vec_kernel<SDT, DDT>), grid, dim3(256), 0, stream, src, st[0], st[1], st[2], dst, pos, \
+                       (int)Hkv, (int)T, (int)D, cap, n8, tab, nd, nx)
+    if (ddt == GT_F32) GT_KV_APPEND_VEC(GT_F32);
+    else if (ddt == GT_F16) GT_KV_APPEND_VEC(GT_F16);
+    else if (ddt == GT_BF16) GT_KV_APPEND_VEC(GT_BF16);
+    else GT_KV_APPEND_VEC(GT_Q8_0);
+#undef GT_KV_APPEND_VEC
+    return hipGetLastError();
+}
+
 hipError_t gt_launch_kv_append(const void *src, int src_dtype, const int64_t *src_strides, void *dst, int dst_dtype,
                                const int32_t *pos, int64_t B, int64_t Hkv, int64_t T, int64_t D, int64_t cap,
                                const gt_rope_apply *rope, hipStream_t stream) {
@@ -466,6 +602,20 @@ hipError_t gt_launch_kv_append(const void *src, int src_dtype, const int64_t *sr
     const int64_t blocks = (n + 255) / 256;
     if (blocks > 0x7fffffffLL) return hipErrorInvalidConfiguration;
     if (rope && (rope->n_dims < 2 || rope->n_dims % 2 != 0 || rope->n_dims > D)) return hipErrorInvalidValue;
+    // fast path: contiguous rows of a float32 / float16 / bfloat16 source starting 16-byte aligned
+    const int es = src_dtype == GT_F32 ? 4 : 2;
+    const bool vec_src = src_dtype == GT_F32 || src_dtype == GT_F16 || src_dtype == GT_BF16;
+    const bool vec_dst = dst_dtype == GT_F32 || dst_dtype == GT_F16 || dst_dtype == GT_BF16 || dst_dtype == GT_Q8_0;
+    if (vec_src && vec_dst && src_strides[3] == 1 && D % 8 == 0 && (uintptr_t)src % 16 == 0 &&
+        (src_strides[0] * es) % 16 == 0 && (src_strides[1] * es) % 16 == 0 && (src_strides[2] * es) % 16 == 0 &&
+        (uintptr_t)dst % 16 == 0 && (!rope || rope->n_dims % 16 == 0) && T < (1LL << 31) && D < (1LL << 31) &&
+        Hkv < (1LL << 31) && (dst_dtype != GT_Q8_0 || D % 32 == 0)) {
+        const int64_t n8 = n / 8;
+        if ((n8 + 255) / 256 > 0x7fffffffLL) return hipErrorInvalidConfiguration;
+        if (src_dtype == GT_F32) return launch_kv_append_vec<GT_F32>(src, src_strides, dst, dst_dtype, pos, Hkv, T, D, cap, n8, rope, stream);
+        if (src_dtype == GT_F16) return launch_kv_append_vec<GT_F16>(src, src_strides, dst, dst_dtype, pos, Hkv, T, D, cap, n8, rope, stream);
+        return launch_kv_append_vec<GT_BF16>(src, src_strides, dst, dst_dtype, pos, Hkv, T, D, cap, n8, rope, stream);
+    }
     hipLaunchKernelGGL(kv_append_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, src, src_dtype, src_strides[0],
                        src_strides[1], src_strides[2], src_strides[3], dst, dst_dtype, pos, Hkv, T, D, cap, n,
                        rope ? (const float2 *)rope->table : nullptr, rope ? rope->n_dims : 0, rope ? rope->neox : 0);

@@ -111,6 +111,35 @@ def test_q8_0_cache_rows_and_attention(dev, D):
         assert_close(got, want, torch.float16, f"q8_0 L={L}")
 
 
+@pytest.mark.parametrize("rope", [None, {"mode": 0}, {"mode": 2}, {"mode": 2, "n_dims": 64}, {"mode": 0, "n_dims": 40}])
+@pytest.mark.parametrize("cache_dtype,src_dtype", [
+    (torch.float16, torch.float16), (torch.bfloat16, torch.bfloat16), (torch.float32, torch.float32),
+    (torch.float16, torch.float32), (torch.bfloat16, torch.float16), (torch.float32, torch.bfloat16),
+    ("q8_0", torch.float32), ("q8_0", torch.float16), ("q8_0", torch.bfloat16)])
+def test_dense_rows_append_the_same_bytes_as_strided_rows(dev, cache_dtype, src_dtype, rope):
+    """Dense, 16-byte aligned source rows (appended 8 elements per thread) and the same values as
+    a view with a non-unit stride along D (one element per thread) fill the cache with the same
+    bytes, RoPE on append included (n_dims 40 is not a multiple of 16: both take the general
+    path there)."""
+    B, Hkv, D = 2, 3, 128
+    dense = g.KVCache(B, Hkv, 64, D, cache_dtype, dev)
+    strided = g.KVCache(B, Hkv, 64, D, cache_dtype, dev)
+    for T, seed in ((45, 1), (7, 2)):
+        k = randn((B, Hkv, T, D), seed, src_dtype, scale=3.0).to(dev)
+        v = randn((B, Hkv, T, D), seed + 10, src_dtype, scale=3.0).to(dev)
+        k[0, 0, 0, :32] = 0.0  # an all-zero Q8_0 block
+        ks, vs = (x.transpose(2, 3).contiguous().transpose(2, 3) for x in (k, v))
+        assert ks.stride(3) == T and torch.equal(ks, k)
+        dense.append(k, v, rope=rope)
+        strided.append(ks, vs, rope=rope)
+    for a, b in ((dense.keys(), strided.keys()), (dense.values(), strided.values())):
+        if cache_dtype == "q8_0":
+            assert torch.equal(a.data, b.data)
+        else:
+            assert torch.equal(a.view(torch.int16 if a.element_size() == 2 else torch.int32),
+                               b.view(torch.int16 if b.element_size() == 2 else torch.int32))
+
+
 @pytest.mark.parametrize("dtype", [torch.float16, "q8_0"])
 def test_a_new_cache_starts_zero_filled(dev, dtype):
     """A cache's storage is zero-filled when it is created (by a fill kernel, byte by byte past
