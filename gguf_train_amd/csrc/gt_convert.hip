@@ -509,6 +509,46 @@ __global__ void unpad_rows_kernel(const E *__restrict__ src, int64_t Dp, E *__re
         dst[i] = src[(i / D) * Dp + i % D];
 }
 
+// The same two copies with 8 elements of ES bytes (16 or 32 bytes) per thread, for D % 8 == 0
+// and 16-byte aligned rows: a destination chunk of pad_rows is all source or all zero, and
+// every chunk starts at a 16-byte boundary on both sides.
+template <int ES>
+__global__ void pad_rows_vec_kernel(const uint8_t *__restrict__ src, int64_t sb, int64_t sh, int64_t sl, int64_t H,
+                                    int64_t L, int D, uint8_t *__restrict__ dst, int Dp, int64_t n8) {
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    const int per = Dp / 8;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n8; i += stride) {
+        const int64_t r = i / per;
+        const int d0 = 8 * (int)(i - r * per);
+        const int64_t l = r % L, bh = r / L, h = bh % H, b = bh / H;
+        uint4 x[ES / 2];
+#pragma unroll
+        for (int k = 0; k < ES / 2; ++k) x[k] = make_uint4(0u, 0u, 0u, 0u);
+        if (d0 < D) {
+            const uint4 *sp = (const uint4 *)(src + (b * sb + h * sh + l * sl + d0) * ES);
+#pragma unroll
+            for (int k = 0; k < ES / 2; ++k) x[k] = sp[k];
+        }
+        uint4 *dp = (uint4 *)(dst + i * 8 * ES);
+#pragma unroll
+        for (int k = 0; k < ES / 2; ++k) dp[k] = x[k];
+    }
+}
+template <int ES>
+__global__ void unpad_rows_vec_kernel(const uint8_t *__restrict__ src, int Dp, uint8_t *__restrict__ dst, int D,
+                                      int64_t n8) {
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    const int per = D / 8;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n8; i += stride) {
+        const int64_t r = i / per;
+        const int d0 = 8 * (int)(i - r * per);
+        const uint4 *sp = (const uint4 *)(src + (r * Dp + d0) * ES);
+        uint4 *dp = (uint4 *)(dst + i * 8 * ES);
+#pragma unroll
+        for (int k = 0; k < ES / 2; ++k) dp[k] = sp[k];
+    }
+}
+
 inline unsigned grid_for(int64_t n, int block) {
     const int64_t g = (n + block - 1) / block;
     return (unsigned)(g < 65536 * 16 ? (g > 0 ? g : 1) : 65536 * 16);
@@ -638,6 +678,20 @@ hipError_t gt_launch_pad_rows(const void *src, int elem_bytes, const int64_t *st
                               int64_t D, void *dst, int64_t Dp, hipStream_t stream) {
     const int64_t n = B * H * L * Dp;
     if (n <= 0) return hipSuccess;
+    const bool vec = (elem_bytes == 2 || elem_bytes == 4) && D % 8 == 0 && Dp % 8 == 0 && (uintptr_t)src % 16 == 0 &&
+                     (uintptr_t)dst % 16 == 0 && (strides[0] * elem_bytes) % 16 == 0 &&
+                     (strides[1] * elem_bytes) % 16 == 0 && (strides[2] * elem_bytes) % 16 == 0 && Dp < (1LL << 30);
+    if (vec) {
+        if (elem_bytes == 2)
+            hipLaunchKernelGGL(pad_rows_vec_kernel<2>, dim3(grid_for(n / 8, 256)), dim3(256), 0, stream,
+                               (const uint8_t *)src, strides[0], strides[1], strides[2], H, L, (int)D, (uint8_t *)dst,
+                               (int)Dp, n / 8);
+        else
+            hipLaunchKernelGGL(pad_rows_vec_kernel<4>, dim3(grid_for(n / 8, 256)), dim3(256), 0, stream,
+                               (const uint8_t *)src, strides[0], strides[1], strides[2], H, L, (int)D, (uint8_t *)dst,
+                               (int)Dp, n / 8);
+        return hipGetLastError();
+    }
     if (elem_bytes == 2)
         hipLaunchKernelGGL(pad_rows_kernel<uint16_t>, dim3(grid_for(n, 256)), dim3(256), 0, stream, (const uint16_t *)src,
                            strides[0], strides[1], strides[2], H, L, D, (uint16_t *)dst, Dp, n);
@@ -653,6 +707,16 @@ hipError_t gt_launch_unpad_rows(const void *src, int elem_bytes, int64_t rows, i
                                 hipStream_t stream) {
     const int64_t n = rows * D;
     if (n <= 0) return hipSuccess;
+    if ((elem_bytes == 2 || elem_bytes == 4) && D % 8 == 0 && Dp % 8 == 0 && (uintptr_t)src % 16 == 0 &&
+        (uintptr_t)dst % 16 == 0 && Dp < (1LL << 30)) {
+        if (elem_bytes == 2)
+            hipLaunchKernelGGL(unpad_rows_vec_kernel<2>, dim3(grid_for(n / 8, 256)), dim3(256), 0, stream,
+                               (const uint8_t *)src, (int)Dp, (uint8_t *)dst, (int)D, n / 8);
+        else
+            hipLaunchKernelGGL(unpad_rows_vec_kernel<4>, dim3(grid_for(n / 8, 256)), dim3(256), 0, stream,
+                               (const uint8_t *)src, (int)Dp, (uint8_t *)dst, (int)D, n / 8);
+        return hipGetLastError();
+    }
     if (elem_bytes == 2)
         hipLaunchKernelGGL(unpad_rows_kernel<uint16_t>, dim3(grid_for(n, 256)), dim3(256), 0, stream,
                            (const uint16_t *)src, Dp, (uint16_t *)dst, D, n);

@@ -66,7 +66,9 @@ def test_padded_heads_match_the_oracle(dev, dtype, B, H, Hkv, L, S, D, Dv, causa
         assert_close(got, ref, torch.bfloat16, name, out_dtype=torch.float32)
 
 
-@pytest.mark.parametrize("dtype,D", [(torch.float16, 96), (torch.bfloat16, 40)])
+# D % 8 == 0: the 8-element pad / unpad copies; 100 and 36: the one-element copies
+@pytest.mark.parametrize("dtype,D", [(torch.float16, 96), (torch.bfloat16, 40), (torch.float16, 100),
+                                     (torch.bfloat16, 36)])
 def test_padding_is_the_unpadded_kernel_on_zero_padded_heads(dev, dtype, D):
     B, H, L, S = 2, 4, 130, 130
     Dp = 64 if D <= 64 else 128
