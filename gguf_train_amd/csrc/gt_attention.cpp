@@ -536,29 +536,41 @@ extern "C" gt_tensor *gt_flash_attention_rope(const gt_tensor *q, const gt_tenso
     Temps tmp;
     const gt_tensor *kd =
         k->device_type == GT_DEV_CUDA && k->device_index == dev ? k : tmp.keep(gt_to_device_dense(k, dev, -1));
-    const gt_tensor *kr = kd ? tmp.keep(gt_rope(kd, pos, n_dims, mode, 0, freq_base, freq_scale)) : nullptr;
-    if (!kr) return nullptr;
+    if (!kd) return nullptr;
     gt_tensor *o = nullptr;
     const bool key_padding = !mask || (mask->dtype != GT_BOOL && mask->shape[mask->ndim - 2] == 1);
     if ((q->dtype == GT_F16 || q->dtype == GT_BF16) && k->dtype == q->dtype && v->dtype == q->dtype &&
-        q->device_type == GT_DEV_CUDA && n_dims == D && (D == 64 || D == 128) && L > 1 && key_padding) {
+        q->device_type == GT_DEV_CUDA && n_dims == D && (D == 64 || D == 128) && L > 1 && key_padding &&
+        kd->ndim == 4) {
+        // one int32 copy of the positions and one (cos, sin) table for the first max(L, S) of them:
+        // the keys are rotated with it here, the prefill kernel rotates the queries (rows 0..L-1)
+        // as it loads them; the same values as gt_rope's own table for either
         const gt_tensor *pd = (pos->device_type == GT_DEV_CUDA && pos->device_index == dev && pos->dtype == GT_I32 &&
                                gt_is_dense(pos))
                                   ? pos
                                   : tmp.keep(gt_to_device_dense(pos, dev, GT_I32));
         gt_scratch table;
-        if (!pd || !gt_scratch_alloc(table, (size_t)L * (size_t)(D / 2) * 2 * sizeof(float), dev) ||
-            !gt_hip_check(gt_launch_rope_table((const int32_t *)gt_data(pd), nullptr, 1, L, n_dims,
+        gt_tensor *kr = pd ? tmp.keep(gt_new_tensor(4, kd->shape, kd->dtype, GT_DEV_CUDA, dev)) : nullptr;
+        if (!kr || !gt_scratch_alloc(table, (size_t)need * (size_t)(D / 2) * 2 * sizeof(float), dev) ||
+            !gt_hip_check(gt_launch_rope_table((const int32_t *)gt_data(pd), nullptr, 1, need, n_dims,
                                                gt_rope_theta_scale(freq_base, n_dims), freq_scale, 0, table.ptr(),
                                                gt_stream()),
-                          "rope table kernel"))
+                          "rope table kernel") ||
+            !gt_hip_check(gt_launch_rope(gt_data(kd), kd->dtype, kd->strides, gt_data(kr), table.ptr(), 0, kd->shape[0],
+                                         kd->shape[1], S, D, n_dims, mode, gt_stream()),
+                          "rope kernel"))
             return nullptr;
         const QRope qr{table.ptr(), mode == 2 ? 1 : 0};
         const int rc = attention_forward(who, q, kr, v, mask, scale, is_causal, &o, nullptr, nullptr, &qr);
         if (rc < 0) return nullptr;
         if (rc == 0) return o;
+        // the kernel declined the rotated-query form (rc > 0): rotate q and attend below
+        const gt_tensor *qr2 = tmp.keep(gt_rope(q, pd, n_dims, mode, 0, freq_base, freq_scale));
+        if (!qr2 || attention_forward(who, qr2, kr, v, mask, scale, is_causal, &o, nullptr) != 0) return nullptr;
+        return o;
     }
-    const gt_tensor *qr = tmp.keep(gt_rope(q, pos, n_dims, mode, 0, freq_base, freq_scale));
+    const gt_tensor *kr = tmp.keep(gt_rope(kd, pos, n_dims, mode, 0, freq_base, freq_scale));
+    const gt_tensor *qr = kr ? tmp.keep(gt_rope(q, pos, n_dims, mode, 0, freq_base, freq_scale)) : nullptr;
     if (!qr || attention_forward(who, qr, kr, v, mask, scale, is_causal, &o, nullptr) != 0) return nullptr;
     return o;
 }
