@@ -118,6 +118,118 @@ __global__ __launch_bounds__(64 * WQ) void attn_weights_kernel(AttnFwdArgs f, vo
     }
 }
 
+// The same weights for S % 8 == 0 and a 16-byte aligned output: key tiles of 64 (two 32-key
+// blocks), S^T = K.Q^T so that a lane holds one query row (its log-sum-exp in one register) and
+// four consecutive keys per register group, Q in registers when there is one head, blocks with
+// every weight visible and no mask computed without the per-element tests, and the wavefront's
+// 32 x 64 tile transposed through LDS (8-byte writes, rows padded by 16 bytes) so that each lane
+// stores 16-byte pieces: 8 lanes write a row's 64 keys (128 bytes) where attn_weights_kernel
+// stores 2 bytes per lane.  The same operations per weight, so the same bits.
+template <typename T, int D, bool CAUSAL, int MASK, bool AVG>
+__global__ __launch_bounds__(64 * WQ) void attn_weights_vec_kernel(AttnFwdArgs f, void *wout, int64_t nrb) {
+    using M = Mfma<T>;
+    using V8 = typename M::V8;
+    constexpr int DT = D / 16;
+    constexpr int RP = 64 + 8;  // LDS row pitch (elements): 64 keys and 16 bytes of padding
+    __shared__ __attribute__((aligned(16))) T tile[WQ][32 * RP];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int lrow = lane & 31, half = lane >> 5;
+    const int64_t rb = blockIdx.x % nrb, g = blockIdx.x / nrb;
+    const int64_t b = AVG ? g : g / f.H;
+    const int L = (int)f.L, S = (int)f.S;
+    const int q0 = (int)rb * 32 * WQ + 32 * w;  // first query row of this wavefront
+    const int q = q0 + lrow;                    // this lane's query row
+    const int qc = min(q, L - 1);
+    const float c = f.scale * kLog2e;
+    const int nh = AVG ? (int)f.H : 1;
+    const float inv_h = 1.0f / (float)nh;
+    const int kv_end = CAUSAL ? min(q0 + 32, S) : S;  // keys any of the wave's rows can see
+    const int nkt = (S + 63) / 64;
+    T *tw = tile[w];
+    // one head: its Q fragments (query row lrow, d = 16t + 8half + 0..7) and log2(e) * lse
+    V8 qf[DT];
+    float ls1 = 0.0f;
+    if (!AVG) {
+        const int64_t h = g % f.H;
+        const T *qr = (const T *)f.q + b * f.q_sb + h * f.q_sh + (int64_t)qc * f.q_sl + 8 * half;
+#pragma unroll
+        for (int t = 0; t < DT; ++t) qf[t] = __builtin_bit_cast(V8, *(const u32x4 *)(qr + 16 * t));
+        ls1 = ((const float *)f.lse)[g * f.L + qc] * kLog2e;
+    }
+    const int64_t base = AVG ? b * f.L : g * f.L;
+    for (int kt = 0; kt < nkt; ++kt) {
+        const int k0 = kt * 64;
+        f32x16 acc[2];
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) acc[kb][i] = 0.0f;
+        for (int hh = 0; hh < nh; ++hh) {
+            const int64_t h = AVG ? hh : g % f.H;
+            const int64_t hk = h / (f.H / f.Hkv);
+            V8 qa[DT];
+            float ls = ls1;
+            if constexpr (AVG) {
+                const T *qr = (const T *)f.q + b * f.q_sb + h * f.q_sh + (int64_t)qc * f.q_sl + 8 * half;
+#pragma unroll
+                for (int t = 0; t < DT; ++t) qa[t] = __builtin_bit_cast(V8, *(const u32x4 *)(qr + 16 * t));
+                ls = ((const float *)f.lse)[(b * f.H + h) * f.L + qc] * kLog2e;
+            } else {
+#pragma unroll
+                for (int t = 0; t < DT; ++t) qa[t] = qf[t];
+            }
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) {
+                const int kb0 = k0 + 32 * kb;
+                if (kb0 >= kv_end) continue;  // every weight of the block is 0 (acc stays 0)
+                // A = K rows (key kb0 + lrow), B = Q rows: sc[i] is key kb0 + 8(i/4) + 4half + i%4, query q
+                const T *kr = (const T *)f.k + b * f.k_sb + hk * f.k_sh + (int64_t)min(kb0 + lrow, S - 1) * f.k_ss + 8 * half;
+                f32x16 sc;
+#pragma unroll
+                for (int i = 0; i < 16; ++i) sc[i] = 0.0f;
+#pragma unroll
+                for (int t = 0; t < DT; ++t) sc = M::mma(__builtin_bit_cast(V8, *(const u32x4 *)(kr + 16 * t)), qa[t], sc);
+                const bool interior = MASK == 0 && kb0 + 31 < S && q0 + 31 < L && (!CAUSAL || kb0 + 31 <= q0);
+                if (interior) {
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) {
+                        const float p = exp2f(fmaf(sc[i], c, 0.0f * kLog2e - ls));
+                        acc[kb][i] += AVG ? p * inv_h : p;
+                    }
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) {
+                        const int key = kb0 + 8 * (i / 4) + 4 * half + (i % 4);
+                        bool blocked = key >= S || q >= L || (CAUSAL && key > q);
+                        const float add = mask_term<MASK>(f, b, h, qc, min(key, S - 1), blocked);
+                        const float p = blocked ? 0.0f : exp2f(fmaf(sc[i], c, add * kLog2e - ls));
+                        acc[kb][i] += AVG ? p * inv_h : p;
+                    }
+                }
+            }
+        }
+        // the tile into LDS as rows (query) x keys, four keys per 8-byte write, then 16-byte pieces
+        // out: piece u * 64 + lane is row (u * 64 + lane) / 8, keys 8 * (lane % 8) .. +7
+        __builtin_amdgcn_wave_barrier();  // the previous tile's reads are done
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int gq = 0; gq < 4; ++gq) {
+                T v4[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) v4[e] = (T)acc[kb][4 * gq + e];
+                *(u32x2 *)&tw[lrow * RP + 32 * kb + 8 * gq + 4 * half] = __builtin_bit_cast(u32x2, v4);
+            }
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int pc = u * 64 + lane, row = pc >> 3, key0 = k0 + 8 * (pc & 7);
+            const u32x4 piece = *(const u32x4 *)&tw[row * RP + 8 * (pc & 7)];
+            if (q0 + row < L && key0 < S) *(u32x4 *)((T *)wout + (base + q0 + row) * f.S + key0) = piece;
+        }
+    }
+}
+
 // Generic: one thread per (query, key), any float dtype, accumulation in A (double for float64).
 template <typename T, typename A, bool AVG>
 __global__ __launch_bounds__(256) void attn_weights_generic_kernel(AttnFwdArgs f, void *wout) {
@@ -180,7 +292,13 @@ hipError_t launch_mfma(const AttnFwdArgs &f, void *w, hipStream_t st) {
     const int64_t grid = nrb * (AVG ? f.B : f.B * f.H);
     if (grid > 0x7fffffffLL) return hipErrorInvalidConfiguration;
     const int mode = !f.mask ? 0 : (f.mask_bool ? 1 : 2);
-#define GT_W(C, MK) hipLaunchKernelGGL((attn_weights_kernel<T, D, C, MK, AVG>), dim3((unsigned)grid), dim3(64 * WQ), 0, st, f, w, nrb)
+    // whole 16-byte pieces of every row: the LDS-transposed kernel
+    const bool vec = f.S % 8 == 0 && (uintptr_t)w % 16 == 0;
+#define GT_W(C, MK)                                                                                                     \
+    do {                                                                                                                \
+        if (vec) hipLaunchKernelGGL((attn_weights_vec_kernel<T, D, C, MK, AVG>), dim3((unsigned)grid), dim3(64 * WQ), 0, st, f, w, nrb); \
+        else hipLaunchKernelGGL((attn_weights_kernel<T, D, C, MK, AVG>), dim3((unsigned)grid), dim3(64 * WQ), 0, st, f, w, nrb); \
+    } while (0)
     if (f.causal) {
         if (mode == 0) GT_W(true, 0);
         else if (mode == 1) GT_W(true, 1);
