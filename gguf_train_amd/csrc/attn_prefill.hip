@@ -642,9 +642,284 @@ hipError_t launch_variant(const AttnFwdArgs &a, int nq, int npairs, int64_t grid
     return hipGetLastError();
 }
 
+// ---- float32 --------------------------------------------------------------------------------
+// Float32 prefill (D = Dv = 64 or 128, no mask or a key-padding row): the structure of
+// prefill_fwd_kernel (query tiles of 128 rows in pairs, K/V tiles streamed into LDS by DMA, one
+// barrier per tile, the same lazy online softmax and causal / edge handling) on
+// v_mfma_f32_32x32x2_f32, whose products and sums are float32 like the generic kernel's.  The
+// MFMA's k index is free as long as both operands agree:
+//   S^T = K.Q^T: k-step t takes dim t + (D/2)(lane/32), so a lane's Q values are the dims
+//   [(D/2)(lane/32), +D/2) of its row, held in registers, and its K values come 4 at a time from
+//   one 16-byte LDS read;
+//   O^T += V^T.P^T: k-step s takes key 8(s/4) + 4(lane/32) + s%4, the key of the lane's S^T
+//   accumulator entry s, so P^T's operand for step s is that entry as it stands.
+// 32-key tiles: 16-byte chunk c of tile row r sits at chunk c ^ (r & 15), so the 16 rows one
+// quarter-wave reads land on 16 different chunks mod 16 (different LDS banks).
+constexpr int F32_NW = 4, F32_BM = 32 * F32_NW, F32_BN = 32, F32_NST = 2;
+
+__device__ inline f32x16 mfma_f32x2(float a, float b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+}
+
+template <int D, bool CAUSAL, int MASK>
+__global__ __launch_bounds__(64 * F32_NW, 2) void prefill_f32_kernel(AttnFwdArgs a, int nq, int npairs) {
+    constexpr int NW = F32_NW, BM = F32_BM, BN = F32_BN, NST = F32_NST;
+    constexpr int CH = D / 4;               // 16-byte chunks per row
+    constexpr int TILE = BN * D;            // floats per tile
+    constexpr int NPW = BN * CH / 64 / NW;  // 1 KB wave loads per operand, wave and tile
+    constexpr int DB = D / 32;              // d blocks of O^T
+    constexpr int DH = D / 2;               // dims per lane half in S^T
+    constexpr bool MROW = MASK == 4;
+    constexpr int PER = 2 * NPW + (MROW ? 1 : 0);  // loads per wave and tile
+    static_assert(NPW >= 1 && CH >= 16 && PER < 64, "tile split");
+    __shared__ __attribute__((aligned(1024))) float sK[NST][TILE];
+    __shared__ __attribute__((aligned(1024))) float sV[NST][TILE];
+    __shared__ __attribute__((aligned(16))) float sMk[MROW ? NST : 1][64];  // keys k0 .. k0+63 (32 used)
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lrow = lane & 31, half = lane >> 5;
+    const int64_t BH = a.B * a.H;
+    int pair;
+    int64_t bh;
+    if (BH % 8 == 0) {
+        const int64_t hpx = BH / 8, i = blockIdx.x / 8;
+        pair = (int)(i % npairs);
+        bh = (int64_t)(blockIdx.x % 8) * hpx + i / npairs;
+    } else {
+        pair = (int)(blockIdx.x % npairs);
+        bh = (int64_t)blockIdx.x / npairs;
+    }
+    const int64_t b = bh / a.H, h = bh % a.H, hk = h / (a.H / a.Hkv);
+    const int L = (int)a.L, S = (int)a.S;
+    const int nkv = attn_kv_len(a, b), qpos = attn_q_pos(a, b);
+    const int qa = nq - 1 - pair, qb = pair;
+    const int nparts = qa == qb ? 1 : 2;
+    const int na = key_tiles<CAUSAL, BM, BN>(qa, nkv, qpos);
+    const int total = na + (nparts == 2 ? key_tiles<CAUSAL, BM, BN>(qb, nkv, qpos) : 0);
+
+    const float *kbase = (const float *)a.k + b * a.k_sb + hk * a.k_sh;
+    const float *vbase = (const float *)a.v + b * a.v_sb + hk * a.v_sh;
+    const float c = a.scale * kLog2e;
+    const float inv_scale = 1.0f / a.scale;
+    const uint32_t k_row = (uint32_t)a.k_ss * 4, v_row = (uint32_t)a.v_ss * 4;
+    int lrow_n[NPW];
+    uint32_t lcol_n[NPW], kofs_n[NPW], vofs_n[NPW];
+#pragma unroll
+    for (int n = 0; n < NPW; ++n) {
+        const int slot = (w * NPW + n) * 64 + lane;
+        lrow_n[n] = slot / CH;
+        lcol_n[n] = 16u * (uint32_t)((slot % CH) ^ (lrow_n[n] & 15));
+        kofs_n[n] = (uint32_t)lrow_n[n] * k_row + lcol_n[n];
+        vofs_n[n] = (uint32_t)lrow_n[n] * v_row + lcol_n[n];
+    }
+    const float *mrow = MROW ? (const float *)a.mask + b * a.m_sb + h * a.m_sh : nullptr;
+    auto issue = [&](int step) {
+        const int kt = step < na ? step : step - na;
+        const int st = step % NST;
+        if constexpr (MROW)
+            lds_dma4(lds_addr(&sMk[st][0]), mrow, (uint32_t)min(kt * BN + lane, S - 1) * (uint32_t)a.m_ss * 4u);
+        const uint32_t dk = lds_addr(&sK[st][0]) + w * NPW * 1024;
+        const uint32_t dv = lds_addr(&sV[st][0]) + w * NPW * 1024;
+        if (kt * BN + BN <= S) {
+            const char *kb = (const char *)kbase + (uint64_t)(kt * BN) * k_row;
+            const char *vb = (const char *)vbase + (uint64_t)(kt * BN) * v_row;
+#pragma unroll
+            for (int n = 0; n < NPW; ++n) {
+                lds_dma16(dk + n * 1024, kb, kofs_n[n]);
+                lds_dma16(dv + n * 1024, vb, vofs_n[n]);
+            }
+        } else {
+#pragma unroll
+            for (int n = 0; n < NPW; ++n) {
+                const uint32_t key = (uint32_t)min(kt * BN + lrow_n[n], S - 1);
+                lds_dma16(dk + n * 1024, kbase, key * k_row + lcol_n[n]);
+                lds_dma16(dv + n * 1024, vbase, key * v_row + lcol_n[n]);
+            }
+        }
+    };
+    // LDS float offsets of this lane's fragments within a tile, as a per-lane part plus a
+    // compile-time part (the XOR swizzle only touches chunk bits 0..3, so it splits):
+    //   K, dims 4u .. 4u+3 of its half: row lrow, chunk (u + (D/8) half) ^ (lrow & 15)
+    //     = lrow D + (4u ^ 4 ((lrow & 15) ^ (D/8) half))  (u < D/8: u + (D/8) half = u ^ (D/8) half)
+    //   V, k-step s, d block db: row r = 8(s/4) + 4half + s%4, float d = 32db + lrow, chunk
+    //     (d/4) ^ (r & 15) = (8db ^ 8((s/4) & 1)) + ((lrow/4) ^ 4half ^ (s%4))
+    const int kbase0 = lrow * D, kx = 4 * ((lrow & 15) ^ ((D / 8) * half));
+    auto kofs = [&](int u) { return kbase0 + ((4 * u) ^ kx); };
+    const int vy = (lrow >> 2) ^ (4 * half);
+    int vx[4];
+#pragma unroll
+    for (int cc = 0; cc < 4; ++cc) vx[cc] = 4 * D * half + (lrow & 3) + 4 * (vy ^ cc);
+    auto vofs = [&](int s, int db) {
+        return vx[s & 3] + 8 * D * (s >> 2) + D * (s & 3) + 4 * ((8 * db) ^ (8 * ((s >> 2) & 1)));
+    };
+
+#pragma unroll
+    for (int st = 0; st < NST - 1; ++st)
+        if (st < total) issue(st);
+
+    int step = 0;
+    for (int part = 0; part < nparts; ++part) {
+        const int qt = part == 0 ? qa : qb;
+        const int ntiles = part == 0 ? na : total - na;
+        const int wq0 = qt * BM + 32 * w;
+        const int lq = wq0 + lrow;
+        // Q^T as B operands: dims (D/2) half .. +D/2 of row lq (rows past L read row L-1)
+        float qf[DH];
+        {
+            const float *qr = (const float *)a.q + b * a.q_sb + h * a.q_sh + (int64_t)min(lq, L - 1) * a.q_sl + DH * half;
+#pragma unroll
+            for (int u = 0; u < DH / 4; ++u) {
+                const f32x4 x = *(const f32x4 *)(qr + 4 * u);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) qf[4 * u + e] = x[e];
+            }
+#pragma unroll
+            for (int u = 0; u < DH; ++u) asm volatile("" ::"v"(qf[u]));
+        }
+        f32x16 o[DB];
+#pragma unroll
+        for (int db = 0; db < DB; ++db)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) o[db][i] = 0.0f;
+        float m = -INFINITY, mthr = -INFINITY, lsum = 0.0f;
+
+        for (int j = 0; j < ntiles; ++j, ++step) {
+            const int k0 = j * BN;
+            const int later = min(NST - 2, total - 1 - step);
+            if (later >= 1) wait_vm<PER>();
+            else wait_vm<0>();
+            __syncthreads();
+            const float *cK = sK[step % NST];
+            const float *cV = sV[step % NST];
+            // ---- S^T = K . Q^T: s[i] is key k0 + 8(i/4) + 4half + i%4, query lq ----
+            f32x16 s;
+            if constexpr (MROW) {
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const f32x4 mv4 = *(const f32x4 *)&sMk[step % NST][8 * g + 4 * half];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) s[4 * g + e] = mv4[e] * inv_scale;
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < 16; ++i) s[i] = 0.0f;
+            }
+#pragma unroll
+            for (int u = 0; u < DH / 4; ++u) {
+                const f32x4 kv = *(const f32x4 *)&cK[kofs(u)];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) s = mfma_f32x2(kv[e], qf[4 * u + e], s);
+            }
+            // the next tile's loads into the stage every wavefront finished with before the barrier
+            if (step + NST - 1 < total) issue(step + NST - 1);
+
+            const bool edge = k0 + BN > nkv || (CAUSAL && k0 + BN - 1 > wq0 + qpos);
+            if (edge) {
+                const int vis = min(nkv - 1, CAUSAL ? lq + qpos : nkv - 1) - (k0 + 4 * half);
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    const bool blocked = 8 * (i / 4) + (i % 4) > vis;
+                    s[i] = blocked ? -INFINITY : s[i];
+                }
+            }
+            float tmax = max3(s[0], s[1], s[2]);
+#pragma unroll
+            for (int i = 3; i < 15; i += 2) tmax = max3(tmax, s[i], s[i + 1]);
+            tmax = max3(tmax, s[15], s[15]);
+            tmax = xhalf_max(tmax);
+            const float tm = tmax * c;
+            const bool move = tm > mthr;
+            if (!__all(!move)) {
+                const float mnew = move ? tm + huge_margin(tm) : m;
+                const float alpha = move ? fast_exp2(m - mnew) : 1.0f;
+                lsum *= alpha;
+#pragma unroll
+                for (int db = 0; db < DB; ++db)
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) o[db][i] *= alpha;
+                m = mnew;
+                mthr = m + kLazy - 0.5f * huge_margin(m);
+            }
+            const float msub = m == -INFINITY ? 0.0f : m;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                s[i] = fast_exp2(fmaf(s[i], c, -msub));
+                lsum += s[i];
+            }
+            // ---- O^T += V^T . P^T ----
+#pragma unroll
+            for (int st2 = 0; st2 < 16; ++st2)
+#pragma unroll
+                for (int db = 0; db < DB; ++db) o[db] = mfma_f32x2(cV[vofs(st2, db)], s[st2], o[db]);
+        }
+
+        const float ltot = xhalf_sum(lsum);
+        const float inv = ltot > 0.0f ? 1.0f / ltot : 0.0f;
+        if (lq < L) {
+            float *orow = (float *)a.o + (bh * a.L + lq) * D;
+            float *row32 = a.o32 ? (float *)a.o32 + (bh * a.L + lq) * D : nullptr;
+#pragma unroll
+            for (int db = 0; db < DB; ++db)
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const f32x4 v = {o[db][4 * g] * inv, o[db][4 * g + 1] * inv, o[db][4 * g + 2] * inv,
+                                     o[db][4 * g + 3] * inv};
+                    *(f32x4 *)(orow + 32 * db + 8 * g + 4 * half) = v;
+                    if (row32) *(f32x4 *)(row32 + 32 * db + 8 * g + 4 * half) = v;
+                }
+            if (a.lse && half == 0)
+                ((float *)a.lse)[bh * a.L + lq] = ltot > 0.0f ? (m + log2f(ltot)) * kLn2 : INFINITY;
+        }
+    }
+}
+
+bool prefill_f32_supported(const AttnFwdArgs &f) {
+    if (f.out_dtype != GT_F32 || f.D != f.Dv || (f.D != 64 && f.D != 128)) return false;
+    if (f.dropout || f.rope_q) return false;
+    const int mode = attn_mask_mode(f);
+    if (mode != 0 && mode != 4) return false;
+    if (f.L < 1 || f.S < 1 || !(f.scale > 0.0f)) return false;
+    if (f.L >= (1LL << 30) || f.S >= (1LL << 30)) return false;
+    const int64_t strides[] = {f.q_sb, f.q_sh, f.q_sl, f.k_sb, f.k_sh, f.k_ss, f.v_sb, f.v_sh, f.v_ss};
+    for (int64_t st : strides) if (st % 4 != 0 || st < 0) return false;  // 16-byte rows
+    for (const void *p : {f.q, f.k, f.v, (const void *)f.o}) if ((uintptr_t)p % 16 != 0) return false;
+    if (f.o32 && (uintptr_t)f.o32 % 16 != 0) return false;
+    if ((f.S - 1) * f.k_ss * 4 + f.D * 4 > 0xffffffffLL) return false;
+    if ((f.S - 1) * f.v_ss * 4 + f.Dv * 4 > 0xffffffffLL) return false;
+    if (mode == 4 && (f.m_ss < 0 || (f.S - 1) * f.m_ss * 4 + 4 > 0xffffffffLL)) return false;
+    return true;
+}
+
+template <int D>
+hipError_t launch_prefill_f32_d(const AttnFwdArgs &a, int nq, int npairs, int64_t grid, hipStream_t s) {
+    const int mode = attn_mask_mode(a);
+#define GT_F32_LAUNCH(C, MK) \
+    hipLaunchKernelGGL((prefill_f32_kernel<D, C, MK>), dim3((unsigned)grid), dim3(64 * F32_NW), 0, s, a, nq, npairs)
+    if (a.causal) {
+        if (mode == 0) GT_F32_LAUNCH(true, 0);
+        else GT_F32_LAUNCH(true, 4);
+    } else {
+        if (mode == 0) GT_F32_LAUNCH(false, 0);
+        else GT_F32_LAUNCH(false, 4);
+    }
+#undef GT_F32_LAUNCH
+    return hipGetLastError();
+}
+
+hipError_t launch_prefill_f32(const AttnFwdArgs &a, hipStream_t s) {
+    const int nq = (int)((a.L + F32_BM - 1) / F32_BM);
+    const int npairs = (nq + 1) / 2;
+    const int64_t grid = (int64_t)npairs * a.B * a.H;
+    if (grid <= 0) return hipSuccess;
+    if (grid > 0x7fffffffLL) return hipErrorInvalidConfiguration;
+    return a.D == 128 ? launch_prefill_f32_d<128>(a, nq, npairs, grid, s) : launch_prefill_f32_d<64>(a, nq, npairs, grid, s);
+}
+
 }  // namespace
 
 bool attn_prefill_supported(const AttnFwdArgs &f, int cd) {
+    if (cd == GT_F32) return prefill_f32_supported(f);
     if (cd != GT_F16 && cd != GT_BF16) return false;
     if (f.rope_q && f.mask && (f.mask_bool || f.m_sl != 0)) return false;  // fused RoPE: no mask or key padding
     if (f.rope_q && f.dropout) return false;
@@ -663,6 +938,7 @@ bool attn_prefill_supported(const AttnFwdArgs &f, int cd) {
 }
 
 hipError_t launch_attn_prefill(const AttnFwdArgs &a, int cd, hipStream_t s) {
+    if (cd == GT_F32) return launch_prefill_f32(a, s);
     if (attn_prefill_asm_supported(a, cd)) return launch_attn_prefill_asm(a, s);
     const int BM = a.D == 64 ? bm_of<64>() : bm_of<128>();
     const int nq = (int)((a.L + BM - 1) / BM);

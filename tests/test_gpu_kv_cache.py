@@ -202,7 +202,9 @@ def test_q8_0_cache_prefill_chunk_on_mfma(dev, qdtype):
     q = randn((B, H, L, D), 33, qdtype, 0.5)
     got = cache.attention(q.to(dev))
     launch = _C.last_launch()
-    want_kernel = "prefill f16 D=128" if qdtype == torch.float16 else "generic f32"
+    # float16 queries: float16 K/V and the fp16 kernel; float32: the float32 MFMA kernel; bfloat16
+    # queries over float32 K/V (mixed dtypes, bfloat16 output): the generic kernel in float32
+    want_kernel = {torch.float16: "prefill f16 D=128", torch.float32: "prefill f32 D=128"}.get(qdtype, "generic f32")
     assert launch.startswith("dequantize q8_0 cache rows") and want_kernel in launch, launch
     K, V = dense_kv(cache, torch.float32)
     want = oracle_forward(q, K[:, :, :T].cpu(), V[:, :, :T].cpu(), mask=cache_mask(cache.lengths, L, T, True))

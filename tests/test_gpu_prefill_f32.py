@@ -1,0 +1,81 @@
+"""Float32 attention on v_mfma_f32_32x32x2_f32 (prefill_f32_kernel: head sizes 64 and 128, no
+mask or a key-padding row) against the float64 oracle at the float32 bar (max-abs 1e-4): ragged
+query and key counts around the 128-row query tiles and 32-key K/V tiles, one query row, one
+key, GQA, causal or not, the log-sum-exp and the training forward's float32 output, and the
+launch log naming the kernel.  Other masks keep the generic kernel."""
+
+import numpy as np
+import pytest
+import torch
+
+import gguf_train_amd as g
+from gguf_train_amd import _C
+
+from _util import assert_close, oracle_forward, randn
+
+pytestmark = pytest.mark.gpu
+
+CASES = [
+    # B, H, Hkv, L, S, D, causal, key padding
+    (1, 2, 2, 128, 128, 64, True, False),
+    (2, 4, 2, 300, 300, 128, True, False),
+    (1, 2, 1, 37, 257, 128, False, False),
+    (2, 2, 2, 129, 33, 64, False, True),
+    (1, 3, 1, 1, 640, 128, False, False),
+    (2, 2, 1, 257, 1, 64, False, False),
+    (1, 2, 2, 200, 31, 128, True, True),
+    (2, 4, 4, 513, 513, 64, True, True),
+]
+
+
+def _keypad(B, S, seed):
+    rng = np.random.default_rng(seed)
+    m = torch.zeros(B, 1, 1, S)
+    for b in range(B):
+        m[b, ..., int(rng.integers(1, S + 1)):] = float("-inf")
+    return m
+
+
+@pytest.mark.parametrize("B,H,Hkv,L,S,D,causal,kp", CASES)
+def test_float32_prefill_against_the_oracle(dev, B, H, Hkv, L, S, D, causal, kp):
+    seed = B + 10 * H + L + 7 * S + D
+    q, k, v = randn((B, H, L, D), seed), randn((B, Hkv, S, D), seed + 1), randn((B, Hkv, S, D), seed + 2)
+    mask = _keypad(B, S, seed) if kp else None
+    md = None if mask is None else mask.to(dev)
+    out, lse = g.flash_attention_lse(q.to(dev), k.to(dev), v.to(dev), md, 0.0, causal)
+    launch = _C.last_launch()
+    what = f"B{B} H{H}/{Hkv} L{L} S{S} D{D} causal={causal} keypad={kp}"
+    assert launch.startswith(f"prefill f32 D={D}"), (what, launch)
+    want = oracle_forward(q, k, v, mask=mask, is_causal=causal)
+    assert_close(out, want, torch.float32, what)
+    # the log-sum-exp: natural log of the row's sum of exp(score) (scores scaled), +inf with nothing visible
+    s = torch.einsum("bhld,bhsd->bhls", q.double(), k.double().repeat_interleave(H // Hkv, dim=1)) / np.sqrt(D)
+    if mask is not None:
+        s = s + mask.double()
+    if causal:
+        s = s.masked_fill(torch.ones(L, S, dtype=torch.bool).triu(1), float("-inf"))
+    want_lse = torch.logsumexp(s, dim=-1)
+    got_lse = lse.cpu().double()
+    fin = torch.isfinite(want_lse)
+    assert torch.equal(torch.isinf(got_lse), ~fin), what
+    assert (got_lse[fin] - want_lse[fin]).abs().max().item() < 1e-4, what
+
+
+def test_float32_training_forward_writes_the_float32_output(dev):
+    B, H, L, D = 2, 4, 150, 64
+    q, k, v = (randn((B, H, L, D), 40 + i) for i in range(3))
+    mask = _keypad(B, L, 3)
+    out, lse, out32 = g.flash_attention_train(q.to(dev), k.to(dev), v.to(dev), mask.to(dev), 0.0, True)
+    assert _C.last_launch().startswith("prefill f32 D=64")
+    assert out32 is None or torch.equal(out32, out)
+    assert_close(out, oracle_forward(q, k, v, mask=mask, is_causal=True), torch.float32, "train forward f32")
+
+
+def test_other_masks_keep_the_generic_kernel(dev):
+    B, H, L, S, D = 1, 2, 70, 90, 64
+    q, k, v = randn((B, H, L, D), 50), randn((B, H, S, D), 51), randn((B, H, S, D), 52)
+    m = torch.from_numpy(np.random.default_rng(5).random((L, S)) < 0.7)
+    m[:, 0] = True
+    out = g.flash_attention(q.to(dev), k.to(dev), v.to(dev), m.to(dev), 0.0, False)
+    assert _C.last_launch() == "generic f32"
+    assert_close(out, oracle_forward(q, k, v, mask=m), torch.float32, "bool mask f32")

@@ -199,7 +199,9 @@ def test_prefill_chunks_over_q8_0_kv_run_on_mfma(dev, qdtype, L, causal):
     vq = g.QuantizedTensor(torch.from_numpy(vb).to(dev), tuple(v.shape))
     got = g.flash_attention(q.to(dev), kq, vq, None, 0.0, causal)
     launch = _C.last_launch()
-    want_kernel = "prefill f16 D=128" if qdtype == torch.float16 else "generic f32"
+    # float16 queries: float16 K/V and the fp16 kernel; float32: the float32 MFMA kernel; bfloat16
+    # queries over float32 K/V (mixed dtypes, bfloat16 output): the generic kernel in float32
+    want_kernel = {torch.float16: "prefill f16 D=128", torch.float32: "prefill f32 D=128"}.get(qdtype, "generic f32")
     assert launch.startswith("dequantize q8_0 k/v") and want_kernel in launch, launch
     kd = torch.from_numpy(oracle.q8_0_dequantize(kb).reshape(k.shape))
     vd = torch.from_numpy(oracle.q8_0_dequantize(vb).reshape(v.shape))
