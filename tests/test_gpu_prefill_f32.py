@@ -1,8 +1,9 @@
 """Float32 attention on v_mfma_f32_32x32x2_f32 (prefill_f32_kernel: head sizes 64 and 128, no
-mask or a key-padding row) against the float64 oracle at the float32 bar (max-abs 1e-4): ragged
-query and key counts around the 128-row query tiles and 32-key K/V tiles, one query row, one
-key, GQA, causal or not, the log-sum-exp and the training forward's float32 output, and the
-launch log naming the kernel.  Other masks keep the generic kernel."""
+mask or a key-padding row, 16 query rows or more) against the float64 oracle at the float32 bar
+(max-abs 1e-4): ragged query and key counts around the 128-row query tiles and 32-key K/V
+tiles, one key, GQA, causal or not, the log-sum-exp and the training forward's float32 output,
+and the launch log naming the kernel.  Fewer query rows and other masks keep the generic
+kernel."""
 
 import numpy as np
 import pytest
@@ -22,6 +23,7 @@ CASES = [
     (1, 2, 1, 37, 257, 128, False, False),
     (2, 2, 2, 129, 33, 64, False, True),
     (1, 3, 1, 1, 640, 128, False, False),
+    (2, 2, 2, 16, 300, 64, True, True),
     (2, 2, 1, 257, 1, 64, False, False),
     (1, 2, 2, 200, 31, 128, True, True),
     (2, 4, 4, 513, 513, 64, True, True),
@@ -45,7 +47,8 @@ def test_float32_prefill_against_the_oracle(dev, B, H, Hkv, L, S, D, causal, kp)
     out, lse = g.flash_attention_lse(q.to(dev), k.to(dev), v.to(dev), md, 0.0, causal)
     launch = _C.last_launch()
     what = f"B{B} H{H}/{Hkv} L{L} S{S} D{D} causal={causal} keypad={kp}"
-    assert launch.startswith(f"prefill f32 D={D}"), (what, launch)
+    # fewer than 16 query rows stay on the generic kernel (measured as fast or faster there)
+    assert launch.startswith(f"prefill f32 D={D}" if L >= 16 else "generic f32"), (what, launch)
     want = oracle_forward(q, k, v, mask=mask, is_causal=causal)
     assert_close(out, want, torch.float32, what)
     # the log-sum-exp: natural log of the row's sum of exp(score) (scores scaled), +inf with nothing visible
