@@ -31,6 +31,7 @@
 #include "attn_common.h"
 #include "gt_internal.h"
 #include "mfma_util.h"
+#include "lds_dma.h"
 
 #include <cmath>
 
@@ -641,10 +642,434 @@ hipError_t launch_bwd_d(const AttnBwdArgs &a, hipStream_t s) {
     return launch_bwd_typed<T, D, false, 2>(a, s);
 }
 
+// ---- float32 ----------------------------------------------------------------------------------
+// Float32 backward (D = Dv = 64 or 128, no mask or a key-padding row, no dropout) on
+// v_mfma_f32_32x32x2_f32, with the division of work of the kernels above (dQ first, writing
+// delta = rowsum(dO.O); then dK/dV) and the float32 forward's operand mapping: a 32-row block's
+// row fragments take k-step t = dim t + (D/2)(lane/32), four k-steps per 16-byte LDS read, and the
+// products with P or dS take k-step s = the key (dQ) or query (dK/dV) of accumulator entry s,
+// 8(s/4) + 4(lane/32) + s%4, so P and dS enter as they stand.  Tiles reach LDS by DMA, 16-byte
+// chunk c of tile row r at chunk c ^ (r & 15).  Float32 operands keep 24 bits: no hi/lo split.
+
+// Tile element offsets: float d of tile row r sits at r*D + 4((d/4) ^ (r & 15)) + d%4; the
+// 16-byte fragment of dims (D/2) half + 4u .. +3 of row r at r*D + 4(((D/8) half + u) ^ (r & 15)),
+// which is r*D + ((4u) ^ 4((r & 15) ^ (D/8) half)) as u < D/8.
+// f32_elem_ofs<D>(32m + 8(s/4) + 4 half + s%4, 32 db + lrow), the element k-step s of a 32-row
+// block m and column 32 db + lrow, split into a per-lane part (one of four, by s % 4) and a
+// compile-time part, so the reads take immediate offsets
+template <int D>
+__device__ inline int f32_col_lane(int lrow, int half, int c) {
+    return 4 * D * half + (lrow & 3) + 4 * (((lrow >> 2) ^ (4 * half)) ^ c);
+}
+template <int D>
+__host__ __device__ constexpr int f32_col_const(int s, int db, int m) {
+    return 32 * m * D + 8 * D * (s >> 2) + D * (s & 3) + 4 * ((8 * db) ^ (8 * ((s >> 2) & 1)));
+}
+__device__ inline f32x16 mma_f32x2(float a, float b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+}
+
+// dQ: a workgroup owns 128 query rows (32 per wavefront), K/V tiles of 32 keys.
+template <int D, bool CAUSAL, int MASK>
+__global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void bwd_dq_f32_kernel(AttnBwdArgs a, int nq) {
+    constexpr int NW = 4, BM = 128, BN = 32, NST = 2;
+    constexpr int CH = D / 4, TILE = BN * D, NPW = BN * CH / 64 / NW, DB = D / 32, DH = D / 2;
+    constexpr bool MROW = MASK == 4;
+    static_assert(NPW >= 1 && CH >= 16, "tile split");
+    __shared__ __attribute__((aligned(1024))) float sK[NST][TILE];
+    __shared__ __attribute__((aligned(1024))) float sV[NST][TILE];
+    __shared__ __attribute__((aligned(16))) float sMk[MROW ? NST : 1][64];  // keys k0 .. k0+63 (32 used)
+
+    const AttnFwdArgs &f = a.f;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lrow = lane & 31, half = lane >> 5;
+    const int64_t BH = f.B * f.H;
+    const int qt = nq - 1 - (int)(blockIdx.x / BH);
+    const int64_t bh = (int64_t)blockIdx.x % BH;
+    const int64_t b = bh / f.H, h = bh % f.H, hk = h / (f.H / f.Hkv);
+    const int L = (int)f.L, S = (int)f.S;
+    const int q0 = qt * BM, wq0 = q0 + 32 * w, lq = wq0 + lrow, lqc = min(lq, L - 1);
+    const float c = f.scale * kLog2e, inv_scale = 1.0f / f.scale;
+
+    // Q and dO of row lq, dims (D/2) half .. +D/2 (B operands of S^T and dP^T)
+    float qf[DH], gf[DH];
+    float dlt;
+    {
+        const float *qr = (const float *)f.q + b * f.q_sb + h * f.q_sh + (int64_t)lqc * f.q_sl + DH * half;
+        const float *gr = (const float *)a.dout + (bh * f.L + lqc) * D + DH * half;
+        const float *orow = (const float *)f.o + (bh * f.L + lqc) * D + DH * half;
+        float part = 0.0f;
+#pragma unroll
+        for (int u = 0; u < DH / 4; ++u) {
+            const f32x4 x = *(const f32x4 *)(qr + 4 * u), g = *(const f32x4 *)(gr + 4 * u);
+            const f32x4 o4 = *(const f32x4 *)(orow + 4 * u);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                qf[4 * u + e] = x[e];
+                gf[4 * u + e] = g[e];
+                part = fmaf(g[e], o4[e], part);
+            }
+        }
+        // delta = rowsum(dO * O) of this row (the two lanes of a row hold half each), for dK/dV
+        dlt = xhalf_sum(part);
+        if (half == 0 && lq < L) ((float *)a.delta)[bh * f.L + lq] = dlt;
+#pragma unroll
+        for (int u = 0; u < DH; ++u) asm volatile("" ::"v"(qf[u]), "v"(gf[u]));
+    }
+    const float lse2 = ((const float *)f.lse)[bh * f.L + lqc] * kLog2e;
+    f32x16 dq[DB];
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) dq[db][i] = 0.0f;
+
+    const float *kbase = (const float *)f.k + b * f.k_sb + hk * f.k_sh;
+    const float *vbase = (const float *)f.v + b * f.v_sb + hk * f.v_sh;
+    const int kv_end = CAUSAL ? min(q0 + BM, S) : S;
+    const int ntiles = (kv_end + BN - 1) / BN;
+    const uint32_t k_row = (uint32_t)f.k_ss * 4, v_row = (uint32_t)f.v_ss * 4;
+    int lrow_n[NPW];
+    uint32_t lcol_n[NPW], kofs_n[NPW], vofs_n[NPW];
+#pragma unroll
+    for (int n = 0; n < NPW; ++n) {
+        const int slot = (w * NPW + n) * 64 + lane;
+        lrow_n[n] = slot / CH;
+        lcol_n[n] = 16u * (uint32_t)((slot % CH) ^ (lrow_n[n] & 15));
+        kofs_n[n] = (uint32_t)lrow_n[n] * k_row + lcol_n[n];
+        vofs_n[n] = (uint32_t)lrow_n[n] * v_row + lcol_n[n];
+    }
+    int cx[4];
+#pragma unroll
+    for (int c4 = 0; c4 < 4; ++c4) cx[c4] = f32_col_lane<D>(lrow, half, c4);
+    const int kx = 4 * ((lrow & 15) ^ ((D / 8) * half));  // row fragments: lrow * D + ((4u) ^ kx)
+    const float *mrow = MROW ? (const float *)f.mask + b * f.m_sb + h * f.m_sh : nullptr;
+    auto issue = [&](int j) {
+        const int st = j % NST;
+        if constexpr (MROW)
+            lds_dma4(lds_addr(&sMk[st][0]), mrow, (uint32_t)min(j * BN + lane, S - 1) * (uint32_t)f.m_ss * 4u);
+        const uint32_t dk = lds_addr(&sK[st][0]) + w * NPW * 1024;
+        const uint32_t dv = lds_addr(&sV[st][0]) + w * NPW * 1024;
+        if (j * BN + BN <= S) {
+            const char *kb = (const char *)kbase + (uint64_t)(j * BN) * k_row;
+            const char *vb = (const char *)vbase + (uint64_t)(j * BN) * v_row;
+#pragma unroll
+            for (int n = 0; n < NPW; ++n) {
+                lds_dma16(dk + n * 1024, kb, kofs_n[n]);
+                lds_dma16(dv + n * 1024, vb, vofs_n[n]);
+            }
+        } else {
+#pragma unroll
+            for (int n = 0; n < NPW; ++n) {
+                const uint32_t key = (uint32_t)min(j * BN + lrow_n[n], S - 1);
+                lds_dma16(dk + n * 1024, kbase, key * k_row + lcol_n[n]);
+                lds_dma16(dv + n * 1024, vbase, key * v_row + lcol_n[n]);
+            }
+        }
+    };
+
+    if (ntiles > 0) issue(0);
+    for (int j = 0; j < ntiles; ++j) {
+        wait_vm<0>();
+        __syncthreads();
+        const int st = j % NST, k0 = j * BN;
+        const float *cK = sK[st];
+        const float *cV = sV[st];
+        if (j + 1 < ntiles) issue(j + 1);  // stage (j+1) % 2 was last read before this barrier
+        if (CAUSAL && k0 > wq0 + 31) continue;  // every key of the tile follows the wave's rows
+        // S^T = K.Q^T (onto the key-padding terms), dP^T = V.dO^T (onto -delta):
+        // entry i is key k0 + 8(i/4) + 4half + i%4, query lq
+        f32x16 sc, dp;
+        if constexpr (MROW) {
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const f32x4 mv4 = *(const f32x4 *)&sMk[st][8 * g + 4 * half];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) sc[4 * g + e] = mv4[e] * inv_scale;
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) sc[i] = 0.0f;
+        }
+#pragma unroll
+        for (int i = 0; i < 16; ++i) dp[i] = -dlt;
+#pragma unroll
+        for (int u = 0; u < DH / 4; ++u) {
+            const int o = lrow * D + ((4 * u) ^ kx);
+            const f32x4 kv = *(const f32x4 *)&cK[o], vv = *(const f32x4 *)&cV[o];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                sc = mma_f32x2(kv[e], qf[4 * u + e], sc);
+                dp = mma_f32x2(vv[e], gf[4 * u + e], dp);
+            }
+        }
+        float ds[16];
+        const bool interior = k0 + BN - 1 < S && wq0 + 31 < L && (!CAUSAL || wq0 >= k0 + BN - 1);
+        if (interior) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) ds[i] = fast_exp2(fmaf(sc[i], c, -lse2)) * dp[i];
+        } else {
+            // key k0 + 4half + (8(i/4) + i%4) is visible to this lane's row when that offset <= vis
+            const int vis = (lq < L ? (CAUSAL ? min(lq, S - 1) : S - 1) : -1) - (k0 + 4 * half);
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const bool ok = 8 * (i / 4) + (i % 4) <= vis;
+                ds[i] = (ok ? fast_exp2(fmaf(sc[i], c, -lse2)) : 0.0f) * dp[i];
+            }
+        }
+        // dQ^T += K^T . dS^T: k-step s2 is key 8(s2/4) + 4half + s2%4, A = K[that key][32db + lrow]
+#pragma unroll
+        for (int s2 = 0; s2 < 16; ++s2)
+#pragma unroll
+            for (int db = 0; db < DB; ++db)
+                dq[db] = mma_f32x2(cK[cx[s2 & 3] + f32_col_const<D>(s2, db, 0)], ds[s2], dq[db]);
+    }
+    if (lq < L) {
+        float *row = (float *)a.dq + (bh * f.L + lq) * D;
+#pragma unroll
+        for (int db = 0; db < DB; ++db)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const f32x4 v = {dq[db][4 * g] * f.scale, dq[db][4 * g + 1] * f.scale, dq[db][4 * g + 2] * f.scale,
+                                 dq[db][4 * g + 3] * f.scale};
+                *(f32x4 *)(row + 32 * db + 8 * g + 4 * half) = v;
+            }
+    }
+}
+
+// dK, dV: a workgroup owns 128 keys of one kv head (32 per wavefront, K and V rows in registers)
+// and walks query steps of 64 rows over every query head of its group; Q, dO, lse and delta of a
+// step reach LDS by DMA.
+template <int D, bool CAUSAL, int MASK>
+__global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void bwd_dkdv_f32_kernel(AttnBwdArgs a) {
+    constexpr int BKV = 128, BQ = 64, NST = 2, NW = 4;
+    constexpr int CH = D / 4, TILE = BQ * D, NPW = BQ * CH / 64 / NW, DB = D / 32, DH = D / 2;
+    static_assert(NPW >= 1 && CH >= 16, "tile split");
+    __shared__ __attribute__((aligned(1024))) float sQ[NST][TILE];
+    __shared__ __attribute__((aligned(1024))) float sG[NST][TILE];  // dO
+    __shared__ __attribute__((aligned(16))) float sL[NST][BQ];      // lse (natural log)
+    __shared__ __attribute__((aligned(16))) float sD[NST][BQ];      // delta
+
+    const AttnFwdArgs &f = a.f;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lrow = lane & 31, half = lane >> 5;
+    const int64_t nbk = f.B * f.Hkv;
+    const int kt = (int)(blockIdx.x / nbk);
+    const int64_t bk = blockIdx.x % nbk, b = bk / f.Hkv, hk = bk % f.Hkv;
+    const int G = (int)(f.H / f.Hkv);
+    const int L = (int)f.L, S = (int)f.S;
+    const int k0 = kt * BKV, wk0 = k0 + 32 * w, key = wk0 + lrow;
+    const float c = f.scale * kLog2e, inv_scale = 1.0f / f.scale;
+
+    // K and V of this lane's key, dims (D/2) half .. +D/2 (B operands of S and dP)
+    float kf[DH], vf[DH];
+    {
+        const int kk = min(key, S - 1);
+        const float *kr = (const float *)f.k + b * f.k_sb + hk * f.k_sh + (int64_t)kk * f.k_ss + DH * half;
+        const float *vr = (const float *)f.v + b * f.v_sb + hk * f.v_sh + (int64_t)kk * f.v_ss + DH * half;
+#pragma unroll
+        for (int u = 0; u < DH / 4; ++u) {
+            const f32x4 x = *(const f32x4 *)(kr + 4 * u), y = *(const f32x4 *)(vr + 4 * u);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                kf[4 * u + e] = x[e];
+                vf[4 * u + e] = y[e];
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < DH; ++u) asm volatile("" ::"v"(kf[u]), "v"(vf[u]));
+    }
+    f32x16 dk[DB], dv[DB];
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) dk[db][i] = dv[db][i] = 0.0f;
+
+    const int qstart = CAUSAL ? (k0 / BQ) * BQ : 0;
+    const int nqs = L > qstart ? (L - qstart + BQ - 1) / BQ : 0;
+    const int nsteps = nqs * G;
+    const uint32_t q_row = (uint32_t)f.q_sl * 4, g_row = (uint32_t)D * 4;
+    int lrow_n[NPW];
+    uint32_t lcol_n[NPW], qofs_n[NPW], gofs_n[NPW];
+#pragma unroll
+    for (int n = 0; n < NPW; ++n) {
+        const int slot = (w * NPW + n) * 64 + lane;
+        lrow_n[n] = slot / CH;
+        lcol_n[n] = 16u * (uint32_t)((slot % CH) ^ (lrow_n[n] & 15));
+        qofs_n[n] = (uint32_t)lrow_n[n] * q_row + lcol_n[n];
+        gofs_n[n] = (uint32_t)lrow_n[n] * g_row + lcol_n[n];
+    }
+    int cx[4];
+#pragma unroll
+    for (int c4 = 0; c4 < 4; ++c4) cx[c4] = f32_col_lane<D>(lrow, half, c4);
+    const int kx = 4 * ((lrow & 15) ^ ((D / 8) * half));  // row fragments: (32m + lrow) * D + ((4u) ^ kx)
+    auto issue = [&](int st) {
+        const int hh = st / nqs, qs0 = qstart + (st % nqs) * BQ, sg = st % NST;
+        const int64_t h = hk * G + hh;
+        const float *qb = (const float *)f.q + b * f.q_sb + h * f.q_sh;
+        const float *gb = (const float *)a.dout + ((b * f.H + h) * f.L) * D;
+        const float *lb = (const float *)f.lse + (b * f.H + h) * f.L;
+        const float *db = (const float *)a.delta + (b * f.H + h) * f.L;
+        const uint32_t rq = (uint32_t)min(qs0 + lane, L - 1) * 4u;  // lane's row of lse / delta
+        lds_dma4(lds_addr(&sL[sg][0]), lb, rq);
+        lds_dma4(lds_addr(&sD[sg][0]), db, rq);
+        const uint32_t dq = lds_addr(&sQ[sg][0]) + w * NPW * 1024;
+        const uint32_t dg = lds_addr(&sG[sg][0]) + w * NPW * 1024;
+        if (qs0 + BQ <= L) {
+            const char *qr = (const char *)qb + (uint64_t)qs0 * q_row;
+            const char *gr = (const char *)gb + (uint64_t)qs0 * g_row;
+#pragma unroll
+            for (int n = 0; n < NPW; ++n) {
+                lds_dma16(dq + n * 1024, qr, qofs_n[n]);
+                lds_dma16(dg + n * 1024, gr, gofs_n[n]);
+            }
+        } else {
+#pragma unroll
+            for (int n = 0; n < NPW; ++n) {
+                const uint32_t r = (uint32_t)min(qs0 + lrow_n[n], L - 1);
+                lds_dma16(dq + n * 1024, qb, r * q_row + lcol_n[n]);
+                lds_dma16(dg + n * 1024, gb, r * g_row + lcol_n[n]);
+            }
+        }
+    };
+
+    float madd = 0.0f;  // MASK 4: the key's additive term for the current head (raw units)
+    if (nsteps > 0) issue(0);
+    for (int st = 0; st < nsteps; ++st) {
+        wait_vm<0>();
+        __syncthreads();
+        const int sg = st % NST;
+        const int hh = st / nqs, qs0 = qstart + (st % nqs) * BQ;
+        const int64_t h = hk * G + hh;
+        if (st + 1 < nsteps) issue(st + 1);  // stage (st+1) % 2 was last read before this barrier
+        if (MASK == 4 && st % nqs == 0) {
+            madd = ((const float *)f.mask)[b * f.m_sb + h * f.m_sh + (int64_t)min(key, S - 1) * f.m_ss] * inv_scale;
+        }
+        const float *cQ = sQ[sg];
+        const float *cG = sG[sg];
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb) {
+            const int q0 = qs0 + 32 * qb;
+            if (CAUSAL && q0 + 31 < wk0) continue;  // every query of the block precedes our keys
+            // S = Q.K^T (onto the key's mask term), dP = dO.V^T (onto -delta): entry i is query
+            // q0 + 8(i/4) + 4half + i%4 (tile row 32qb + 8(i/4) + 4half + i%4), key `key`
+            f32x16 sc, dp;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) sc[i] = madd;
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const f32x4 d4 = *(const f32x4 *)&sD[sg][32 * qb + 8 * g + 4 * half];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) dp[4 * g + e] = -d4[e];
+            }
+#pragma unroll
+            for (int u = 0; u < DH / 4; ++u) {
+                const int o = (32 * qb + lrow) * D + ((4 * u) ^ kx);
+                const f32x4 qa = *(const f32x4 *)&cQ[o], ga = *(const f32x4 *)&cG[o];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    sc = mma_f32x2(qa[e], kf[4 * u + e], sc);
+                    dp = mma_f32x2(ga[e], vf[4 * u + e], dp);
+                }
+            }
+            float p[16], ds[16];
+            const bool interior = wk0 + 31 < S && q0 + 31 < L && (!CAUSAL || q0 >= wk0 + 31);
+            // query q0 + 4half + c (c = 8(i/4) + i%4) sees this lane's key when lo <= c <= lo + span
+            int lo = (CAUSAL ? key : 0) - (q0 + 4 * half);
+            int span = (L - 1 - (q0 + 4 * half)) - lo;
+            if (key >= S || span < 0) {
+                lo = 32;  // no c in 0..27 passes
+                span = 0;
+            }
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const f32x4 l4 = *(const f32x4 *)&sL[sg][32 * qb + 8 * g + 4 * half];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int i = 4 * g + e;
+                    const bool ok = interior || (uint32_t)(8 * g + e - lo) <= (uint32_t)span;
+                    const float pv = ok ? fast_exp2(fmaf(sc[i], c, -l4[e] * kLog2e)) : 0.0f;
+                    p[i] = pv;
+                    ds[i] = pv * dp[i];
+                }
+            }
+            // dV += P^T.dO, dK += dS^T.Q: k-step s2 is query 8(s2/4) + 4half + s2%4 of the block
+#pragma unroll
+            for (int s2 = 0; s2 < 16; ++s2) {
+#pragma unroll
+                for (int db = 0; db < DB; ++db) {
+                    const int o = cx[s2 & 3] + f32_col_const<D>(s2, db, qb);
+                    dv[db] = mma_f32x2(p[s2], cG[o], dv[db]);
+                    dk[db] = mma_f32x2(ds[s2], cQ[o], dk[db]);
+                }
+            }
+        }
+    }
+
+    // dK[key][d] (scaled) and dV[key][d]: accumulator row = key wk0 + 8(i/4) + 4half + i%4, column d
+    float *dkp = (float *)a.dk + (bk * f.S) * D;
+    float *dvp = (float *)a.dv + (bk * f.S) * D;
+#pragma unroll
+    for (int db = 0; db < DB; ++db) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int kr = wk0 + 8 * (i / 4) + 4 * half + (i % 4);
+            if (kr < S) {
+                dkp[(int64_t)kr * D + 32 * db + lrow] = dk[db][i] * f.scale;
+                dvp[(int64_t)kr * D + 32 * db + lrow] = dv[db][i];
+            }
+        }
+    }
+}
+
+template <int D, bool CAUSAL, int MASK>
+hipError_t launch_bwd_f32_cm(const AttnBwdArgs &a, hipStream_t s) {
+    const AttnFwdArgs &f = a.f;
+    const int nq = (int)((f.L + 127) / 128);
+    hipLaunchKernelGGL((bwd_dq_f32_kernel<D, CAUSAL, MASK>), dim3((unsigned)(nq * f.B * f.H)), dim3(256), 0, s, a, nq);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const int nkt = (int)((f.S + 127) / 128);
+    hipLaunchKernelGGL((bwd_dkdv_f32_kernel<D, CAUSAL, MASK>), dim3((unsigned)(nkt * f.B * f.Hkv)), dim3(256), 0, s, a);
+    return hipGetLastError();
+}
+
+template <int D>
+hipError_t launch_bwd_f32_d(const AttnBwdArgs &a, hipStream_t s) {
+    const bool kp = attn_mask_mode(a.f) == 4;
+    if (a.f.causal) return kp ? launch_bwd_f32_cm<D, true, 4>(a, s) : launch_bwd_f32_cm<D, true, 0>(a, s);
+    return kp ? launch_bwd_f32_cm<D, false, 4>(a, s) : launch_bwd_f32_cm<D, false, 0>(a, s);
+}
+
+bool bwd_f32_supported(const AttnBwdArgs &a) {
+    const AttnFwdArgs &f = a.f;
+    if (f.D != f.Dv || (f.D != 64 && f.D != 128) || f.dropout || f.kv_len || f.q_pos) return false;
+    const int mode = attn_mask_mode(f);
+    if (mode != 0 && mode != 4) return false;
+    // as the forward: fewer than 16 query rows stay on the generic kernels
+    if (f.L < 16 || f.S < 1 || !(f.scale > 0.0f) || !f.o || !f.lse) return false;  // f.o: float32 output
+    // fewer than 32 dQ workgroups leave the MFMA kernels latency-bound: the generic kernels, which
+    // spread the rows thinner, measured faster there (B1 H4 L128 D64 causal 38.0 us against 45.7,
+    // B1 H2 L1024 D64 231 against 277) and slower from 32 on (B1 H32 L128 D64 57.6 against 46.3)
+    if (f.B * f.H * ((f.L + 127) / 128) < 32) return false;
+    if (f.L >= (1LL << 30) || f.S >= (1LL << 30)) return false;
+    const int64_t strides[] = {f.q_sb, f.q_sh, f.q_sl, f.k_sb, f.k_sh, f.k_ss, f.v_sb, f.v_sh, f.v_ss};
+    for (int64_t st : strides) if (st % 4 != 0 || st < 0) return false;  // 16-byte rows
+    for (const void *p : {f.q, f.k, f.v, (const void *)a.dout, (const void *)f.o, (const void *)a.dq})
+        if ((uintptr_t)p % 16 != 0) return false;
+    // 32-bit byte offsets from the per-head bases: K/V rows (dQ tiles), Q and dO rows (dK/dV steps)
+    if ((f.S - 1) * f.k_ss * 4 + f.D * 4 > 0xffffffffLL || (f.S - 1) * f.v_ss * 4 + f.D * 4 > 0xffffffffLL) return false;
+    if ((f.L - 1) * f.q_sl * 4 + f.D * 4 > 0xffffffffLL || (f.L - 1) * f.D * 4 + f.D * 4 > 0xffffffffLL) return false;
+    if (mode == 4 && (f.m_ss < 0 || (f.S - 1) * f.m_ss * 4 + 4 > 0xffffffffLL)) return false;
+    return true;
+}
+
 }  // namespace
 
 bool attn_bwd_mfma_supported(const AttnBwdArgs &a, int cd) {
     const AttnFwdArgs &f = a.f;
+    if (cd == GT_F32) return bwd_f32_supported(a);
     if (cd != GT_F16 && cd != GT_BF16) return false;
     if (f.D != f.Dv || (f.D != 64 && f.D != 128)) return false;
     if (f.L < 1 || f.S < 1 || !(f.scale > 0.0f) || !f.o || !f.lse) return false;
@@ -657,6 +1082,7 @@ bool attn_bwd_mfma_supported(const AttnBwdArgs &a, int cd) {
 }
 
 hipError_t launch_attn_bwd_mfma(const AttnBwdArgs &a, int cd, hipStream_t s) {
+    if (cd == GT_F32) return a.f.D == 128 ? launch_bwd_f32_d<128>(a, s) : launch_bwd_f32_d<64>(a, s);
     if (cd == GT_F16) return a.f.D == 128 ? launch_bwd_d<_Float16, 128>(a, s) : launch_bwd_d<_Float16, 64>(a, s);
     return a.f.D == 128 ? launch_bwd_d<__bf16, 128>(a, s) : launch_bwd_d<__bf16, 64>(a, s);
 }

@@ -1,0 +1,133 @@
+"""Float32 backward on v_mfma_f32_32x32x2_f32 (bwd_dq_f32_kernel, then bwd_dkdv_f32_kernel: head
+sizes 64 and 128, no mask or a key-padding row, no dropout, 16 query rows or more) against the
+float64 oracle's gradients at the float32 bar (max-abs 1e-4): ragged query and key counts around
+the dQ kernel's 128-row query tiles and 32-key K/V tiles and the dK/dV kernel's 128-key tiles and
+64-row query steps, one key, GQA and MQA, causal or not, keys no query sees (causal, S > L),
+fully padded rows, and the launch log naming the kernel.  Fewer query rows and other masks keep
+the generic kernel."""
+
+import numpy as np
+import pytest
+import torch
+
+import gguf_train_amd as g
+from gguf_train_amd import _C
+
+import oracle
+from _util import assert_close, randn, to_oracle
+
+pytestmark = pytest.mark.gpu
+
+CASES = [
+    # B, H, Hkv, L, S, D, causal, key padding (B * H * ceil(L / 128) >= 32: smaller grids take
+    # the generic kernels)
+    (1, 32, 32, 128, 128, 64, True, False),
+    (2, 8, 2, 300, 300, 128, True, True),
+    (2, 16, 1, 37, 257, 128, False, False),
+    (2, 8, 8, 129, 33, 64, False, True),
+    (2, 16, 16, 16, 300, 64, True, True),
+    (2, 16, 16, 257, 1, 64, False, False),
+    (1, 16, 16, 200, 31, 128, True, True),
+    (2, 4, 4, 513, 513, 64, True, True),
+    (4, 8, 2, 65, 200, 64, True, False),
+    (2, 16, 4, 96, 160, 128, False, True),
+]
+
+
+def _keypad(B, S, seed, empty_row=False):
+    rng = np.random.default_rng(seed)
+    m = torch.zeros(B, 1, 1, S)
+    for b in range(B):
+        m[b, ..., int(rng.integers(1, S + 1)):] = float("-inf")
+    if empty_row:
+        m[B - 1] = float("-inf")  # the last sequence sees no key at all
+    return m
+
+
+def _grads(dev, q, k, v, dout, mask, causal, with_residuals=True):
+    md = None if mask is None else mask.to(dev)
+    qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
+    out = lse = None
+    if with_residuals:
+        out, lse = g.flash_attention_lse(qd, kd, vd, md, 0.0, causal)
+    dq, dk, dv = g.flash_attention_backward(dout.to(dev), qd, kd, vd, md, out, lse, 0.0, causal)
+    return dq, dk, dv, _C.last_launch()
+
+
+def _oracle_grads(dout, q, k, v, mask, causal):
+    return oracle.flash_attention_backward(to_oracle(dout), to_oracle(q), to_oracle(k), to_oracle(v),
+                                           mask=None if mask is None else to_oracle(mask), is_causal=causal)
+
+
+@pytest.mark.parametrize("B,H,Hkv,L,S,D,causal,kp", CASES)
+def test_float32_backward_against_the_oracle(dev, B, H, Hkv, L, S, D, causal, kp):
+    seed = 3 * B + 11 * H + L + 5 * S + D
+    q, k, v = randn((B, H, L, D), seed), randn((B, Hkv, S, D), seed + 1), randn((B, Hkv, S, D), seed + 2)
+    dout = randn((B, H, L, D), seed + 3)
+    mask = _keypad(B, S, seed) if kp else None
+    dq, dk, dv, launch = _grads(dev, q, k, v, dout, mask, causal)
+    what = f"B{B} H{H}/{Hkv} L{L} S{S} D{D} causal={causal} keypad={kp}"
+    assert launch == f"backward mfma f32 D={D}", (what, launch)
+    assert dq.dtype == dk.dtype == dv.dtype == torch.float32
+    wq, wk, wv = _oracle_grads(dout, q, k, v, mask, causal)
+    assert_close(dq, wq, torch.float32, "dq " + what)
+    assert_close(dk, wk, torch.float32, "dk " + what)
+    assert_close(dv, wv, torch.float32, "dv " + what)
+
+
+def test_one_key_seen_by_every_query_of_an_mqa_group(dev):
+    # dV of the single key sums dO over all 16 x 257 query rows of the group (P = 1) in one
+    # float32 accumulator: values of magnitude ~60, where a sequential float32 sum of 4112 normal
+    # terms is itself off by up to 2.5e-4 (64 trials); it is held to 1e-4 relative to
+    # max(1, |ref|).  The softmax over one key is constant, so dQ and dK are 0 up to rounding and
+    # keep the absolute bar.
+    B, H, L, D = 2, 16, 257, 64
+    q, k, v, dout = randn((B, H, L, D), 90), randn((B, 1, 1, D), 91), randn((B, 1, 1, D), 92), randn((B, H, L, D), 93)
+    dq, dk, dv, launch = _grads(dev, q, k, v, dout, None, False)
+    assert launch == "backward mfma f32 D=64", launch
+    wq, wk, wv = _oracle_grads(dout, q, k, v, None, False)
+    assert_close(dq, wq, torch.float32, "dq one key")
+    assert_close(dk, wk, torch.float32, "dk one key")
+    got = dv.double().cpu().numpy()
+    assert np.abs(wv).max() > 10  # the long sums this test is about
+    worst = (np.abs(got - wv) / (1e-4 * np.maximum(1.0, np.abs(wv)))).max()
+    assert worst <= 1.0, f"dv one key: {worst:.3f}x the bound"
+
+
+def test_float32_backward_without_residuals_and_with_an_empty_row(dev):
+    # no output or log-sum-exp given: the forward is recomputed; the last sequence's rows see no
+    # key (log-sum-exp +inf), so its gradients are zero
+    B, H, L, D = 2, 16, 70, 128
+    q, k, v, dout = (randn((B, H, L, D), 60 + i) for i in range(4))
+    mask = _keypad(B, L, 9, empty_row=True)
+    dq, dk, dv, launch = _grads(dev, q, k, v, dout, mask, False, with_residuals=False)
+    # the log names the recomputed forward first
+    assert launch.startswith("prefill f32 D=128") and launch.endswith("; backward mfma f32 D=128"), launch
+    for got, want, name in zip((dq, dk, dv), _oracle_grads(dout, q, k, v, mask, False), ("dq", "dk", "dv")):
+        assert_close(got, want, torch.float32, name + " empty row")
+        assert torch.count_nonzero(got[B - 1]).item() == 0, name
+
+
+def test_fewer_rows_small_grids_and_other_masks_keep_the_generic_backward(dev):
+    B, H, S, D = 1, 32, 90, 64
+    q, k, v, dout = randn((B, H, 15, D), 70), randn((B, H, S, D), 71), randn((B, H, S, D), 72), randn((B, H, 15, D), 73)
+    dq, dk, dv, launch = _grads(dev, q, k, v, dout, None, False)
+    assert launch == "backward generic f32", launch
+    for got, want, name in zip((dq, dk, dv), _oracle_grads(dout, q, k, v, None, False), ("dq", "dk", "dv")):
+        assert_close(got, want, torch.float32, name + " L=15")
+    # 31 dQ workgroups (B * H * ceil(L / 128)): generic; 32: MFMA
+    for H2, want_launch in ((31, "backward generic f32"), (32, "backward mfma f32 D=64")):
+        q2, k2, v2, g2 = (randn((1, H2, 128, D), 80 + i) for i in range(4))
+        dq, dk, dv, launch = _grads(dev, q2, k2, v2, g2, None, True)
+        assert launch == want_launch, (H2, launch)
+        for got, want, name in zip((dq, dk, dv), _oracle_grads(g2, q2, k2, v2, None, True), ("dq", "dk", "dv")):
+            assert_close(got, want, torch.float32, f"{name} H={H2}")
+    # 32 workgroups, but a boolean mask
+    L = 40
+    q, dout = randn((B, H, L, D), 74), randn((B, H, L, D), 75)
+    m = torch.from_numpy(np.random.default_rng(6).random((L, S)) < 0.7)
+    m[:, 0] = True
+    dq, dk, dv, launch = _grads(dev, q, k, v, dout, m, False)
+    assert launch == "backward generic f32", launch
+    for got, want, name in zip((dq, dk, dv), _oracle_grads(dout, q, k, v, m, False), ("dq", "dk", "dv")):
+        assert_close(got, want, torch.float32, name + " bool mask")
