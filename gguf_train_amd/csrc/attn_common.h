@@ -104,6 +104,7 @@ struct AttnBwdArgs {
 // take several workgroups over the same keys, each re-reading them.
 constexpr int kDecodeMaxTile = 16;   // fp16/bf16 streaming kernel (16 heads: P.V on MFMA)
 constexpr int kDecodeQ8MaxTile = 8;  // Q8_0 kernels (16 measured slower: half the workgroups)
+constexpr int kDecodeF32MaxTile = 8; // float32 kernel (VALU P.V: acc[G][4] per lane)
 inline int decode_head_tile(int64_t gtot, int max_tile) {
     const int t = gtot > 8 ? 16 : gtot > 4 ? 8 : gtot > 2 ? 4 : (int)gtot;
     return t < max_tile ? t : max_tile;
@@ -154,6 +155,7 @@ hipError_t launch_attn_generic_bwd(const AttnBwdArgs &a, int cd, hipStream_t s);
 
 bool attn_decode_supported(const AttnFwdArgs &f, int cd);
 int attn_decode_splits(const AttnFwdArgs &f, int cd);
+int attn_decode_max_tile(int cd);  // query heads per workgroup at most (decode_units' max_tile)
 hipError_t launch_attn_decode(const DecodeArgs &a, int cd, hipStream_t s);
 
 bool attn_prefill_supported(const AttnFwdArgs &f, int cd);

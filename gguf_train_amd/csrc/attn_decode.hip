@@ -402,6 +402,218 @@ __global__ __launch_bounds__(256, 2) void decode_stream_kernel(DecodeArgs a) {
     if (a.nsplit > 1 && a.counters) gtdecode::finish_split<T, D>(a, bkg, b * f.H + h0, gv);
 }
 
+// Float32 K/V, D = 64, 128: the streaming kernel's decomposition (workgroup = (sequence, kv
+// head, head group) x split; each wave owns its keys of every step end to end; the waves combine
+// once at the end; the last split merges in the kernel) with float32 operands and 16 keys per
+// wave and step.  Scores S^T = K.Q^T on v_mfma_f32_16x16x4_f32 with the heads as its columns:
+// lane (l16, q4) reads 16 bytes of key l16's row at dims 16t + 4q4 .. +3 (four lanes read 64
+// consecutive bytes), and MFMA (t, e) takes k index q4 as dim 16t + 4q4 + e, the same dim in the
+// lane's Q^T operand; accumulator entry i is key 4q4 + i, head l16.  P.V on the VALU in float32
+// over 16-byte V rows, the probabilities shared through LDS.  Groups of up to 8 heads.
+// v_mfma_f32_16x16x4_f32 layouts (lane l): A[m = l%16][k = l/16], B[k = l/16][n = l%16],
+// C[m = 4(l/16) + i][n = l%16], i = 0..3.
+constexpr int kStepF32 = 64;  // keys per step of a workgroup (16 per wave)
+
+// D = 128 with 8 heads holds two 16 KB tiles, Q and acc[8][4] per lane: one workgroup per CU
+// (512 registers; two would spill), whose 4 waves x 2 tiles in flight still cover the CU's
+// share of the memory latency.
+template <int D, int G, int MASK>
+__global__ __launch_bounds__(256, (D == 128 && G == 8) ? 1 : 2) void decode_f32_kernel(DecodeArgs a) {
+    constexpr int NT = D / 16;     // 16-byte K pieces per lane and key block (4 MFMAs each)
+    constexpr int LPR = D / 4;     // lanes per V row (16 bytes each)
+    constexpr int RPW = 64 / LPR;  // V rows per wave load
+    constexpr int NV = 16 / RPW;   // V loads per lane and step
+    static_assert(G <= kDecodeF32MaxTile && NV >= 1, "decode_f32 tile");
+    __shared__ __attribute__((aligned(16))) float s_p[4][16][G];  // per-wave probabilities
+    __shared__ float s_m[4][G], s_l[4][G];
+    __shared__ float s_o[4][G][D];
+
+    const AttnFwdArgs &f = a.f;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int l16 = lane & 15, q4 = lane >> 4;
+    const int sub = lane % LPR, vrow = lane / LPR;
+    // blockIdx.x = (sequence, kv head, head group), blockIdx.y = split (an XCD gets whole slices)
+    const int split = blockIdx.y;
+    const int gtot = (int)(f.H / f.Hkv), ngrp = (gtot + G - 1) / G;
+    const int64_t bkg = blockIdx.x, bk = bkg / ngrp, b = bk / f.Hkv, hk = bk % f.Hkv;
+    const int hg = (int)(bkg % ngrp);
+    const int h0 = (int)hk * gtot + hg * G, gv = min(G, gtot - hg * G);
+    const int S = (int)f.S;
+    const int span = ((S + kStepF32 - 1) / kStepF32 + a.nsplit - 1) / a.nsplit * kStepF32;  // keys per split
+    const int kbeg = split * span, kend = min(attn_decode_end(f, b), kbeg + span);
+    const int nsteps = kend > kbeg ? (kend - kbeg + kStepF32 - 1) / kStepF32 : 0;
+
+    // B operand (Q^T): lane holds Q[head h0 + l16][16t + 4q4 .. +3]; columns l16 >= gv repeat
+    // head h0 + gv - 1 and are discarded
+    f32x4 qb[NT];
+    {
+        const float *qr = (const float *)f.q + b * f.q_sb + (h0 + min(l16, gv - 1)) * f.q_sh + 4 * q4;
+#pragma unroll
+        for (int t = 0; t < NT; ++t) qb[t] = *(const f32x4 *)(qr + 16 * t);
+    }
+    // K/V rows of a step; keys past S read row S-1 (finite; masked to -inf / weight 0).  Byte
+    // offsets from the (b, kv head) bases fit 32 bits (checked by the launcher); nontemporal
+    // loads, every byte is read once.
+    const char *kbase = (const char *)((const float *)f.k + b * f.k_sb + hk * f.k_sh);
+    const char *vbase = (const char *)((const float *)f.v + b * f.v_sb + hk * f.v_sh);
+    const uint32_t krow = (uint32_t)f.k_ss * 4u, vrowb = (uint32_t)f.v_ss * 4u;
+    struct Tile {
+        f32x4 k[NT];  // K[key l16 of the wave's 16][16t + 4q4 .. +3]
+        f32x4 v[NV];  // V rows RPW*i + vrow of the wave's 16, dims 4 sub .. +3
+    };
+    auto load = [&](int step, Tile &tl) {
+        const int k0 = kbeg + step * kStepF32 + 16 * w;
+        const uint32_t koff = (uint32_t)min(k0 + l16, S - 1) * krow + 16u * q4;
+#pragma unroll
+        for (int t = 0; t < NT; ++t) tl.k[t] = __builtin_nontemporal_load((const f32x4 *)(kbase + koff + 64 * t));
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            const uint32_t off = (uint32_t)min(k0 + RPW * i + vrow, S - 1) * vrowb + 16u * sub;
+            tl.v[i] = __builtin_nontemporal_load((const f32x4 *)(vbase + off));
+        }
+    };
+
+    const float cs = f.scale * kLog2e;
+    const int64_t mrow = b * f.m_sb + (h0 + min(l16, gv - 1)) * f.m_sh;
+    float m = -INFINITY;  // running max of head l16 (log2 domain), same in the 4 lanes of a head
+    float lsum = 0.0f;    // running sum of head l16
+    float acc[G][4];      // unnormalised O of every head, dims 4 sub .. +3, this lane's rows
+#pragma unroll
+    for (int h = 0; h < G; ++h)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[h][j] = 0.0f;
+
+    auto compute = [&](int step, const Tile &tl) {
+        const int k0 = kbeg + step * kStepF32 + 16 * w;
+        // two accumulators (even and odd pieces) halve the dependent MFMA chain
+        f32x4 ca = {0.0f, 0.0f, 0.0f, 0.0f}, cb = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int t = 0; t < NT; t += 2)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                ca = __builtin_amdgcn_mfma_f32_16x16x4f32(tl.k[t][e], qb[t][e], ca, 0, 0, 0);
+                cb = __builtin_amdgcn_mfma_f32_16x16x4f32(tl.k[t + 1][e], qb[t + 1][e], cb, 0, 0, 0);
+            }
+        float sc[4];
+        float cm = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int key = k0 + 4 * q4 + i;
+            float x = (ca[i] + cb[i]) * cs;
+            bool blocked = key >= kend || l16 >= gv;
+            if (MASK != 0) {
+                const int64_t mi = mrow + (int64_t)min(key, S - 1) * f.m_ss;
+                if (MASK == 1) blocked = blocked || !((const uint8_t *)f.mask)[mi];
+                else x = fmaf(((const float *)f.mask)[mi], kLog2e, x);
+            }
+            x = blocked ? -INFINITY : x;
+            sc[i] = x;
+            cm = fmaxf(cm, x);
+        }
+        cm = fmaxf(cm, __shfl_xor(cm, 16, 64));
+        cm = fmaxf(cm, __shfl_xor(cm, 32, 64));
+        const float mnew = fmaxf(m, cm);
+        const float msub = mnew == -INFINITY ? 0.0f : mnew;
+        const float alpha = mnew == -INFINITY ? 1.0f : fast_exp2(m - mnew);  // m = -inf: 0
+        m = mnew;
+        float ps = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            sc[i] = fast_exp2(sc[i] - msub);  // -inf -> 0
+            ps += sc[i];
+        }
+        ps += __shfl_xor(ps, 16, 64);
+        ps += __shfl_xor(ps, 32, 64);
+        lsum = fmaf(lsum, alpha, ps);
+        if (l16 < G) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) s_p[w][4 * q4 + i][l16] = sc[i];
+        }
+        // the head-h rescale factor sits in lane h
+        float al[G];
+#pragma unroll
+        for (int h = 0; h < G; ++h) al[h] = __shfl(alpha, h, 64);
+        __builtin_amdgcn_wave_barrier();  // s_p written by this wave before it is read
+#pragma unroll
+        for (int h = 0; h < G; ++h)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[h][j] *= al[h];
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            const int r = RPW * i + vrow;
+#pragma unroll
+            for (int h = 0; h < G; ++h) {
+                const float p = s_p[w][r][h];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) acc[h][j] = fmaf(p, tl.v[i][j], acc[h][j]);
+            }
+        }
+        __builtin_amdgcn_wave_barrier();  // s_p read before the next step overwrites it
+    };
+
+    // two tiles in flight, unrolled by two so they swap roles without copies; wave priority
+    // follows the step (the two workgroups on a CU stay level)
+    Tile ta, tb;
+    if (nsteps > 0) load(0, ta);
+    for (int st = 0; st < nsteps; st += 2) {
+        progress_priority(st);
+        if (st + 1 < nsteps) load(st + 1, tb);
+        __builtin_amdgcn_sched_barrier(0);
+        compute(st, ta);
+        if (st + 1 < nsteps) {
+            progress_priority(st + 1);
+            if (st + 2 < nsteps) load(st + 2, ta);
+            __builtin_amdgcn_sched_barrier(0);
+            compute(st + 1, tb);
+        }
+    }
+    __builtin_amdgcn_s_setprio(3);
+
+    // ---- combine the four waves ----
+    if (lane < G) {
+        s_m[w][lane] = m;
+        s_l[w][lane] = lsum;
+    }
+#pragma unroll
+    for (int h = 0; h < G; ++h)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int mm = LPR; mm < 64; mm <<= 1) acc[h][j] += __shfl_xor(acc[h][j], mm, 64);
+    if (lane < LPR) {
+#pragma unroll
+        for (int h = 0; h < G; ++h)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) s_o[w][h][4 * sub + j] = acc[h][j];
+    }
+    __syncthreads();
+    for (int e = tid; e < gv * D; e += 256) {
+        const int h = e / D, d = e % D;
+        const float M = fmaxf(fmaxf(s_m[0][h], s_m[1][h]), fmaxf(s_m[2][h], s_m[3][h]));
+        float o = 0.0f, L = 0.0f;
+#pragma unroll
+        for (int ww = 0; ww < 4; ++ww) {
+            const float wg = s_m[ww][h] == -INFINITY ? 0.0f : fast_exp2(s_m[ww][h] - M);
+            o = fmaf(wg, s_o[ww][h][d], o);
+            L = fmaf(wg, s_l[ww][h], L);
+        }
+        const int64_t row = b * f.H + h0 + h;
+        if (a.nsplit == 1) {
+            store_t<float>(f.o, row * D + d, L > 0.0f ? o / L : 0.0f);
+            if (f.lse && d == 0) ((float *)f.lse)[row] = L > 0.0f ? (M + log2f(L)) * kLn2 : INFINITY;
+        } else {
+            const int64_t pr = row * a.nsplit + split;
+            a.part_o[pr * D + d] = o;
+            if (d == 0) {
+                a.part_ml[pr * 2 + 0] = M;
+                a.part_ml[pr * 2 + 1] = L;
+            }
+        }
+    }
+    if (a.nsplit > 1 && a.counters) gtdecode::finish_split<float, D>(a, bkg, b * f.H + h0, gv);
+}
+
 // D = 256: a key row is split over D/8 lanes (16-byte loads), dot products reduced across lanes.
 template <typename T, int D, int G>
 __global__ __launch_bounds__(256) void decode_rows_kernel(DecodeArgs a) {
@@ -648,6 +860,32 @@ hipError_t launch_d(const DecodeArgs &a, int G, hipStream_t s) {
     }
 }
 
+template <int D, int G>
+hipError_t launch_f32_g(const DecodeArgs &a, hipStream_t s) {
+    const dim3 grid((unsigned)decode_units(a.f.B, a.f.H, a.f.Hkv, kDecodeF32MaxTile), (unsigned)a.nsplit);
+    const int mode = !a.f.mask ? 0 : (a.f.mask_bool ? 1 : 2);
+    if (mode == 0) hipLaunchKernelGGL((decode_f32_kernel<D, G, 0>), grid, dim3(256), 0, s, a);
+    else if (mode == 1) hipLaunchKernelGGL((decode_f32_kernel<D, G, 1>), grid, dim3(256), 0, s, a);
+    else hipLaunchKernelGGL((decode_f32_kernel<D, G, 2>), grid, dim3(256), 0, s, a);
+    hipError_t e = hipGetLastError();
+    // one split, or the last split merged in the kernel: it wrote the output
+    if (e != hipSuccess || a.nsplit == 1 || a.counters) return e;
+    const int64_t rows = a.f.B * a.f.H;
+    hipLaunchKernelGGL((decode_merge_kernel<float, D>), dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, s, a);
+    return hipGetLastError();
+}
+
+template <int D>
+hipError_t launch_f32_d(const DecodeArgs &a, hipStream_t s) {
+    switch (decode_head_tile(a.f.H / a.f.Hkv, kDecodeF32MaxTile)) {
+        case 1: return launch_f32_g<D, 1>(a, s);
+        case 2: return launch_f32_g<D, 2>(a, s);
+        case 4: return launch_f32_g<D, 4>(a, s);
+        case 8: return launch_f32_g<D, 8>(a, s);
+        default: return hipErrorInvalidValue;
+    }
+}
+
 template <typename TO>
 hipError_t launch_merge_t(const DecodeArgs &a, hipStream_t s) {
     const int64_t rows = a.f.B * a.f.H;
@@ -690,7 +928,27 @@ const void *stream_kernel_d(const AttnFwdArgs &f, int G) {
 #undef GT_SK
 }
 
+template <int D>
+const void *f32_kernel_d(const AttnFwdArgs &f, int G) {
+    const int mode = !f.mask ? 0 : (f.mask_bool ? 1 : 2);
+#define GT_FK(GG) \
+    (mode == 0 ? (const void *)decode_f32_kernel<D, GG, 0> \
+               : mode == 1 ? (const void *)decode_f32_kernel<D, GG, 1> : (const void *)decode_f32_kernel<D, GG, 2>)
+    switch (G) {
+        case 1: return GT_FK(1);
+        case 2: return GT_FK(2);
+        case 4: return GT_FK(4);
+        case 8: return GT_FK(8);
+        default: return nullptr;
+    }
+#undef GT_FK
+}
+
 const void *stream_kernel(const AttnFwdArgs &f, int cd) {
+    if (cd == GT_F32) {
+        const int G = decode_head_tile(f.H / f.Hkv, kDecodeF32MaxTile);
+        return f.D == 128 ? f32_kernel_d<128>(f, G) : f32_kernel_d<64>(f, G);
+    }
     const int G = decode_head_tile(f.H / f.Hkv, kDecodeMaxTile);
     if (cd == GT_F16) return f.D == 128 ? stream_kernel_d<_Float16, 128>(f, G) : stream_kernel_d<_Float16, 64>(f, G);
     return f.D == 128 ? stream_kernel_d<__bf16, 128>(f, G) : stream_kernel_d<__bf16, 64>(f, G);
@@ -721,11 +979,26 @@ int attn_decode_splits(const AttnFwdArgs &f, int cd) {
     // without a partial last round; each extra split costs a little merge work.
     const void *kernel = stream_kernel(f, cd);
     const int64_t slots = kernel ? resident_slots(kernel) : 512;
-    const int64_t steps = (f.S + kStep - 1) / kStep;
-    return decode_split_count(decode_units(f.B, f.H, f.Hkv, kDecodeMaxTile), steps, slots, std::min<int64_t>(64, steps));
+    const int64_t step = cd == GT_F32 ? kStepF32 : kStep;
+    const int64_t steps = (f.S + step - 1) / step;
+    return decode_split_count(decode_units(f.B, f.H, f.Hkv, attn_decode_max_tile(cd)), steps, slots,
+                              std::min<int64_t>(64, steps));
 }
 
+int attn_decode_max_tile(int cd) { return cd == GT_F32 ? kDecodeF32MaxTile : kDecodeMaxTile; }
+
 bool attn_decode_supported(const AttnFwdArgs &f, int cd) {
+    if (cd == GT_F32) {
+        if (f.L != 1 || f.S <= 0 || f.D != f.Dv || (f.D != 64 && f.D != 128)) return false;
+        if (f.S >= (1LL << 30)) return false;  // 32-bit key indices
+        if ((f.S - 1) * f.k_ss * 4 + f.D * 4 > 0xffffffffLL || (f.S - 1) * f.v_ss * 4 + f.D * 4 > 0xffffffffLL) return false;
+        if (decode_units(f.B, f.H, f.Hkv, kDecodeF32MaxTile) >= (1LL << 31)) return false;  // grid.x
+        // 16-byte row loads: every row start must be 16-byte aligned
+        const int64_t strides[] = {f.q_sb, f.q_sh, f.k_sb, f.k_sh, f.k_ss, f.v_sb, f.v_sh, f.v_ss};
+        for (int64_t st : strides) if (st % 4 != 0) return false;
+        for (const void *p : {f.q, f.k, f.v}) if ((uintptr_t)p % 16 != 0) return false;
+        return true;
+    }
     if (cd != GT_F16 && cd != GT_BF16) return false;
     if (f.L != 1 || f.S <= 0 || f.D != f.Dv) return false;
     if (f.S >= (1LL << 30)) return false;  // 32-bit key indices
@@ -748,5 +1021,6 @@ hipError_t launch_attn_decode(const DecodeArgs &a, int cd, hipStream_t s) {
     const int G = decode_head_tile(a.f.H / a.f.Hkv, kDecodeMaxTile);
     if (cd == GT_F16) return launch_d<_Float16>(a, G, s);
     if (cd == GT_BF16) return launch_d<__bf16>(a, G, s);
+    if (cd == GT_F32) return a.f.D == 128 ? launch_f32_d<128>(a, s) : launch_f32_d<64>(a, s);
     return hipErrorInvalidValue;
 }

@@ -244,8 +244,9 @@ bool dispatch_forward(const AttnFwdArgs &a, int cd, int dev) {
         da.f = a;
         da.nsplit = attn_decode_splits(a, cd);
         gt_scratch ws;
-        if (!decode_partials(da, decode_units(a.B, a.H, a.Hkv, kDecodeMaxTile), dev, ws)) return false;
-        note_launch(decode_note((std::string("decode ") + dtype_tag(cd)).c_str(), da, kDecodeMaxTile));
+        const int tile = attn_decode_max_tile(cd);
+        if (!decode_partials(da, decode_units(a.B, a.H, a.Hkv, tile), dev, ws)) return false;
+        note_launch(decode_note((std::string("decode ") + dtype_tag(cd)).c_str(), da, tile));
         return gt_hip_check(launch_attn_decode(da, cd, gt_stream()), "flash_attention decode kernel");
     }
     if (attn_prefill_supported(a, cd)) {
@@ -1022,7 +1023,7 @@ extern "C" int gt_flash_attention_noalloc(const gt_tensor *q, const gt_tensor *k
             da.part_ml = da.part_o + rows * (size_t)D;
         }
         note_launch(q8 ? decode_note("decode q8_0", da, kDecodeQ8MaxTile)
-                       : decode_note((std::string("decode ") + dtype_tag(cd)).c_str(), da, kDecodeMaxTile));
+                       : decode_note((std::string("decode ") + dtype_tag(cd)).c_str(), da, attn_decode_max_tile(cd)));
         const hipError_t e = q8 ? launch_attn_decode_q8(da, gt_stream()) : launch_attn_decode(da, cd, gt_stream());
         if (partials) scratch_release(dev, held);
         return gt_hip_check(e, "flash_attention_noalloc decode kernel") ? 0 : -1;

@@ -54,7 +54,7 @@ def test_two_pieces_equal_the_whole_sequence(dev, dtype, D):
     assert_close(torch.cat([head, tail], dim=2), want, dtype, "two pieces")
 
 
-@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
 def test_decode_steps_equal_prefill_rows(dev, dtype):
     B, H, Hkv, T, D = 3, 8, 2, 40, 128
     q, k, v = randn((B, H, T, D), 4, dtype), randn((B, Hkv, T, D), 5, dtype), randn((B, Hkv, T, D), 6, dtype)
