@@ -173,6 +173,7 @@ hipError_t launch_attn_decode_merge(const DecodeArgs &a, int out_dtype, hipStrea
 // Explicit attention weights from the forward's log-sum-exp: (B,H,L,S), or (B,L,S) averaged
 // over the heads, in f.out_dtype.
 hipError_t launch_attn_weights(const AttnFwdArgs &f, int cd, void *w, bool average, hipStream_t s);
+bool attn_weights_mfma(const AttnFwdArgs &f, int cd);  // the MFMA weights kernels take `f`
 // Dropout decisions of `rows` attention rows of S keys as bytes (1 = kept; all 1 when keep_all).
 hipError_t launch_dropout_mask(const GtDropout &d, bool keep_all, int64_t rows, int64_t S, uint8_t *out, hipStream_t s);
 

@@ -13,6 +13,7 @@
 // S[query = 8(i/4) + 4half + i%4][key = lane % 32], so the 32 lanes of a half store 32
 // consecutive keys of one query row.  HBM-bound: the weights written dominate the traffic.
 // Averaged weights: a workgroup walks all H heads of its rows and writes the mean once.
+// float32, head size 64 or 128: the same on v_mfma_f32_32x32x2_f32 (attn_weights_f32_kernel).
 // Other dtypes / head sizes: one thread per (query, key) in the compute precision.
 // Dropout (f.dropout): the weights are those the dropout forward multiplied V by, P * m with the
 // element's multiplier m (gt_philox.h); computed by the per-element kernel.
@@ -21,6 +22,7 @@
 #include "gt_internal.h"
 #include "mfma_util.h"
 
+#include <algorithm>
 #include <cmath>
 
 namespace {
@@ -69,7 +71,7 @@ __global__ __launch_bounds__(64 * WQ) void attn_weights_kernel(AttnFwdArgs f, vo
 #pragma unroll
         for (int i = 0; i < 16; ++i) lsv[i] = lse[min(q0 + 8 * (i / 4) + 4 * half + (i % 4), L - 1)] * kLog2e;
     }
-    for (int kt = 0; kt < nkt; ++kt) {
+    for (int kt = blockIdx.y; kt < nkt; kt += gridDim.y) {  // key tiles split over blockIdx.y
         const int k0 = kt * 32;
         f32x16 acc;
 #pragma unroll
@@ -157,7 +159,7 @@ __global__ __launch_bounds__(64 * WQ) void attn_weights_vec_kernel(AttnFwdArgs f
         ls1 = ((const float *)f.lse)[g * f.L + qc] * kLog2e;
     }
     const int64_t base = AVG ? b * f.L : g * f.L;
-    for (int kt = 0; kt < nkt; ++kt) {
+    for (int kt = blockIdx.y; kt < nkt; kt += gridDim.y) {  // key tiles split over blockIdx.y
         const int k0 = kt * 64;
         f32x16 acc[2];
 #pragma unroll
@@ -230,6 +232,131 @@ __global__ __launch_bounds__(64 * WQ) void attn_weights_vec_kernel(AttnFwdArgs f
     }
 }
 
+// Float32 weights, head size 64 or 128: the structure of attn_weights_vec_kernel on
+// v_mfma_f32_32x32x2_f32.  S^T = K.Q^T with k-step (u, e) = dim (D/2)(lane/32) + 4u + e: a lane's
+// Q values are half of its query row (D/2 floats in registers) and its K values come four
+// k-steps at a time from one 16-byte load of key row lrow.  The wavefront's 32 x 64 tile goes
+// through LDS (16-byte writes, rows padded by 16 bytes) and out as 16-byte pieces when S % 4 == 0
+// and the output is 16-byte aligned (VEC), else as 4-byte stores of 64 consecutive keys.
+template <int D, bool CAUSAL, int MASK, bool AVG, bool VEC>
+__global__ __launch_bounds__(64 * WQ) void attn_weights_f32_kernel(AttnFwdArgs f, void *wout, int64_t nrb) {
+    constexpr int DH = D / 2;
+    constexpr int RP = 64 + 4;  // LDS row pitch (floats): 64 keys and 16 bytes of padding
+    __shared__ __attribute__((aligned(16))) float tile[WQ][32 * RP];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int lrow = lane & 31, half = lane >> 5;
+    const int64_t rb = blockIdx.x % nrb, g = blockIdx.x / nrb;
+    const int64_t b = AVG ? g : g / f.H;
+    const int L = (int)f.L, S = (int)f.S;
+    const int q0 = (int)rb * 32 * WQ + 32 * w;  // first query row of this wavefront
+    const int q = q0 + lrow;                    // this lane's query row
+    const int qc = min(q, L - 1);
+    const float c = f.scale * kLog2e;
+    const int nh = AVG ? (int)f.H : 1;
+    const float inv_h = 1.0f / (float)nh;
+    const int kv_end = CAUSAL ? min(q0 + 32, S) : S;  // keys any of the wave's rows can see
+    const int nkt = (S + 63) / 64;
+    float *tw = tile[w];
+    // one head: its Q values (query row qc, dims DH half .. +DH) and log2(e) * lse
+    float qf[DH];
+    float ls1 = 0.0f;
+    if (!AVG) {
+        const int64_t h = g % f.H;
+        const float *qr = (const float *)f.q + b * f.q_sb + h * f.q_sh + (int64_t)qc * f.q_sl + DH * half;
+#pragma unroll
+        for (int u = 0; u < DH / 4; ++u) {
+            const f32x4 x = *(const f32x4 *)(qr + 4 * u);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) qf[4 * u + e] = x[e];
+        }
+        ls1 = ((const float *)f.lse)[g * f.L + qc] * kLog2e;
+    }
+    const int64_t base = AVG ? b * f.L : g * f.L;
+    for (int kt = blockIdx.y; kt < nkt; kt += gridDim.y) {  // key tiles split over blockIdx.y
+        const int k0 = kt * 64;
+        f32x16 acc[2];
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) acc[kb][i] = 0.0f;
+        for (int hh = 0; hh < nh; ++hh) {
+            const int64_t h = AVG ? hh : g % f.H;
+            const int64_t hk = h / (f.H / f.Hkv);
+            float ls = ls1;
+            if constexpr (AVG) {
+                const float *qr = (const float *)f.q + b * f.q_sb + h * f.q_sh + (int64_t)qc * f.q_sl + DH * half;
+#pragma unroll
+                for (int u = 0; u < DH / 4; ++u) {
+                    const f32x4 x = *(const f32x4 *)(qr + 4 * u);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) qf[4 * u + e] = x[e];
+                }
+                ls = ((const float *)f.lse)[(b * f.H + h) * f.L + qc] * kLog2e;
+            }
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) {
+                const int kb0 = k0 + 32 * kb;
+                if (kb0 >= kv_end) continue;  // every weight of the block is 0 (acc stays 0)
+                // A = K rows (key kb0 + lrow), B = Q: sc[i] is key kb0 + 8(i/4) + 4half + i%4, query q
+                const float *kr =
+                    (const float *)f.k + b * f.k_sb + hk * f.k_sh + (int64_t)min(kb0 + lrow, S - 1) * f.k_ss + DH * half;
+                f32x16 sc;
+#pragma unroll
+                for (int i = 0; i < 16; ++i) sc[i] = 0.0f;
+#pragma unroll
+                for (int u = 0; u < DH / 4; ++u) {
+                    const f32x4 kv = *(const f32x4 *)(kr + 4 * u);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) sc = __builtin_amdgcn_mfma_f32_32x32x2f32(kv[e], qf[4 * u + e], sc, 0, 0, 0);
+                }
+                const bool interior = MASK == 0 && kb0 + 31 < S && q0 + 31 < L && (!CAUSAL || kb0 + 31 <= q0);
+                if (interior) {
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) {
+                        const float p = exp2f(fmaf(sc[i], c, 0.0f * kLog2e - ls));
+                        acc[kb][i] += AVG ? p * inv_h : p;
+                    }
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) {
+                        const int key = kb0 + 8 * (i / 4) + 4 * half + (i % 4);
+                        bool blocked = key >= S || q >= L || (CAUSAL && key > q);
+                        const float add = mask_term<MASK>(f, b, h, qc, min(key, S - 1), blocked);
+                        const float p = blocked ? 0.0f : exp2f(fmaf(sc[i], c, add * kLog2e - ls));
+                        acc[kb][i] += AVG ? p * inv_h : p;
+                    }
+                }
+            }
+        }
+        // the tile into LDS as rows (query) x keys, four keys per 16-byte write
+        __builtin_amdgcn_wave_barrier();  // the previous tile's reads are done
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int gq = 0; gq < 4; ++gq) {
+                const f32x4 v4 = {acc[kb][4 * gq], acc[kb][4 * gq + 1], acc[kb][4 * gq + 2], acc[kb][4 * gq + 3]};
+                *(f32x4 *)&tw[lrow * RP + 32 * kb + 8 * gq + 4 * half] = v4;
+            }
+        __builtin_amdgcn_wave_barrier();
+        if constexpr (VEC) {
+            // piece u * 64 + lane: row (u * 64 + lane) / 16, keys 4 * (lane % 16) .. +3
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int pc = u * 64 + lane, row = pc >> 4, key0 = k0 + 4 * (pc & 15);
+                const f32x4 piece = *(const f32x4 *)&tw[row * RP + 4 * (pc & 15)];
+                if (q0 + row < L && key0 < S) *(f32x4 *)((float *)wout + (base + q0 + row) * f.S + key0) = piece;
+            }
+        } else {
+            // row r: lanes write its 64 keys
+#pragma unroll 4
+            for (int r = 0; r < 32; ++r) {
+                const int key = k0 + lane;
+                if (q0 + r < L && key < S) ((float *)wout)[(base + q0 + r) * f.S + key] = tw[r * RP + lane];
+            }
+        }
+    }
+}
+
 // Generic: one thread per (query, key), any float dtype, accumulation in A (double for float64).
 template <typename T, typename A, bool AVG>
 __global__ __launch_bounds__(256) void attn_weights_generic_kernel(AttnFwdArgs f, void *wout) {
@@ -286,6 +413,14 @@ __global__ __launch_bounds__(256) void dropout_mask_kernel(GtDropout d, int keep
         if (s0 + j < S) out[row * S + s0 + j] = keep_all || x.w[j] < d.thresh ? 1 : 0;
 }
 
+// Averaged weights run every head inside one workgroup, whose grid (query blocks x B) can be
+// far smaller than the GPU: their key tiles are split over blockIdx.y up to ~1024 workgroups.
+// Each weight is still computed and written by one workgroup, in the same order: the same bits.
+unsigned key_splits(int64_t grid, int64_t nkt, bool avg) {
+    if (!avg || grid <= 0) return 1;
+    return (unsigned)std::max<int64_t>(1, std::min<int64_t>(nkt, (1024 + grid - 1) / grid));
+}
+
 template <typename T, int D, bool AVG>
 hipError_t launch_mfma(const AttnFwdArgs &f, void *w, hipStream_t st) {
     const int64_t nrb = (f.L + 32 * WQ - 1) / (32 * WQ);
@@ -294,10 +429,11 @@ hipError_t launch_mfma(const AttnFwdArgs &f, void *w, hipStream_t st) {
     const int mode = !f.mask ? 0 : (f.mask_bool ? 1 : 2);
     // whole 16-byte pieces of every row: the LDS-transposed kernel
     const bool vec = f.S % 8 == 0 && (uintptr_t)w % 16 == 0;
+    const unsigned ny = key_splits(grid, vec ? (f.S + 63) / 64 : (f.S + 31) / 32, AVG);
 #define GT_W(C, MK)                                                                                                     \
     do {                                                                                                                \
-        if (vec) hipLaunchKernelGGL((attn_weights_vec_kernel<T, D, C, MK, AVG>), dim3((unsigned)grid), dim3(64 * WQ), 0, st, f, w, nrb); \
-        else hipLaunchKernelGGL((attn_weights_kernel<T, D, C, MK, AVG>), dim3((unsigned)grid), dim3(64 * WQ), 0, st, f, w, nrb); \
+        if (vec) hipLaunchKernelGGL((attn_weights_vec_kernel<T, D, C, MK, AVG>), dim3((unsigned)grid, ny), dim3(64 * WQ), 0, st, f, w, nrb); \
+        else hipLaunchKernelGGL((attn_weights_kernel<T, D, C, MK, AVG>), dim3((unsigned)grid, ny), dim3(64 * WQ), 0, st, f, w, nrb); \
     } while (0)
     if (f.causal) {
         if (mode == 0) GT_W(true, 0);
@@ -309,6 +445,32 @@ hipError_t launch_mfma(const AttnFwdArgs &f, void *w, hipStream_t st) {
         else GT_W(false, 2);
     }
 #undef GT_W
+    return hipGetLastError();
+}
+
+template <int D, bool AVG>
+hipError_t launch_f32(const AttnFwdArgs &f, void *w, hipStream_t st) {
+    const int64_t nrb = (f.L + 32 * WQ - 1) / (32 * WQ);
+    const int64_t grid = nrb * (AVG ? f.B : f.B * f.H);
+    if (grid > 0x7fffffffLL) return hipErrorInvalidConfiguration;
+    const int mode = !f.mask ? 0 : (f.mask_bool ? 1 : 2);
+    const bool vec = f.S % 4 == 0 && (uintptr_t)w % 16 == 0;
+    const unsigned ny = key_splits(grid, (f.S + 63) / 64, AVG);
+#define GT_WF(C, MK)                                                                                                    \
+    do {                                                                                                                \
+        if (vec) hipLaunchKernelGGL((attn_weights_f32_kernel<D, C, MK, AVG, true>), dim3((unsigned)grid, ny), dim3(64 * WQ), 0, st, f, w, nrb); \
+        else hipLaunchKernelGGL((attn_weights_f32_kernel<D, C, MK, AVG, false>), dim3((unsigned)grid, ny), dim3(64 * WQ), 0, st, f, w, nrb); \
+    } while (0)
+    if (f.causal) {
+        if (mode == 0) GT_WF(true, 0);
+        else if (mode == 1) GT_WF(true, 1);
+        else GT_WF(true, 2);
+    } else {
+        if (mode == 0) GT_WF(false, 0);
+        else if (mode == 1) GT_WF(false, 1);
+        else GT_WF(false, 2);
+    }
+#undef GT_WF
     return hipGetLastError();
 }
 
@@ -326,11 +488,22 @@ hipError_t launch_generic(const AttnFwdArgs &f, void *w, bool avg, hipStream_t s
 
 // `f` as for the forward (q, k, mask, lse of the same call; out_dtype = dtype of the weights);
 // `w` receives (B,H,L,S), or (B,L,S) when averaging over the heads.
+bool attn_weights_mfma(const AttnFwdArgs &f, int cd) {
+    if ((cd != GT_F16 && cd != GT_BF16 && cd != GT_F32) || (f.D != 64 && f.D != 128) || f.out_dtype != cd) return false;
+    if (f.kv_len || f.q_pos || f.dropout || (uintptr_t)f.q % 16 != 0 || (uintptr_t)f.k % 16 != 0) return false;
+    const int64_t rows = cd == GT_F32 ? 4 : 8;  // 16-byte rows
+    for (int64_t st : {f.q_sb, f.q_sh, f.q_sl, f.k_sb, f.k_sh, f.k_ss})
+        if (st % rows != 0) return false;
+    return true;
+}
+
 hipError_t launch_attn_weights(const AttnFwdArgs &f, int cd, void *w, bool average, hipStream_t st) {
     if (f.B * f.L * f.S == 0 || f.H == 0) return hipSuccess;
-    bool mfma = (cd == GT_F16 || cd == GT_BF16) && (f.D == 64 || f.D == 128) && f.out_dtype == cd && !f.kv_len &&
-                !f.q_pos && !f.dropout && (uintptr_t)f.q % 16 == 0 && (uintptr_t)f.k % 16 == 0;
-    for (int64_t st8 : {f.q_sb, f.q_sh, f.q_sl, f.k_sb, f.k_sh, f.k_ss}) mfma = mfma && st8 % 8 == 0;
+    const bool mfma = attn_weights_mfma(f, cd);
+    if (mfma && cd == GT_F32) {
+        if (f.D == 128) return average ? launch_f32<128, true>(f, w, st) : launch_f32<128, false>(f, w, st);
+        return average ? launch_f32<64, true>(f, w, st) : launch_f32<64, false>(f, w, st);
+    }
     if (mfma) {
         if (cd == GT_F16) {
             if (f.D == 128) return average ? launch_mfma<_Float16, 128, true>(f, w, st) : launch_mfma<_Float16, 128, false>(f, w, st);

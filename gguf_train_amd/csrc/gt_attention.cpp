@@ -1147,6 +1147,8 @@ gt_tensor *attention_weights(const gt_tensor *q, const gt_tensor *k, const gt_te
     gt_tensor *w = average_heads ? gt_new_tensor(3, wsh3, q->dtype, GT_DEV_CUDA, dev)
                                  : gt_new_tensor(4, wsh4, q->dtype, GT_DEV_CUDA, dev);
     if (!w) return nullptr;
+    note_launch(std::string("weights ") + (attn_weights_mfma(a, cd) ? "mfma " : "generic ") + dtype_tag(cd) +
+                " D=" + std::to_string(D));
     if (!gt_hip_check(launch_attn_weights(a, cd, gt_data(w), average_heads != 0, gt_stream()),
                       "attention weights kernel")) {
         gt_tensor_free(w);
