@@ -329,19 +329,27 @@ void apply_dropout(AttnFwdArgs &a, const Dropout *drop) {
 }
 
 // ---- head padding ----------------------------------------------------------------------------
-// The MFMA kernels take head sizes 64 and 128.  Float16/bfloat16 attention with another head size
-// up to 128 and more than one query row runs on them with q, k, v (and in the backward dO and the
-// output) zero-padded to 64 or 128 dims: the zero dims add nothing to Q.K^T (the scale stays that
-// of the real head size), padded V columns give output columns that are dropped, and the padded
-// columns of dQ, dK, dV are zero and dropped.  Single-query rows keep their kernels (padding would
-// copy the whole K/V).
+// The MFMA kernels take head sizes 64 and 128.  Attention with another head size up to 128 and
+// more than one query row runs on them with q, k, v (and in the backward dO and the output)
+// zero-padded to 64 or 128 dims: the zero dims add nothing to Q.K^T (the scale stays that of the
+// real head size), padded V columns give output columns that are dropped, and the padded columns
+// of dQ, dK, dV are zero and dropped.  Single-query rows keep their kernels (padding would copy
+// the whole K/V).  Float32 pads only calls its MFMA kernels take (16 query rows or more, no
+// dropout, no mask or a key-padding row: f32_pads), the rest keep the generic kernels unpadded.
 int64_t mfma_head(int64_t d) { return d <= 0 ? 0 : d <= 64 ? 64 : d <= 128 ? 128 : 0; }
 
 int64_t padded_head(int cd, int64_t L, int64_t D, int64_t Dv) {
-    if ((cd != GT_F16 && cd != GT_BF16) || L <= 1) return 0;
+    if ((cd != GT_F16 && cd != GT_BF16 && cd != GT_F32) || L <= 1) return 0;
+    if (cd == GT_F32 && L < 16) return 0;
     if (D == Dv && (D == 64 || D == 128)) return 0;
     if (!mfma_head(D) || !mfma_head(Dv)) return 0;
     return std::max(mfma_head(D), mfma_head(Dv));
+}
+
+// Float32 calls whose padded form the float32 MFMA kernels take (masks staged, dropout applied).
+bool f32_pads(const AttnFwdArgs &a) {
+    const int mode = attn_mask_mode(a);
+    return !a.dropout && !a.kv_len && !a.q_pos && (mode == 0 || mode == 4);
 }
 
 // A dense (d0, d1, d2, Dp) copy of the 4-D device tensor t (innermost contiguous, 2- or 4-byte
@@ -448,7 +456,7 @@ int attention_forward(const char *who, const gt_tensor *q, const gt_tensor *k, c
             apply_dropout(a, drop);
             // heads padded to the MFMA kernels' sizes (output and float32 output unpadded after)
             const gt_tensor *po = nullptr, *po32 = nullptr;
-            const int64_t Dp = qrope || a.out_dtype != cd ? 0 : padded_head(cd, L, D, Dv);
+            const int64_t Dp = qrope || a.out_dtype != cd || (cd == GT_F32 && !f32_pads(a)) ? 0 : padded_head(cd, L, D, Dv);
             if (Dp) {
                 const gt_tensor *qp = pad_heads(qs, Dp, dev, tmp), *kp = pad_heads(ks, Dp, dev, tmp);
                 const gt_tensor *vp = pad_heads(vs, Dp, dev, tmp);
@@ -637,7 +645,7 @@ int attention_backward(const char *who, const gt_tensor *grad_out, const gt_tens
     // into every dS, so that case recomputes the float32 output (the forward is deterministic:
     // it is the training forward's copy bit for bit).
     const gt_tensor *lse_s = nullptr, *out_s = nullptr;
-    const int64_t Dp = padded_head(cd, L, D, Dv);  // heads padded for the MFMA kernels (0: none)
+    int64_t Dp = padded_head(cd, L, D, Dv);  // heads padded for the MFMA kernels (0: none)
     const bool mfma_shape = ((cd == GT_F16 || cd == GT_BF16) && D == Dv && (D == 64 || D == 128)) || Dp != 0;
     if (!lse || !out || (mfma_shape && out->dtype != GT_F32)) {
         gt_tensor *o2 = nullptr, *l2 = nullptr, *o32 = nullptr;
@@ -688,7 +696,9 @@ int attention_backward(const char *who, const gt_tensor *grad_out, const gt_tens
         a.f.o = const_cast<void *>(gt_data(out_s));
         a.o_f32 = od == GT_F32 && cd != GT_F32;
         apply_dropout(a.f, drop);
-        // heads padded to the MFMA kernels' sizes: padded inputs, padded gradients unpadded after
+        // heads padded to the MFMA kernels' sizes: padded inputs, padded gradients unpadded after.
+        // Float32: only where its MFMA backward takes the padded call (32 dQ workgroups or more)
+        if (cd == GT_F32 && !(f32_pads(a.f) && B * H * ((L + 127) / 128) >= 32)) Dp = 0;
         const gt_tensor *pq = nullptr, *pk = nullptr, *pv = nullptr;
         if (Dp) {
             const gt_tensor *qp = pad_heads(qs, Dp, dev, tmp), *kp = pad_heads(ks, Dp, dev, tmp);
