@@ -670,7 +670,7 @@ __device__ inline f32x16 mma_f32x2(float a, float b, f32x16 c) {
 }
 
 // dQ: a workgroup owns 128 query rows (32 per wavefront), K/V tiles of 32 keys.
-template <int D, bool CAUSAL, int MASK>
+template <int D, bool CAUSAL, int MASK, bool DROP>
 __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void bwd_dq_f32_kernel(AttnBwdArgs a, int nq) {
     constexpr int NW = 4, BM = 128, BN = 32, NST = 2;
     constexpr int CH = D / 4, TILE = BN * D, NPW = BN * CH / 64 / NW, DB = D / 32, DH = D / 2;
@@ -718,6 +718,9 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void bwd_dq_f32_kernel(AttnBw
         for (int u = 0; u < DH; ++u) asm volatile("" ::"v"(qf[u]), "v"(gf[u]));
     }
     const float lse2 = ((const float *)f.lse)[bh * f.L + lqc] * kLog2e;
+    // dropout: Philox block of keys 0..3 of this lane's row (rows past L draw unused words)
+    const uint64_t drow = DROP ? (uint64_t)(bh * f.L + lq) * (uint64_t)((f.S + 3) / 4) : 0;
+    const int64_t dwords = (f.S + 31) / 32;  // decision words per row
     f32x16 dq[DB];
 #pragma unroll
     for (int db = 0; db < DB; ++db)
@@ -792,7 +795,7 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void bwd_dq_f32_kernel(AttnBw
             for (int i = 0; i < 16; ++i) sc[i] = 0.0f;
         }
 #pragma unroll
-        for (int i = 0; i < 16; ++i) dp[i] = -dlt;
+        for (int i = 0; i < 16; ++i) dp[i] = DROP ? 0.0f : -dlt;
 #pragma unroll
         for (int u = 0; u < DH / 4; ++u) {
             const int o = lrow * D + ((4 * u) ^ kx);
@@ -802,6 +805,25 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void bwd_dq_f32_kernel(AttnBw
                 sc = mma_f32x2(kv[e], qf[4 * u + e], sc);
                 dp = mma_f32x2(vv[e], gf[4 * u + e], dp);
             }
+        }
+        if constexpr (DROP) {
+            // entries 4g .. 4g+3 are keys k0 + 8g + 4half + 0..3: one Philox block; dP = m dO.V - delta
+            const float dscale = (float)f.drop.scale;
+            uint32_t word = 0u;  // bit k: key k0 + k kept
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const GtWord4 x = gt_philox4x32_10(drow + (uint64_t)((k0 + 8 * g + 4 * half) >> 2), f.drop.offset,
+                                                   f.drop.seed);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const bool keep = x.w[e] < f.drop.thresh;
+                    dp[4 * g + e] = fmaf(dp[4 * g + e], keep ? dscale : 0.0f, -dlt);
+                    word |= (keep ? 1u : 0u) << (8 * g + 4 * half + e);
+                }
+            }
+            // the row's word for these 32 keys (the two halves hold complementary keys), for dK/dV
+            const auto r = __builtin_amdgcn_permlane32_swap(word, word, false, false);
+            if (a.dbits && half == 0 && lq < L && k0 < S) a.dbits[(bh * f.L + lq) * dwords + k0 / 32] = r[0] | r[1];
         }
         float ds[16];
         const bool interior = k0 + BN - 1 < S && wq0 + 31 < L && (!CAUSAL || wq0 >= k0 + BN - 1);
@@ -840,7 +862,7 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void bwd_dq_f32_kernel(AttnBw
 // dK, dV: a workgroup owns 128 keys of one kv head (32 per wavefront, K and V rows in registers)
 // and walks query steps of 64 rows over every query head of its group; Q, dO, lse and delta of a
 // step reach LDS by DMA.
-template <int D, bool CAUSAL, int MASK>
+template <int D, bool CAUSAL, int MASK, bool DROP>
 __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void bwd_dkdv_f32_kernel(AttnBwdArgs a) {
     constexpr int BKV = 128, BQ = 64, NST = 2, NW = 4;
     constexpr int CH = D / 4, TILE = BQ * D, NPW = BQ * CH / 64 / NW, DB = D / 32, DH = D / 2;
@@ -849,6 +871,8 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void bwd_dkdv_f32_kernel(Attn
     __shared__ __attribute__((aligned(1024))) float sG[NST][TILE];  // dO
     __shared__ __attribute__((aligned(16))) float sL[NST][BQ];      // lse (natural log)
     __shared__ __attribute__((aligned(16))) float sD[NST][BQ];      // delta
+    // dropout decisions: word [w][r] = keys 32w .. 32w+31 of the tile for query r of the step
+    __shared__ __attribute__((aligned(16))) uint32_t sDm[DROP ? NST : 1][DROP ? NW * BQ : 1];
 
     const AttnFwdArgs &f = a.f;
     const int tid = threadIdx.x, lane = tid & 63;
@@ -914,6 +938,14 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void bwd_dkdv_f32_kernel(Attn
         const uint32_t rq = (uint32_t)min(qs0 + lane, L - 1) * 4u;  // lane's row of lse / delta
         lds_dma4(lds_addr(&sL[sg][0]), lb, rq);
         lds_dma4(lds_addr(&sD[sg][0]), db, rq);
+        if constexpr (DROP) {
+            // the dQ kernel's word (row qs0 + lane, keys of this wave); 32-bit byte offsets
+            // (the launcher checks the buffer's size)
+            const int64_t dwords = (f.S + 31) / 32;
+            const int64_t drow = (b * f.H + h) * f.L + min(qs0 + lane, L - 1);
+            const uint32_t off = (uint32_t)((drow * dwords + min((int64_t)(k0 / 32 + w), dwords - 1)) * 4);
+            lds_dma4(lds_addr(&sDm[sg][w * BQ]), a.dbits, off);
+        }
         const uint32_t dq = lds_addr(&sQ[sg][0]) + w * NPW * 1024;
         const uint32_t dg = lds_addr(&sG[sg][0]) + w * NPW * 1024;
         if (qs0 + BQ <= L) {
@@ -961,7 +993,7 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void bwd_dkdv_f32_kernel(Attn
             for (int g = 0; g < 4; ++g) {
                 const f32x4 d4 = *(const f32x4 *)&sD[sg][32 * qb + 8 * g + 4 * half];
 #pragma unroll
-                for (int e = 0; e < 4; ++e) dp[4 * g + e] = -d4[e];
+                for (int e = 0; e < 4; ++e) dp[4 * g + e] = DROP ? 0.0f : -d4[e];
             }
 #pragma unroll
             for (int u = 0; u < DH / 4; ++u) {
@@ -971,6 +1003,22 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void bwd_dkdv_f32_kernel(Attn
                 for (int e = 0; e < 4; ++e) {
                     sc = mma_f32x2(qa[e], kf[4 * u + e], sc);
                     dp = mma_f32x2(ga[e], vf[4 * u + e], dp);
+                }
+            }
+            // dropout: multiplier of entry i (query 32qb + 8(i/4) + 4half + i%4 of the step, this
+            // lane's key): bit lrow of word [w][query]; dP = m dO.V - delta
+            uint32_t keep = 0u;  // bit i: entry i kept
+            if constexpr (DROP) {
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const u32x4 dw = *(const u32x4 *)&sDm[sg][w * BQ + 32 * qb + 8 * g + 4 * half];
+                    const f32x4 d4 = *(const f32x4 *)&sD[sg][32 * qb + 8 * g + 4 * half];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const uint32_t bit = (dw[e] >> lrow) & 1u;
+                        keep |= bit << (4 * g + e);
+                        dp[4 * g + e] = fmaf(dp[4 * g + e], bit ? (float)f.drop.scale : 0.0f, -d4[e]);
+                    }
                 }
             }
             float p[16], ds[16];
@@ -990,7 +1038,7 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void bwd_dkdv_f32_kernel(Attn
                     const int i = 4 * g + e;
                     const bool ok = interior || (uint32_t)(8 * g + e - lo) <= (uint32_t)span;
                     const float pv = ok ? fast_exp2(fmaf(sc[i], c, -l4[e] * kLog2e)) : 0.0f;
-                    p[i] = pv;
+                    p[i] = DROP ? ((keep >> i) & 1u ? pv * (float)f.drop.scale : 0.0f) : pv;
                     ds[i] = pv * dp[i];
                 }
             }
@@ -1023,28 +1071,38 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void bwd_dkdv_f32_kernel(Attn
     }
 }
 
-template <int D, bool CAUSAL, int MASK>
+template <int D, bool CAUSAL, int MASK, bool DROP>
 hipError_t launch_bwd_f32_cm(const AttnBwdArgs &a, hipStream_t s) {
     const AttnFwdArgs &f = a.f;
     const int nq = (int)((f.L + 127) / 128);
-    hipLaunchKernelGGL((bwd_dq_f32_kernel<D, CAUSAL, MASK>), dim3((unsigned)(nq * f.B * f.H)), dim3(256), 0, s, a, nq);
+    hipLaunchKernelGGL((bwd_dq_f32_kernel<D, CAUSAL, MASK, DROP>), dim3((unsigned)(nq * f.B * f.H)), dim3(256), 0, s, a, nq);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const int nkt = (int)((f.S + 127) / 128);
-    hipLaunchKernelGGL((bwd_dkdv_f32_kernel<D, CAUSAL, MASK>), dim3((unsigned)(nkt * f.B * f.Hkv)), dim3(256), 0, s, a);
+    hipLaunchKernelGGL((bwd_dkdv_f32_kernel<D, CAUSAL, MASK, DROP>), dim3((unsigned)(nkt * f.B * f.Hkv)), dim3(256), 0, s, a);
     return hipGetLastError();
+}
+
+template <int D, bool DROP>
+hipError_t launch_bwd_f32_dd(const AttnBwdArgs &a, hipStream_t s) {
+    const bool kp = attn_mask_mode(a.f) == 4;
+    if (a.f.causal) return kp ? launch_bwd_f32_cm<D, true, 4, DROP>(a, s) : launch_bwd_f32_cm<D, true, 0, DROP>(a, s);
+    return kp ? launch_bwd_f32_cm<D, false, 4, DROP>(a, s) : launch_bwd_f32_cm<D, false, 0, DROP>(a, s);
 }
 
 template <int D>
 hipError_t launch_bwd_f32_d(const AttnBwdArgs &a, hipStream_t s) {
-    const bool kp = attn_mask_mode(a.f) == 4;
-    if (a.f.causal) return kp ? launch_bwd_f32_cm<D, true, 4>(a, s) : launch_bwd_f32_cm<D, true, 0>(a, s);
-    return kp ? launch_bwd_f32_cm<D, false, 4>(a, s) : launch_bwd_f32_cm<D, false, 0>(a, s);
+    if (!a.f.dropout) return launch_bwd_f32_dd<D, false>(a, s);
+    // dropout: the dK/dV kernel reads the dQ kernel's decision words (it does not draw them)
+    // through 32-bit byte offsets
+    const int64_t bytes = a.f.B * a.f.H * a.f.L * ((a.f.S + 31) / 32) * 4;
+    if (!a.dbits || bytes > 0xffffffffLL) return hipErrorInvalidValue;
+    return launch_bwd_f32_dd<D, true>(a, s);
 }
 
 bool bwd_f32_supported(const AttnBwdArgs &a) {
     const AttnFwdArgs &f = a.f;
-    if (f.D != f.Dv || (f.D != 64 && f.D != 128) || f.dropout || f.kv_len || f.q_pos) return false;
+    if (f.D != f.Dv || (f.D != 64 && f.D != 128) || f.kv_len || f.q_pos) return false;
     const int mode = attn_mask_mode(f);
     if (mode != 0 && mode != 4) return false;
     // as the forward: fewer than 16 query rows stay on the generic kernels

@@ -615,7 +615,9 @@ __device__ inline f32x16 mfma_f32x2(float a, float b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
 }
 
-template <int D, bool CAUSAL, int MASK>
+// DROP: P.V takes P times the element's multiplier (gt_philox.h); the lane's entries 4g .. 4g+3
+// are 4 consecutive keys of its row, one Philox block.  The running sum keeps the undropped P.
+template <int D, bool CAUSAL, int MASK, bool DROP = false>
 __global__ __launch_bounds__(64 * F32_NW, 2) void prefill_f32_kernel(AttnFwdArgs a, int nq, int npairs) {
     constexpr int NW = F32_NW, BM = F32_BM, BN = F32_BN, NST = F32_NST;
     constexpr int CH = D / 4;               // 16-byte chunks per row
@@ -737,6 +739,8 @@ __global__ __launch_bounds__(64 * F32_NW, 2) void prefill_f32_kernel(AttnFwdArgs
 #pragma unroll
             for (int i = 0; i < 16; ++i) o[db][i] = 0.0f;
         float m = -INFINITY, mthr = -INFINITY, lsum = 0.0f;
+        // dropout: Philox block of keys 0..3 of this lane's row (rows past L draw unused words)
+        const uint64_t drow = DROP ? (uint64_t)(bh * a.L + lq) * (uint64_t)((a.S + 3) / 4) : 0;
 
         for (int j = 0; j < ntiles; ++j, ++step) {
             const int k0 = j * BN;
@@ -801,6 +805,16 @@ __global__ __launch_bounds__(64 * F32_NW, 2) void prefill_f32_kernel(AttnFwdArgs
                 s[i] = fast_exp2(fmaf(s[i], c, -msub));
                 lsum += s[i];
             }
+            if constexpr (DROP) {
+                const float dscale = (float)a.drop.scale;
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const GtWord4 x = gt_philox4x32_10(drow + (uint64_t)((k0 + 8 * g + 4 * half) >> 2), a.drop.offset,
+                                                       a.drop.seed);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) s[4 * g + e] *= x.w[e] < a.drop.thresh ? dscale : 0.0f;
+                }
+            }
             // ---- O^T += V^T . P^T ----
 #pragma unroll
             for (int st2 = 0; st2 < 16; ++st2)
@@ -830,7 +844,7 @@ __global__ __launch_bounds__(64 * F32_NW, 2) void prefill_f32_kernel(AttnFwdArgs
 
 bool prefill_f32_supported(const AttnFwdArgs &f) {
     if (f.out_dtype != GT_F32 || f.D != f.Dv || (f.D != 64 && f.D != 128)) return false;
-    if (f.dropout || f.rope_q) return false;
+    if (f.rope_q) return false;
     const int mode = attn_mask_mode(f);
     if (mode != 0 && mode != 4) return false;
     // fewer than 16 query rows: one mostly empty 128-row tile per head walking every key; the
@@ -849,8 +863,25 @@ bool prefill_f32_supported(const AttnFwdArgs &f) {
 }
 
 template <int D>
+hipError_t launch_prefill_f32_drop(const AttnFwdArgs &a, int nq, int npairs, int64_t grid, hipStream_t s) {
+    const int mode = attn_mask_mode(a);
+#define GT_F32_LAUNCH(C, MK) \
+    hipLaunchKernelGGL((prefill_f32_kernel<D, C, MK, true>), dim3((unsigned)grid), dim3(64 * F32_NW), 0, s, a, nq, npairs)
+    if (a.causal) {
+        if (mode == 0) GT_F32_LAUNCH(true, 0);
+        else GT_F32_LAUNCH(true, 4);
+    } else {
+        if (mode == 0) GT_F32_LAUNCH(false, 0);
+        else GT_F32_LAUNCH(false, 4);
+    }
+#undef GT_F32_LAUNCH
+    return hipGetLastError();
+}
+
+template <int D>
 hipError_t launch_prefill_f32_d(const AttnFwdArgs &a, int nq, int npairs, int64_t grid, hipStream_t s) {
     const int mode = attn_mask_mode(a);
+    if (a.dropout) return launch_prefill_f32_drop<D>(a, nq, npairs, grid, s);
 #define GT_F32_LAUNCH(C, MK) \
     hipLaunchKernelGGL((prefill_f32_kernel<D, C, MK>), dim3((unsigned)grid), dim3(64 * F32_NW), 0, s, a, nq, npairs)
     if (a.causal) {

@@ -334,8 +334,8 @@ void apply_dropout(AttnFwdArgs &a, const Dropout *drop) {
 // zero-padded to 64 or 128 dims: the zero dims add nothing to Q.K^T (the scale stays that of the
 // real head size), padded V columns give output columns that are dropped, and the padded columns
 // of dQ, dK, dV are zero and dropped.  Single-query rows keep their kernels (padding would copy
-// the whole K/V).  Float32 pads only calls its MFMA kernels take (16 query rows or more, no
-// dropout, no mask or a key-padding row: f32_pads), the rest keep the generic kernels unpadded.
+// the whole K/V).  Float32 pads only calls its MFMA kernels take (16 query rows or more, no mask
+// or a key-padding row: f32_pads), the rest keep the generic kernels unpadded.
 int64_t mfma_head(int64_t d) { return d <= 0 ? 0 : d <= 64 ? 64 : d <= 128 ? 128 : 0; }
 
 int64_t padded_head(int cd, int64_t L, int64_t D, int64_t Dv) {
@@ -349,7 +349,7 @@ int64_t padded_head(int cd, int64_t L, int64_t D, int64_t Dv) {
 // Float32 calls whose padded form the float32 MFMA kernels take (masks staged, dropout applied).
 bool f32_pads(const AttnFwdArgs &a) {
     const int mode = attn_mask_mode(a);
-    return !a.dropout && !a.kv_len && !a.q_pos && (mode == 0 || mode == 4);
+    return !a.kv_len && !a.q_pos && (mode == 0 || mode == 4);
 }
 
 // A dense (d0, d1, d2, Dp) copy of the 4-D device tensor t (innermost contiguous, 2- or 4-byte
@@ -719,8 +719,11 @@ int attention_backward(const char *who, const gt_tensor *grad_out, const gt_tens
             }
         }
         gt_scratch bits;  // dropout on the MFMA kernels: the dQ kernel's decisions for dK/dV, 1 bit each
-        if (ok && attn_bwd_mfma_supported(a, cd)) {
-            const size_t nbits = (size_t)(B * H * L) * (size_t)((S + 31) / 32) * sizeof(uint32_t);
+        const size_t nbits = (size_t)(B * H * L) * (size_t)((S + 31) / 32) * sizeof(uint32_t);
+        // the float32 dK/dV kernel takes dropout only with those bits (it does not draw its own),
+        // addressed by 32-bit byte offsets
+        const bool f32_drop_ok = cd != GT_F32 || !a.f.dropout || (nbits <= dropout_bits_max() && nbits <= 0xffffffffull);
+        if (ok && f32_drop_ok && attn_bwd_mfma_supported(a, cd)) {
             if (a.f.dropout && nbits <= dropout_bits_max()) {
                 ok = gt_scratch_alloc(bits, nbits, dev);
                 a.dbits = (uint32_t *)bits.ptr();
