@@ -643,7 +643,7 @@ hipError_t launch_bwd_d(const AttnBwdArgs &a, hipStream_t s) {
 }
 
 // ---- float32 ----------------------------------------------------------------------------------
-// Float32 backward (D = Dv = 64 or 128, no mask or a key-padding row, no dropout) on
+// Float32 backward (D = Dv = 64 or 128, no mask or a key-padding row, dropout (DROP)) on
 // v_mfma_f32_32x32x2_f32, with the division of work of the kernels above (dQ first, writing
 // delta = rowsum(dO.O); then dK/dV) and the float32 forward's operand mapping: a 32-row block's
 // row fragments take k-step t = dim t + (D/2)(lane/32), four k-steps per 16-byte LDS read, and the
