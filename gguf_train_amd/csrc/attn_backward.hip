@@ -675,6 +675,9 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void bwd_dq_f32_kernel(AttnBw
     constexpr int NW = 4, BM = 128, BN = 32, NST = 2;
     constexpr int CH = D / 4, TILE = BN * D, NPW = BN * CH / 64 / NW, DB = D / 32, DH = D / 2;
     constexpr bool MROW = MASK == 4;
+    constexpr bool MEL = MASK == 1 || MASK == 2 || MASK >= 5;  // per-element mask
+    constexpr bool MVEC = MASK >= 5;                           // 4 keys per mask load
+    constexpr bool MBOOL = MASK == 1 || MASK == 5;
     static_assert(NPW >= 1 && CH >= 16, "tile split");
     __shared__ __attribute__((aligned(1024))) float sK[NST][TILE];
     __shared__ __attribute__((aligned(1024))) float sV[NST][TILE];
@@ -721,6 +724,8 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void bwd_dq_f32_kernel(AttnBw
     // dropout: Philox block of keys 0..3 of this lane's row (rows past L draw unused words)
     const uint64_t drow = DROP ? (uint64_t)(bh * f.L + lq) * (uint64_t)((f.S + 3) / 4) : 0;
     const int64_t dwords = (f.S + 31) / 32;  // decision words per row
+    // per-element mask: element offset of this lane's mask row
+    const int64_t mrb = MEL ? b * f.m_sb + h * f.m_sh + (int64_t)lqc * f.m_sl : 0;
     f32x16 dq[DB];
 #pragma unroll
     for (int db = 0; db < DB; ++db)
@@ -780,6 +785,18 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void bwd_dq_f32_kernel(AttnBw
         const float *cV = sV[st];
         if (j + 1 < ntiles) issue(j + 1);  // stage (j+1) % 2 was last read before this barrier
         if (CAUSAL && k0 > wq0 + 31) continue;  // every key of the tile follows the wave's rows
+        // MVEC: the mask of keys k0 + 8g + 4half + 0..3 of this lane's row (groups past the last
+        // 4 keys read those: their scores are blocked below)
+        f32x4 mvf[MVEC && !MBOOL ? 4 : 1];
+        uint32_t mvb[MVEC && MBOOL ? 4 : 1];
+        if constexpr (MVEC) {
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const int64_t at = mrb + min(k0 + 8 * g + 4 * half, S - 4);
+                if constexpr (MBOOL) mvb[g] = *(const uint32_t *)((const uint8_t *)f.mask + at);
+                else mvf[g] = *(const f32x4 *)((const float *)f.mask + at);
+            }
+        }
         // S^T = K.Q^T (onto the key-padding terms), dP^T = V.dO^T (onto -delta):
         // entry i is key k0 + 8(i/4) + 4half + i%4, query lq
         f32x16 sc, dp;
@@ -826,7 +843,7 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void bwd_dq_f32_kernel(AttnBw
             if (a.dbits && half == 0 && lq < L && k0 < S) a.dbits[(bh * f.L + lq) * dwords + k0 / 32] = r[0] | r[1];
         }
         float ds[16];
-        const bool interior = k0 + BN - 1 < S && wq0 + 31 < L && (!CAUSAL || wq0 >= k0 + BN - 1);
+        const bool interior = !MEL && k0 + BN - 1 < S && wq0 + 31 < L && (!CAUSAL || wq0 >= k0 + BN - 1);
         if (interior) {
 #pragma unroll
             for (int i = 0; i < 16; ++i) ds[i] = fast_exp2(fmaf(sc[i], c, -lse2)) * dp[i];
@@ -835,8 +852,17 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void bwd_dq_f32_kernel(AttnBw
             const int vis = (lq < L ? (CAUSAL ? min(lq, S - 1) : S - 1) : -1) - (k0 + 4 * half);
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
-                const bool ok = 8 * (i / 4) + (i % 4) <= vis;
-                ds[i] = (ok ? fast_exp2(fmaf(sc[i], c, -lse2)) : 0.0f) * dp[i];
+                bool ok = 8 * (i / 4) + (i % 4) <= vis;
+                float x = sc[i];
+                if constexpr (MVEC) {
+                    if constexpr (MBOOL) ok = ok && ((mvb[i / 4] >> (8 * (i % 4))) & 0xffu) != 0u;
+                    else x = fmaf(mvf[i / 4][i % 4], inv_scale, x);
+                } else if constexpr (MEL) {
+                    const int64_t mi = mrb + (int64_t)min(k0 + 8 * (i / 4) + 4 * half + (i % 4), S - 1) * f.m_ss;
+                    if constexpr (MBOOL) ok = ok && ((const uint8_t *)f.mask)[mi] != 0;
+                    else x = fmaf(((const float *)f.mask)[mi], inv_scale, x);
+                }
+                ds[i] = (ok ? fast_exp2(fmaf(x, c, -lse2)) : 0.0f) * dp[i];
             }
         }
         // dQ^T += K^T . dS^T: k-step s2 is key 8(s2/4) + 4half + s2%4, A = K[that key][32db + lrow]
@@ -862,8 +888,9 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void bwd_dq_f32_kernel(AttnBw
 // dK, dV: a workgroup owns 128 keys of one kv head (32 per wavefront, K and V rows in registers)
 // and walks query steps of 64 rows over every query head of its group; Q, dO, lse and delta of a
 // step reach LDS by DMA.
+// (head size 64 with dropout and a per-element mask: one workgroup per CU, two would spill)
 template <int D, bool CAUSAL, int MASK, bool DROP>
-__global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void bwd_dkdv_f32_kernel(AttnBwdArgs a) {
+__global__ __launch_bounds__(256, D <= 64 && !(DROP && (MASK == 1 || MASK == 2)) ? 2 : 1) void bwd_dkdv_f32_kernel(AttnBwdArgs a) {
     constexpr int BKV = 128, BQ = 64, NST = 2, NW = 4;
     constexpr int CH = D / 4, TILE = BQ * D, NPW = BQ * CH / 64 / NW, DB = D / 32, DH = D / 2;
     static_assert(NPW >= 1 && CH >= 16, "tile split");
@@ -980,6 +1007,8 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void bwd_dkdv_f32_kernel(Attn
         }
         const float *cQ = sQ[sg];
         const float *cG = sG[sg];
+        // per-element mask (MASK 1, 2): element offset of this head's mask at this lane's key
+        const int64_t mel0 = MASK == 1 || MASK == 2 ? b * f.m_sb + h * f.m_sh + (int64_t)min(key, S - 1) * f.m_ss : 0;
 #pragma unroll
         for (int qb = 0; qb < 2; ++qb) {
             const int q0 = qs0 + 32 * qb;
@@ -1022,7 +1051,7 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void bwd_dkdv_f32_kernel(Attn
                 }
             }
             float p[16], ds[16];
-            const bool interior = wk0 + 31 < S && q0 + 31 < L && (!CAUSAL || q0 >= wk0 + 31);
+            const bool interior = MASK != 1 && MASK != 2 && wk0 + 31 < S && q0 + 31 < L && (!CAUSAL || q0 >= wk0 + 31);
             // query q0 + 4half + c (c = 8(i/4) + i%4) sees this lane's key when lo <= c <= lo + span
             int lo = (CAUSAL ? key : 0) - (q0 + 4 * half);
             int span = (L - 1 - (q0 + 4 * half)) - lo;
@@ -1036,8 +1065,15 @@ __global__ __launch_bounds__(256, D <= 64 ? 2 : 1) void bwd_dkdv_f32_kernel(Attn
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     const int i = 4 * g + e;
-                    const bool ok = interior || (uint32_t)(8 * g + e - lo) <= (uint32_t)span;
-                    const float pv = ok ? fast_exp2(fmaf(sc[i], c, -l4[e] * kLog2e)) : 0.0f;
+                    bool ok = interior || (uint32_t)(8 * g + e - lo) <= (uint32_t)span;
+                    float x = sc[i];
+                    if constexpr (MASK == 1 || MASK == 2) {
+                        // per-element mask of query q0 + 8g + 4half + e, this lane's key
+                        const int64_t mi = mel0 + (int64_t)min(q0 + 8 * g + 4 * half + e, L - 1) * f.m_sl;
+                        if constexpr (MASK == 1) ok = ok && ((const uint8_t *)f.mask)[mi] != 0;
+                        else x = fmaf(((const float *)f.mask)[mi], inv_scale, x);
+                    }
+                    const float pv = ok ? fast_exp2(fmaf(x, c, -l4[e] * kLog2e)) : 0.0f;
                     p[i] = DROP ? ((keep >> i) & 1u ? pv * (float)f.drop.scale : 0.0f) : pv;
                     ds[i] = pv * dp[i];
                 }
@@ -1079,15 +1115,28 @@ hipError_t launch_bwd_f32_cm(const AttnBwdArgs &a, hipStream_t s) {
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const int nkt = (int)((f.S + 127) / 128);
-    hipLaunchKernelGGL((bwd_dkdv_f32_kernel<D, CAUSAL, MASK, DROP>), dim3((unsigned)(nkt * f.B * f.Hkv)), dim3(256), 0, s, a);
+    // dK/dV reads a per-element mask one element at a time whatever its layout: modes 5, 6 as 1, 2
+    constexpr int MKV = MASK == 5 ? 1 : MASK == 6 ? 2 : MASK;
+    hipLaunchKernelGGL((bwd_dkdv_f32_kernel<D, CAUSAL, MKV, DROP>), dim3((unsigned)(nkt * f.B * f.Hkv)), dim3(256), 0, s, a);
     return hipGetLastError();
+}
+
+template <int D, bool CAUSAL, bool DROP>
+hipError_t launch_bwd_f32_cd(const AttnBwdArgs &a, hipStream_t s) {
+    switch (attn_mask_mode(a.f)) {
+        case 0: return launch_bwd_f32_cm<D, CAUSAL, 0, DROP>(a, s);
+        case 1: return launch_bwd_f32_cm<D, CAUSAL, 1, DROP>(a, s);
+        case 2: return launch_bwd_f32_cm<D, CAUSAL, 2, DROP>(a, s);
+        case 4: return launch_bwd_f32_cm<D, CAUSAL, 4, DROP>(a, s);
+        case 5: return launch_bwd_f32_cm<D, CAUSAL, 5, DROP>(a, s);
+        case 6: return launch_bwd_f32_cm<D, CAUSAL, 6, DROP>(a, s);
+        default: return hipErrorInvalidValue;
+    }
 }
 
 template <int D, bool DROP>
 hipError_t launch_bwd_f32_dd(const AttnBwdArgs &a, hipStream_t s) {
-    const bool kp = attn_mask_mode(a.f) == 4;
-    if (a.f.causal) return kp ? launch_bwd_f32_cm<D, true, 4, DROP>(a, s) : launch_bwd_f32_cm<D, true, 0, DROP>(a, s);
-    return kp ? launch_bwd_f32_cm<D, false, 4, DROP>(a, s) : launch_bwd_f32_cm<D, false, 0, DROP>(a, s);
+    return a.f.causal ? launch_bwd_f32_cd<D, true, DROP>(a, s) : launch_bwd_f32_cd<D, false, DROP>(a, s);
 }
 
 template <int D>
@@ -1104,7 +1153,6 @@ bool bwd_f32_supported(const AttnBwdArgs &a) {
     const AttnFwdArgs &f = a.f;
     if (f.D != f.Dv || (f.D != 64 && f.D != 128) || f.kv_len || f.q_pos) return false;
     const int mode = attn_mask_mode(f);
-    if (mode != 0 && mode != 4) return false;
     // as the forward: fewer than 16 query rows stay on the generic kernels
     if (f.L < 16 || f.S < 1 || !(f.scale > 0.0f) || !f.o || !f.lse) return false;  // f.o: float32 output
     // fewer than 32 dQ workgroups leave the MFMA kernels latency-bound: the generic kernels, which

@@ -626,6 +626,9 @@ __global__ __launch_bounds__(64 * F32_NW, 2) void prefill_f32_kernel(AttnFwdArgs
     constexpr int DB = D / 32;              // d blocks of O^T
     constexpr int DH = D / 2;               // dims per lane half in S^T
     constexpr bool MROW = MASK == 4;
+    constexpr bool MEL = MASK == 1 || MASK == 2 || MASK >= 5;  // per-element mask
+    constexpr bool MVEC = MASK >= 5;                           // 4 keys per mask load
+    constexpr bool MBOOL = MASK == 1 || MASK == 5;
     constexpr int PER = 2 * NPW + (MROW ? 1 : 0);  // loads per wave and tile
     static_assert(NPW >= 1 && CH >= 16 && PER < 64, "tile split");
     __shared__ __attribute__((aligned(1024))) float sK[NST][TILE];
@@ -741,6 +744,8 @@ __global__ __launch_bounds__(64 * F32_NW, 2) void prefill_f32_kernel(AttnFwdArgs
         float m = -INFINITY, mthr = -INFINITY, lsum = 0.0f;
         // dropout: Philox block of keys 0..3 of this lane's row (rows past L draw unused words)
         const uint64_t drow = DROP ? (uint64_t)(bh * a.L + lq) * (uint64_t)((a.S + 3) / 4) : 0;
+        // per-element mask: element offset of this lane's mask row
+        const int64_t mrb = MEL ? b * a.m_sb + h * a.m_sh + (int64_t)min(lq, L - 1) * a.m_sl : 0;
 
         for (int j = 0; j < ntiles; ++j, ++step) {
             const int k0 = j * BN;
@@ -750,6 +755,18 @@ __global__ __launch_bounds__(64 * F32_NW, 2) void prefill_f32_kernel(AttnFwdArgs
             __syncthreads();
             const float *cK = sK[step % NST];
             const float *cV = sV[step % NST];
+            // MVEC: the mask of keys k0 + 8g + 4half + 0..3 of this lane's row, loaded before the
+            // MFMAs (groups past the last 4 keys read those: their scores are blocked below)
+            f32x4 mvf[MVEC && !MBOOL ? 4 : 1];
+            uint32_t mvb[MVEC && MBOOL ? 4 : 1];
+            if constexpr (MVEC) {
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const int64_t at = mrb + min(k0 + 8 * g + 4 * half, S - 4);
+                    if constexpr (MBOOL) mvb[g] = *(const uint32_t *)((const uint8_t *)a.mask + at);
+                    else mvf[g] = *(const f32x4 *)((const float *)a.mask + at);
+                }
+            }
             // ---- S^T = K . Q^T: s[i] is key k0 + 8(i/4) + 4half + i%4, query lq ----
             f32x16 s;
             if constexpr (MROW) {
@@ -773,12 +790,22 @@ __global__ __launch_bounds__(64 * F32_NW, 2) void prefill_f32_kernel(AttnFwdArgs
             if (step + NST - 1 < total) issue(step + NST - 1);
 
             const bool edge = k0 + BN > nkv || (CAUSAL && k0 + BN - 1 > wq0 + qpos);
-            if (edge) {
+            if (MEL || edge) {
                 const int vis = min(nkv - 1, CAUSAL ? lq + qpos : nkv - 1) - (k0 + 4 * half);
 #pragma unroll
                 for (int i = 0; i < 16; ++i) {
+                    float x = s[i];
+                    if constexpr (MVEC) {
+                        if constexpr (MBOOL) x = (mvb[i / 4] >> (8 * (i % 4))) & 0xffu ? x : -INFINITY;
+                        else x = fmaf(mvf[i / 4][i % 4], inv_scale, x);
+                    } else if constexpr (MEL) {
+                        const int key = min(k0 + 8 * (i / 4) + 4 * half + (i % 4), S - 1);
+                        const int64_t mi = mrb + (int64_t)key * a.m_ss;
+                        if constexpr (MBOOL) x = ((const uint8_t *)a.mask)[mi] ? x : -INFINITY;
+                        else x = fmaf(((const float *)a.mask)[mi], inv_scale, x);
+                    }
                     const bool blocked = 8 * (i / 4) + (i % 4) > vis;
-                    s[i] = blocked ? -INFINITY : s[i];
+                    s[i] = blocked ? -INFINITY : x;
                 }
             }
             float tmax = max3(s[0], s[1], s[2]);
@@ -846,7 +873,6 @@ bool prefill_f32_supported(const AttnFwdArgs &f) {
     if (f.out_dtype != GT_F32 || f.D != f.Dv || (f.D != 64 && f.D != 128)) return false;
     if (f.rope_q) return false;
     const int mode = attn_mask_mode(f);
-    if (mode != 0 && mode != 4) return false;
     // fewer than 16 query rows: one mostly empty 128-row tile per head walking every key; the
     // generic kernel measured as fast or faster there (one row: 1.14 against 2.02 ms at B32
     // H32/8 S4096 D128; 16 rows: even)
@@ -862,17 +888,18 @@ bool prefill_f32_supported(const AttnFwdArgs &f) {
     return true;
 }
 
-template <int D>
-hipError_t launch_prefill_f32_drop(const AttnFwdArgs &a, int nq, int npairs, int64_t grid, hipStream_t s) {
-    const int mode = attn_mask_mode(a);
-#define GT_F32_LAUNCH(C, MK) \
-    hipLaunchKernelGGL((prefill_f32_kernel<D, C, MK, true>), dim3((unsigned)grid), dim3(64 * F32_NW), 0, s, a, nq, npairs)
-    if (a.causal) {
-        if (mode == 0) GT_F32_LAUNCH(true, 0);
-        else GT_F32_LAUNCH(true, 4);
-    } else {
-        if (mode == 0) GT_F32_LAUNCH(false, 0);
-        else GT_F32_LAUNCH(false, 4);
+template <int D, bool CAUSAL, bool DROP>
+hipError_t launch_prefill_f32_cd(const AttnFwdArgs &a, int nq, int npairs, int64_t grid, hipStream_t s) {
+#define GT_F32_LAUNCH(MK) \
+    hipLaunchKernelGGL((prefill_f32_kernel<D, CAUSAL, MK, DROP>), dim3((unsigned)grid), dim3(64 * F32_NW), 0, s, a, nq, npairs)
+    switch (attn_mask_mode(a)) {
+        case 0: GT_F32_LAUNCH(0); break;
+        case 1: GT_F32_LAUNCH(1); break;
+        case 2: GT_F32_LAUNCH(2); break;
+        case 4: GT_F32_LAUNCH(4); break;
+        case 5: GT_F32_LAUNCH(5); break;
+        case 6: GT_F32_LAUNCH(6); break;
+        default: return hipErrorInvalidValue;
     }
 #undef GT_F32_LAUNCH
     return hipGetLastError();
@@ -880,19 +907,11 @@ hipError_t launch_prefill_f32_drop(const AttnFwdArgs &a, int nq, int npairs, int
 
 template <int D>
 hipError_t launch_prefill_f32_d(const AttnFwdArgs &a, int nq, int npairs, int64_t grid, hipStream_t s) {
-    const int mode = attn_mask_mode(a);
-    if (a.dropout) return launch_prefill_f32_drop<D>(a, nq, npairs, grid, s);
-#define GT_F32_LAUNCH(C, MK) \
-    hipLaunchKernelGGL((prefill_f32_kernel<D, C, MK>), dim3((unsigned)grid), dim3(64 * F32_NW), 0, s, a, nq, npairs)
-    if (a.causal) {
-        if (mode == 0) GT_F32_LAUNCH(true, 0);
-        else GT_F32_LAUNCH(true, 4);
-    } else {
-        if (mode == 0) GT_F32_LAUNCH(false, 0);
-        else GT_F32_LAUNCH(false, 4);
-    }
-#undef GT_F32_LAUNCH
-    return hipGetLastError();
+    if (a.dropout)
+        return a.causal ? launch_prefill_f32_cd<D, true, true>(a, nq, npairs, grid, s)
+                        : launch_prefill_f32_cd<D, false, true>(a, nq, npairs, grid, s);
+    return a.causal ? launch_prefill_f32_cd<D, true, false>(a, nq, npairs, grid, s)
+                    : launch_prefill_f32_cd<D, false, false>(a, nq, npairs, grid, s);
 }
 
 hipError_t launch_prefill_f32(const AttnFwdArgs &a, hipStream_t s) {

@@ -334,8 +334,9 @@ void apply_dropout(AttnFwdArgs &a, const Dropout *drop) {
 // zero-padded to 64 or 128 dims: the zero dims add nothing to Q.K^T (the scale stays that of the
 // real head size), padded V columns give output columns that are dropped, and the padded columns
 // of dQ, dK, dV are zero and dropped.  Single-query rows keep their kernels (padding would copy
-// the whole K/V).  Float32 pads only calls its MFMA kernels take (16 query rows or more, no mask
-// or a key-padding row: f32_pads), the rest keep the generic kernels unpadded.
+// the whole K/V).  Float32 pads only calls its MFMA kernels take (16 query rows or more, no KV
+// cache lengths: f32_pads; the backward also 32 dQ workgroups), the rest keep the generic kernels
+// unpadded.
 int64_t mfma_head(int64_t d) { return d <= 0 ? 0 : d <= 64 ? 64 : d <= 128 ? 128 : 0; }
 
 int64_t padded_head(int cd, int64_t L, int64_t D, int64_t Dv) {
@@ -347,10 +348,7 @@ int64_t padded_head(int cd, int64_t L, int64_t D, int64_t Dv) {
 }
 
 // Float32 calls whose padded form the float32 MFMA kernels take (masks staged, dropout applied).
-bool f32_pads(const AttnFwdArgs &a) {
-    const int mode = attn_mask_mode(a);
-    return !a.kv_len && !a.q_pos && (mode == 0 || mode == 4);
-}
+bool f32_pads(const AttnFwdArgs &a) { return !a.kv_len && !a.q_pos; }
 
 // A dense (d0, d1, d2, Dp) copy of the 4-D device tensor t (innermost contiguous, 2- or 4-byte
 // elements) whose dims past t's last are zero; kept in tmp.

@@ -1,11 +1,11 @@
 """Float32 backward on v_mfma_f32_32x32x2_f32 (bwd_dq_f32_kernel, then bwd_dkdv_f32_kernel: head
-sizes 64 and 128, no mask or a key-padding row, 16 query rows or more; dropout in
-test_gpu_dropout_f32.py) against the
+sizes 64 and 128, any mask, 16 query rows or more; dropout in test_gpu_dropout_f32.py)
+against the
 float64 oracle's gradients at the float32 bar (max-abs 1e-4): ragged query and key counts around
 the dQ kernel's 128-row query tiles and 32-key K/V tiles and the dK/dV kernel's 128-key tiles and
 64-row query steps, one key, GQA and MQA, causal or not, keys no query sees (causal, S > L),
-fully padded rows, and the launch log naming the kernel.  Fewer query rows and other masks keep
-the generic kernel."""
+fully padded rows, per-element bool / additive masks, and the launch log naming the kernel.
+Fewer query rows and small grids keep the generic kernels."""
 
 import numpy as np
 import pytest
@@ -109,7 +109,7 @@ def test_float32_backward_without_residuals_and_with_an_empty_row(dev):
         assert torch.count_nonzero(got[B - 1]).item() == 0, name
 
 
-def test_fewer_rows_small_grids_and_other_masks_keep_the_generic_backward(dev):
+def test_fewer_rows_and_small_grids_keep_the_generic_backward(dev):
     B, H, S, D = 1, 32, 90, 64
     q, k, v, dout = randn((B, H, 15, D), 70), randn((B, H, S, D), 71), randn((B, H, S, D), 72), randn((B, H, 15, D), 73)
     dq, dk, dv, launch = _grads(dev, q, k, v, dout, None, False)
@@ -123,12 +123,25 @@ def test_fewer_rows_small_grids_and_other_masks_keep_the_generic_backward(dev):
         assert launch == want_launch, (H2, launch)
         for got, want, name in zip((dq, dk, dv), _oracle_grads(g2, q2, k2, v2, None, True), ("dq", "dk", "dv")):
             assert_close(got, want, torch.float32, f"{name} H={H2}")
-    # 32 workgroups, but a boolean mask
-    L = 40
-    q, dout = randn((B, H, L, D), 74), randn((B, H, L, D), 75)
-    m = torch.from_numpy(np.random.default_rng(6).random((L, S)) < 0.7)
-    m[:, 0] = True
-    dq, dk, dv, launch = _grads(dev, q, k, v, dout, m, False)
-    assert launch == "backward generic f32", launch
-    for got, want, name in zip((dq, dk, dv), _oracle_grads(dout, q, k, v, m, False), ("dq", "dk", "dv")):
-        assert_close(got, want, torch.float32, name + " bool mask")
+
+
+# per-element masks: S % 4 == 0 reads 4 keys per load in dQ (modes 5, 6), other S one key; dK/dV
+# reads one element per (query, key)
+@pytest.mark.parametrize("kind", ["bool", "add"])
+@pytest.mark.parametrize("B,H,Hkv,L,S,D,causal", [(1, 32, 16, 70, 92, 64, False), (2, 16, 8, 130, 131, 128, True),
+                                                  (1, 32, 32, 40, 256, 128, False), (2, 16, 4, 100, 33, 64, True)])
+def test_float32_backward_with_per_element_masks(dev, kind, B, H, Hkv, L, S, D, causal):
+    seed = L + S + D + 1
+    q, k, v = randn((B, H, L, D), seed), randn((B, Hkv, S, D), seed + 1), randn((B, Hkv, S, D), seed + 2)
+    dout = randn((B, H, L, D), seed + 3)
+    rng = np.random.default_rng(seed)
+    if kind == "bool":
+        m = torch.from_numpy(rng.random((L, S)) < 0.7)
+        m[:, 0] = True
+    else:
+        m = torch.from_numpy((rng.standard_normal((B, H, L, S)) * 2).astype(np.float32))
+    dq, dk, dv, launch = _grads(dev, q, k, v, dout, m, causal)
+    what = f"{kind} B{B} H{H}/{Hkv} L{L} S{S} D{D} causal={causal}"
+    assert launch == f"backward mfma f32 D={D}", (what, launch)
+    for got, want, name in zip((dq, dk, dv), _oracle_grads(dout, q, k, v, m, causal), ("dq", "dk", "dv")):
+        assert_close(got, want, torch.float32, f"{name} {what}")

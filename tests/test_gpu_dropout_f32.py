@@ -1,6 +1,6 @@
 """Dropout on the float32 MFMA kernels (prefill_f32_kernel, bwd_dq_f32_kernel and
-bwd_dkdv_f32_kernel with DROP: head sizes 64 and 128, padded heads, no mask or a key-padding
-row) against the oracle's composition under the oracle's Philox4x32-10 decisions, at the float32
+bwd_dkdv_f32_kernel with DROP: head sizes 64 and 128, padded heads, key padding or per-element
+masks) against the oracle's composition under the oracle's Philox4x32-10 decisions, at the float32
 bar: forward output and the undropped log-sum-exp, dQ, dK, dV; several key tiles, causal or not,
 GQA, p from 0.05 to 1, the launch log naming the kernels, and the generic backward when the
 decision buffer would exceed GT_ATTN_DROPOUT_BITS_MAX (the float32 dK/dV kernel reads the dQ
@@ -19,7 +19,8 @@ from _util import assert_close, randn, to_oracle
 pytestmark = pytest.mark.gpu
 
 CASES = [
-    # B, H, Hkv, L, S, D, causal, key lengths (key padding), p; B * H * ceil(L / 128) >= 32
+    # B, H, Hkv, L, S, D, causal, key lengths (key padding) or a per-element mask, p;
+    # B * H * ceil(L / 128) >= 32
     (2, 16, 8, 300, 300, 64, True, (300, 211), 0.1),
     (1, 32, 32, 257, 257, 128, False, (), 0.5),
     (2, 16, 4, 130, 260, 64, False, (260, 100), 0.2),
@@ -28,6 +29,9 @@ CASES = [
     (1, 32, 32, 64, 64, 64, True, (), 1.0),
     (2, 16, 16, 16, 50, 64, False, (), 0.4),
     (2, 16, 8, 100, 120, 80, True, (), 0.3),  # heads padded to 128
+    # per-element masks with dropout (bool: one workgroup per CU for head size 64's dK/dV)
+    (2, 16, 8, 130, 200, 64, True, "bool", 0.2),
+    (1, 32, 16, 96, 131, 128, False, "add", 0.3),
 ]
 
 
@@ -63,7 +67,13 @@ def test_float32_dropout_matches_the_oracle(dev, B, H, Hkv, L, S, D, causal, len
     q, k, v = randn((B, H, L, D), s0), randn((B, Hkv, S, D), s0 + 1), randn((B, Hkv, S, D), s0 + 2)
     dout = randn((B, H, L, D), s0 + 3)
     mask = None
-    if lens:
+    rng = np.random.default_rng(s0)
+    if lens == "bool":
+        mask = torch.from_numpy(rng.random((L, S)) < 0.7)
+        mask[:, 0] = True
+    elif lens == "add":
+        mask = torch.from_numpy((rng.standard_normal((B, H, L, S)) * 2).astype(np.float32))
+    elif lens:
         mask = torch.zeros(B, 1, 1, S)
         for b, n in enumerate(lens):
             mask[b, ..., int(n):] = float("-inf")

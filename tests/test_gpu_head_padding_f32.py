@@ -3,8 +3,8 @@ kernels with the heads zero-padded: forward (output, log-sum-exp) and backward a
 float64 oracle at the float32 bar, GQA, causal or not, key padding, D != Dv, the 8-element and
 one-element pad copies, the launch log naming the padded kernels, a check that padding is what
 ran (the result equals the unpadded kernels' on explicitly zero-padded inputs, bit for bit), and
-the calls the float32 kernels do not take (fewer than 16 query rows, per-element masks, a small
-backward grid), which stay unpadded on the generic kernels."""
+the calls the float32 kernels do not take (fewer than 16 query rows, a small backward grid),
+which stay unpadded on the generic kernels; per-element masks are padded."""
 
 import numpy as np
 import pytest
@@ -89,13 +89,13 @@ def test_float32_calls_the_mfma_kernels_do_not_take_stay_unpadded(dev):
     out = g.flash_attention(q.to(dev), k, v, None, 0.0, False)
     assert _C.last_launch() == "generic f32", _C.last_launch()
     assert_close(out, oracle_forward(q, k.cpu(), v.cpu()), torch.float32, "L=15")
-    # a per-element bool mask: the generic forward
+    # a per-element bool mask: the padded MFMA forward
     L = 40
     q, dout = randn((B, H, L, D), 43), randn((B, H, L, D), 44)
     m = torch.from_numpy(np.random.default_rng(8).random((L, S)) < 0.7)
     m[:, 0] = True
     out = g.flash_attention(q.to(dev), k, v, m.to(dev), 0.0, False)
-    assert _C.last_launch() == "generic f32", _C.last_launch()
+    assert _C.last_launch().startswith("prefill f32 D=128 "), _C.last_launch()
     assert_close(out, oracle_forward(q, k.cpu(), v.cpu(), mask=m), torch.float32, "bool mask")
     # 4 dQ workgroups: the padded MFMA forward, the generic backward on the unpadded heads
     out, lse = g.flash_attention_lse(q.to(dev), k, v, None, 0.0, True)

@@ -1,9 +1,9 @@
 """Float32 attention on v_mfma_f32_32x32x2_f32 (prefill_f32_kernel: head sizes 64 and 128, no
-mask or a key-padding row, 16 query rows or more) against the float64 oracle at the float32 bar
+mask, a key-padding row or a per-element mask, 16 query rows or more) against the float64 oracle at the float32 bar
 (max-abs 1e-4): ragged query and key counts around the 128-row query tiles and 32-key K/V
-tiles, one key, GQA, causal or not, the log-sum-exp and the training forward's float32 output,
-and the launch log naming the kernel.  One query row takes the decode kernel; 2 to 15 rows and
-other masks keep the generic kernel."""
+tiles, one key, GQA, causal or not, key padding and per-element bool / additive masks (4-key and
+one-key loads), the log-sum-exp and the training forward's float32 output, and the launch log
+naming the kernel.  One query row takes the decode kernel; 2 to 15 rows the generic kernel."""
 
 import numpy as np
 import pytest
@@ -76,11 +76,28 @@ def test_float32_training_forward_writes_the_float32_output(dev):
     assert_close(out, oracle_forward(q, k, v, mask=mask, is_causal=True), torch.float32, "train forward f32")
 
 
-def test_other_masks_keep_the_generic_kernel(dev):
-    B, H, L, S, D = 1, 2, 70, 90, 64
-    q, k, v = randn((B, H, L, D), 50), randn((B, H, S, D), 51), randn((B, H, S, D), 52)
-    m = torch.from_numpy(np.random.default_rng(5).random((L, S)) < 0.7)
-    m[:, 0] = True
-    out = g.flash_attention(q.to(dev), k.to(dev), v.to(dev), m.to(dev), 0.0, False)
-    assert _C.last_launch() == "generic f32"
-    assert_close(out, oracle_forward(q, k, v, mask=m), torch.float32, "bool mask f32")
+def _elem_mask(kind, B, H, L, S, seed):
+    rng = np.random.default_rng(seed)
+    if kind == "bool":
+        m = torch.from_numpy(rng.random((L, S)) < 0.7)
+        m[:, 0] = True
+        return m
+    return torch.from_numpy((rng.standard_normal((B, H, L, S)) * 2).astype(np.float32))
+
+
+# per-element masks: S % 4 == 0 reads 4 keys per load (modes 5, 6), other S one key (modes 1, 2)
+@pytest.mark.parametrize("kind", ["bool", "add"])
+@pytest.mark.parametrize("B,H,Hkv,L,S,D,causal", [(1, 2, 2, 70, 92, 64, False), (2, 2, 1, 130, 131, 128, True),
+                                                  (1, 4, 2, 200, 256, 128, False), (2, 2, 2, 40, 33, 64, True)])
+def test_float32_prefill_with_per_element_masks(dev, kind, B, H, Hkv, L, S, D, causal):
+    seed = L + S + D
+    q, k, v = randn((B, H, L, D), seed), randn((B, Hkv, S, D), seed + 1), randn((B, Hkv, S, D), seed + 2)
+    m = _elem_mask(kind, B, H, L, S, seed)
+    out, lse = g.flash_attention_lse(q.to(dev), k.to(dev), v.to(dev), m.to(dev), 0.0, causal)
+    what = f"{kind} B{B} H{H}/{Hkv} L{L} S{S} D{D} causal={causal}"
+    assert _C.last_launch().startswith(f"prefill f32 D={D}"), (what, _C.last_launch())
+    want, want_lse = oracle_forward(q, k, v, mask=m, is_causal=causal, return_lse=True)
+    assert_close(out, want, torch.float32, what)
+    fin = np.isfinite(want_lse)
+    assert np.array_equal(np.isinf(lse.cpu().numpy()), ~fin), what
+    assert np.abs(lse.cpu().double().numpy()[fin] - want_lse[fin]).max() < 1e-4, what
