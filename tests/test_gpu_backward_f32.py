@@ -1,7 +1,6 @@
 """Float32 backward on v_mfma_f32_32x32x2_f32 (bwd_dq_f32_kernel, then bwd_dkdv_f32_kernel: head
-sizes 64 and 128, any mask, 16 query rows or more; dropout in test_gpu_dropout_f32.py)
-against the
-float64 oracle's gradients at the float32 bar (max-abs 1e-4): ragged query and key counts around
+sizes 64 and 128, any mask, 16 query rows or more; dropout in test_gpu_dropout_f32.py) against
+the float64 oracle's gradients at the float32 bar (max-abs 1e-4): ragged query and key counts around
 the dQ kernel's 128-row query tiles and 32-key K/V tiles and the dK/dV kernel's 128-key tiles and
 64-row query steps, one key, GQA and MQA, causal or not, keys no query sees (causal, S > L),
 fully padded rows, per-element bool / additive masks, and the launch log naming the kernel.
