@@ -163,6 +163,7 @@ bool attn_prefill_supported(const AttnFwdArgs &f, int cd);
 // attn_prefill_asm_supported holds, the HIP prefill kernel otherwise)
 hipError_t launch_attn_prefill(const AttnFwdArgs &a, int cd, hipStream_t s);
 bool attn_prefill_asm_supported(const AttnFwdArgs &f, int cd);
+bool attn_prefill_f32_split(const AttnFwdArgs &f, int cd);  // float32: the small-grid kernel
 hipError_t launch_attn_prefill_asm(const AttnFwdArgs &a, hipStream_t s);
 
 bool attn_decode_q8_supported(const AttnFwdArgs &f, int q_dtype);

@@ -869,6 +869,151 @@ __global__ __launch_bounds__(64 * F32_NW, 2) void prefill_f32_kernel(AttnFwdArgs
     }
 }
 
+// Float32 prefill for small grids (few heads of short sequences, where prefill_f32_kernel has
+// fewer workgroups than the GPU has CUs and each wavefront's walk over the key tiles is the whole
+// time): one workgroup per 32 query rows, its 4 wavefronts splitting the key tiles (tile t to
+// wavefront t % 4) with an online softmax each, then merging the four (max, sum, O) states
+// through LDS.  The operand mapping is prefill_f32_kernel's (S^T = K.Q^T with k-step t = dim
+// t + (D/2)(lane/32) and Q in registers; O^T += V^T.P^T with k-step s = the key of accumulator
+// entry s), but each wavefront reads its K rows (16-byte pieces) and V^T values straight from
+// memory: they are few and stay in L2.  No mask, dropout or KV-cache lengths (prefill_f32_split).
+template <int D, bool CAUSAL>
+__global__ __launch_bounds__(256) void prefill_f32_split_kernel(AttnFwdArgs a, int ng) {
+    constexpr int DH = D / 2, DB = D / 32, OP = D + 4;  // OP: LDS row pitch of the partial O
+    __shared__ __attribute__((aligned(16))) float sO[4][32][OP];
+    __shared__ float sM[4][32], sL[4][32];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int lrow = lane & 31, half = lane >> 5;
+    const int64_t bh = blockIdx.x / ng;
+    const int rg = (int)(blockIdx.x % ng);
+    const int64_t b = bh / a.H, h = bh % a.H, hk = h / (a.H / a.Hkv);
+    const int L = (int)a.L, S = (int)a.S;
+    const int q0 = 32 * rg, lq = q0 + lrow, lqc = min(lq, L - 1);
+    const int kv_end = CAUSAL ? min(q0 + 32, S) : S;  // keys any row of the group sees
+    const int nt = (kv_end + 31) / 32;
+    const float c = a.scale * kLog2e;
+
+    float qf[DH];  // Q of row lqc, dims DH half .. +DH (B operand of S^T)
+    {
+        const float *qr = (const float *)a.q + b * a.q_sb + h * a.q_sh + (int64_t)lqc * a.q_sl + DH * half;
+#pragma unroll
+        for (int u = 0; u < DH / 4; ++u) {
+            const f32x4 x = *(const f32x4 *)(qr + 4 * u);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) qf[4 * u + e] = x[e];
+        }
+    }
+    const float *kbase = (const float *)a.k + b * a.k_sb + hk * a.k_sh;
+    const float *vbase = (const float *)a.v + b * a.v_sb + hk * a.v_sh;
+    f32x16 o[DB];
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) o[db][i] = 0.0f;
+    float m = -INFINITY, lsum = 0.0f;  // running max (log2 domain) and this half's share of the sum
+
+    for (int t = w; t < nt; t += 4) {
+        const int k0 = 32 * t;
+        // S^T: s[i] is key k0 + 8(i/4) + 4half + i%4, query lq
+        const float *kr = kbase + (int64_t)min(k0 + lrow, S - 1) * a.k_ss + DH * half;
+        f32x16 s;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) s[i] = 0.0f;
+#pragma unroll
+        for (int u = 0; u < DH / 4; ++u) {
+            const f32x4 kv = *(const f32x4 *)(kr + 4 * u);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) s = mfma_f32x2(kv[e], qf[4 * u + e], s);
+        }
+        const int vis = (CAUSAL ? min(lq, S - 1) : S - 1) - (k0 + 4 * half);
+        float tmax = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            s[i] = 8 * (i / 4) + (i % 4) > vis ? -INFINITY : s[i] * c;
+            tmax = fmaxf(tmax, s[i]);
+        }
+        const float mnew = fmaxf(m, xhalf_max(tmax));
+        const float msub = mnew == -INFINITY ? 0.0f : mnew;
+        if (mnew != m) {
+            const float alpha = fast_exp2(m - msub);  // m = -inf: 0 (O and the sum are 0)
+            lsum *= alpha;
+#pragma unroll
+            for (int db = 0; db < DB; ++db)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) o[db][i] *= alpha;
+            m = mnew;
+        }
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            s[i] = fast_exp2(s[i] - msub);  // -inf -> 0
+            lsum += s[i];
+        }
+        // O^T += V^T . P^T: k-step s2 is key k0 + 8(s2/4) + 4half + s2%4, A = V[that key][32 db + lrow]
+#pragma unroll
+        for (int s2 = 0; s2 < 16; ++s2) {
+            const float *vr = vbase + (int64_t)min(k0 + 8 * (s2 >> 2) + 4 * half + (s2 & 3), S - 1) * a.v_ss + lrow;
+#pragma unroll
+            for (int db = 0; db < DB; ++db) o[db] = mfma_f32x2(vr[32 * db], s[s2], o[db]);
+        }
+    }
+
+    // ---- merge the four wavefronts' states ----
+    const float ltot = xhalf_sum(lsum);
+    if (half == 0) {
+        sM[w][lrow] = m;
+        sL[w][lrow] = ltot;
+    }
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const f32x4 v = {o[db][4 * g], o[db][4 * g + 1], o[db][4 * g + 2], o[db][4 * g + 3]};
+            *(f32x4 *)&sO[w][lrow][32 * db + 8 * g + 4 * half] = v;
+        }
+    __syncthreads();
+    // thread: row r of the group, dims (D/8) part .. +D/8
+    const int r = threadIdx.x >> 3, part = threadIdx.x & 7;
+    float M = -INFINITY;
+#pragma unroll
+    for (int ww = 0; ww < 4; ++ww) M = fmaxf(M, sM[ww][r]);
+    float wg[4], Lt = 0.0f;
+#pragma unroll
+    for (int ww = 0; ww < 4; ++ww) {
+        wg[ww] = sM[ww][r] == -INFINITY ? 0.0f : fast_exp2(sM[ww][r] - M);
+        Lt = fmaf(wg[ww], sL[ww][r], Lt);
+    }
+    const float inv = Lt > 0.0f ? 1.0f / Lt : 0.0f;
+    if (q0 + r < L) {
+        float *orow = (float *)a.o + (bh * a.L + q0 + r) * D + (D / 8) * part;
+#pragma unroll
+        for (int j = 0; j < D / 32; ++j) {
+            f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int ww = 0; ww < 4; ++ww) {
+                const f32x4 x = *(const f32x4 *)&sO[ww][r][(D / 8) * part + 4 * j];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) acc[e] = fmaf(wg[ww], x[e], acc[e]);
+            }
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[e] *= inv;
+            *(f32x4 *)(orow + 4 * j) = acc;
+        }
+        if (a.lse && part == 0) ((float *)a.lse)[bh * a.L + q0 + r] = Lt > 0.0f ? (M + log2f(Lt)) * kLn2 : INFINITY;
+    }
+}
+
+// The calls prefill_f32_split_kernel takes: no mask, dropout or KV-cache lengths, at most 64
+// workgroups of prefill_f32_kernel (B * H * query-tile pairs) and at most 4096 keys.  Measured
+// against the tiled kernel: faster at every grid of up to 64 of its workgroups (B2 H8 L=S=1024
+// D128: 107 against 276 us; B1 H8 L=S=2048 D128 causal: 207 against 295 us), mixed at 128,
+// twice as slow at 256 (each 32-row group reads its keys' K and V itself, where the tiled
+// kernel shares a tile among 128 rows).
+bool prefill_f32_split(const AttnFwdArgs &f) {
+    if (f.mask || f.dropout || f.kv_len || f.q_pos || f.o32 || f.rope_q || f.S > 4096) return false;
+    const int64_t pairs = ((f.L + F32_BM - 1) / F32_BM + 1) / 2;
+    return f.B * f.H * pairs <= 64;
+}
+
 bool prefill_f32_supported(const AttnFwdArgs &f) {
     if (f.out_dtype != GT_F32 || f.D != f.Dv || (f.D != 64 && f.D != 128)) return false;
     if (f.rope_q) return false;
@@ -915,6 +1060,18 @@ hipError_t launch_prefill_f32_d(const AttnFwdArgs &a, int nq, int npairs, int64_
 }
 
 hipError_t launch_prefill_f32(const AttnFwdArgs &a, hipStream_t s) {
+    if (prefill_f32_split(a)) {
+        const int ng = (int)((a.L + 31) / 32);
+        const dim3 grid((unsigned)(a.B * a.H * ng));
+        if (a.D == 128) {
+            if (a.causal) hipLaunchKernelGGL((prefill_f32_split_kernel<128, true>), grid, dim3(256), 0, s, a, ng);
+            else hipLaunchKernelGGL((prefill_f32_split_kernel<128, false>), grid, dim3(256), 0, s, a, ng);
+        } else {
+            if (a.causal) hipLaunchKernelGGL((prefill_f32_split_kernel<64, true>), grid, dim3(256), 0, s, a, ng);
+            else hipLaunchKernelGGL((prefill_f32_split_kernel<64, false>), grid, dim3(256), 0, s, a, ng);
+        }
+        return hipGetLastError();
+    }
     const int nq = (int)((a.L + F32_BM - 1) / F32_BM);
     const int npairs = (nq + 1) / 2;
     const int64_t grid = (int64_t)npairs * a.B * a.H;
@@ -924,6 +1081,10 @@ hipError_t launch_prefill_f32(const AttnFwdArgs &a, hipStream_t s) {
 }
 
 }  // namespace
+
+bool attn_prefill_f32_split(const AttnFwdArgs &f, int cd) {
+    return cd == GT_F32 && prefill_f32_supported(f) && prefill_f32_split(f);
+}
 
 bool attn_prefill_supported(const AttnFwdArgs &f, int cd) {
     if (cd == GT_F32) return prefill_f32_supported(f);

@@ -235,7 +235,8 @@ std::string decode_note(const char *kind, const DecodeArgs &da, int max_tile) {
 
 std::string prefill_note(const AttnFwdArgs &a, int cd) {
     return std::string(attn_prefill_asm_supported(a, cd) ? "prefill pipelined " : "prefill ") + dtype_tag(cd) + " D=" + std::to_string(a.D) + " B=" + std::to_string(a.B) +
-           " H=" + std::to_string(a.H) + " L=" + std::to_string(a.L) + " S=" + std::to_string(a.S);
+           " H=" + std::to_string(a.H) + " L=" + std::to_string(a.L) + " S=" + std::to_string(a.S) +
+           (attn_prefill_f32_split(a, cd) ? " split" : "");
 }
 
 bool dispatch_forward(const AttnFwdArgs &a, int cd, int dev) {

@@ -123,5 +123,6 @@ def test_fp32_workload_whole(dev):
     cfg = _cfg("fp32")
     q, k, v = bench.forward_inputs(cfg, dev)[0]
     out = g.flash_attention(q, k, v, None, 0.0, True)
-    assert _C.last_launch() == "prefill f32 D=64 B=1 H=4 L=128 S=128"  # the float32 MFMA kernel
+    # the float32 MFMA kernel for small grids (4 wavefronts splitting each 32-row group's keys)
+    assert _C.last_launch() == "prefill f32 D=64 B=1 H=4 L=128 S=128 split"
     assert_close(out, oracle_forward(q, k, v, is_causal=True), torch.float32, "fp32 B1 H4 L128 D64")

@@ -101,3 +101,23 @@ def test_float32_prefill_with_per_element_masks(dev, kind, B, H, Hkv, L, S, D, c
     fin = np.isfinite(want_lse)
     assert np.array_equal(np.isinf(lse.cpu().numpy()), ~fin), what
     assert np.abs(lse.cpu().double().numpy()[fin] - want_lse[fin]).max() < 1e-4, what
+
+
+# small grids (at most 64 workgroups of the tiled kernel, B * H * query-tile pairs, and at most
+# 4096 keys; no mask, no dropout): the split kernel, whose 4 wavefronts split a 32-row group's key
+# tiles and merge; larger grids or longer key ranges: the tiled kernel
+@pytest.mark.parametrize("B,H,Hkv,L,S,D,causal,split", [
+    (1, 4, 4, 128, 128, 64, True, True), (1, 16, 16, 1024, 1024, 64, True, True),
+    (1, 17, 17, 1024, 1024, 64, True, False), (2, 3, 1, 33, 300, 128, False, True),
+    (1, 2, 2, 16, 1, 128, False, True), (2, 2, 2, 100, 77, 128, True, True),
+    (1, 1, 1, 500, 700, 64, False, True), (1, 2, 1, 40, 4097, 64, False, False)])
+def test_float32_split_kernel_for_small_grids(dev, B, H, Hkv, L, S, D, causal, split):
+    seed = 7 * L + S + D
+    q, k, v = randn((B, H, L, D), seed), randn((B, Hkv, S, D), seed + 1), randn((B, Hkv, S, D), seed + 2)
+    out, lse = g.flash_attention_lse(q.to(dev), k.to(dev), v.to(dev), None, 0.0, causal)
+    launch = _C.last_launch()
+    what = f"B{B} H{H}/{Hkv} L{L} S{S} D{D} causal={causal}"
+    assert launch.startswith(f"prefill f32 D={D} ") and launch.endswith(" split") == split, (what, launch)
+    want, want_lse = oracle_forward(q, k, v, is_causal=causal, return_lse=True)
+    assert_close(out, want, torch.float32, what)
+    assert np.abs(lse.cpu().double().numpy() - want_lse).max() < 1e-4, what
