@@ -876,10 +876,13 @@ __global__ __launch_bounds__(64 * F32_NW, 2) void prefill_f32_kernel(AttnFwdArgs
 // through LDS.  The operand mapping is prefill_f32_kernel's (S^T = K.Q^T with k-step t = dim
 // t + (D/2)(lane/32) and Q in registers; O^T += V^T.P^T with k-step s = the key of accumulator
 // entry s), but each wavefront reads its K rows (16-byte pieces) and V^T values straight from
-// memory: they are few and stay in L2.  No mask, dropout or KV-cache lengths (prefill_f32_split).
-template <int D, bool CAUSAL>
+// memory: they are few and stay in L2.  Masks, dropout and KV-cache lengths as prefill_f32_kernel
+// takes them (the mask read per score, or 4 keys per load for modes 5 and 6).
+template <int D, bool CAUSAL, int MASK, bool DROP>
 __global__ __launch_bounds__(256) void prefill_f32_split_kernel(AttnFwdArgs a, int ng) {
     constexpr int DH = D / 2, DB = D / 32, OP = D + 4;  // OP: LDS row pitch of the partial O
+    constexpr bool MVEC = MASK >= 5;                    // 4 keys per mask load
+    constexpr bool MBOOL = MASK == 1 || MASK == 5;
     __shared__ __attribute__((aligned(16))) float sO[4][32][OP];
     __shared__ float sM[4][32], sL[4][32];
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
@@ -889,9 +892,14 @@ __global__ __launch_bounds__(256) void prefill_f32_split_kernel(AttnFwdArgs a, i
     const int64_t b = bh / a.H, h = bh % a.H, hk = h / (a.H / a.Hkv);
     const int L = (int)a.L, S = (int)a.S;
     const int q0 = 32 * rg, lq = q0 + lrow, lqc = min(lq, L - 1);
-    const int kv_end = CAUSAL ? min(q0 + 32, S) : S;  // keys any row of the group sees
-    const int nt = (kv_end + 31) / 32;
+    const int nkv = attn_kv_len(a, b), qpos = attn_q_pos(a, b);
+    const int kv_end = CAUSAL ? min(q0 + 32 + qpos, nkv) : nkv;  // keys any row of the group sees
+    const int nt = kv_end > 0 ? (kv_end + 31) / 32 : 0;
     const float c = a.scale * kLog2e;
+    // element offset of this lane's mask row (MASK 4: the key-padding row, m_sl = 0)
+    const int64_t mrb = MASK != 0 ? b * a.m_sb + h * a.m_sh + (int64_t)lqc * a.m_sl : 0;
+    // dropout: Philox block of keys 0..3 of this lane's row (rows past L draw unused words)
+    const uint64_t drow = DROP ? (uint64_t)(bh * a.L + lq) * (uint64_t)((a.S + 3) / 4) : 0;
 
     float qf[DH];  // Q of row lqc, dims DH half .. +DH (B operand of S^T)
     {
@@ -925,11 +933,33 @@ __global__ __launch_bounds__(256) void prefill_f32_split_kernel(AttnFwdArgs a, i
 #pragma unroll
             for (int e = 0; e < 4; ++e) s = mfma_f32x2(kv[e], qf[4 * u + e], s);
         }
-        const int vis = (CAUSAL ? min(lq, S - 1) : S - 1) - (k0 + 4 * half);
+        const int vis = min(nkv - 1, CAUSAL ? lq + qpos : nkv - 1) - (k0 + 4 * half);
+        // MVEC: the mask of keys k0 + 8g + 4half + 0..3 (groups past the last 4 keys read those:
+        // their scores are blocked)
+        f32x4 mvf[MVEC && !MBOOL ? 4 : 1];
+        uint32_t mvb[MVEC && MBOOL ? 4 : 1];
+        if constexpr (MVEC) {
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const int64_t at = mrb + min(k0 + 8 * g + 4 * half, S - 4);
+                if constexpr (MBOOL) mvb[g] = *(const uint32_t *)((const uint8_t *)a.mask + at);
+                else mvf[g] = *(const f32x4 *)((const float *)a.mask + at);
+            }
+        }
         float tmax = -INFINITY;
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-            s[i] = 8 * (i / 4) + (i % 4) > vis ? -INFINITY : s[i] * c;
+            float x = s[i] * c;
+            bool blocked = 8 * (i / 4) + (i % 4) > vis;
+            if constexpr (MVEC) {
+                if constexpr (MBOOL) blocked = blocked || ((mvb[i / 4] >> (8 * (i % 4))) & 0xffu) == 0u;
+                else x = fmaf(mvf[i / 4][i % 4], kLog2e, x);
+            } else if constexpr (MASK != 0) {
+                const int64_t mi = mrb + (int64_t)min(k0 + 8 * (i / 4) + 4 * half + (i % 4), S - 1) * a.m_ss;
+                if constexpr (MBOOL) blocked = blocked || ((const uint8_t *)a.mask)[mi] == 0;
+                else x = fmaf(((const float *)a.mask)[mi], kLog2e, x);
+            }
+            s[i] = blocked ? -INFINITY : x;
             tmax = fmaxf(tmax, s[i]);
         }
         const float mnew = fmaxf(m, xhalf_max(tmax));
@@ -947,6 +977,17 @@ __global__ __launch_bounds__(256) void prefill_f32_split_kernel(AttnFwdArgs a, i
         for (int i = 0; i < 16; ++i) {
             s[i] = fast_exp2(s[i] - msub);  // -inf -> 0
             lsum += s[i];
+        }
+        if constexpr (DROP) {
+            // entries 4g .. 4g+3 are keys k0 + 8g + 4half + 0..3: one Philox block
+            const float dscale = (float)a.drop.scale;
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const GtWord4 x = gt_philox4x32_10(drow + (uint64_t)((k0 + 8 * g + 4 * half) >> 2), a.drop.offset,
+                                                   a.drop.seed);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) s[4 * g + e] *= x.w[e] < a.drop.thresh ? dscale : 0.0f;
+            }
         }
         // O^T += V^T . P^T: k-step s2 is key k0 + 8(s2/4) + 4half + s2%4, A = V[that key][32 db + lrow]
 #pragma unroll
@@ -1002,14 +1043,14 @@ __global__ __launch_bounds__(256) void prefill_f32_split_kernel(AttnFwdArgs a, i
     }
 }
 
-// The calls prefill_f32_split_kernel takes: no mask, dropout or KV-cache lengths, at most 64
-// workgroups of prefill_f32_kernel (B * H * query-tile pairs) and at most 4096 keys.  Measured
+// The calls prefill_f32_split_kernel takes: at most 64 workgroups of prefill_f32_kernel
+// (B * H * query-tile pairs) and at most 4096 keys.  Measured
 // against the tiled kernel: faster at every grid of up to 64 of its workgroups (B2 H8 L=S=1024
 // D128: 107 against 276 us; B1 H8 L=S=2048 D128 causal: 207 against 295 us), mixed at 128,
 // twice as slow at 256 (each 32-row group reads its keys' K and V itself, where the tiled
 // kernel shares a tile among 128 rows).
 bool prefill_f32_split(const AttnFwdArgs &f) {
-    if (f.mask || f.dropout || f.kv_len || f.q_pos || f.o32 || f.rope_q || f.S > 4096) return false;
+    if (f.o32 || f.rope_q || f.S > 4096) return false;
     const int64_t pairs = ((f.L + F32_BM - 1) / F32_BM + 1) / 2;
     return f.B * f.H * pairs <= 64;
 }
@@ -1059,18 +1100,32 @@ hipError_t launch_prefill_f32_d(const AttnFwdArgs &a, int nq, int npairs, int64_
                     : launch_prefill_f32_cd<D, false, false>(a, nq, npairs, grid, s);
 }
 
+template <int D, bool CAUSAL, bool DROP>
+hipError_t launch_split(const AttnFwdArgs &a, dim3 grid, int ng, hipStream_t s) {
+#define GT_SPLIT(MK) hipLaunchKernelGGL((prefill_f32_split_kernel<D, CAUSAL, MK, DROP>), grid, dim3(256), 0, s, a, ng)
+    switch (attn_mask_mode(a)) {
+        case 0: GT_SPLIT(0); break;
+        case 1: GT_SPLIT(1); break;
+        case 2: GT_SPLIT(2); break;
+        case 4: GT_SPLIT(4); break;
+        case 5: GT_SPLIT(5); break;
+        case 6: GT_SPLIT(6); break;
+        default: return hipErrorInvalidValue;
+    }
+#undef GT_SPLIT
+    return hipGetLastError();
+}
+
 hipError_t launch_prefill_f32(const AttnFwdArgs &a, hipStream_t s) {
     if (prefill_f32_split(a)) {
         const int ng = (int)((a.L + 31) / 32);
         const dim3 grid((unsigned)(a.B * a.H * ng));
         if (a.D == 128) {
-            if (a.causal) hipLaunchKernelGGL((prefill_f32_split_kernel<128, true>), grid, dim3(256), 0, s, a, ng);
-            else hipLaunchKernelGGL((prefill_f32_split_kernel<128, false>), grid, dim3(256), 0, s, a, ng);
-        } else {
-            if (a.causal) hipLaunchKernelGGL((prefill_f32_split_kernel<64, true>), grid, dim3(256), 0, s, a, ng);
-            else hipLaunchKernelGGL((prefill_f32_split_kernel<64, false>), grid, dim3(256), 0, s, a, ng);
+            if (a.dropout) return a.causal ? launch_split<128, true, true>(a, grid, ng, s) : launch_split<128, false, true>(a, grid, ng, s);
+            return a.causal ? launch_split<128, true, false>(a, grid, ng, s) : launch_split<128, false, false>(a, grid, ng, s);
         }
-        return hipGetLastError();
+        if (a.dropout) return a.causal ? launch_split<64, true, true>(a, grid, ng, s) : launch_split<64, false, true>(a, grid, ng, s);
+        return a.causal ? launch_split<64, true, false>(a, grid, ng, s) : launch_split<64, false, false>(a, grid, ng, s);
     }
     const int nq = (int)((a.L + F32_BM - 1) / F32_BM);
     const int npairs = (nq + 1) / 2;

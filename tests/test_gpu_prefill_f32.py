@@ -121,3 +121,42 @@ def test_float32_split_kernel_for_small_grids(dev, B, H, Hkv, L, S, D, causal, s
     want, want_lse = oracle_forward(q, k, v, is_causal=causal, return_lse=True)
     assert_close(out, want, torch.float32, what)
     assert np.abs(lse.cpu().double().numpy() - want_lse).max() < 1e-4, what
+
+
+# the split kernel with every mask mode (key padding 4; bool 5 / 1 and float 6 / 2 with S a
+# multiple of 4 or not) and with dropout (against the oracle's composition under its decisions)
+@pytest.mark.parametrize("kind,S", [("pad", 77), ("bool", 128), ("bool", 77), ("add", 128), ("add", 77)])
+@pytest.mark.parametrize("causal", [False, True])
+def test_float32_split_kernel_with_masks(dev, kind, S, causal):
+    B, H, Hkv, L, D = 2, 2, 1, 100, 128
+    seed = S + (3 if causal else 0) + len(kind)
+    q, k, v = randn((B, H, L, D), seed), randn((B, Hkv, S, D), seed + 1), randn((B, Hkv, S, D), seed + 2)
+    if kind == "pad":
+        m = _keypad(B, S, seed)
+    else:
+        m = _elem_mask(kind, B, H, L, S, seed)
+    out, lse = g.flash_attention_lse(q.to(dev), k.to(dev), v.to(dev), m.to(dev), 0.0, causal)
+    launch = _C.last_launch()
+    what = f"{kind} S{S} causal={causal}"
+    assert launch.endswith(" split"), (what, launch)
+    want, want_lse = oracle_forward(q, k, v, mask=m, is_causal=causal, return_lse=True)
+    assert_close(out, want, torch.float32, what)
+    fin = np.isfinite(want_lse)
+    assert np.array_equal(np.isinf(lse.cpu().numpy()), ~fin), what
+    assert np.abs(lse.cpu().double().numpy()[fin] - want_lse[fin]).max() < 1e-4, what
+
+
+@pytest.mark.parametrize("masked", [False, True])
+def test_float32_split_kernel_with_dropout(dev, masked):
+    import oracle
+    from _util import to_oracle
+    B, H, L, S, D, p, seed = 1, 4, 128, 128, 64, 0.3, 11
+    q, k, v = randn((B, H, L, D), 20), randn((B, H, S, D), 21), randn((B, H, S, D), 22)
+    m = _keypad(B, S, 5) if masked else None
+    out, lse, _ = g.flash_attention_dropout(q.to(dev), k.to(dev), v.to(dev), None if m is None else m.to(dev), 0.0,
+                                            True, p, seed)
+    assert _C.last_launch().endswith(" split"), _C.last_launch()
+    keep = oracle.dropout_keep(B, H, L, S, p, seed, 0)
+    ref = oracle.attention_dropout(to_oracle(q), to_oracle(k), to_oracle(v), keep, p,
+                                   mask=None if m is None else to_oracle(m), is_causal=True, out_dtype=oracle.F64)
+    assert_close(out, ref, torch.float32, f"dropout masked={masked}")
