@@ -1149,16 +1149,298 @@ hipError_t launch_bwd_f32_d(const AttnBwdArgs &a, hipStream_t s) {
     return launch_bwd_f32_dd<D, true>(a, s);
 }
 
+// ---- float32, small grids ----
+// Fewer than 32 dQ workgroups (few heads of one or two sequences) leave the kernels above with a
+// long walk per wavefront and most CUs idle.  Here a workgroup owns 32 query rows (dQ) or 32 keys
+// (dK/dV) and its 4 wavefronts split the key tiles (dQ) or the (query head, query tile) steps
+// (dK/dV), each accumulating its own partial gradient; the partials are summed through LDS.  The
+// operand mapping is that of the kernels above; Q, K, V and dO are read straight from memory
+// (16-byte row pieces as the row fragments, single floats as the per-element operands), as they
+// are few and stay in L2.  No dropout (the launcher sends dropout to the kernels above).
+
+// element MASK term of score (q, key) in raw score units (MASK 4: the key's, MASK 2: the
+// element's), and whether a bool mask (MASK 1) blocks it
+template <int MASK>
+__device__ inline float f32s_mask(const AttnFwdArgs &f, int64_t b, int64_t h, int q, int key, bool &ok) {
+    if constexpr (MASK == 0) return 0.0f;
+    const int64_t mi = b * f.m_sb + h * f.m_sh + (int64_t)q * f.m_sl + (int64_t)key * f.m_ss;
+    if constexpr (MASK == 1) {
+        ok = ok && ((const uint8_t *)f.mask)[mi] != 0;
+        return 0.0f;
+    } else {
+        return ((const float *)f.mask)[mi] / f.scale;
+    }
+}
+
+template <int D, bool CAUSAL, int MASK>
+__global__ __launch_bounds__(256) void bwd_dq_f32s_kernel(AttnBwdArgs a, int ng) {
+    constexpr int DH = D / 2, DB = D / 32, OP = D + 4;
+    __shared__ __attribute__((aligned(16))) float sQ[4][32][OP];
+    const AttnFwdArgs &f = a.f;
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int lrow = lane & 31, half = lane >> 5;
+    const int64_t bh = blockIdx.x / ng;
+    const int rg = (int)(blockIdx.x % ng);
+    const int64_t b = bh / f.H, h = bh % f.H, hk = h / (f.H / f.Hkv);
+    const int L = (int)f.L, S = (int)f.S;
+    const int q0 = 32 * rg, lq = q0 + lrow, lqc = min(lq, L - 1);
+    const float c = f.scale * kLog2e;
+
+    float qf[DH], gf[DH];  // Q and dO of row lqc, dims DH half .. +DH
+    float dlt;
+    {
+        const float *qr = (const float *)f.q + b * f.q_sb + h * f.q_sh + (int64_t)lqc * f.q_sl + DH * half;
+        const float *gr = (const float *)a.dout + (bh * f.L + lqc) * D + DH * half;
+        const float *orow = (const float *)f.o + (bh * f.L + lqc) * D + DH * half;
+        float part = 0.0f;
+#pragma unroll
+        for (int u = 0; u < DH / 4; ++u) {
+            const f32x4 x = *(const f32x4 *)(qr + 4 * u), g = *(const f32x4 *)(gr + 4 * u);
+            const f32x4 o4 = *(const f32x4 *)(orow + 4 * u);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                qf[4 * u + e] = x[e];
+                gf[4 * u + e] = g[e];
+                part = fmaf(g[e], o4[e], part);
+            }
+        }
+        // delta = rowsum(dO * O), for dK/dV
+        dlt = xhalf_sum(part);
+        if (w == 0 && half == 0 && lq < L) ((float *)a.delta)[bh * f.L + lq] = dlt;
+    }
+    const float lse2 = ((const float *)f.lse)[bh * f.L + lqc] * kLog2e;
+    const float *kbase = (const float *)f.k + b * f.k_sb + hk * f.k_sh;
+    const float *vbase = (const float *)f.v + b * f.v_sb + hk * f.v_sh;
+    const int kv_end = CAUSAL ? min(q0 + 32, S) : S;
+    const int nt = (kv_end + 31) / 32;
+    f32x16 dq[DB];
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) dq[db][i] = 0.0f;
+
+    for (int t = w; t < nt; t += 4) {
+        const int k0 = 32 * t;
+        // S^T = K.Q^T, dP^T = V.dO^T - delta: entry i is key k0 + 8(i/4) + 4half + i%4, query lq
+        const float *kr = kbase + (int64_t)min(k0 + lrow, S - 1) * f.k_ss + DH * half;
+        const float *vr = vbase + (int64_t)min(k0 + lrow, S - 1) * f.v_ss + DH * half;
+        f32x16 sc, dp;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            sc[i] = 0.0f;
+            dp[i] = -dlt;
+        }
+#pragma unroll
+        for (int u = 0; u < DH / 4; ++u) {
+            const f32x4 kv = *(const f32x4 *)(kr + 4 * u), vv = *(const f32x4 *)(vr + 4 * u);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                sc = mma_f32x2(kv[e], qf[4 * u + e], sc);
+                dp = mma_f32x2(vv[e], gf[4 * u + e], dp);
+            }
+        }
+        const int vis = (lq < L ? (CAUSAL ? min(lq, S - 1) : S - 1) : -1) - (k0 + 4 * half);
+        float ds[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            bool ok = 8 * (i / 4) + (i % 4) <= vis;
+            const int key = min(k0 + 8 * (i / 4) + 4 * half + (i % 4), S - 1);
+            const float x = sc[i] + f32s_mask<MASK>(f, b, h, lqc, key, ok);
+            ds[i] = (ok ? fast_exp2(fmaf(x, c, -lse2)) : 0.0f) * dp[i];
+        }
+        // dQ^T += K^T . dS^T: k-step s2 is key k0 + 8(s2/4) + 4half + s2%4, A = K[that key][32db + lrow]
+#pragma unroll
+        for (int s2 = 0; s2 < 16; ++s2) {
+            const float *kk = kbase + (int64_t)min(k0 + 8 * (s2 >> 2) + 4 * half + (s2 & 3), S - 1) * f.k_ss + lrow;
+#pragma unroll
+            for (int db = 0; db < DB; ++db) dq[db] = mma_f32x2(kk[32 * db], ds[s2], dq[db]);
+        }
+    }
+    // sum the four partials: entry i of dq[db] is dim 32db + 8(i/4) + 4half + i%4 of query lrow
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const f32x4 v = {dq[db][4 * g], dq[db][4 * g + 1], dq[db][4 * g + 2], dq[db][4 * g + 3]};
+            *(f32x4 *)&sQ[w][lrow][32 * db + 8 * g + 4 * half] = v;
+        }
+    __syncthreads();
+    const int r = threadIdx.x >> 3, part = threadIdx.x & 7;
+    if (q0 + r < L) {
+        float *row = (float *)a.dq + (bh * f.L + q0 + r) * D + (D / 8) * part;
+#pragma unroll
+        for (int j = 0; j < D / 32; ++j) {
+            f32x4 acc = *(const f32x4 *)&sQ[0][r][(D / 8) * part + 4 * j];
+#pragma unroll
+            for (int ww = 1; ww < 4; ++ww) {
+                const f32x4 x = *(const f32x4 *)&sQ[ww][r][(D / 8) * part + 4 * j];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) acc[e] += x[e];
+            }
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[e] *= f.scale;
+            *(f32x4 *)(row + 4 * j) = acc;
+        }
+    }
+}
+
+template <int D, bool CAUSAL, int MASK>
+__global__ __launch_bounds__(256, 1) void bwd_dkdv_f32s_kernel(AttnBwdArgs a, int nkg) {
+    constexpr int DH = D / 2, DB = D / 32, OP = D + 4;
+    __shared__ __attribute__((aligned(16))) float sK[4][32][OP];
+    const AttnFwdArgs &f = a.f;
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int lrow = lane & 31, half = lane >> 5;
+    const int64_t bk = blockIdx.x / nkg;
+    const int kg = (int)(blockIdx.x % nkg);
+    const int64_t b = bk / f.Hkv, hk = bk % f.Hkv;
+    const int G = (int)(f.H / f.Hkv);
+    const int L = (int)f.L, S = (int)f.S;
+    const int k0 = 32 * kg, key = k0 + lrow, kc = min(key, S - 1);
+    const float c = f.scale * kLog2e;
+
+    float kf[DH], vf[DH];  // K and V of this lane's key, dims DH half .. +DH
+    {
+        const float *kr = (const float *)f.k + b * f.k_sb + hk * f.k_sh + (int64_t)kc * f.k_ss + DH * half;
+        const float *vr = (const float *)f.v + b * f.v_sb + hk * f.v_sh + (int64_t)kc * f.v_ss + DH * half;
+#pragma unroll
+        for (int u = 0; u < DH / 4; ++u) {
+            const f32x4 x = *(const f32x4 *)(kr + 4 * u), y = *(const f32x4 *)(vr + 4 * u);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                kf[4 * u + e] = x[e];
+                vf[4 * u + e] = y[e];
+            }
+        }
+    }
+    f32x16 dk[DB], dv[DB];
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) dk[db][i] = dv[db][i] = 0.0f;
+
+    // steps: (query head hh of the group, 32-row query tile) for the tiles that can see these keys
+    const int qt0 = CAUSAL ? k0 / 32 : 0;
+    const int nqt = max(0, (L + 31) / 32 - qt0);
+    for (int j = w; j < G * nqt; j += 4) {
+        const int hh = j / nqt, q0 = 32 * (qt0 + j % nqt);
+        const int64_t h = hk * G + hh, bh = b * f.H + h;
+        // S = Q.K^T, dP = dO.V^T - delta: entry i is query q0 + 8(i/4) + 4half + i%4, this lane's key
+        const float *qr = (const float *)f.q + b * f.q_sb + h * f.q_sh + (int64_t)min(q0 + lrow, L - 1) * f.q_sl + DH * half;
+        const float *gr = (const float *)a.dout + (bh * f.L + min(q0 + lrow, L - 1)) * D + DH * half;
+        f32x16 sc, dp;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int q = min(q0 + 8 * (i / 4) + 4 * half + (i % 4), L - 1);
+            sc[i] = 0.0f;
+            dp[i] = -((const float *)a.delta)[bh * f.L + q];
+        }
+#pragma unroll
+        for (int u = 0; u < DH / 4; ++u) {
+            const f32x4 qa = *(const f32x4 *)(qr + 4 * u), ga = *(const f32x4 *)(gr + 4 * u);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                sc = mma_f32x2(qa[e], kf[4 * u + e], sc);
+                dp = mma_f32x2(ga[e], vf[4 * u + e], dp);
+            }
+        }
+        float p[16], ds[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int qq = q0 + 8 * (i / 4) + 4 * half + (i % 4), q = min(qq, L - 1);
+            bool ok = key < S && qq < L && (!CAUSAL || qq >= key);
+            const float x = sc[i] + f32s_mask<MASK>(f, b, h, q, kc, ok);
+            const float ls = ((const float *)f.lse)[bh * f.L + q] * kLog2e;
+            p[i] = ok ? fast_exp2(fmaf(x, c, -ls)) : 0.0f;
+            ds[i] = p[i] * dp[i];
+        }
+        // dV += P^T.dO, dK += dS^T.Q: k-step s2 is query q0 + 8(s2/4) + 4half + s2%4
+#pragma unroll
+        for (int s2 = 0; s2 < 16; ++s2) {
+            const int q = min(q0 + 8 * (s2 >> 2) + 4 * half + (s2 & 3), L - 1);
+            const float *qq = (const float *)f.q + b * f.q_sb + h * f.q_sh + (int64_t)q * f.q_sl + lrow;
+            const float *gg = (const float *)a.dout + (bh * f.L + q) * D + lrow;
+#pragma unroll
+            for (int db = 0; db < DB; ++db) {
+                dv[db] = mma_f32x2(p[s2], gg[32 * db], dv[db]);
+                dk[db] = mma_f32x2(ds[s2], qq[32 * db], dk[db]);
+            }
+        }
+    }
+    // sum the four partials (dK, then dV through the same buffer): entry i of dk[db] is key
+    // 8(i/4) + 4half + i%4 of the group, dim 32db + lrow
+    const int r = threadIdx.x >> 3, part = threadIdx.x & 7;
+#pragma unroll
+    for (int which = 0; which < 2; ++which) {
+        if (which) __syncthreads();  // the dK sums are read before dV overwrites the buffer
+#pragma unroll
+        for (int db = 0; db < DB; ++db)
+#pragma unroll
+            for (int i = 0; i < 16; ++i)
+                sK[w][8 * (i / 4) + 4 * half + (i % 4)][32 * db + lrow] = which ? dv[db][i] : dk[db][i];
+        __syncthreads();
+        if (k0 + r < S) {
+            float *row = (float *)(which ? a.dv : a.dk) + (bk * f.S + k0 + r) * D + (D / 8) * part;
+            const float mul = which ? 1.0f : f.scale;
+#pragma unroll
+            for (int j = 0; j < D / 32; ++j) {
+                f32x4 acc = *(const f32x4 *)&sK[0][r][(D / 8) * part + 4 * j];
+#pragma unroll
+                for (int ww = 1; ww < 4; ++ww) {
+                    const f32x4 x = *(const f32x4 *)&sK[ww][r][(D / 8) * part + 4 * j];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) acc[e] += x[e];
+                }
+#pragma unroll
+                for (int e = 0; e < 4; ++e) acc[e] *= mul;
+                *(f32x4 *)(row + 4 * j) = acc;
+            }
+        }
+    }
+}
+
+template <int D, bool CAUSAL, int MASK>
+hipError_t launch_bwd_f32s_cm(const AttnBwdArgs &a, hipStream_t s) {
+    const AttnFwdArgs &f = a.f;
+    const int ng = (int)((f.L + 31) / 32), nkg = (int)((f.S + 31) / 32);
+    hipLaunchKernelGGL((bwd_dq_f32s_kernel<D, CAUSAL, MASK>), dim3((unsigned)(f.B * f.H * ng)), dim3(256), 0, s, a, ng);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL((bwd_dkdv_f32s_kernel<D, CAUSAL, MASK>), dim3((unsigned)(f.B * f.Hkv * nkg)), dim3(256), 0, s, a, nkg);
+    return hipGetLastError();
+}
+
+template <int D, bool CAUSAL>
+hipError_t launch_bwd_f32s_c(const AttnBwdArgs &a, hipStream_t s) {
+    switch (attn_mask_mode(a.f)) {
+        case 0: return launch_bwd_f32s_cm<D, CAUSAL, 0>(a, s);
+        case 1: case 5: return launch_bwd_f32s_cm<D, CAUSAL, 1>(a, s);
+        case 2: case 6: return launch_bwd_f32s_cm<D, CAUSAL, 2>(a, s);
+        case 4: return launch_bwd_f32s_cm<D, CAUSAL, 2>(a, s);  // the key-padding row as a float mask with m_sl = 0
+        default: return hipErrorInvalidValue;
+    }
+}
+
+// fewer than 128 dQ workgroups of the kernels above (and at most 4096 query rows and keys):
+// measured faster there (B2 H4 L=S=512 D64 causal 60 against 149 us, B1 H8 L=S=512 D128 142
+// against 261, B1 H24 L=S=512 D64 125 against 149), mixed at 128 (B2 H8 L=S=1024 D64 227
+// against 288 us, B1 H8 L=S=2048 D128 1022 against 958), slower from 192 on (B2 H16 L=S=1024
+// D64 418 against 284 us): each 32-row or 32-key workgroup reads its operands itself
+bool bwd_f32_small(const AttnFwdArgs &f) {
+    return f.B * f.H * ((f.L + 127) / 128) < 128 && f.L <= 4096 && f.S <= 4096;
+}
+
 bool bwd_f32_supported(const AttnBwdArgs &a) {
     const AttnFwdArgs &f = a.f;
     if (f.D != f.Dv || (f.D != 64 && f.D != 128) || f.kv_len || f.q_pos) return false;
     const int mode = attn_mask_mode(f);
     // as the forward: fewer than 16 query rows stay on the generic kernels
     if (f.L < 16 || f.S < 1 || !(f.scale > 0.0f) || !f.o || !f.lse) return false;  // f.o: float32 output
-    // fewer than 32 dQ workgroups leave the MFMA kernels latency-bound: the generic kernels, which
-    // spread the rows thinner, measured faster there (B1 H4 L128 D64 causal 38.0 us against 45.7,
-    // B1 H2 L1024 D64 231 against 277) and slower from 32 on (B1 H32 L128 D64 57.6 against 46.3)
-    if (f.B * f.H * ((f.L + 127) / 128) < 32) return false;
+    // small grids take the small-grid kernels (bwd_f32_small), which have no dropout; with
+    // dropout, grids of 32 to 127 dQ workgroups take the tiled kernels and fewer the generic
+    // ones (the tiled kernels measured slower than those below 32: B1 H4 L128 D64 causal 45.7
+    // against 38.0 us, B1 H2 L1024 D64 277 against 231)
+    if (bwd_f32_small(f) && f.dropout && f.B * f.H * ((f.L + 127) / 128) < 32) return false;
     if (f.L >= (1LL << 30) || f.S >= (1LL << 30)) return false;
     const int64_t strides[] = {f.q_sb, f.q_sh, f.q_sl, f.k_sb, f.k_sh, f.k_ss, f.v_sb, f.v_sh, f.v_ss};
     for (int64_t st : strides) if (st % 4 != 0 || st < 0) return false;  // 16-byte rows
@@ -1187,7 +1469,13 @@ bool attn_bwd_mfma_supported(const AttnBwdArgs &a, int cd) {
     return true;
 }
 
+bool attn_bwd_f32_split(const AttnBwdArgs &a) { return bwd_f32_small(a.f) && !a.f.dropout; }
+
 hipError_t launch_attn_bwd_mfma(const AttnBwdArgs &a, int cd, hipStream_t s) {
+    if (cd == GT_F32 && attn_bwd_f32_split(a)) {
+        if (a.f.D == 128) return a.f.causal ? launch_bwd_f32s_c<128, true>(a, s) : launch_bwd_f32s_c<128, false>(a, s);
+        return a.f.causal ? launch_bwd_f32s_c<64, true>(a, s) : launch_bwd_f32s_c<64, false>(a, s);
+    }
     if (cd == GT_F32) return a.f.D == 128 ? launch_bwd_f32_d<128>(a, s) : launch_bwd_f32_d<64>(a, s);
     if (cd == GT_F16) return a.f.D == 128 ? launch_bwd_d<_Float16, 128>(a, s) : launch_bwd_d<_Float16, 64>(a, s);
     return a.f.D == 128 ? launch_bwd_d<__bf16, 128>(a, s) : launch_bwd_d<__bf16, 64>(a, s);

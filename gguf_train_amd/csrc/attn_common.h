@@ -179,4 +179,5 @@ bool attn_weights_mfma(const AttnFwdArgs &f, int cd);  // the MFMA weights kerne
 hipError_t launch_dropout_mask(const GtDropout &d, bool keep_all, int64_t rows, int64_t S, uint8_t *out, hipStream_t s);
 
 bool attn_bwd_mfma_supported(const AttnBwdArgs &a, int cd);
+bool attn_bwd_f32_split(const AttnBwdArgs &a);  // float32: the small-grid backward kernels
 hipError_t launch_attn_bwd_mfma(const AttnBwdArgs &a, int cd, hipStream_t s);

@@ -696,8 +696,9 @@ int attention_backward(const char *who, const gt_tensor *grad_out, const gt_tens
         a.o_f32 = od == GT_F32 && cd != GT_F32;
         apply_dropout(a.f, drop);
         // heads padded to the MFMA kernels' sizes: padded inputs, padded gradients unpadded after.
-        // Float32: only where its MFMA backward takes the padded call (32 dQ workgroups or more)
-        if (cd == GT_F32 && !(f32_pads(a.f) && B * H * ((L + 127) / 128) >= 32)) Dp = 0;
+        // Float32: only where its MFMA backward takes the padded call (with dropout, 32 dQ
+        // workgroups or more)
+        if (cd == GT_F32 && !(f32_pads(a.f) && (B * H * ((L + 127) / 128) >= 32 || !a.f.dropout))) Dp = 0;
         const gt_tensor *pq = nullptr, *pk = nullptr, *pv = nullptr;
         if (Dp) {
             const gt_tensor *qp = pad_heads(qs, Dp, dev, tmp), *kp = pad_heads(ks, Dp, dev, tmp);
@@ -727,7 +728,9 @@ int attention_backward(const char *who, const gt_tensor *grad_out, const gt_tens
                 ok = gt_scratch_alloc(bits, nbits, dev);
                 a.dbits = (uint32_t *)bits.ptr();
             }
-            if (ok) note_launch(std::string("backward mfma ") + dtype_tag(cd) + " D=" + std::to_string(a.f.D));
+            if (ok)
+                note_launch(std::string("backward mfma ") + dtype_tag(cd) + " D=" + std::to_string(a.f.D) +
+                            (cd == GT_F32 && attn_bwd_f32_split(a) ? " split" : ""));
             ok = ok && gt_hip_check(launch_attn_bwd_mfma(a, cd, gt_stream()), "flash_attention_backward kernel");
         } else if (ok) {
             note_launch(std::string("backward generic ") + dtype_tag(cd));

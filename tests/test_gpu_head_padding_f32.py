@@ -3,8 +3,8 @@ kernels with the heads zero-padded: forward (output, log-sum-exp) and backward a
 float64 oracle at the float32 bar, GQA, causal or not, key padding, D != Dv, the 8-element and
 one-element pad copies, the launch log naming the padded kernels, a check that padding is what
 ran (the result equals the unpadded kernels' on explicitly zero-padded inputs, bit for bit), and
-the calls the float32 kernels do not take (fewer than 16 query rows, a small backward grid),
-which stay unpadded on the generic kernels; per-element masks are padded."""
+the calls the float32 kernels do not take (fewer than 16 query rows), which stay unpadded on the
+generic kernels; per-element masks and small backward grids are padded."""
 
 import numpy as np
 import pytest
@@ -55,7 +55,8 @@ def test_float32_padded_heads_match_the_oracle(dev, B, H, Hkv, L, S, D, Dv, caus
     fin = np.isfinite(want_lse)
     assert np.abs(lse.cpu().double().numpy()[fin] - want_lse[fin]).max() < 1e-4, what
     dq, dk, dv = g.flash_attention_backward(dout.to(dev), q.to(dev), k.to(dev), v.to(dev), md, out, lse, 0.0, causal)
-    assert _C.last_launch() == f"backward mfma f32 D={Dp}", (what, _C.last_launch())
+    small = B * H * ((L + 127) // 128) < 128  # the small-grid kernels
+    assert _C.last_launch() == f"backward mfma f32 D={Dp}" + (" split" if small else ""), (what, _C.last_launch())
     assert dq.shape == q.shape and dk.shape == k.shape and dv.shape == v.shape
     wq, wk, wv = oracle.flash_attention_backward(to_oracle(dout), to_oracle(q), to_oracle(k), to_oracle(v),
                                                  mask=None if mask is None else to_oracle(mask), is_causal=causal)
@@ -81,7 +82,7 @@ def test_float32_padding_is_the_unpadded_kernel_on_zero_padded_heads(dev, D):
         assert not b[..., D:].any()
 
 
-def test_float32_calls_the_mfma_kernels_do_not_take_stay_unpadded(dev):
+def test_float32_padding_of_short_rows_masks_and_small_grids(dev):
     B, H, S, D = 1, 4, 90, 96
     k, v = randn((B, H, S, D), 41).to(dev), randn((B, H, S, D), 42).to(dev)
     # 15 query rows: the generic forward
@@ -97,11 +98,11 @@ def test_float32_calls_the_mfma_kernels_do_not_take_stay_unpadded(dev):
     out = g.flash_attention(q.to(dev), k, v, m.to(dev), 0.0, False)
     assert _C.last_launch().startswith("prefill f32 D=128 "), _C.last_launch()
     assert_close(out, oracle_forward(q, k.cpu(), v.cpu(), mask=m), torch.float32, "bool mask")
-    # 4 dQ workgroups: the padded MFMA forward, the generic backward on the unpadded heads
+    # 4 dQ workgroups: the padded small-grid kernels, forward and backward
     out, lse = g.flash_attention_lse(q.to(dev), k, v, None, 0.0, True)
     assert _C.last_launch().startswith("prefill f32 D=128 "), _C.last_launch()
     dq, dk, dv = g.flash_attention_backward(dout.to(dev), q.to(dev), k, v, None, out, lse, 0.0, True)
-    assert _C.last_launch() == "backward generic f32", _C.last_launch()
+    assert _C.last_launch() == "backward mfma f32 D=128 split", _C.last_launch()
     wq, wk, wv = oracle.flash_attention_backward(to_oracle(dout), to_oracle(q), to_oracle(k.cpu()), to_oracle(v.cpu()),
                                                  is_causal=True)
     for name, got, ref in (("dq", dq, wq), ("dk", dk, wk), ("dv", dv, wv)):
