@@ -3,7 +3,8 @@ mask, a key-padding row or a per-element mask, 16 query rows or more) against th
 (max-abs 1e-4): ragged query and key counts around the 128-row query tiles and 32-key K/V
 tiles, one key, GQA, causal or not, key padding and per-element bool / additive masks (4-key and
 one-key loads), the log-sum-exp and the training forward's float32 output, and the launch log
-naming the kernel.  One query row takes the decode kernel; 2 to 15 rows the generic kernel."""
+naming the kernel.  One query row takes the decode kernel; 2 to 15 rows the small-grid kernel on
+small grids, else the generic kernel."""
 
 import numpy as np
 import pytest
@@ -160,3 +161,24 @@ def test_float32_split_kernel_with_dropout(dev, masked):
     ref = oracle.attention_dropout(to_oracle(q), to_oracle(k), to_oracle(v), keep, p,
                                    mask=None if m is None else to_oracle(m), is_causal=True, out_dtype=oracle.F64)
     assert_close(out, ref, torch.float32, f"dropout masked={masked}")
+
+
+# 2 to 15 query rows on a small grid (e.g. draft tokens against a cache): the split kernel; on a
+# large grid: the generic kernel
+@pytest.mark.parametrize("B,H,Hkv,L,S,D,causal,kp,split", [
+    (1, 8, 2, 4, 1000, 128, False, False, True), (2, 4, 4, 8, 300, 64, True, True, True),
+    (1, 4, 1, 2, 77, 64, False, True, True), (1, 2, 2, 15, 130, 128, True, False, True),
+    (17, 8, 8, 3, 64, 64, False, False, False)])
+def test_float32_few_query_rows(dev, B, H, Hkv, L, S, D, causal, kp, split):
+    seed = 11 * L + S + D
+    q, k, v = randn((B, H, L, D), seed), randn((B, Hkv, S, D), seed + 1), randn((B, Hkv, S, D), seed + 2)
+    mask = _keypad(B, S, seed) if kp else None
+    out, lse = g.flash_attention_lse(q.to(dev), k.to(dev), v.to(dev), None if mask is None else mask.to(dev), 0.0,
+                                     causal)
+    launch = _C.last_launch()
+    what = f"B{B} H{H}/{Hkv} L{L} S{S} D{D} causal={causal} keypad={kp}"
+    assert launch == (f"prefill f32 D={D} B={B} H={H} L={L} S={S} split" if split else "generic f32"), (what, launch)
+    want, want_lse = oracle_forward(q, k, v, mask=mask, is_causal=causal, return_lse=True)
+    assert_close(out, want, torch.float32, what)
+    fin = np.isfinite(want_lse)
+    assert np.abs(lse.cpu().double().numpy()[fin] - want_lse[fin]).max() < 1e-4, what
