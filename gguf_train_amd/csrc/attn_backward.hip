@@ -1434,8 +1434,9 @@ bool bwd_f32_supported(const AttnBwdArgs &a) {
     const AttnFwdArgs &f = a.f;
     if (f.D != f.Dv || (f.D != 64 && f.D != 128) || f.kv_len || f.q_pos) return false;
     const int mode = attn_mask_mode(f);
-    // as the forward: fewer than 16 query rows stay on the generic kernels
-    if (f.L < 16 || f.S < 1 || !(f.scale > 0.0f) || !f.o || !f.lse) return false;  // f.o: float32 output
+    // as the forward: fewer than 16 query rows take the small-grid kernels or the generic ones
+    if ((f.L < 16 && !(bwd_f32_small(f) && !f.dropout)) || f.L < 1 || f.S < 1 || !(f.scale > 0.0f) || !f.o || !f.lse)
+        return false;  // f.o: float32 output
     // small grids take the small-grid kernels (bwd_f32_small), which have no dropout; with
     // dropout, grids of 32 to 127 dQ workgroups take the tiled kernels and fewer the generic
     // ones (the tiled kernels measured slower than those below 32: B1 H4 L128 D64 causal 45.7

@@ -6,7 +6,8 @@ the dQ kernel's 128-row query tiles and 32-key K/V tiles and the dK/dV kernel's 
 fully padded rows, per-element bool / additive masks, and the launch log naming the kernel.
 Grids of fewer than 128 dQ workgroups of the tiled kernels take the small-grid kernels
 (bwd_dq_f32s_kernel, bwd_dkdv_f32s_kernel: 4 wavefronts per workgroup splitting the key tiles or
-query steps); fewer than 16 query rows keep the generic kernels."""
+query steps), fewer than 16 query rows included; larger grids with fewer than 16 rows keep the
+generic kernels."""
 
 import numpy as np
 import pytest
@@ -117,13 +118,17 @@ def test_float32_backward_without_residuals_and_with_an_empty_row(dev):
         assert torch.count_nonzero(got[B - 1]).item() == 0, name
 
 
-def test_fewer_rows_keep_the_generic_and_small_grids_take_the_split_backward(dev):
-    B, H, S, D = 1, 32, 90, 64
-    q, k, v, dout = randn((B, H, 15, D), 70), randn((B, H, S, D), 71), randn((B, H, S, D), 72), randn((B, H, 15, D), 73)
-    dq, dk, dv, launch = _grads(dev, q, k, v, dout, None, False)
-    assert launch == "backward generic f32", launch
-    for got, want, name in zip((dq, dk, dv), _oracle_grads(dout, q, k, v, None, False), ("dq", "dk", "dv")):
-        assert_close(got, want, torch.float32, name + " L=15")
+def test_small_grids_take_the_split_backward(dev):
+    # 15 and 3 query rows: the small-grid kernels (32-row groups); the same rows on a grid of 128
+    # or more tiled workgroups: the generic kernels
+    S, D = 90, 64
+    for B, H, L, want_launch in ((1, 32, 15, "backward mfma f32 D=64 split"), (2, 8, 3, "backward mfma f32 D=64 split"),
+                                 (4, 32, 15, "backward generic f32")):
+        q, k, v, dout = randn((B, H, L, D), 70), randn((B, H, S, D), 71), randn((B, H, S, D), 72), randn((B, H, L, D), 73)
+        dq, dk, dv, launch = _grads(dev, q, k, v, dout, None, L == 3)
+        assert launch == want_launch, (B, H, L, launch)
+        for got, want, name in zip((dq, dk, dv), _oracle_grads(dout, q, k, v, None, L == 3), ("dq", "dk", "dv")):
+            assert_close(got, want, torch.float32, f"{name} B{B} H{H} L={L}")
     # 127 dQ workgroups of the tiled kernels (B * H * ceil(L / 128)): the small-grid kernels; 128: tiled
     for H2, want_launch in ((127, "backward mfma f32 D=64 split"), (128, "backward mfma f32 D=64")):
         q2, k2, v2, g2 = (randn((1, H2, 128, D), 80 + i) for i in range(4))
