@@ -1156,7 +1156,9 @@ hipError_t launch_bwd_f32_d(const AttnBwdArgs &a, hipStream_t s) {
 // (dK/dV), each accumulating its own partial gradient; the partials are summed through LDS.  The
 // operand mapping is that of the kernels above; Q, K, V and dO are read straight from memory
 // (16-byte row pieces as the row fragments, single floats as the per-element operands), as they
-// are few and stay in L2.  No dropout (the launcher sends dropout to the kernels above).
+// are few and stay in L2.  Dropout (DROP) as in the kernels above: dQ draws the decisions and
+// writes them as one word per (query row, 32 keys), each (row, tile) by the one wavefront that
+// owns the tile; dK/dV reads the words of its 32 keys.
 
 // element MASK term of score (q, key) in raw score units (MASK 4: the key's, MASK 2: the
 // element's), and whether a bool mask (MASK 1) blocks it
@@ -1172,7 +1174,7 @@ __device__ inline float f32s_mask(const AttnFwdArgs &f, int64_t b, int64_t h, in
     }
 }
 
-template <int D, bool CAUSAL, int MASK>
+template <int D, bool CAUSAL, int MASK, bool DROP>
 __global__ __launch_bounds__(256) void bwd_dq_f32s_kernel(AttnBwdArgs a, int ng) {
     constexpr int DH = D / 2, DB = D / 32, OP = D + 4;
     __shared__ __attribute__((aligned(16))) float sQ[4][32][OP];
@@ -1213,6 +1215,9 @@ __global__ __launch_bounds__(256) void bwd_dq_f32s_kernel(AttnBwdArgs a, int ng)
     const float *vbase = (const float *)f.v + b * f.v_sb + hk * f.v_sh;
     const int kv_end = CAUSAL ? min(q0 + 32, S) : S;
     const int nt = (kv_end + 31) / 32;
+    // dropout: Philox block of keys 0..3 of this lane's row (rows past L draw unused words)
+    const uint64_t drow = DROP ? (uint64_t)(bh * f.L + lq) * (uint64_t)((f.S + 3) / 4) : 0;
+    const int64_t dwords = (f.S + 31) / 32;  // decision words per row
     f32x16 dq[DB];
 #pragma unroll
     for (int db = 0; db < DB; ++db)
@@ -1228,7 +1233,7 @@ __global__ __launch_bounds__(256) void bwd_dq_f32s_kernel(AttnBwdArgs a, int ng)
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
             sc[i] = 0.0f;
-            dp[i] = -dlt;
+            dp[i] = DROP ? 0.0f : -dlt;
         }
 #pragma unroll
         for (int u = 0; u < DH / 4; ++u) {
@@ -1238,6 +1243,25 @@ __global__ __launch_bounds__(256) void bwd_dq_f32s_kernel(AttnBwdArgs a, int ng)
                 sc = mma_f32x2(kv[e], qf[4 * u + e], sc);
                 dp = mma_f32x2(vv[e], gf[4 * u + e], dp);
             }
+        }
+        if constexpr (DROP) {
+            // entries 4g .. 4g+3 are keys k0 + 8g + 4half + 0..3: one Philox block; dP = m dO.V - delta
+            const float dscale = (float)f.drop.scale;
+            uint32_t word = 0u;  // bit k: key k0 + k kept
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const GtWord4 x = gt_philox4x32_10(drow + (uint64_t)((k0 + 8 * g + 4 * half) >> 2), f.drop.offset,
+                                                   f.drop.seed);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const bool keep = x.w[e] < f.drop.thresh;
+                    dp[4 * g + e] = fmaf(dp[4 * g + e], keep ? dscale : 0.0f, -dlt);
+                    word |= (keep ? 1u : 0u) << (8 * g + 4 * half + e);
+                }
+            }
+            // the row's word for these 32 keys (the two halves hold complementary keys)
+            const auto rw = __builtin_amdgcn_permlane32_swap(word, word, false, false);
+            if (half == 0 && lq < L) a.dbits[(bh * f.L + lq) * dwords + t] = rw[0] | rw[1];
         }
         const int vis = (lq < L ? (CAUSAL ? min(lq, S - 1) : S - 1) : -1) - (k0 + 4 * half);
         float ds[16];
@@ -1284,7 +1308,7 @@ __global__ __launch_bounds__(256) void bwd_dq_f32s_kernel(AttnBwdArgs a, int ng)
     }
 }
 
-template <int D, bool CAUSAL, int MASK>
+template <int D, bool CAUSAL, int MASK, bool DROP>
 __global__ __launch_bounds__(256, 1) void bwd_dkdv_f32s_kernel(AttnBwdArgs a, int nkg) {
     constexpr int DH = D / 2, DB = D / 32, OP = D + 4;
     __shared__ __attribute__((aligned(16))) float sK[4][32][OP];
@@ -1333,7 +1357,7 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv_f32s_kernel(AttnBwdArgs a, in
         for (int i = 0; i < 16; ++i) {
             const int q = min(q0 + 8 * (i / 4) + 4 * half + (i % 4), L - 1);
             sc[i] = 0.0f;
-            dp[i] = -((const float *)a.delta)[bh * f.L + q];
+            dp[i] = DROP ? 0.0f : -((const float *)a.delta)[bh * f.L + q];
         }
 #pragma unroll
         for (int u = 0; u < DH / 4; ++u) {
@@ -1351,8 +1375,17 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv_f32s_kernel(AttnBwdArgs a, in
             bool ok = key < S && qq < L && (!CAUSAL || qq >= key);
             const float x = sc[i] + f32s_mask<MASK>(f, b, h, q, kc, ok);
             const float ls = ((const float *)f.lse)[bh * f.L + q] * kLog2e;
-            p[i] = ok ? fast_exp2(fmaf(x, c, -ls)) : 0.0f;
-            ds[i] = p[i] * dp[i];
+            const float pv = ok ? fast_exp2(fmaf(x, c, -ls)) : 0.0f;
+            if constexpr (DROP) {
+                // the dQ kernel's decision for (query q, this lane's key): bit lrow of its word
+                const bool keep = (a.dbits[(bh * f.L + q) * ((f.S + 31) / 32) + kg] >> lrow) & 1u;
+                const float m = keep ? (float)f.drop.scale : 0.0f;
+                dp[i] = fmaf(dp[i], m, -((const float *)a.delta)[bh * f.L + q]);
+                p[i] = pv * m;
+            } else {
+                p[i] = pv;
+            }
+            ds[i] = pv * dp[i];
         }
         // dV += P^T.dO, dK += dS^T.Q: k-step s2 is query q0 + 8(s2/4) + 4half + s2%4
 #pragma unroll
@@ -1399,15 +1432,22 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv_f32s_kernel(AttnBwdArgs a, in
     }
 }
 
-template <int D, bool CAUSAL, int MASK>
-hipError_t launch_bwd_f32s_cm(const AttnBwdArgs &a, hipStream_t s) {
+template <int D, bool CAUSAL, int MASK, bool DROP>
+hipError_t launch_bwd_f32s_cmd(const AttnBwdArgs &a, hipStream_t s) {
     const AttnFwdArgs &f = a.f;
     const int ng = (int)((f.L + 31) / 32), nkg = (int)((f.S + 31) / 32);
-    hipLaunchKernelGGL((bwd_dq_f32s_kernel<D, CAUSAL, MASK>), dim3((unsigned)(f.B * f.H * ng)), dim3(256), 0, s, a, ng);
+    hipLaunchKernelGGL((bwd_dq_f32s_kernel<D, CAUSAL, MASK, DROP>), dim3((unsigned)(f.B * f.H * ng)), dim3(256), 0, s, a, ng);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL((bwd_dkdv_f32s_kernel<D, CAUSAL, MASK>), dim3((unsigned)(f.B * f.Hkv * nkg)), dim3(256), 0, s, a, nkg);
+    hipLaunchKernelGGL((bwd_dkdv_f32s_kernel<D, CAUSAL, MASK, DROP>), dim3((unsigned)(f.B * f.Hkv * nkg)), dim3(256), 0, s, a, nkg);
     return hipGetLastError();
+}
+
+template <int D, bool CAUSAL, int MASK>
+hipError_t launch_bwd_f32s_cm(const AttnBwdArgs &a, hipStream_t s) {
+    if (!a.f.dropout) return launch_bwd_f32s_cmd<D, CAUSAL, MASK, false>(a, s);
+    if (!a.dbits) return hipErrorInvalidValue;  // dK/dV reads the dQ kernel's decision words
+    return launch_bwd_f32s_cmd<D, CAUSAL, MASK, true>(a, s);
 }
 
 template <int D, bool CAUSAL>
@@ -1435,13 +1475,9 @@ bool bwd_f32_supported(const AttnBwdArgs &a) {
     if (f.D != f.Dv || (f.D != 64 && f.D != 128) || f.kv_len || f.q_pos) return false;
     const int mode = attn_mask_mode(f);
     // as the forward: fewer than 16 query rows take the small-grid kernels or the generic ones
-    if ((f.L < 16 && !(bwd_f32_small(f) && !f.dropout)) || f.L < 1 || f.S < 1 || !(f.scale > 0.0f) || !f.o || !f.lse)
+    if ((f.L < 16 && !bwd_f32_small(f)) || f.L < 1 || f.S < 1 || !(f.scale > 0.0f) || !f.o || !f.lse)
         return false;  // f.o: float32 output
-    // small grids take the small-grid kernels (bwd_f32_small), which have no dropout; with
-    // dropout, grids of 32 to 127 dQ workgroups take the tiled kernels and fewer the generic
-    // ones (the tiled kernels measured slower than those below 32: B1 H4 L128 D64 causal 45.7
-    // against 38.0 us, B1 H2 L1024 D64 277 against 231)
-    if (bwd_f32_small(f) && f.dropout && f.B * f.H * ((f.L + 127) / 128) < 32) return false;
+    // small grids take the small-grid kernels (bwd_f32_small)
     if (f.L >= (1LL << 30) || f.S >= (1LL << 30)) return false;
     const int64_t strides[] = {f.q_sb, f.q_sh, f.q_sl, f.k_sb, f.k_sh, f.k_ss, f.v_sb, f.v_sh, f.v_ss};
     for (int64_t st : strides) if (st % 4 != 0 || st < 0) return false;  // 16-byte rows
@@ -1470,7 +1506,7 @@ bool attn_bwd_mfma_supported(const AttnBwdArgs &a, int cd) {
     return true;
 }
 
-bool attn_bwd_f32_split(const AttnBwdArgs &a) { return bwd_f32_small(a.f) && !a.f.dropout; }
+bool attn_bwd_f32_split(const AttnBwdArgs &a) { return bwd_f32_small(a.f); }
 
 hipError_t launch_attn_bwd_mfma(const AttnBwdArgs &a, int cd, hipStream_t s) {
     if (cd == GT_F32 && attn_bwd_f32_split(a)) {

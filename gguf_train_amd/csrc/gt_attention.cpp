@@ -696,9 +696,8 @@ int attention_backward(const char *who, const gt_tensor *grad_out, const gt_tens
         a.o_f32 = od == GT_F32 && cd != GT_F32;
         apply_dropout(a.f, drop);
         // heads padded to the MFMA kernels' sizes: padded inputs, padded gradients unpadded after.
-        // Float32: only where its MFMA backward takes the padded call (with dropout, 32 dQ
-        // workgroups or more)
-        if (cd == GT_F32 && !(f32_pads(a.f) && (B * H * ((L + 127) / 128) >= 32 || !a.f.dropout))) Dp = 0;
+        // Float32: only where its MFMA backward takes the padded call
+        if (cd == GT_F32 && !f32_pads(a.f)) Dp = 0;
         const gt_tensor *pq = nullptr, *pk = nullptr, *pv = nullptr;
         if (Dp) {
             const gt_tensor *qp = pad_heads(qs, Dp, dev, tmp), *kp = pad_heads(ks, Dp, dev, tmp);

@@ -2,9 +2,9 @@
 bwd_dkdv_f32_kernel with DROP: head sizes 64 and 128, padded heads, key padding or per-element
 masks) against the oracle's composition under the oracle's Philox4x32-10 decisions, at the float32
 bar: forward output and the undropped log-sum-exp, dQ, dK, dV; several key tiles, causal or not,
-GQA, p from 0.05 to 1, the launch log naming the kernels, and the generic backward when the
-decision buffer would exceed GT_ATTN_DROPOUT_BITS_MAX (the float32 dK/dV kernel reads the dQ
-kernel's decisions and does not draw its own)."""
+GQA, p from 0.05 to 1, tiled and small-grid kernels, the launch log naming the kernels, and the
+generic backward when the decision buffer would exceed GT_ATTN_DROPOUT_BITS_MAX (the float32
+dK/dV kernels read the dQ kernel's decisions and do not draw their own)."""
 
 import numpy as np
 import pytest
@@ -19,8 +19,8 @@ from _util import assert_close, randn, to_oracle
 pytestmark = pytest.mark.gpu
 
 CASES = [
-    # B, H, Hkv, L, S, D, causal, key lengths (key padding) or a per-element mask, p;
-    # B * H * ceil(L / 128) >= 32
+    # B, H, Hkv, L, S, D, causal, key lengths (key padding) or a per-element mask, p (below 128
+    # dQ workgroups of the tiled kernels, B * H * ceil(L / 128): the small-grid kernels)
     (2, 16, 8, 300, 300, 64, True, (300, 211), 0.1),
     (1, 32, 32, 257, 257, 128, False, (), 0.5),
     (2, 16, 4, 130, 260, 64, False, (260, 100), 0.2),
@@ -32,6 +32,10 @@ CASES = [
     # per-element masks with dropout (bool: one workgroup per CU for head size 64's dK/dV)
     (2, 16, 8, 130, 200, 64, True, "bool", 0.2),
     (1, 32, 16, 96, 131, 128, False, "add", 0.3),
+    # tiny grids (the small-grid kernels, 4 dQ workgroups of the tiled ones)
+    (1, 4, 4, 128, 128, 64, True, (), 0.2),
+    (1, 2, 1, 40, 300, 128, False, (211,), 0.3),
+    (1, 4, 2, 12, 77, 64, True, "bool", 0.5),
 ]
 
 
@@ -82,7 +86,8 @@ def test_float32_dropout_matches_the_oracle(dev, B, H, Hkv, L, S, D, causal, len
     Dp = 64 if D <= 64 else 128
     what = f"B{B} H{H}/{Hkv} L{L} S{S} D{D} causal={causal} lens={lens} p={p}"
     assert fwd.startswith(f"prefill f32 D={Dp} "), (what, fwd)
-    assert bwd == f"backward mfma f32 D={Dp}", (what, bwd)
+    small = B * H * ((L + 127) // 128) < 128  # the small-grid kernels
+    assert bwd == f"backward mfma f32 D={Dp}" + (" split" if small else ""), (what, bwd)
     _check(q, k, v, dout, mask, causal, p, seed, out, lse, grads, what)
     if p == 1.0:
         assert not out.any() and not any(t.any() for t in grads)
